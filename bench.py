@@ -1,0 +1,245 @@
+"""Benchmark: GeneT5 MoE layer forward (16 experts, top-2, SwiGLU d=768 F=3072) on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config 2|3] [--no-cpu-baseline]
+
+A step is one whole layer forward (router -> dispatch -> gate|up GEMM + SwiGLU
+-> down GEMM -> combine) through the C ABI's g5moe_forward, on synthetic
+inputs already resident in HBM (config 2: 36,400 tokens bf16, uniform routing).
+Prints ONE JSON line.  `value` is tokens/s of the whole layer; `roofline` is
+for the dominant kernel (the grouped gate|up GEMM), its average launch time
+taken from HIP events recorded around that kernel on the stream it runs on, in
+a second timed loop that enqueues the stages one by one.  `cpu_baseline` times
+the CPU oracle (fp32, numpy/BLAS) on a bounded token sample of the same
+workload on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+METRIC = "MoE layer tokens/s + expert-GEMM TFLOP/s (% bf16 peak), 36.4k tok, 16e top-2"
+PEAK_BF16_TFLOPS = 2516.6   # MI355X dense bf16 MFMA (256 CU x 2.4 GHz x 4096 FLOP/clk)
+PEAK_HBM_GBS = 8000.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", type=int, default=2, choices=(2, 3))
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
+    return ap.parse_args()
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return model
+
+
+def blas_threads() -> int:
+    try:
+        from threadpoolctl import threadpool_info
+        n = [i.get("num_threads", 1) for i in threadpool_info() if i.get("user_api") == "blas"]
+        return int(max(n)) if n else 1
+    except Exception:
+        return 1
+
+
+def cpu_baseline(inp, n_sample: int) -> dict:
+    """Oracle (fp32 numpy/BLAS) on the first n_sample tokens of the workload."""
+    import oracle
+    from genet5_amd import synth
+    x = inp.x[:n_sample]
+    wg = synth.bf16_bits_to_f32(inp.w_gate)
+    wu = synth.bf16_bits_to_f32(inp.w_up)
+    wd = synth.bf16_bits_to_f32(inp.w_down)
+    run = lambda: oracle.moe_forward(x, inp.w_router, wg, wu, wd, inp.top_k, bias=inp.bias)
+    run()  # warm-up
+    ts = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        run()
+        ts.append(time.perf_counter() - t0)
+    t = float(np.median(ts))
+    return {
+        "value": n_sample / t,
+        "unit": "tokens/s",
+        "cores": blas_threads(),
+        "kind": "port",
+        "sample": (f"oracle.moe_forward (C router + numpy fp32 BLAS experts) on the first "
+                   f"{n_sample} tokens of the same workload, median of 3 after 1 warm-up, "
+                   f"{t * 1e3:.1f} ms per run; host {cpu_info()}, os.cpu_count()={os.cpu_count()}"),
+        "expert_tflops": 6 * 768 * 3072 * n_sample * inp.top_k / t / 1e12,
+    }
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no "
+              "multi-GPU path; the layer would shard by tokens (data parallel) or by experts, "
+              "neither of which is built here.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from genet5_amd import ops, synth
+
+    dev = torch.device("cuda:0")
+    cfg = args.config
+    inp = synth.make_config(cfg, seed=0)
+    N, d = inp.x.shape
+    E, F = inp.w_gate.shape[0], inp.w_gate.shape[1]
+    k = inp.top_k
+    tt = synth.to_torch(inp, dev)
+    x, wr, bias = tt["x"], tt["w_router"], tt["bias"]
+    wgu = ops.pack_gate_up(tt["w_gate"], tt["w_up"])
+    wd = tt["w_down"]
+    del tt
+    buf = ops.ForwardBuffers(N, d, F, E, k, x.dtype, dev)
+    torch.cuda.synchronize()
+
+    def step():
+        ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+
+    # Per-stage times: same kernels enqueued stage by stage with events between.
+    r = buf.routing
+    y_perm = torch.empty((N * k, d), dtype=torch.bfloat16, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    names = ["router", "dispatch", "gate_up", "down", "combine"]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+    acc = {n: 0.0 for n in names}
+    import ctypes
+    from genet5_amd import _lib
+    P = ops._ptr
+    shape = buf.shape
+    S = ops._stream(dev)
+    ws = buf.ws
+
+    def staged():
+        ev[0].record(stream)
+        _lib.call("g5moe_router_topk", P(x), P(wr), P(bias), P(r.topk_idx), P(r.topk_w), None,
+                  ctypes.byref(shape), S)
+        ev[1].record(stream)
+        _lib.call("g5moe_dispatch", P(r.topk_idx), P(r.counts), P(r.offsets), P(r.perm),
+                  P(r.inv_pos), P(ws), ctypes.byref(shape), S)
+        ev[2].record(stream)
+        _lib.call("g5moe_expert_gate_up", P(x), P(r.perm), P(r.offsets), P(wgu), P(ws),
+                  ctypes.byref(shape), S)
+        ev[3].record(stream)
+        _lib.call("g5moe_expert_down", P(r.offsets), P(wd), P(y_perm), P(ws), ctypes.byref(shape), S)
+        ev[4].record(stream)
+        _lib.call("g5moe_combine", P(y_perm), P(r.inv_pos), P(r.topk_w), P(buf.y),
+                  ctypes.byref(shape), S)
+        ev[5].record(stream)
+
+    for _ in range(3):
+        staged()
+    torch.cuda.synchronize()
+    n_staged = max(10, args.steps)
+    for _ in range(n_staged):
+        staged()
+        torch.cuda.synchronize()
+        for i, n in enumerate(names):
+            acc[n] += ev[i].elapsed_time(ev[i + 1])
+    stage_ms = {n: acc[n] / n_staged for n in names}
+
+    flops_gu = 4 * d * F * N * k
+    flops_dn = 2 * d * F * N * k
+    gu_tflops = flops_gu / (stage_ms["gate_up"] * 1e-3) / 1e12
+    dn_tflops = flops_dn / (stage_ms["down"] * 1e-3) / 1e12
+    gemm_ms = stage_ms["gate_up"] + stage_ms["down"]
+    gemm_tflops = (flops_gu + flops_dn) / (gemm_ms * 1e-3) / 1e12
+    router_bytes = N * d * 2 + E * d * 2 + N * k * 8
+    combine_bytes = N * k * d * 2 + N * k * 8 + N * d * 2
+
+    # Routing parity on the benchmark inputs (outside the timed regions).
+    import oracle
+    ref_l = oracle.router_logits(inp.x, inp.w_router, inp.bias)
+    ref_i, _ = oracle.topk_gates_c(ref_l, k)
+    rc, ro, rp, ri = oracle.dispatch(ref_i, E)
+    step()
+    torch.cuda.synchronize()
+    routing_exact = bool(
+        np.array_equal(r.topk_idx.cpu().numpy(), ref_i)
+        and np.array_equal(r.counts.cpu().numpy(), rc)
+        and np.array_equal(r.perm.cpu().numpy(), rp)
+        and np.array_equal(r.inv_pos.cpu().numpy(), ri))
+
+    traffic = None
+    tf_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                           "gate_up_traffic.json")
+    if os.path.exists(tf_path):
+        with open(tf_path) as f:
+            traffic = json.load(f).get("bytes_per_launch")
+
+    out = {
+        "metric": METRIC,
+        "value": N / (ms * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": synth.CONFIGS[cfg]["name"],
+            "n_tokens": N, "d_model": d, "d_ff": F, "n_experts": E, "top_k": k,
+            "seed": 0,
+        },
+        "expert_gemm_tflops": gemm_tflops,
+        "expert_gemm_pct_bf16_peak": 100.0 * gemm_tflops / PEAK_BF16_TFLOPS,
+        "stage_ms": stage_ms,
+        "stage_rates": {
+            "gate_up_tflops": gu_tflops,
+            "down_tflops": dn_tflops,
+            "router_gbs": router_bytes / (stage_ms["router"] * 1e-3) / 1e9,
+            "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
+        },
+        "roofline": {
+            "kernel": "grouped_gemm_kernel<256,256,2,4,true> (gate|up + SwiGLU)",
+            "bound": "mfma",
+            "achieved": gu_tflops,
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": gu_tflops / PEAK_BF16_TFLOPS,
+            "traffic": traffic,
+            "flop_per_launch": flops_gu,
+        },
+        "routing_bit_exact_vs_oracle": routing_exact,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(inp, min(args.cpu_sample_tokens, N))
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,115 @@
+"""ctypes binding of libg5moe.so (the C ABI declared in include/g5moe.h).
+
+The library is loaded from this package directory.  There is no fallback: if
+the shared library is missing, `lib()` raises, so no caller can silently run a
+CPU or PyTorch path in its place.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libg5moe.so"
+
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+
+STATUS_NAMES = {0: "OK", 1: "INVALID_ARG", 2: "UNSUPPORTED", 3: "HIP_ERROR"}
+
+EXPORTED = (
+    "g5moe_last_error",
+    "g5moe_version",
+    "g5moe_workspace_size",
+    "g5moe_pack_gate_up",
+    "g5moe_router_topk",
+    "g5moe_dispatch",
+    "g5moe_expert_gate_up",
+    "g5moe_expert_down",
+    "g5moe_expert_swiglu",
+    "g5moe_combine",
+    "g5moe_forward",
+)
+
+
+class Shape(ctypes.Structure):
+    """Mirror of `g5moe_shape`."""
+
+    _fields_ = [
+        ("n_tokens", ctypes.c_int64),
+        ("d_model", ctypes.c_int32),
+        ("d_ff", ctypes.c_int32),
+        ("n_experts", ctypes.c_int32),
+        ("top_k", ctypes.c_int32),
+        ("x_dtype", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+class G5MoEError(RuntimeError):
+    """A nonzero g5moe_status, with the library's message."""
+
+    def __init__(self, status: int, func: str, message: str):
+        self.status = status
+        super().__init__(f"{func} failed with {STATUS_NAMES.get(status, status)}: {message}")
+
+
+_P = ctypes.c_void_p
+_SHAPE_P = ctypes.POINTER(Shape)
+_SIGS = {
+    "g5moe_last_error": ([], ctypes.c_char_p),
+    "g5moe_version": ([], ctypes.c_int32),
+    "g5moe_workspace_size": ([_SHAPE_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
+    "g5moe_pack_gate_up": ([_P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_router_topk": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_dispatch": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_expert_gate_up": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_expert_down": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_expert_swiglu": ([_P, _P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_combine": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load (once) and return the shared library; raises if it is not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise ImportError(
+                    f"{LIB_PATH} is missing: build it with `python -m genet5_amd.build` "
+                    "(there is no CPU fallback)")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            for name, (argtypes, restype) in _SIGS.items():
+                fn = getattr(handle, name)
+                fn.argtypes = argtypes
+                fn.restype = restype
+            _lib = handle
+    return _lib
+
+
+def call(name: str, *args) -> None:
+    """Call `name` and raise G5MoEError on a nonzero status."""
+    L = lib()
+    st = getattr(L, name)(*args)
+    if st != 0:
+        msg = L.g5moe_last_error().decode(errors="replace")
+        raise G5MoEError(st, name, msg)
+
+
+def make_shape(n_tokens: int, d_model: int, d_ff: int, n_experts: int, top_k: int,
+               x_dtype: int) -> Shape:
+    return Shape(int(n_tokens), int(d_model), int(d_ff), int(n_experts), int(top_k),
+                 int(x_dtype), 0)
+
+
+def workspace_size(shape: Shape) -> int:
+    n = ctypes.c_size_t(0)
+    call("g5moe_workspace_size", ctypes.byref(shape), ctypes.byref(n))
+    return int(n.value)

@@ -1,0 +1,221 @@
+// C ABI of libg5moe.so: argument validation, workspace carving, launches.
+// Declarations and contracts live in include/g5moe.h.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "g5moe_internal.h"
+
+using namespace g5moe;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+g5moe_status fail(g5moe_status st, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return st;
+}
+
+g5moe_status hip_status(hipError_t e, const char* where) {
+  if (e == hipSuccess) return G5MOE_OK;
+  return fail(G5MOE_ERR_HIP, "%s: HIP error %d (%s)", where, int(e), hipGetErrorString(e));
+}
+
+g5moe_status check_shape(const g5moe_shape* s) {
+  if (s == nullptr) return fail(G5MOE_ERR_INVALID_ARG, "shape is NULL");
+  if (s->reserved != 0) return fail(G5MOE_ERR_INVALID_ARG, "shape.reserved must be 0");
+  if (s->n_tokens < 0) return fail(G5MOE_ERR_INVALID_ARG, "n_tokens < 0");
+  if (s->x_dtype != G5MOE_DTYPE_BF16 && s->x_dtype != G5MOE_DTYPE_F32)
+    return fail(G5MOE_ERR_INVALID_ARG, "x_dtype %d is neither bf16 (0) nor f32 (1)",
+                int(s->x_dtype));
+  const int d = s->d_model;
+  if (d != 128 && d != 256 && d != 512 && d != 768)
+    return fail(G5MOE_ERR_UNSUPPORTED, "d_model %d not in {128, 256, 512, 768}", d);
+  if (s->d_ff < 128 || s->d_ff % 128 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "d_ff %d is not a positive multiple of 128",
+                int(s->d_ff));
+  if (s->n_experts < 1 || s->n_experts > kMaxExperts)
+    return fail(G5MOE_ERR_UNSUPPORTED, "n_experts %d not in [1, %d]", int(s->n_experts),
+                kMaxExperts);
+  if (s->top_k < 1 || s->top_k > kMaxTopK || s->top_k > s->n_experts)
+    return fail(G5MOE_ERR_UNSUPPORTED, "top_k %d not in [1, min(n_experts, %d)]",
+                int(s->top_k), kMaxTopK);
+  // Sorted positions and row offsets are int32; h rows are addressed as int32 * F.
+  if (s->n_tokens * s->top_k > int64_t(INT32_MAX) / 2)
+    return fail(G5MOE_ERR_UNSUPPORTED, "n_tokens * top_k = %lld exceeds the int32 index range",
+                (long long)(s->n_tokens * s->top_k));
+  return G5MOE_OK;
+}
+
+#define G5_CHECK(expr)                   \
+  do {                                   \
+    const g5moe_status _st = (expr);     \
+    if (_st != G5MOE_OK) return _st;     \
+  } while (0)
+
+#define G5_NONNULL(p)                                                             \
+  do {                                                                            \
+    if ((p) == nullptr) return fail(G5MOE_ERR_INVALID_ARG, "%s is NULL", #p);     \
+  } while (0)
+
+inline hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// The bf16 view of x the expert GEMMs read: x itself, or its rounded copy.
+const uint16_t* gemm_input(const void* x, char* ws, const g5moe_shape& s, hipStream_t st,
+                           hipError_t* err) {
+  *err = hipSuccess;
+  if (s.x_dtype == G5MOE_DTYPE_BF16) return static_cast<const uint16_t*>(x);
+  const WorkspaceLayout L = workspace_layout(s);
+  uint16_t* xb = reinterpret_cast<uint16_t*>(ws + L.xb);
+  *err = launch_cast_f32_bf16(static_cast<const float*>(x), xb, s.n_tokens * s.d_model, st);
+  return xb;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* g5moe_last_error(void) { return g_err; }
+
+int32_t g5moe_version(void) { return (1 << 16) | 0; }
+
+g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(bytes);
+  *bytes = workspace_layout(*shape).total;
+  return G5MOE_OK;
+}
+
+g5moe_status g5moe_pack_gate_up(const void* w_gate, const void* w_up, void* w_gate_up,
+                                const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(w_gate);
+  G5_NONNULL(w_up);
+  G5_NONNULL(w_gate_up);
+  return hip_status(launch_pack_gate_up(static_cast<const uint16_t*>(w_gate),
+                                        static_cast<const uint16_t*>(w_up),
+                                        static_cast<uint16_t*>(w_gate_up), *shape,
+                                        as_stream(stream)),
+                    "g5moe_pack_gate_up");
+}
+
+g5moe_status g5moe_router_topk(const void* x, const void* w_router, const float* bias,
+                               int32_t* topk_idx, float* topk_w, float* logits,
+                               const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(x);
+  G5_NONNULL(w_router);
+  G5_NONNULL(topk_idx);
+  G5_NONNULL(topk_w);
+  return hip_status(
+      launch_router(x, w_router, bias, topk_idx, topk_w, logits, *shape, as_stream(stream)),
+      "g5moe_router_topk");
+}
+
+g5moe_status g5moe_dispatch(const int32_t* topk_idx, int32_t* counts, int32_t* offsets,
+                            int32_t* perm, int32_t* inv_pos, void* ws,
+                            const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(counts);
+  G5_NONNULL(offsets);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(topk_idx);
+    G5_NONNULL(perm);
+    G5_NONNULL(inv_pos);
+    G5_NONNULL(ws);
+  }
+  return hip_status(launch_dispatch(topk_idx, counts, offsets, perm, inv_pos,
+                                    static_cast<char*>(ws), *shape, as_stream(stream)),
+                    "g5moe_dispatch");
+}
+
+g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int32_t* offsets,
+                                  const void* w_gate_up, void* ws,
+                                  const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(x);
+  G5_NONNULL(perm);
+  G5_NONNULL(offsets);
+  G5_NONNULL(w_gate_up);
+  G5_NONNULL(ws);
+  char* w = static_cast<char*>(ws);
+  const hipStream_t st = as_stream(stream);
+  hipError_t err;
+  const uint16_t* xb = gemm_input(x, w, *shape, st, &err);
+  G5_CHECK(hip_status(err, "g5moe_expert_gate_up (cast)"));
+  const WorkspaceLayout L = workspace_layout(*shape);
+  return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
+                                   reinterpret_cast<uint16_t*>(w + L.h), *shape, st),
+                    "g5moe_expert_gate_up");
+}
+
+g5moe_status g5moe_expert_down(const int32_t* offsets, const void* w_down, void* y_perm,
+                               void* ws, const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(offsets);
+  G5_NONNULL(w_down);
+  G5_NONNULL(y_perm);
+  G5_NONNULL(ws);
+  const WorkspaceLayout L = workspace_layout(*shape);
+  const uint16_t* h = reinterpret_cast<const uint16_t*>(static_cast<char*>(ws) + L.h);
+  return hip_status(launch_down(h, offsets, static_cast<const uint16_t*>(w_down),
+                                static_cast<uint16_t*>(y_perm), *shape, as_stream(stream)),
+                    "g5moe_expert_down");
+}
+
+g5moe_status g5moe_expert_swiglu(const void* x, const int32_t* perm, const int32_t* offsets,
+                                 const void* w_gate_up, const void* w_down, void* y_perm,
+                                 void* ws, const g5moe_shape* shape, void* stream) {
+  G5_CHECK(g5moe_expert_gate_up(x, perm, offsets, w_gate_up, ws, shape, stream));
+  return g5moe_expert_down(offsets, w_down, y_perm, ws, shape, stream);
+}
+
+g5moe_status g5moe_combine(const void* y_perm, const int32_t* inv_pos, const float* topk_w,
+                           void* y, const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(y_perm);
+  G5_NONNULL(inv_pos);
+  G5_NONNULL(topk_w);
+  G5_NONNULL(y);
+  return hip_status(launch_combine(static_cast<const uint16_t*>(y_perm), inv_pos, topk_w, y,
+                                   *shape, as_stream(stream)),
+                    "g5moe_combine");
+}
+
+g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bias,
+                           const void* w_gate_up, const void* w_down, void* y,
+                           int32_t* topk_idx, float* topk_w, int32_t* counts,
+                           int32_t* offsets, int32_t* perm, int32_t* inv_pos, void* ws,
+                           const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(counts);
+  G5_NONNULL(offsets);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(x);
+    G5_NONNULL(w_router);
+    G5_NONNULL(w_gate_up);
+    G5_NONNULL(w_down);
+    G5_NONNULL(y);
+    G5_NONNULL(topk_idx);
+    G5_NONNULL(topk_w);
+    G5_NONNULL(perm);
+    G5_NONNULL(inv_pos);
+    G5_NONNULL(ws);
+  }
+  G5_CHECK(g5moe_router_topk(x, w_router, bias, topk_idx, topk_w, nullptr, shape, stream));
+  G5_CHECK(g5moe_dispatch(topk_idx, counts, offsets, perm, inv_pos, ws, shape, stream));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  const WorkspaceLayout L = workspace_layout(*shape);
+  void* y_perm = static_cast<char*>(ws) + L.y_perm;
+  G5_CHECK(g5moe_expert_swiglu(x, perm, offsets, w_gate_up, w_down, y_perm, ws, shape, stream));
+  return g5moe_combine(y_perm, inv_pos, topk_w, y, shape, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,72 @@
+// Gated combine / unpermute back to token order.
+//
+// New stage (no reference counterpart; its result takes the place of
+// `self.wo(hidden)` in FeedForward.forward, lib/blocks/_component.py:52).
+// y[t, :] = sum over slots s in increasing order of w[t, s] * y_perm[inv_pos[t, s], :],
+// accumulated in fp32 (acc = fma(w, v, acc) from acc = 0), rounded once.
+//
+// One thread produces 8 consecutive outputs (16 bytes of bf16 input per slot),
+// so a wavefront reads and writes contiguous 1 KB row segments.  HBM-bound:
+// N*k*d*2 + N*k*8 + N*d*2 bytes (168.3 MB at N = 36,400, k = 2, d = 768).
+#include "g5moe_internal.h"
+
+namespace g5moe {
+namespace {
+
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y_perm,
+                                                      const int32_t* __restrict__ inv_pos,
+                                                      const float* __restrict__ w,
+                                                      void* __restrict__ y, int64_t n_tokens,
+                                                      int d, int topk) {
+  const int cpr = d / 8;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_tokens * cpr) return;
+  const int64_t t = i / cpr;
+  const int ch = int(i - t * cpr);
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int s = 0; s < topk; ++s) {
+    const int32_t p = inv_pos[t * topk + s];
+    if (p < 0) continue;
+    const float ws = w[t * topk + s];
+    const uint4 v = *reinterpret_cast<const uint4*>(y_perm + int64_t(p) * d + ch * 8);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] = __builtin_fmaf(ws, __uint_as_float(vv[j] << 16), acc[2 * j]);
+      acc[2 * j + 1] = __builtin_fmaf(ws, __uint_as_float(vv[j] & 0xffff0000u), acc[2 * j + 1]);
+    }
+  }
+  if constexpr (OUT_F32) {
+    float4* o = reinterpret_cast<float4*>(static_cast<float*>(y) + t * d + ch * 8);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  } else {
+    uint4 o;
+    o.x = pack_bf16x2(acc[0], acc[1]);
+    o.y = pack_bf16x2(acc[2], acc[3]);
+    o.z = pack_bf16x2(acc[4], acc[5]);
+    o.w = pack_bf16x2(acc[6], acc[7]);
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(y) + t * d + ch * 8) = o;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
+                          void* y, const g5moe_shape& s, hipStream_t st) {
+  const int64_t work = s.n_tokens * (s.d_model / 8);
+  if (work == 0) return hipSuccess;
+  const unsigned grid = unsigned((work + 255) / 256);
+  if (s.x_dtype == G5MOE_DTYPE_F32)
+    hipLaunchKernelGGL(combine_kernel<true>, dim3(grid), dim3(256), 0, st, y_perm, inv_pos, w,
+                       y, s.n_tokens, s.d_model, s.top_k);
+  else
+    hipLaunchKernelGGL(combine_kernel<false>, dim3(grid), dim3(256), 0, st, y_perm, inv_pos, w,
+                       y, s.n_tokens, s.d_model, s.top_k);
+  return hipGetLastError();
+}
+
+}  // namespace g5moe

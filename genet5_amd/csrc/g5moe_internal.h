@@ -1,0 +1,86 @@
+// Internal declarations shared by the gfx950 kernels and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "../../include/g5moe.h"
+
+namespace g5moe {
+
+constexpr int kMaxExperts = 16;
+constexpr int kMaxTopK = 4;
+constexpr int kDispatchBlock = 256;  // assignments per dispatch block
+
+// Byte offsets of the workspace regions (each 256-byte aligned).
+struct WorkspaceLayout {
+  size_t xb;         // bf16 copy of x when x is f32        [N, d]
+  size_t blk_counts; // per-dispatch-block expert counts    [nblk, E]
+  size_t colprefix;  // exclusive prefix over blocks        [nblk, E]
+  size_t rank;       // stable rank inside the block        [N*k]
+  size_t h;          // SwiGLU activations, bf16            [N*k, F]
+  size_t y_perm;     // expert outputs, bf16                [N*k, d]
+  size_t total;
+  int64_t nblk;      // dispatch blocks
+};
+
+inline size_t align256(size_t v) { return (v + 255) & ~size_t(255); }
+
+inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
+  WorkspaceLayout w{};
+  const int64_t nk = s.n_tokens * s.top_k;
+  w.nblk = (nk + kDispatchBlock - 1) / kDispatchBlock;
+  size_t off = 0;
+  w.xb = off;
+  off += align256(s.x_dtype == G5MOE_DTYPE_F32 ? size_t(s.n_tokens) * s.d_model * 2 : 0);
+  w.blk_counts = off;
+  off += align256(size_t(w.nblk) * s.n_experts * 4);
+  w.colprefix = off;
+  off += align256(size_t(w.nblk) * s.n_experts * 4);
+  w.rank = off;
+  off += align256(size_t(nk) * 4);
+  w.h = off;
+  off += align256(size_t(nk) * s.d_ff * 2);
+  w.y_perm = off;
+  off += align256(size_t(nk) * s.d_model * 2);
+  w.total = off;
+  return w;
+}
+
+// ---- kernel launchers (each returns hipSuccess or the launch error) -------
+hipError_t launch_router(const void* x, const void* wr, const float* bias, int32_t* idx,
+                         float* w, float* logits, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets,
+                           int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
+                           hipStream_t st);
+hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
+                          const uint16_t* wgu, uint16_t* h, const g5moe_shape& s,
+                          hipStream_t st);
+hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
+                       uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
+                          void* y, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_pack_gate_up(const uint16_t* wg, const uint16_t* wu, uint16_t* wgu,
+                               const g5moe_shape& s, hipStream_t st);
+hipError_t launch_cast_f32_bf16(const float* x, uint16_t* xb, int64_t n, hipStream_t st);
+
+// ---- device helpers -------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {
+  return __uint_as_float(b << 16);
+}
+
+// Round-to-nearest-even fp32 -> bf16 bits (NaN stays NaN, quieted).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return uint16_t(u >> 16);
+}
+
+// Two fp32 -> packed bf16x2 (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+}
+
+}  // namespace g5moe

@@ -1,0 +1,135 @@
+"""MoEFeedForward — drop-in for GeneT5's FeedForward with 16 SwiGLU experts, top-2.
+
+Reference interface (lib/blocks/_component.py:35-52): `FeedForward(embed_dim,
+ff_dim, dropout=0.0, activation='gelu_new')`, constructed positionally as
+`FeedForward(embed_dim, ff_dim, dropout)` at lib/blocks/encoder.py:69 and called
+as `self.ff(normed)` at lib/blocks/encoder.py:88, whose single tensor result
+(same shape and dtype as the input) is added into the residual at :89.  The
+expert body is that module's formula with activation='silu':
+`wo(silu(wi_0 x) * wi_1 x)`, bias-free (:42-44, :48-52).
+
+This module keeps that constructor prefix and forward contract and adds
+`num_experts` and `top_k`.  Every forward runs the HIP kernels of
+libg5moe.so on the input's GPU; there is no CPU or eager-PyTorch fallback.
+Parameters, in nn.Linear orientation [out, in]:
+    router.weight  [E, d]      (dtype of the model)
+    w_gate         [E, F, d]   expert gate projections  (wi_0 of each expert)
+    w_up           [E, F, d]   expert up projections    (wi_1 of each expert)
+    w_down         [E, d, F]   expert down projections  (wo of each expert)
+    router_bias    [E] fp32 buffer, optional (added to the logits before top-k)
+The expert GEMMs run in bf16 with fp32 accumulation whatever the parameter
+dtype; the interleaved gate|up copy they read is cached and rebuilt only when a
+weight changes.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import ops
+
+
+@torch.library.custom_op("g5moe::moe_forward", mutates_args=())
+def _moe_forward_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
+                    w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int) -> torch.Tensor:
+    return ops.moe_forward(x, w_router, w_gate_up, w_down, top_k, bias=bias)
+
+
+@_moe_forward_op.register_fake
+def _(x, w_router, bias, w_gate_up, w_down, top_k):
+    return torch.empty_like(x)
+
+
+class MoEFeedForward(nn.Module):
+    """Top-k routed mixture of SwiGLU experts (forward only)."""
+
+    def __init__(self, embed_dim: int, ff_dim: int, dropout: float = 0.0,
+                 activation: str = "silu", num_experts: int = 16, top_k: int = 2,
+                 router_bias: bool = False):
+        super().__init__()
+        if activation != "silu":
+            raise ValueError(
+                f"MoEFeedForward experts are SwiGLU (activation='silu'); got {activation!r}")
+        if embed_dim not in ops.SUPPORTED_D_MODEL:
+            raise ValueError(f"embed_dim {embed_dim} not in {ops.SUPPORTED_D_MODEL}")
+        if ff_dim % 128 != 0 or ff_dim <= 0:
+            raise ValueError(f"ff_dim {ff_dim} must be a positive multiple of 128")
+        if not (1 <= num_experts <= ops.MAX_EXPERTS):
+            raise ValueError(f"num_experts {num_experts} not in [1, {ops.MAX_EXPERTS}]")
+        if not (1 <= top_k <= min(num_experts, ops.MAX_TOP_K)):
+            raise ValueError(f"top_k {top_k} not in [1, min(num_experts, {ops.MAX_TOP_K})]")
+        self.embed_dim = embed_dim
+        self.ff_dim = ff_dim
+        self.num_experts = num_experts
+        self.top_k = top_k
+        self.dropout = float(dropout)
+        self.router = nn.Linear(embed_dim, num_experts, bias=False)
+        self.w_gate = nn.Parameter(torch.empty(num_experts, ff_dim, embed_dim))
+        self.w_up = nn.Parameter(torch.empty(num_experts, ff_dim, embed_dim))
+        self.w_down = nn.Parameter(torch.empty(num_experts, embed_dim, ff_dim))
+        if router_bias:
+            self.register_buffer("router_bias", torch.zeros(num_experts, dtype=torch.float32))
+        else:
+            self.router_bias = None
+        self.reset_parameters()
+        self._packed_key = None
+        self._packed = None
+
+    def reset_parameters(self) -> None:
+        # nn.Linear's default init, per expert matrix.
+        for w in (self.w_gate, self.w_up, self.w_down):
+            bound = 1.0 / math.sqrt(w.shape[-1])
+            nn.init.uniform_(w, -bound, bound)
+        self.router.reset_parameters()
+
+    @torch.no_grad()
+    def load_dense(self, wi_0: torch.Tensor, wi_1: torch.Tensor, wo: torch.Tensor) -> None:
+        """Upcycle a dense FeedForward (wi_0/wi_1/wo weights) into every expert."""
+        self.w_gate.copy_(wi_0.unsqueeze(0).expand_as(self.w_gate))
+        self.w_up.copy_(wi_1.unsqueeze(0).expand_as(self.w_up))
+        self.w_down.copy_(wo.unsqueeze(0).expand_as(self.w_down))
+
+    def _expert_weights(self):
+        """bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F], cached by version."""
+        key = (self.w_gate.data_ptr(), self.w_gate._version, self.w_up.data_ptr(),
+               self.w_up._version, self.w_down.data_ptr(), self.w_down._version,
+               self.w_gate.device, self.w_gate.dtype)
+        if self._packed_key != key:
+            with torch.no_grad():
+                wg = self.w_gate.detach().to(torch.bfloat16).contiguous()
+                wu = self.w_up.detach().to(torch.bfloat16).contiguous()
+                wd = self.w_down.detach().to(torch.bfloat16).contiguous()
+                self._packed = (ops.pack_gate_up(wg, wu), wd)
+            self._packed_key = key
+        return self._packed
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.training and self.dropout > 0.0:
+            raise NotImplementedError(
+                "MoEFeedForward is forward-only: dropout on the expert hidden state in "
+                "training mode is not implemented")
+        if x.shape[-1] != self.embed_dim:
+            raise ValueError(f"last dim {x.shape[-1]} != embed_dim {self.embed_dim}")
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.embed_dim)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        w_router = self.router.weight
+        if w_router.dtype != x2.dtype:
+            w_router = w_router.to(x2.dtype)
+        wgu, wd = self._expert_weights()
+        y = _moe_forward_op(x2, w_router.contiguous(), self.router_bias, wgu, wd, self.top_k)
+        return y.view(*lead, self.embed_dim)
+
+    def forward_with_routing(self, x: torch.Tensor):
+        """Forward that also returns the routing tensors (ops.Routing)."""
+        lead = x.shape[:-1]
+        x2 = x.reshape(-1, self.embed_dim).contiguous()
+        w_router = self.router.weight.to(x2.dtype).contiguous()
+        wgu, wd = self._expert_weights()
+        y, r = ops.moe_forward(x2, w_router, wgu, wd, self.top_k, bias=self.router_bias,
+                               return_routing=True)
+        return y.view(*lead, self.embed_dim), r

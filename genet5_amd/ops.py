@@ -1,0 +1,227 @@
+"""Functional PyTorch wrappers over the C ABI (include/g5moe.h).
+
+Each wrapper checks device, dtype, contiguity and shapes on the host (the C
+ABI cannot see buffer sizes), allocates its outputs with the PyTorch caching
+allocator, and enqueues the HIP kernels on the current stream of the input's
+device.  Nothing here synchronises the host, and nothing falls back to a CPU
+path: a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+SUPPORTED_D_MODEL = (128, 256, 512, 768)
+MAX_EXPERTS = 16
+MAX_TOP_K = 4
+
+
+def _ptr(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def _dtype_code(dt: torch.dtype) -> int:
+    if dt == torch.bfloat16:
+        return _lib.DTYPE_BF16
+    if dt == torch.float32:
+        return _lib.DTYPE_F32
+    raise TypeError(f"g5moe supports bfloat16 and float32 activations, got {dt}")
+
+
+def _require(t: torch.Tensor, name: str, shape, dtype, device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_device(x: torch.Tensor) -> torch.device:
+    if x.device.type != "cuda":
+        raise RuntimeError(
+            f"g5moe runs on the GPU only (got a tensor on {x.device}); there is no CPU path")
+    return x.device
+
+
+def make_shape(x2d: torch.Tensor, d_ff: int, n_experts: int, top_k: int) -> _lib.Shape:
+    return _lib.make_shape(x2d.shape[0], x2d.shape[1], d_ff, n_experts, top_k,
+                           _dtype_code(x2d.dtype))
+
+
+def workspace(shape: _lib.Shape, device: torch.device) -> torch.Tensor:
+    return torch.empty(_lib.workspace_size(shape), dtype=torch.uint8, device=device)
+
+
+def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    """[E, F, d] gate and up (bf16) -> interleaved [E, 2F, d] (32-row groups)."""
+    dev = _check_device(w_gate)
+    E, F, d = w_gate.shape
+    _require(w_gate, "w_gate", (E, F, d), torch.bfloat16, dev)
+    _require(w_up, "w_up", (E, F, d), torch.bfloat16, dev)
+    out = torch.empty((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
+    shape = _lib.make_shape(0, d, F, E, 1, _lib.DTYPE_BF16)
+    _lib.call("g5moe_pack_gate_up", _ptr(w_gate), _ptr(w_up), _ptr(out), ctypes.byref(shape),
+              _stream(dev))
+    return out
+
+
+def router_topk(x2d: torch.Tensor, w_router: torch.Tensor, top_k: int,
+                bias: Optional[torch.Tensor] = None, return_logits: bool = False):
+    """Router on [N, d] -> (topk_idx int32 [N, k], topk_w fp32 [N, k][, logits fp32 [N, E]])."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E = w_router.shape[0]
+    _require(x2d, "x", (N, d), x2d.dtype, dev)
+    _require(w_router, "w_router", (E, d), x2d.dtype, dev)
+    if bias is not None:
+        _require(bias, "bias", (E,), torch.float32, dev)
+    shape = _lib.make_shape(N, d, 128, E, top_k, _dtype_code(x2d.dtype))
+    idx = torch.empty((N, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((N, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((N, E), dtype=torch.float32, device=dev) if return_logits else None
+    _lib.call("g5moe_router_topk", _ptr(x2d), _ptr(w_router), _ptr(bias), _ptr(idx), _ptr(w),
+              _ptr(logits), ctypes.byref(shape), _stream(dev))
+    return (idx, w, logits) if return_logits else (idx, w)
+
+
+def dispatch(topk_idx: torch.Tensor, n_experts: int, d_model: int = 128):
+    """topk_idx int32 [N, k] -> (counts [E], offsets [E+1], perm [N*k], inv_pos [N*k])."""
+    dev = _check_device(topk_idx)
+    N, k = topk_idx.shape
+    _require(topk_idx, "topk_idx", (N, k), torch.int32, dev)
+    shape = _lib.make_shape(N, d_model, 128, n_experts, k, _lib.DTYPE_BF16)
+    counts = torch.empty((n_experts,), dtype=torch.int32, device=dev)
+    offsets = torch.empty((n_experts + 1,), dtype=torch.int32, device=dev)
+    perm = torch.empty((N * k,), dtype=torch.int32, device=dev)
+    inv_pos = torch.empty((N * k,), dtype=torch.int32, device=dev)
+    ws = workspace(shape, dev)
+    _lib.call("g5moe_dispatch", _ptr(topk_idx), _ptr(counts), _ptr(offsets), _ptr(perm),
+              _ptr(inv_pos), _ptr(ws), ctypes.byref(shape), _stream(dev))
+    return counts, offsets, perm, inv_pos
+
+
+def expert_swiglu(x2d: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor,
+                  w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int,
+                  return_h: bool = False):
+    """Both grouped expert GEMMs -> y_perm bf16 [N*k, d] (and h bf16 [N*k, F] if asked)."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E, F2, _ = w_gate_up.shape
+    F = F2 // 2
+    _require(x2d, "x", (N, d), x2d.dtype, dev)
+    _require(perm, "perm", (N * top_k,), torch.int32, dev)
+    _require(offsets, "offsets", (E + 1,), torch.int32, dev)
+    _require(w_gate_up, "w_gate_up", (E, 2 * F, d), torch.bfloat16, dev)
+    _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
+    shape = _lib.make_shape(N, d, F, E, top_k, _dtype_code(x2d.dtype))
+    ws = workspace(shape, dev)
+    y_perm = torch.empty((N * top_k, d), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_expert_swiglu", _ptr(x2d), _ptr(perm), _ptr(offsets), _ptr(w_gate_up),
+              _ptr(w_down), _ptr(y_perm), _ptr(ws), ctypes.byref(shape), _stream(dev))
+    if return_h:
+        off = _h_offset(shape)
+        h = ws[off: off + N * top_k * F * 2].view(torch.bfloat16).view(N * top_k, F)
+        return y_perm, h
+    return y_perm
+
+
+def _h_offset(shape: _lib.Shape) -> int:
+    """Byte offset of h inside the workspace (mirrors WorkspaceLayout in g5moe_internal.h)."""
+    a = lambda v: (v + 255) & ~255
+    N, d, F, E, k = shape.n_tokens, shape.d_model, shape.d_ff, shape.n_experts, shape.top_k
+    nblk = (N * k + 255) // 256
+    off = a(N * d * 2 if shape.x_dtype == _lib.DTYPE_F32 else 0)
+    off += a(nblk * E * 4) * 2
+    off += a(N * k * 4)
+    return off
+
+
+def combine(y_perm: torch.Tensor, inv_pos: torch.Tensor, topk_w: torch.Tensor,
+            out_dtype: torch.dtype) -> torch.Tensor:
+    """y[t] = sum_s w[t, s] * y_perm[inv_pos[t, s]] -> [N, d] in out_dtype."""
+    dev = _check_device(y_perm)
+    N, k = topk_w.shape
+    d = y_perm.shape[1]
+    _require(y_perm, "y_perm", (N * k, d), torch.bfloat16, dev)
+    _require(inv_pos, "inv_pos", (N * k,), torch.int32, dev)
+    _require(topk_w, "topk_w", (N, k), torch.float32, dev)
+    shape = _lib.make_shape(N, d, 128, max(k, 1), k, _dtype_code(out_dtype))
+    y = torch.empty((N, d), dtype=out_dtype, device=dev)
+    _lib.call("g5moe_combine", _ptr(y_perm), _ptr(inv_pos), _ptr(topk_w), _ptr(y),
+              ctypes.byref(shape), _stream(dev))
+    return y
+
+
+@dataclass
+class Routing:
+    topk_idx: torch.Tensor  # int32 [N, k]
+    topk_w: torch.Tensor    # fp32 [N, k]
+    counts: torch.Tensor    # int32 [E]
+    offsets: torch.Tensor   # int32 [E + 1]
+    perm: torch.Tensor      # int32 [N*k]
+    inv_pos: torch.Tensor   # int32 [N*k]
+
+
+class ForwardBuffers:
+    """Preallocated outputs + workspace for repeated g5moe_forward calls of one shape."""
+
+    def __init__(self, n_tokens: int, d_model: int, d_ff: int, n_experts: int, top_k: int,
+                 dtype: torch.dtype, device: torch.device):
+        self.shape = _lib.make_shape(n_tokens, d_model, d_ff, n_experts, top_k,
+                                     _dtype_code(dtype))
+        dev = device
+        self.y = torch.empty((n_tokens, d_model), dtype=dtype, device=dev)
+        self.routing = Routing(
+            topk_idx=torch.empty((n_tokens, top_k), dtype=torch.int32, device=dev),
+            topk_w=torch.empty((n_tokens, top_k), dtype=torch.float32, device=dev),
+            counts=torch.empty((n_experts,), dtype=torch.int32, device=dev),
+            offsets=torch.empty((n_experts + 1,), dtype=torch.int32, device=dev),
+            perm=torch.empty((n_tokens * top_k,), dtype=torch.int32, device=dev),
+            inv_pos=torch.empty((n_tokens * top_k,), dtype=torch.int32, device=dev),
+        )
+        self.ws = workspace(self.shape, dev)
+
+
+def moe_forward(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
+                w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None,
+                buffers: Optional[ForwardBuffers] = None, return_routing: bool = False):
+    """Whole MoE layer forward on [N, d] through g5moe_forward."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E, F2, _ = w_gate_up.shape
+    F = F2 // 2
+    if not (1 <= top_k <= min(E, MAX_TOP_K)):
+        raise ValueError(f"top_k={top_k} not in [1, min(E, {MAX_TOP_K})]")
+    _require(x2d, "x", (N, d), x2d.dtype, dev)
+    _require(w_router, "w_router", (E, d), x2d.dtype, dev)
+    _require(w_gate_up, "w_gate_up", (E, 2 * F, d), torch.bfloat16, dev)
+    _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
+    if bias is not None:
+        _require(bias, "bias", (E,), torch.float32, dev)
+    if buffers is None:
+        buffers = ForwardBuffers(N, d, F, E, top_k, x2d.dtype, dev)
+    else:
+        s = buffers.shape
+        if (s.n_tokens, s.d_model, s.d_ff, s.n_experts, s.top_k, s.x_dtype) != (
+                N, d, F, E, top_k, _dtype_code(x2d.dtype)) or buffers.y.device != dev:
+            raise ValueError("buffers were made for another shape, dtype or device")
+    r = buffers.routing
+    _lib.call("g5moe_forward", _ptr(x2d), _ptr(w_router), _ptr(bias), _ptr(w_gate_up),
+              _ptr(w_down), _ptr(buffers.y), _ptr(r.topk_idx), _ptr(r.topk_w), _ptr(r.counts),
+              _ptr(r.offsets), _ptr(r.perm), _ptr(r.inv_pos), _ptr(buffers.ws),
+              ctypes.byref(buffers.shape), _stream(dev))
+    return (buffers.y, r) if return_routing else buffers.y

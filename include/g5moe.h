@@ -1,0 +1,159 @@
+/*
+ * g5moe.h — C ABI of the MI355X (gfx950) mixture-of-experts layer forward.
+ *
+ * The reference (97YearsOldProgrammer/GeneT5) has no FFI for this path: its
+ * expert body is the Python module `FeedForward` (lib/blocks/_component.py:35-52),
+ * constructed at lib/blocks/encoder.py:69 and called as `self.ff(normed)` at
+ * lib/blocks/encoder.py:88.  The reference snapshot has no router, dispatch or
+ * combine at all; README.md:12 names the layer (16 experts, top-2, upcycled from
+ * the dense FFN).  Each entry point below replaces one stage of that module's
+ * forward, as the comment on it says.  The Python host mirror
+ * (genet5_amd/moe.py, class MoEFeedForward) binds these through ctypes.
+ *
+ * Conventions (all entry points):
+ *   - Every buffer is device memory owned by the caller; the library allocates
+ *     nothing.  `ws` is a caller-provided workspace of g5moe_workspace_size()
+ *     bytes, 256-byte aligned.
+ *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL = the
+ *     null stream) and runs asynchronously; no entry point synchronises the host.
+ *   - Return value 0 (G5MOE_OK) on success; otherwise a status code and a
+ *     message readable through g5moe_last_error() (thread-local).  No C++
+ *     exception crosses the ABI.
+ *   - Results are deterministic: the same inputs give bitwise-identical outputs.
+ *   - Tensors are row-major.  bf16 values are raw IEEE bfloat16 bit patterns
+ *     (uint16); weights use nn.Linear orientation [out, in].
+ */
+#ifndef G5MOE_H
+#define G5MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum g5moe_status {
+  G5MOE_OK = 0,
+  G5MOE_ERR_INVALID_ARG = 1, /* null pointer, negative size, bad dtype      */
+  G5MOE_ERR_UNSUPPORTED = 2, /* valid but unsupported shape (see below)     */
+  G5MOE_ERR_HIP = 3          /* HIP runtime error while enqueueing          */
+} g5moe_status;
+
+typedef enum g5moe_dtype {
+  G5MOE_DTYPE_BF16 = 0,
+  G5MOE_DTYPE_F32 = 1
+} g5moe_dtype;
+
+/* Shape of one MoE layer call.
+ *   n_tokens  N  >= 0 (tokens of the flattened [B, S, d] input)
+ *   d_model   d  in {128, 256, 512, 768}      (router lanes hold d/64 columns)
+ *   d_ff      F  multiple of 128, >= 128
+ *   n_experts E  in [1, 16]
+ *   top_k     k  in [1, min(E, 4)]
+ *   x_dtype   dtype of x, of the router weight and of y (bf16 or f32).
+ *             Expert weights and the expert GEMMs are always bf16 with fp32
+ *             accumulation; an f32 x is rounded to bf16 on its way into them.
+ */
+typedef struct g5moe_shape {
+  int64_t n_tokens;
+  int32_t d_model;
+  int32_t d_ff;
+  int32_t n_experts;
+  int32_t top_k;
+  int32_t x_dtype;
+  int32_t reserved; /* must be 0 */
+} g5moe_shape;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* g5moe_last_error(void);
+
+/* ABI version: (major << 16) | minor. */
+int32_t g5moe_version(void);
+
+/* Bytes of workspace the stage entry points and g5moe_forward need for `shape`. */
+g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes);
+
+/* Repack the two expert input projections into the interleaved gate|up layout
+ * the grouped gate/up GEMM reads.  Replaces holding `wi_0` / `wi_1` as two
+ * nn.Linear weights (lib/blocks/_component.py:42-43; gate = wi_0, up = wi_1 as
+ * lib/model/build.py:30-34 splits the dense checkpoint).
+ *   w_gate, w_up : bf16 [E, F, d]
+ *   w_gate_up    : bf16 [E, 2F, d]; row 64*g + r is gate row 32*g + r for
+ *                  r < 32 and up row 32*g + (r - 32) for r >= 32.          */
+g5moe_status g5moe_pack_gate_up(const void* w_gate, const void* w_up, void* w_gate_up,
+                                const g5moe_shape* shape, void* stream);
+
+/* Router: fp32 logits, top-k with a lower-index tie-break, renormalised gates.
+ * New stage (the reference has no router; README.md:12 "16 experts top-2").
+ *   x        : [N, d] in x_dtype          w_router : [E, d] in x_dtype
+ *   bias     : fp32 [E] or NULL (added to the logits before top-k)
+ *   topk_idx : int32 [N, k] out           topk_w   : fp32 [N, k] out
+ *   logits   : fp32 [N, E] out, or NULL
+ * Logit order (bit-exact contract): lane c in [0, 64) forms the fused
+ * multiply-add chain over columns [c*d/64, (c+1)*d/64) in increasing order
+ * from 0; the 64 partial sums are added pairwise, pairing lanes that differ in
+ * bit 5, then 4, 3, 2, 1, 0; the bias is added last.  Top-k scans experts in
+ * increasing order and replaces the incumbent only on a strictly greater
+ * logit; slot 0 holds the largest.  Gate s = exp(l_s - l_0) / sum_j exp(l_j - l_0). */
+g5moe_status g5moe_router_topk(const void* x, const void* w_router, const float* bias,
+                               int32_t* topk_idx, float* topk_w, float* logits,
+                               const g5moe_shape* shape, void* stream);
+
+/* Dispatch: per-expert counts, exclusive offsets and the stable permutation of
+ * the flattened assignments a = t*k + s into expert-contiguous order.
+ * New stage (no reference counterpart).
+ *   topk_idx : int32 [N, k] in            counts  : int32 [E] out
+ *   offsets  : int32 [E + 1] out          perm    : int32 [N*k] out (sorted
+ *              position -> a; equal to a stable argsort of topk_idx.flatten())
+ *   inv_pos  : int32 [N*k] out (a -> sorted position)
+ * Entries outside [0, E) are not placed: their inv_pos is -1 and they are not
+ * counted. */
+g5moe_status g5moe_dispatch(const int32_t* topk_idx, int32_t* counts, int32_t* offsets,
+                            int32_t* perm, int32_t* inv_pos, void* ws,
+                            const g5moe_shape* shape, void* stream);
+
+/* Grouped gate|up GEMM with SwiGLU: for sorted position p of expert e and
+ * token t = perm[p] / k, h[p] = silu(x[t] . Wg_e^T) * (x[t] . Wu_e^T), stored
+ * bf16 into the workspace.  Replaces `self.wi_0(x)`, `self.wi_1(x)` and the
+ * fused SiLU-mul of FeedForward.forward (lib/blocks/_component.py:50,
+ * _FUSED_ACT['silu'] at :31).
+ *   x : [N, d] in x_dtype;  w_gate_up : packed bf16 [E, 2F, d]. */
+g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int32_t* offsets,
+                                  const void* w_gate_up, void* ws,
+                                  const g5moe_shape* shape, void* stream);
+
+/* Grouped down GEMM: y_perm[p] = h[p] . Wd_e^T (bf16 out, fp32 accumulate),
+ * h read from the workspace written by g5moe_expert_gate_up.  Replaces
+ * `self.wo(hidden)` (lib/blocks/_component.py:44, :52).
+ *   w_down : bf16 [E, d, F];  y_perm : bf16 [N*k, d] out. */
+g5moe_status g5moe_expert_down(const int32_t* offsets, const void* w_down, void* y_perm,
+                               void* ws, const g5moe_shape* shape, void* stream);
+
+/* Both expert GEMMs in order (gate|up + SwiGLU, then down). */
+g5moe_status g5moe_expert_swiglu(const void* x, const int32_t* perm, const int32_t* offsets,
+                                 const void* w_gate_up, const void* w_down, void* y_perm,
+                                 void* ws, const g5moe_shape* shape, void* stream);
+
+/* Gated combine back to token order: y[t] = sum over s in slot order of
+ * topk_w[t, s] * y_perm[inv_pos[t, s]] (fp32 accumulate, one rounding to
+ * x_dtype).  Slots with inv_pos < 0 are skipped.  New stage.
+ *   y : [N, d] in x_dtype out. */
+g5moe_status g5moe_combine(const void* y_perm, const int32_t* inv_pos, const float* topk_w,
+                           void* y, const g5moe_shape* shape, void* stream);
+
+/* The whole layer forward, enqueued as router -> dispatch -> gate|up ->
+ * down -> combine.  Replaces FeedForward.forward (lib/blocks/_component.py:48-52)
+ * when the module is the MoE.  Routing outputs are written to the caller's
+ * buffers so they can be inspected; y_perm lives in the workspace. */
+g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bias,
+                           const void* w_gate_up, const void* w_down, void* y,
+                           int32_t* topk_idx, float* topk_w, int32_t* counts,
+                           int32_t* offsets, int32_t* perm, int32_t* inv_pos, void* ws,
+                           const g5moe_shape* shape, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* G5MOE_H */

@@ -1,0 +1,134 @@
+/*
+ * CPU oracle for the MoE layer's integer and reduction-order-sensitive parts.
+ * TEST INFRASTRUCTURE ONLY: tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library, as the checker.  No product code
+ * path calls it.
+ *
+ * The reference (97YearsOldProgrammer/GeneT5) has no MoE; this restates the
+ * layer whose expert body is FeedForward (lib/blocks/_component.py:35-52,
+ * activation 'silu') and whose router/top-2 is named at README.md:12.
+ *
+ *   router logits : the reduction order the C ABI fixes (include/g5moe.h,
+ *                   g5moe_router_topk): 64 lane chunks of d/64 columns, each a
+ *                   fused multiply-add chain from 0 in increasing column order;
+ *                   chunk sums added pairwise over lane bits 5,4,3,2,1,0; bias
+ *                   added last.
+ *   top-k         : increasing-expert scan, replace on strictly greater.
+ *   dispatch      : stable counting sort of the flattened assignments.
+ *
+ * Build: oracle/build.py (gcc -O2 -ffp-contract=off, so only the explicit
+ * fmaf calls fuse).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+static inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = (uint32_t)b << 16;
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+
+static float tree64(float* p) {
+  for (int m = 32; m >= 1; m >>= 1)
+    for (int l = 0; l < m; ++l) p[l] = p[l] + p[l + m];
+  return p[0];
+}
+
+/* logits[t*E + e] for x, w given as fp32 (already widened from bf16 if needed). */
+static void logits_rowf(const float* xr, const float* w, const float* bias, int d, int E,
+                        float* out) {
+  const int L = d / 64;
+  float p[64];
+  for (int e = 0; e < E; ++e) {
+    const float* wr = w + (size_t)e * d;
+    for (int c = 0; c < 64; ++c) {
+      float acc = 0.0f;
+      for (int i = 0; i < L; ++i) acc = fmaf(xr[c * L + i], wr[c * L + i], acc);
+      p[c] = acc;
+    }
+    float v = tree64(p);
+    if (bias) v = v + bias[e];
+    out[e] = v;
+  }
+}
+
+int g5o_router_logits_f32(const float* x, const float* w, const float* bias, int64_t n,
+                          int d, int E, float* logits) {
+  if (d % 64 != 0 || d <= 0) return 1;
+  for (int64_t t = 0; t < n; ++t)
+    logits_rowf(x + (size_t)t * d, w, bias, d, E, logits + (size_t)t * E);
+  return 0;
+}
+
+int g5o_router_logits_bf16(const uint16_t* x, const uint16_t* w, const float* bias,
+                           int64_t n, int d, int E, float* logits, float* scratch) {
+  /* scratch: (E + 1) * d floats */
+  if (d % 64 != 0 || d <= 0) return 1;
+  float* wf = scratch;
+  float* xf = scratch + (size_t)E * d;
+  for (size_t i = 0; i < (size_t)E * d; ++i) wf[i] = bf16_to_f32(w[i]);
+  for (int64_t t = 0; t < n; ++t) {
+    for (int j = 0; j < d; ++j) xf[j] = bf16_to_f32(x[(size_t)t * d + j]);
+    logits_rowf(xf, wf, bias, d, E, logits + (size_t)t * E);
+  }
+  return 0;
+}
+
+/* Top-k by the scan rule; gates from the textbook softmax (double), renormalised
+ * over the selected experts: w_s = p[i_s] / sum_j p[i_j]. */
+int g5o_topk(const float* logits, int64_t n, int E, int k, int32_t* idx, float* w) {
+  if (k < 1 || k > E || E > 64) return 1;
+  for (int64_t t = 0; t < n; ++t) {
+    const float* l = logits + (size_t)t * E;
+    uint64_t chosen = 0;
+    int sel[64];
+    for (int s = 0; s < k; ++s) {
+      int best = -1;
+      for (int e = 0; e < E; ++e) {
+        if ((chosen >> e) & 1u) continue;
+        if (best < 0 || l[e] > l[best]) best = e;
+      }
+      chosen |= (uint64_t)1 << best;
+      sel[s] = best;
+    }
+    double mx = -INFINITY;
+    for (int e = 0; e < E; ++e)
+      if ((double)l[e] > mx) mx = l[e];
+    double z = 0.0;
+    for (int e = 0; e < E; ++e) z += exp((double)l[e] - mx);
+    double ps = 0.0;
+    for (int s = 0; s < k; ++s) ps += exp((double)l[sel[s]] - mx) / z;
+    for (int s = 0; s < k; ++s) {
+      idx[(size_t)t * k + s] = sel[s];
+      w[(size_t)t * k + s] = (float)((exp((double)l[sel[s]] - mx) / z) / ps);
+    }
+  }
+  return 0;
+}
+
+/* Stable counting sort of a = t*k + s by idx[a]; entries outside [0, E) are
+ * skipped (inv_pos = -1). */
+int g5o_dispatch(const int32_t* idx, int64_t nk, int E, int32_t* counts, int32_t* offsets,
+                 int32_t* perm, int32_t* inv_pos) {
+  for (int e = 0; e < E; ++e) counts[e] = 0;
+  for (int64_t a = 0; a < nk; ++a)
+    if (idx[a] >= 0 && idx[a] < E) counts[idx[a]]++;
+  offsets[0] = 0;
+  for (int e = 0; e < E; ++e) offsets[e + 1] = offsets[e] + counts[e];
+  int32_t fill[64];
+  if (E > 64) return 1;
+  for (int e = 0; e < E; ++e) fill[e] = offsets[e];
+  for (int64_t a = 0; a < nk; ++a) {
+    const int e = idx[a];
+    if (e < 0 || e >= E) {
+      inv_pos[a] = -1;
+      continue;
+    }
+    const int32_t p = fill[e]++;
+    perm[p] = (int32_t)a;
+    inv_pos[a] = p;
+  }
+  return 0;
+}

@@ -1,0 +1,279 @@
+"""CPU restatement of the MoE layer forward — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
+this module, as the checker.
+
+Functions, what they follow, and what pins them (tests/test_oracle.py):
+
+router_logits / router_logits_np
+    logits[t, e] = sum_j x[t, j] * Wr[e, j] (+ b[e]) — nn.Linear(d, E,
+    bias=False) in the orientation of lib/blocks/_component.py:42-44; the
+    router itself is new (README.md:12).  Summation order is the one the C ABI
+    fixes (include/g5moe.h, g5moe_router_topk).  router_logits is the C
+    implementation (oracle/g5moe_oracle.c), router_logits_np an independent
+    vectorised numpy restatement.  Pins: C == numpy bit for bit on bf16 inputs
+    (products exact in fp32); both within fp32 rounding of a float64 matmul;
+    exactly-representable sums (integer-valued inputs) equal the closed form;
+    a permutation of the lane chunks that the order forbids changes bits.
+topk_gates / topk_gates_c
+    Top-k by an increasing-expert scan that replaces only on a strictly greater
+    logit (ties -> lower index; slot 0 = largest); gates = softmax over all
+    experts (float64), renormalised over the k chosen.  Pins: constructed ties,
+    numpy argsort(-logits, stable) on tie-free rows, gates == closed form
+    1 / (1 + exp(l1 - l0)) for k = 2, sum to 1, k = E and E = 1 cases.
+dispatch / dispatch_c
+    counts, exclusive offsets, perm = stable argsort of topk_idx.flatten(),
+    inv_pos = its inverse.  Pins: pure-Python brute force on small inputs,
+    numpy argsort(kind='stable'), bijection and per-token invariants.
+expert_forward
+    h = silu(X Wg^T) * (X Wu^T), y = h Wd^T per expert over its rows —
+    FeedForward.forward (lib/blocks/_component.py:48-52, 'silu' at :31); with
+    storage="bf16" h and y are rounded to bf16 where the bf16 dataflow stores
+    them (round_bf16 is pinned against torch's bf16 cast).  Pins:
+    float64 brute force on tiny inputs; upcycling invariant (all experts equal
+    one dense FeedForward => MoE output == dense output, since the k gates sum
+    to 1); zero down weights => zero output; E = 1, k = 1 reduces to dense.
+combine
+    y[t] = sum_s w[t, s] * y_perm[inv_pos[t, s]], fp32, slot order.  Pins: a
+    permutation-equivariance check (permuting tokens permutes y) and the
+    upcycling invariant above.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+from typing import Optional
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+_LIB = None
+
+
+def _clib():
+    global _LIB
+    if _LIB is None:
+        path = _HERE / "liboracle.so"
+        if not path.exists():
+            from . import build as _b
+            _b.build()
+        L = ctypes.CDLL(str(path))
+        P = ctypes.c_void_p
+        L.g5o_router_logits_f32.argtypes = [P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, P]
+        L.g5o_router_logits_bf16.argtypes = [P, P, P, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                             P, P]
+        L.g5o_topk.argtypes = [P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, P, P]
+        L.g5o_dispatch.argtypes = [P, ctypes.c_int64, ctypes.c_int, P, P, P, P]
+        for f in (L.g5o_router_logits_f32, L.g5o_router_logits_bf16, L.g5o_topk, L.g5o_dispatch):
+            f.restype = ctypes.c_int
+        _LIB = L
+    return _LIB
+
+
+def _p(a: Optional[np.ndarray]):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(a: np.ndarray) -> np.ndarray:
+    """Round to the nearest bf16 (ties to even), returned widened to fp32."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+    r = ((u + (np.uint32(0x7FFF) + ((u >> 16) & 1))) >> 16) << 16
+    return r.astype(np.uint32).view(np.float32)
+
+
+def widen(a: np.ndarray) -> np.ndarray:
+    """uint16 bf16 bits -> fp32; float arrays pass through unchanged."""
+    return bf16_to_f32(a) if a.dtype == np.uint16 else np.asarray(a)
+
+
+# ---- router ------------------------------------------------------------------
+
+def router_logits(x: np.ndarray, w: np.ndarray, bias: Optional[np.ndarray] = None) -> np.ndarray:
+    """C implementation.  x [N, d], w [E, d]: both fp32 or both uint16 bf16 bits."""
+    N, d = x.shape
+    E = w.shape[0]
+    out = np.empty((N, E), dtype=np.float32)
+    b = None if bias is None else np.ascontiguousarray(bias, np.float32)
+    if x.dtype == np.uint16:
+        xx = np.ascontiguousarray(x)
+        ww = np.ascontiguousarray(w, np.uint16)
+        scratch = np.empty((E + 1) * d, dtype=np.float32)
+        rc = _clib().g5o_router_logits_bf16(_p(xx), _p(ww), _p(b), N, d, E, _p(out), _p(scratch))
+    else:
+        xx = np.ascontiguousarray(x, np.float32)
+        ww = np.ascontiguousarray(w, np.float32)
+        rc = _clib().g5o_router_logits_f32(_p(xx), _p(ww), _p(b), N, d, E, _p(out))
+    if rc != 0:
+        raise ValueError("d must be a positive multiple of 64")
+    return out
+
+
+def router_logits_np(x_f32: np.ndarray, w_f32: np.ndarray, bias: Optional[np.ndarray] = None,
+                     chunk: int = 4096) -> np.ndarray:
+    """Vectorised numpy restatement of the same order.  Bit-exact with the C version
+    when every product x*w is exact in fp32 (bf16 inputs); fp32 inputs need the
+    fused multiply-add of the C version."""
+    N, d = x_f32.shape
+    E = w_f32.shape[0]
+    L = d // 64
+    W = np.ascontiguousarray(w_f32, np.float32).reshape(E, 64, L)
+    out = np.empty((N, E), dtype=np.float32)
+    for t0 in range(0, N, chunk):
+        X = np.ascontiguousarray(x_f32[t0:t0 + chunk], np.float32).reshape(-1, 64, L)
+        acc = np.zeros((X.shape[0], E, 64), dtype=np.float32)
+        for i in range(L):
+            acc = acc + X[:, None, :, i] * W[None, :, :, i]
+        m = 32
+        while m >= 1:
+            acc = acc[..., :m] + acc[..., m:2 * m]
+            m //= 2
+        r = acc[..., 0]
+        if bias is not None:
+            r = r + np.asarray(bias, np.float32)[None, :]
+        out[t0:t0 + chunk] = r
+    return out
+
+
+def topk_gates(logits: np.ndarray, k: int):
+    """Scan top-k + renormalised softmax gates (numpy).  -> (idx int32 [N,k], w fp32 [N,k])."""
+    N, E = logits.shape
+    chosen = np.zeros((N, E), dtype=bool)
+    idx = np.empty((N, k), dtype=np.int32)
+    rows = np.arange(N)
+    for s in range(k):
+        best = np.full(N, -1, dtype=np.int64)
+        bv = np.zeros(N, dtype=np.float32)
+        for e in range(E):
+            le = logits[:, e]
+            take = (~chosen[:, e]) & ((best < 0) | (le > bv))
+            best = np.where(take, e, best)
+            bv = np.where(take, le, bv)
+        idx[:, s] = best
+        chosen[rows, best] = True
+    l64 = logits.astype(np.float64)
+    mx = l64.max(axis=1, keepdims=True)
+    p = np.exp(l64 - mx)
+    p /= p.sum(axis=1, keepdims=True)
+    ps = np.take_along_axis(p, idx.astype(np.int64), axis=1)
+    w = (ps / ps.sum(axis=1, keepdims=True)).astype(np.float32)
+    return idx, w
+
+
+def topk_gates_c(logits: np.ndarray, k: int):
+    N, E = logits.shape
+    lg = np.ascontiguousarray(logits, np.float32)
+    idx = np.empty((N, k), dtype=np.int32)
+    w = np.empty((N, k), dtype=np.float32)
+    if _clib().g5o_topk(_p(lg), N, E, k, _p(idx), _p(w)) != 0:
+        raise ValueError("bad k / E")
+    return idx, w
+
+
+# ---- dispatch ----------------------------------------------------------------
+
+def dispatch(topk_idx: np.ndarray, n_experts: int):
+    """-> counts [E], offsets [E+1], perm [N*k], inv_pos [N*k] (all int32)."""
+    flat = np.ascontiguousarray(topk_idx, np.int64).reshape(-1)
+    valid = (flat >= 0) & (flat < n_experts)
+    key = np.where(valid, flat, n_experts)
+    order = np.argsort(key, kind="stable")
+    nvalid = int(valid.sum())
+    perm = order[:nvalid].astype(np.int32)
+    counts = np.bincount(flat[valid], minlength=n_experts).astype(np.int32)
+    offsets = np.zeros(n_experts + 1, dtype=np.int32)
+    offsets[1:] = np.cumsum(counts)
+    inv_pos = np.full(flat.shape[0], -1, dtype=np.int32)
+    inv_pos[perm] = np.arange(nvalid, dtype=np.int32)
+    return counts, offsets, perm, inv_pos
+
+
+def dispatch_c(topk_idx: np.ndarray, n_experts: int):
+    flat = np.ascontiguousarray(topk_idx, np.int32).reshape(-1)
+    nk = flat.shape[0]
+    counts = np.empty(n_experts, np.int32)
+    offsets = np.empty(n_experts + 1, np.int32)
+    perm = np.full(nk, -1, np.int32)
+    inv_pos = np.empty(nk, np.int32)
+    if _clib().g5o_dispatch(_p(flat), nk, n_experts, _p(counts), _p(offsets), _p(perm),
+                            _p(inv_pos)) != 0:
+        raise ValueError("n_experts > 64")
+    return counts, offsets, perm[: int(offsets[-1])], inv_pos
+
+
+# ---- experts and combine ---------------------------------------------------------
+
+def _silu(g: np.ndarray) -> np.ndarray:
+    return g / (1.0 + np.exp(-g))
+
+
+def expert_forward(x_f: np.ndarray, perm: np.ndarray, offsets: np.ndarray, top_k: int,
+                   w_gate: np.ndarray, w_up: np.ndarray, w_down: np.ndarray,
+                   dtype=np.float32, return_h: bool = False, storage: str = "fp32"):
+    """Per-expert SwiGLU over the routed rows, in `dtype` (float32 or float64).
+    Weights may be uint16 bf16 bits or float arrays.  -> y_perm [N*k, d] (and h).
+
+    storage="bf16" rounds h (the down product's input) and y_perm to bf16, the
+    two points where the layer's bf16 dataflow stores bf16 — as the reference's
+    bf16 FeedForward does with the SiLU-mul output and the `wo` output."""
+    if storage not in ("fp32", "bf16"):
+        raise ValueError(storage)
+    E = w_gate.shape[0]
+    F = w_gate.shape[1]
+    d = x_f.shape[1]
+    nk = perm.shape[0]
+    y_perm = np.zeros((nk, d), dtype=dtype)
+    h_all = np.zeros((nk, F), dtype=dtype) if return_h else None
+    for e in range(E):
+        o0, o1 = int(offsets[e]), int(offsets[e + 1])
+        if o1 == o0:
+            continue
+        rows = x_f[perm[o0:o1] // top_k].astype(dtype, copy=False)
+        wg = widen(w_gate[e]).astype(dtype, copy=False)
+        wu = widen(w_up[e]).astype(dtype, copy=False)
+        wd = widen(w_down[e]).astype(dtype, copy=False)
+        h = _silu(rows @ wg.T) * (rows @ wu.T)
+        if storage == "bf16":
+            h = round_bf16(h).astype(dtype)
+        y = h @ wd.T
+        y_perm[o0:o1] = round_bf16(y) if storage == "bf16" else y
+        if return_h:
+            h_all[o0:o1] = h
+    return (y_perm, h_all) if return_h else y_perm
+
+
+def combine(y_perm: np.ndarray, inv_pos: np.ndarray, topk_w: np.ndarray) -> np.ndarray:
+    N, k = topk_w.shape
+    d = y_perm.shape[1]
+    acc_t = np.float64 if y_perm.dtype == np.float64 else np.float32
+    y = np.zeros((N, d), dtype=acc_t)
+    ip = inv_pos.reshape(N, k)
+    for s in range(k):
+        p = ip[:, s]
+        ok = p >= 0
+        y[ok] = y[ok] + topk_w[ok, s:s + 1].astype(acc_t) * y_perm[p[ok]].astype(acc_t)
+    return y
+
+
+def moe_forward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray,
+                w_down: np.ndarray, top_k: int, bias: Optional[np.ndarray] = None,
+                dtype=np.float32, return_h: bool = False, storage: str = "fp32") -> dict:
+    """Whole layer.  x / w_router: fp32 or uint16 bf16 bits (same kind).  Expert
+    weights: bf16 bits or float arrays.  Returns every intermediate."""
+    E = w_router.shape[0]
+    logits = router_logits(x, w_router, bias)
+    idx, w = topk_gates_c(logits, top_k)
+    counts, offsets, perm, inv_pos = dispatch_c(idx, E)
+    xf = widen(x)
+    res = expert_forward(xf, perm, offsets, top_k, w_gate, w_up, w_down, dtype=dtype,
+                         return_h=return_h, storage=storage)
+    y_perm, h = res if return_h else (res, None)
+    y = combine(y_perm, inv_pos, w)
+    out = dict(logits=logits, topk_idx=idx, topk_w=w, counts=counts, offsets=offsets,
+               perm=perm, inv_pos=inv_pos, y_perm=y_perm, y=y)
+    if return_h:
+        out["h"] = h
+    return out

@@ -1,0 +1,146 @@
+"""CPU-side checks of the C ABI and the host wrappers: the library loads, exports
+every symbol include/g5moe.h declares, validates arguments before touching the
+GPU, and the Python layer refuses to run anywhere but on a GPU."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from genet5_amd import _lib, ops
+from genet5_amd.moe import MoEFeedForward
+
+HEADER = Path(__file__).resolve().parent.parent / "include" / "g5moe.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(g5moe_[a-z_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(g5lib):
+    names = declared_functions()
+    assert len(names) >= 10
+    for n in names:
+        assert hasattr(g5lib, n), n
+    assert set(names) == set(_lib.EXPORTED)
+
+
+def test_version(g5lib):
+    v = g5lib.g5moe_version()
+    assert v >> 16 == 1
+
+
+def shape(**kw):
+    base = dict(n_tokens=36400, d_model=768, d_ff=3072, n_experts=16, top_k=2, x_dtype=0)
+    base.update(kw)
+    return _lib.make_shape(**base)
+
+
+def status_of(fn, *args):
+    st = getattr(_lib.lib(), fn)(*args)
+    return st, _lib.lib().g5moe_last_error().decode()
+
+
+def test_workspace_size_layout(g5lib):
+    s = shape()
+    n = _lib.workspace_size(s)
+    nk = 36400 * 2
+    a = lambda v: (v + 255) // 256 * 256
+    nblk = (nk + 255) // 256
+    assert n == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4) + a(nk * 3072 * 2) + a(nk * 768 * 2)
+    n32 = _lib.workspace_size(shape(x_dtype=1))
+    assert n32 == n + a(36400 * 768 * 2)
+    assert ops._h_offset(s) == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(d_model=640), 2, "d_model"),
+    (dict(d_model=64), 2, "d_model"),
+    (dict(d_ff=100), 2, "d_ff"),
+    (dict(n_experts=17), 2, "n_experts"),
+    (dict(n_experts=0), 2, "n_experts"),
+    (dict(top_k=5), 2, "top_k"),
+    (dict(top_k=3, n_experts=2), 2, "top_k"),
+    (dict(x_dtype=7), 1, "x_dtype"),
+    (dict(n_tokens=-1), 1, "n_tokens"),
+    (dict(n_tokens=2 ** 31), 2, "int32"),
+])
+def test_invalid_shapes_rejected(g5lib, kw, code, msg):
+    n = ctypes.c_size_t(0)
+    st, err = status_of("g5moe_workspace_size", ctypes.byref(shape(**kw)), ctypes.byref(n))
+    assert st == code and msg in err
+
+
+def test_reserved_must_be_zero(g5lib):
+    s = shape()
+    s.reserved = 1
+    n = ctypes.c_size_t(0)
+    st, err = status_of("g5moe_workspace_size", ctypes.byref(s), ctypes.byref(n))
+    assert st == 1 and "reserved" in err
+
+
+def test_null_pointers_rejected_before_any_gpu_work(g5lib):
+    s = shape(n_tokens=8)
+    st, err = status_of("g5moe_router_topk", None, None, None, None, None, None,
+                        ctypes.byref(s), None)
+    assert st == 1 and "x is NULL" in err
+    st, err = status_of("g5moe_forward", *([None] * 13), ctypes.byref(s), None)
+    assert st == 1 and "NULL" in err
+    st, err = status_of("g5moe_combine", None, None, None, None, ctypes.byref(s), None)
+    assert st == 1
+    st, err = status_of("g5moe_dispatch", None, None, None, None, None, None, None, None)
+    assert st == 1 and "shape is NULL" in err
+
+
+def test_error_is_raised_as_exception(g5lib):
+    with pytest.raises(_lib.G5MoEError, match="UNSUPPORTED.*d_model"):
+        _lib.workspace_size(shape(d_model=100))
+
+
+def test_wrappers_refuse_cpu_tensors():
+    x = torch.zeros(4, 128, dtype=torch.bfloat16)
+    w = torch.zeros(4, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.router_topk(x, w, 2)
+    m = MoEFeedForward(128, 128, num_experts=4, top_k=2).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        m(torch.zeros(2, 3, 128, dtype=torch.bfloat16))
+
+
+def test_module_constructor_contract():
+    m = MoEFeedForward(768, 3072, 0.0)  # positional like lib/blocks/encoder.py:69
+    assert m.w_gate.shape == (16, 3072, 768) and m.w_down.shape == (16, 768, 3072)
+    assert m.router.weight.shape == (16, 768) and m.top_k == 2
+    with pytest.raises(ValueError, match="silu"):
+        MoEFeedForward(768, 3072, 0.0, "gelu_new")
+    with pytest.raises(ValueError):
+        MoEFeedForward(768, 3000)
+    with pytest.raises(ValueError):
+        MoEFeedForward(768, 3072, num_experts=4, top_k=5)
+    m.train()
+    m.dropout = 0.1
+    with pytest.raises(NotImplementedError):
+        m(torch.zeros(1, 768))
+
+
+def test_module_load_dense_upcycles():
+    m = MoEFeedForward(128, 256, num_experts=4)
+    wi0, wi1, wo = torch.randn(256, 128), torch.randn(256, 128), torch.randn(128, 256)
+    m.load_dense(wi0, wi1, wo)
+    for e in range(4):
+        assert torch.equal(m.w_gate[e], wi0) and torch.equal(m.w_up[e], wi1)
+        assert torch.equal(m.w_down[e], wo)
+
+
+def test_fake_impl_traces_shape():
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from genet5_amd.moe import _moe_forward_op
+    with FakeTensorMode():
+        x = torch.empty(10, 768, dtype=torch.bfloat16)
+        y = _moe_forward_op(x, torch.empty(16, 768, dtype=torch.bfloat16), None,
+                            torch.empty(16, 6144, 768, dtype=torch.bfloat16),
+                            torch.empty(16, 768, 3072, dtype=torch.bfloat16), 2)
+        assert y.shape == x.shape and y.dtype == x.dtype

@@ -1,0 +1,265 @@
+"""GPU parity: each HIP stage, called through the C ABI, against the CPU oracle.
+
+Routing (indices, counts, offsets, permutation) must be bit-exact; router
+logits are bit-exact by the reduction-order contract; gates within 2e-6 of the
+oracle's float64 softmax.  Expert and layer outputs are checked two ways:
+
+* against the oracle in its bf16-storage mode (h and the expert outputs rounded
+  to bf16 where the kernels store bf16), with the north star's normwise
+  tolerance: max|err| / max|ref| <= 2e-2 and mean|err| / mean|ref| <= 2e-3;
+* against the all-fp32 oracle with max <= 2e-2 and mean <= 4e-3.  At config 2
+  the bf16 rounding of the output alone costs a mean of 1.4e-3 and bf16 h
+  another 1.7e-3; the reference's own bf16 FeedForward dataflow (bf16 gate,
+  up, h and output) measures 3.8e-3 against the same fp32 oracle.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from genet5_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL = 2e-2
+MEAN_REL = 2e-3
+MEAN_REL_VS_FP32 = 4e-3
+
+
+def dev_t(a: np.ndarray, device, bf16: bool = False) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    if bf16:
+        t = t.view(torch.bfloat16)
+    return t.to(device)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    t = t.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        return oracle.moe_oracle.bf16_to_f32(t.view(torch.int16).numpy().view(np.uint16))
+    return t.numpy()
+
+
+def normwise(got: np.ndarray, ref: np.ndarray):
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    r = np.abs(ref.astype(np.float64))
+    return err.max() / max(r.max(), 1e-30), err.mean() / max(r.mean(), 1e-30)
+
+
+def layer_tensors(inp: synth.LayerInputs, device):
+    xb = inp.dtype == "bf16"
+    x = dev_t(inp.x, device, xb)
+    wr = dev_t(inp.w_router, device, xb)
+    wg = dev_t(inp.w_gate, device, True)
+    wu = dev_t(inp.w_up, device, True)
+    wd = dev_t(inp.w_down, device, True)
+    b = None if inp.bias is None else dev_t(inp.bias, device)
+    return x, wr, ops.pack_gate_up(wg, wu), wd, b
+
+
+# ---- router -----------------------------------------------------------------
+
+@pytest.mark.parametrize("n,d,E,k,dtype", [
+    (2048, 768, 16, 2, "bf16"),
+    (2048, 768, 16, 2, "f32"),
+    (1000, 512, 8, 2, "bf16"),
+    (333, 256, 16, 4, "bf16"),
+    (65, 128, 5, 1, "f32"),
+    (1, 768, 16, 2, "bf16"),
+    (77, 768, 1, 1, "bf16"),
+    (300, 768, 16, 4, "f32"),
+])
+def test_router_bit_exact(cuda_device, n, d, E, k, dtype):
+    print(f"router n={n} d={d} E={E} k={k} {dtype}", flush=True)
+    inp = synth.make_layer(n, d_model=d, d_ff=128, n_experts=E, top_k=k, seed=7, dtype=dtype)
+    xb = dtype == "bf16"
+    x = dev_t(inp.x, cuda_device, xb)
+    wr = dev_t(inp.w_router, cuda_device, xb)
+    idx, w, logits = ops.router_topk(x, wr, k, return_logits=True)
+    torch.cuda.synchronize()
+    ref_l = oracle.router_logits(inp.x, inp.w_router)
+    ref_i, ref_w = oracle.topk_gates_c(ref_l, k)
+    np.testing.assert_array_equal(host(logits).view(np.uint32), ref_l.view(np.uint32))
+    np.testing.assert_array_equal(host(idx), ref_i)
+    np.testing.assert_allclose(host(w), ref_w, rtol=0, atol=2e-6)
+
+
+def test_router_bias_and_ties(cuda_device):
+    """Zipf bias; rows with exact ties resolve to the lower expert index."""
+    n, d, E, k = 512, 768, 16, 2
+    inp = synth.make_layer(n, d_model=d, d_ff=128, n_experts=E, top_k=k, seed=3,
+                           dtype="bf16", bias="zipf")
+    wr = inp.w_router.copy()
+    wr[5] = wr[2]            # experts 2 and 5 always tie before bias
+    wr[9] = wr[11] = wr[14]  # 9, 11, 14 tie
+    bias = np.zeros(E, np.float32)
+    bias[[2, 5, 9, 11, 14]] = 10.0  # make the tied experts win
+    x = dev_t(inp.x, cuda_device, True)
+    idx, w = ops.router_topk(x, dev_t(wr, cuda_device, True), k, bias=dev_t(bias, cuda_device))
+    ref_l = oracle.router_logits(inp.x, wr, bias)
+    ref_i, ref_w = oracle.topk_gates_c(ref_l, k)
+    got = host(idx)
+    np.testing.assert_array_equal(got, ref_i)
+    tie_25 = (got[:, 0] == 2) | (got[:, 1] == 2)
+    assert tie_25.any()
+    np.testing.assert_allclose(host(w), ref_w, atol=2e-6)
+
+
+# ---- dispatch -----------------------------------------------------------------
+
+def _dispatch_case(kind: str, n: int, E: int, k: int, rng) -> np.ndarray:
+    if kind == "uniform":
+        return np.stack([rng.choice(E, size=k, replace=False) for _ in range(n)]).astype(np.int32)
+    if kind == "two_experts":
+        base = np.tile(np.array([3, 7][:k], dtype=np.int32), (n, 1))
+        return base
+    if kind == "skewed":
+        p = (np.arange(1, E + 1) ** -1.2)
+        p /= p.sum()
+        return np.stack([rng.choice(E, size=k, replace=False, p=p) for _ in range(n)]).astype(np.int32)
+    raise ValueError(kind)
+
+
+@pytest.mark.parametrize("kind,n,E,k", [
+    ("uniform", 36400, 16, 2),
+    ("skewed", 5000, 16, 2),
+    ("two_experts", 1000, 16, 2),
+    ("uniform", 1, 16, 2),
+    ("uniform", 129, 16, 4),
+    ("uniform", 300, 1, 1),
+    ("uniform", 257, 7, 3),
+])
+def test_dispatch_bit_exact(cuda_device, kind, n, E, k):
+    print(f"dispatch {kind} n={n} E={E} k={k}", flush=True)
+    rng = np.random.default_rng(11)
+    idx = _dispatch_case(kind, n, E, k, rng)
+    counts, offsets, perm, inv_pos = ops.dispatch(dev_t(idx, cuda_device), E)
+    rc, ro, rp, ri = oracle.dispatch(idx, E)
+    np.testing.assert_array_equal(host(counts), rc)
+    np.testing.assert_array_equal(host(offsets), ro)
+    np.testing.assert_array_equal(host(perm), rp)
+    np.testing.assert_array_equal(host(inv_pos), ri)
+
+
+def test_dispatch_out_of_range_entries_skipped(cuda_device):
+    idx = np.array([[0, 1], [5, -1], [2, 99], [1, 0]], dtype=np.int32)
+    counts, offsets, perm, inv_pos = ops.dispatch(dev_t(idx, cuda_device), 4)
+    rc, ro, rp, ri = oracle.dispatch(idx, 4)
+    np.testing.assert_array_equal(host(counts), rc)
+    np.testing.assert_array_equal(host(offsets), ro)
+    np.testing.assert_array_equal(host(perm)[: ro[-1]], rp)
+    np.testing.assert_array_equal(host(inv_pos), ri)
+
+
+# ---- expert GEMMs and combine ---------------------------------------------------
+
+@pytest.mark.parametrize("n,d,F,E,k", [
+    (2048, 768, 3072, 16, 2),
+    (300, 256, 512, 4, 2),
+    (1, 128, 128, 2, 1),
+    (513, 512, 384, 3, 3),
+])
+def test_expert_swiglu(cuda_device, n, d, F, E, k):
+    print(f"experts n={n} d={d} F={F} E={E} k={k}", flush=True)
+    inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=5, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    ref_l = oracle.router_logits(inp.x, inp.w_router)
+    ref_i, ref_w = oracle.topk_gates_c(ref_l, k)
+    rc, ro, rp, ri = oracle.dispatch(ref_i, E)
+    y_perm, h = ops.expert_swiglu(x, dev_t(rp, cuda_device), dev_t(ro, cuda_device), wgu, wd, k,
+                                  return_h=True)
+    torch.cuda.synchronize()
+    ref_y, ref_h = oracle.expert_forward(inp.x_f32(), rp, ro, k, inp.w_gate, inp.w_up,
+                                         inp.w_down, return_h=True, storage="bf16")
+    mx, mean = normwise(host(h), ref_h)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    mx, mean = normwise(host(y_perm), ref_y)
+    print(f"y_perm vs bf16-storage oracle: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+def test_expert_gemm_skewed_and_empty_experts(cuda_device):
+    """Experts with 0 rows and one expert holding most rows."""
+    n, d, F, E, k = 1500, 256, 256, 8, 2
+    inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=9, dtype="bf16")
+    x, _, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    rng = np.random.default_rng(2)
+    idx = np.empty((n, k), np.int32)
+    idx[:, 0] = 6
+    idx[:, 1] = np.where(rng.random(n) < 0.9, 1, 3)
+    rc, ro, rp, ri = oracle.dispatch(idx, E)
+    assert (rc == 0).sum() >= 4
+    y_perm = ops.expert_swiglu(x, dev_t(rp, cuda_device), dev_t(ro, cuda_device), wgu, wd, k)
+    ref_y = oracle.expert_forward(inp.x_f32(), rp, ro, k, inp.w_gate, inp.w_up, inp.w_down,
+                                  storage="bf16")
+    mx, mean = normwise(host(y_perm), ref_y)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_combine(cuda_device, out_dtype):
+    n, d, k = 999, 768, 2
+    rng = np.random.default_rng(4)
+    y_perm = synth.f32_to_bf16_bits(rng.standard_normal((n * k, d), dtype=np.float32))
+    inv = rng.permutation(n * k).astype(np.int32)
+    inv[5] = -1
+    w = rng.random((n, k), dtype=np.float32)
+    y = ops.combine(dev_t(y_perm, cuda_device, True), dev_t(inv, cuda_device),
+                    dev_t(w, cuda_device), out_dtype)
+    ref = oracle.combine(synth.bf16_bits_to_f32(y_perm), inv, w)
+    got = host(y)
+    if out_dtype == torch.float32:
+        np.testing.assert_allclose(got, ref, rtol=1e-6, atol=1e-6)
+    else:
+        # one bf16 rounding of an fp32 value that may differ from the oracle's by 1 ulp
+        np.testing.assert_allclose(got, ref, rtol=2.0 ** -8, atol=1e-6)
+
+
+# ---- whole layer ------------------------------------------------------------------
+
+@pytest.mark.parametrize("cfg", [1, 2, 3])
+def test_forward_configs(cuda_device, cfg):
+    """BASELINE configs 1-3 at full size: routing bit-exact, output within tolerance."""
+    print(f"forward cfg{cfg}", flush=True)
+    inp = synth.make_config(cfg, seed=0)
+    x, wr, wgu, wd, b = layer_tensors(inp, cuda_device)
+    y, r = ops.moe_forward(x, wr, wgu, wd, inp.top_k, bias=b, return_routing=True)
+    torch.cuda.synchronize()
+    ref = oracle.moe_forward(inp.x, inp.w_router, inp.w_gate, inp.w_up, inp.w_down, inp.top_k,
+                             bias=inp.bias, storage="bf16")
+    np.testing.assert_array_equal(host(r.topk_idx), ref["topk_idx"])
+    np.testing.assert_array_equal(host(r.counts), ref["counts"])
+    np.testing.assert_array_equal(host(r.offsets), ref["offsets"])
+    np.testing.assert_array_equal(host(r.perm), ref["perm"])
+    np.testing.assert_array_equal(host(r.inv_pos), ref["inv_pos"])
+    np.testing.assert_allclose(host(r.topk_w), ref["topk_w"], atol=2e-6)
+    mx, mean = normwise(host(y), ref["y"])
+    print(f"cfg{cfg} vs bf16-storage oracle: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (mx, mean)
+    y32 = oracle.combine(oracle.expert_forward(
+        oracle.moe_oracle.widen(inp.x_f32()), ref["perm"], ref["offsets"], inp.top_k,
+        inp.w_gate, inp.w_up, inp.w_down), ref["inv_pos"], ref["topk_w"])
+    mx, mean = normwise(host(y), y32)
+    print(f"cfg{cfg} vs fp32 oracle: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+    assert mx <= MAX_REL and mean <= MEAN_REL_VS_FP32, (mx, mean)
+    if cfg == 3:
+        c = np.sort(ref["counts"])[::-1]
+        assert c[:3].sum() / c.sum() > 0.40
+
+
+def test_forward_deterministic(cuda_device):
+    inp = synth.make_layer(4096, seed=1, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    y1 = ops.moe_forward(x, wr, wgu, wd, 2).clone()
+    y2 = ops.moe_forward(x, wr, wgu, wd, 2).clone()
+    assert torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+
+
+def test_forward_empty(cuda_device):
+    inp = synth.make_layer(0, d_model=128, d_ff=128, n_experts=4, top_k=2, seed=1, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    y, r = ops.moe_forward(x, wr, wgu, wd, 2, return_routing=True)
+    torch.cuda.synchronize()
+    assert y.shape == (0, 128)
+    assert host(r.counts).tolist() == [0, 0, 0, 0]
+    assert host(r.offsets).tolist() == [0, 0, 0, 0, 0]
