@@ -225,7 +225,7 @@ def main():
             "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
         },
         "roofline": {
-            "kernel": "grouped_gemm_kernel<256,256,2,4,true> (gate|up + SwiGLU)",
+            "kernel": "grouped_gemm_dma_kernel<256,256,64,2,true> (gate|up + SwiGLU)",
             "bound": "mfma",
             "achieved": gu_tflops,
             "peak": PEAK_BF16_TFLOPS,

@@ -7,10 +7,12 @@ CPU or PyTorch path in its place.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libg5moe.so"
+# G5MOE_LIB may name another build of the same C ABI (e.g. a tuning variant).
+LIB_PATH = Path(os.environ.get("G5MOE_LIB") or Path(__file__).resolve().parent / "libg5moe.so")
 
 DTYPE_BF16 = 0
 DTYPE_F32 = 1

@@ -70,6 +70,12 @@ def build(verbose: bool = False) -> Path:
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr}")
+    # A kernel whose host stub was dropped (e.g. a device builtin the host pass
+    # rejected) links fine and only fails at dlopen; catch it here.
+    nm = subprocess.run(["nm", "-D", "--undefined-only", str(tmp)], capture_output=True, text=True)
+    missing = [l.split()[-1] for l in nm.stdout.splitlines() if "__device_stub__" in l]
+    if missing:
+        raise RuntimeError(f"undefined kernel host stubs in {tmp.name}: {missing}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -78,9 +78,13 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return uint16_t(u >> 16);
 }
 
-// Two fp32 -> packed bf16x2 (lo in bits 0..15).
+// Two fp32 -> packed bf16x2 (lo in bits 0..15), round-to-nearest-even; one
+// v_cvt_pk_bf16_f32 on gfx950.
+typedef __bf16 g5_bf16x2 __attribute__((ext_vector_type(2)));
+typedef float g5_f32x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16_bits(lo)) | (uint32_t(f32_to_bf16_bits(hi)) << 16);
+  const g5_f32x2 v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, g5_bf16x2));
 }
 
 }  // namespace g5moe

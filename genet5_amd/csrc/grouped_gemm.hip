@@ -56,8 +56,10 @@ struct GemmArgs {
 
 __device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 7); }
 
+// silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
+// below the bf16 rounding of the result).
 __device__ __forceinline__ float silu_mul(float g, float u) {
-  return g / (1.0f + __expf(-g)) * u;
+  return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
 template <int BM, int BN, int WM, int WN, bool SWIGLU>
@@ -231,6 +233,313 @@ __global__ __launch_bounds__(WM* WN * 64) void grouped_gemm_kernel(GemmArgs args
   }
 }
 
+// ---- v2: 4 waves of 128x128, direct global->LDS loads ------------------------
+//
+// 256 threads; the waves form a 2 x 2 grid and each owns a (BM/2) x (BN/2)
+// sub-tile, so a 256 x 256 tile keeps 256 fp32 accumulators per lane (in
+// AGPRs).  Per BK = 64 step a wave reads 32 KB of fragments from LDS for 64
+// MFMAs (2048 cycles of one SIMD's matrix core); with the 64 KB the step writes,
+// LDS carries 192 KB per 2048 cycles.  Global tiles go straight to LDS with
+// global_load_lds_dwordx4: one instruction moves 64 x 16 bytes into a
+// contiguous 1 KB of LDS (8 rows of 128 bytes), lane l landing at byte 16*l, so
+// the XOR swizzle is applied by choosing each lane's global source chunk.  Two
+// LDS stages in separate arrays, prefetch distance one step; the k-loop is
+// unrolled by two so every LDS access names its stage statically.
+struct TileCoord {
+  int e, p_begin, p_end, n0;
+};
+
+template <int BM, int BN>
+__device__ __forceinline__ bool decode_tile(const GemmArgs& args, TileCoord& tc) {
+  const int ntn = args.Nout / BN;
+  int total = 0;
+  for (int e = 0; e < args.n_experts; ++e) {
+    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    total += ((cnt + BM - 1) / BM) * ntn;
+  }
+  const int b = blockIdx.x;
+  if (b >= total) return false;
+  const int q = total >> 3, rem = total & 7, xcd = b & 7;
+  int u = xcd * q + min(xcd, rem) + (b >> 3);
+  int e = 0, mt_e = 0;
+  for (; e < args.n_experts; ++e) {
+    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    mt_e = (cnt + BM - 1) / BM;
+    const int t = mt_e * ntn;
+    if (u < t) break;
+    u -= t;
+  }
+  const int g = u / (kGroupM * ntn);
+  const int first_m = g * kGroupM;
+  const int gs = min(kGroupM, mt_e - first_m);
+  const int rr = u - g * kGroupM * ntn;
+  const int mt = first_m + rr % gs;
+  const int nt = rr / gs;
+  tc.e = e;
+  tc.p_begin = args.offsets[e] + mt * BM;
+  tc.p_end = args.offsets[e + 1];
+  tc.n0 = nt * BN;
+  return true;
+}
+
+// 16 bytes per lane from global memory straight into LDS: lane l of the wave
+// writes lds_base + 16*l (lds_base must be wave-uniform).
+__device__ __forceinline__ void lds_dma16(const void* src, char* lds_base) {
+  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0,
+                                   0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Wait until at most n * PER vector-memory instructions of this thread are
+// outstanding, for a wave-uniform n in [0, MAXN] (the immediate must be a
+// constant, so dispatch over the possible values).
+template <int MAXN, int PER>
+__device__ __forceinline__ void wait_vmcnt_upto(int n) {
+  if constexpr (MAXN <= 0) {
+    wait_vmcnt<0>();
+  } else {
+    if (n >= MAXN)
+      wait_vmcnt<MAXN * PER>();
+    else
+      wait_vmcnt_upto<MAXN - 1, PER>(n);
+  }
+}
+
+template <int BM, int BN, int BK, int STAGES, bool SWIGLU>
+__global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int MB = WTM / 32, NB = WTN / 32;
+  constexpr int RB = BK * 2;          // bytes per tile row
+  constexpr int CPR = RB / 16;        // 16-byte chunks per row
+  constexpr int RPB = 1024 / RB;      // rows per 1 KB DMA block
+  constexpr int G = 256 / RB;         // rows sharing one 256-byte line of the 64 banks
+  constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int AI = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage
+  constexpr int BI = B_BYTES / 1024 / 4;
+  constexpr int KS = BK / 16;
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(STAGES >= 2 && STAGES * STAGE <= 160 * 1024, "LDS");
+  static_assert((STAGES - 1) * (AI + BI) < 64, "vmcnt");
+  static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
+
+  TileCoord tc;
+  if (!decode_tile<BM, BN>(args, tc)) return;
+  const int e = tc.e, p_begin = tc.p_begin, p_end = tc.p_end, n0 = tc.n0;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int K = args.K;
+
+  // LDS layout: tile row r holds RB bytes; logical 16-byte chunk c sits at
+  // physical chunk c ^ sw(r), sw(r) = (r / G) % CPR.  The 64 banks span 256
+  // bytes = G rows, so a 16-lane group reading 16 consecutive rows at one
+  // logical chunk lands in 16 distinct 16-byte bank groups.
+  auto sw = [](int r) { return (r / G) % CPR; };
+  // DMA slots: wave w, instruction j fills block blk = w*AI + j (rows
+  // blk*RPB ..); lane l lands in row l / CPR of it at physical chunk l % CPR.
+  const int lrow = lane / CPR;
+  const int lpc = lane % CPR;
+  const uint16_t* a_src[AI];
+#pragma unroll
+  for (int j = 0; j < AI; ++j) {
+    const int r = (wave * AI + j) * RPB + lrow;
+    const int p = min(p_begin + r, p_end - 1);
+    const int64_t row = args.perm ? int64_t(args.perm[p] / args.topk) : int64_t(p);
+    a_src[j] = args.A + row * K + (lpc ^ sw(r)) * 8;
+  }
+  const uint16_t* b_src[BI];
+#pragma unroll
+  for (int j = 0; j < BI; ++j) {
+    const int r = (wave * BI + j) * RPB + lrow;
+    b_src[j] = args.B + (int64_t(e) * args.Nout + n0 + r) * K + (lpc ^ sw(r)) * 8;
+  }
+
+  auto issue = [&](int stage, int k0) {
+    char* As = smem + stage * STAGE;
+    char* Bs = As + A_BYTES;
+#pragma unroll
+    for (int j = 0; j < AI; ++j) lds_dma16(a_src[j] + k0, As + (wave * AI + j) * 1024);
+#pragma unroll
+    for (int j = 0; j < BI; ++j) lds_dma16(b_src[j] + k0, Bs + (wave * BI + j) * 1024);
+  };
+  // VGPR-staged alternative: global loads into registers, stored to LDS later
+  // (same LDS layout as the DMA path: lane l of block blk at blk*1024 + 16*l).
+  uint4 stg[AI + BI];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < AI; ++j) stg[j] = *reinterpret_cast<const uint4*>(a_src[j] + k0);
+#pragma unroll
+    for (int j = 0; j < BI; ++j) stg[AI + j] = *reinterpret_cast<const uint4*>(b_src[j] + k0);
+  };
+  auto sstore = [&](int stage) {
+    char* As = smem + stage * STAGE;
+    char* Bs = As + A_BYTES;
+#pragma unroll
+    for (int j = 0; j < AI; ++j)
+      *reinterpret_cast<uint4*>(As + (wave * AI + j) * 1024 + lane * 16) = stg[j];
+#pragma unroll
+    for (int j = 0; j < BI; ++j)
+      *reinterpret_cast<uint4*>(Bs + (wave * BI + j) * 1024 + lane * 16) = stg[AI + j];
+  };
+
+  // acc[i][j] = D of the MFMA with the weight block as the A operand and the
+  // token block as the B operand: D[feature][token] for feature block i and
+  // token block j, so lane l holds token 32j + l%32 and, in acc[i][j][4q + u],
+  // feature 32i + 8q + 4(l/32) + u — four consecutive output columns.
+  f32x16 acc[NB][MB];
+#pragma unroll
+  for (int i = 0; i < NB; ++i)
+#pragma unroll
+    for (int j = 0; j < MB; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
+
+  // Fragment reads: row r = 32*m + (lane & 31), so sw(r) = sw(lane & 31).
+  const int a_row = (wm * WTM + (lane & 31)) * RB;
+  const int b_row = (wn * WTN + (lane & 31)) * RB;
+  const int khalf = lane >> 5;
+  const int rsw = sw(lane & 31);
+  bf16x8 af[2][MB], bfr[2][NB];
+  // Fragment f of substep ks: f < MB is A block f, otherwise B block f - MB.
+  auto load_frag = [&](const char* As, const char* Bs, int ks, int slot, int f) {
+    const int pc = ((ks * 2 + khalf) ^ rsw) * 16;
+    if (f < MB)
+      af[slot][f] = *reinterpret_cast<const bf16x8*>(As + a_row + f * 32 * RB + pc);
+    else
+      bfr[slot][f - MB] =
+          *reinterpret_cast<const bf16x8*>(Bs + b_row + (f - MB) * 32 * RB + pc);
+  };
+
+  // Pipeline (STAGES LDS buffers, KS substeps of 16 k per stage).  Substep g
+  // of the whole k range uses fragment slot g & 1; while its MFMAs run, the
+  // reads for substep g + 1 go out.  The stage barrier sits inside the MFMA
+  // stream: once the last substep's fragments of stage kt are in registers (all
+  // reads of that buffer are done), the wave waits for stage kt+1's DMA, syncs,
+  // refills the drained buffer with stage kt+STAGES, and runs the last
+  // substep's MFMAs interleaved with the reads of stage kt+1's first substep —
+  // the matrix core keeps its queue across the barrier, and every stage's DMA
+  // has STAGES-1 k-steps to land.
+  static_assert(KS % 2 == 0, "even substeps per stage");
+  constexpr int PER = AI + BI;  // DMA instructions per thread per stage
+  const int nk = K / BK;
+#ifdef G5_STAGE_VGPR
+  static_assert(STAGES == 2, "VGPR staging uses two LDS buffers");
+  gload(0);
+  wait_vmcnt<0>();
+  sstore(0);
+  if (nk > 1) gload(BK);
+  __syncthreads();
+#else
+#pragma unroll
+  for (int s = 0; s < STAGES; ++s)
+    if (s < nk) issue(s, s * BK);
+  // stage 0 landed; min(STAGES, nk) - 1 later stages may still be in flight
+  wait_vmcnt_upto<STAGES - 1, PER>(min(STAGES, nk) - 1);
+  __syncthreads();
+#endif
+#pragma unroll
+  for (int f = 0; f < MB + NB; ++f) load_frag(smem, smem + A_BYTES, 0, 0, f);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt % STAGES;
+    const int nxt = (kt + 1) % STAGES;
+    const char* As = smem + cur * STAGE;
+    const char* Bs = As + A_BYTES;
+    const char* As_next = smem + nxt * STAGE;
+    const char* Bs_next = As_next + A_BYTES;
+    const bool more = kt + 1 < nk;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks == KS - 1) {
+        __builtin_amdgcn_sched_barrier(0);
+#ifdef G5_STAGE_VGPR
+        if (more) {
+          wait_vmcnt<0>();
+          sstore(nxt);
+        }
+        __syncthreads();
+        if (kt + 2 < nk) gload((kt + 2) * BK);
+#else
+        // stage kt+1 landed; stages kt+2 .. min(kt+STAGES-1, nk-1) may be in flight
+        wait_vmcnt_upto<STAGES - 2, PER>(max(0, min(kt + STAGES - 1, nk - 1) - (kt + 1)));
+        __syncthreads();
+        if (kt + STAGES < nk) issue(cur, (kt + STAGES) * BK);
+#endif
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < MB * NB; ++t) {
+        const int i = t / MB, j = t % MB;  // feature block i, token block j
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][i], af[ks & 1][j],
+                                                            acc[i][j], 0, 0, 0);
+        if (t < MB + NB) {
+          if (ks + 1 < KS)
+            load_frag(As, Bs, ks + 1, (ks + 1) & 1, t);
+          else if (more)
+            load_frag(As_next, Bs_next, 0, 0, t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+
+  // Epilogue: lane l owns token row p = p_begin + wm*WTM + 32j + l%32 and, per
+  // q, four consecutive output columns, stored as one 8-byte write.
+  const int tok_l = lane & 31;
+  const int col4 = (lane >> 5) * 4;
+  if constexpr (SWIGLU) {
+    // Feature blocks 2jj / 2jj+1 of the packed gate|up weight are gate / up of
+    // the same 32 h columns.
+    const int f_base = (n0 + wn * WTN) / 2;
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int p = p_begin + wm * WTM + j * 32 + tok_l;
+      if (p < p_end) {
+        uint16_t* crow = args.C + int64_t(p) * args.ldc + f_base + col4;
+#pragma unroll
+        for (int jj = 0; jj < NB / 2; ++jj) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            float h[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+              h[u] = silu_mul(acc[2 * jj][j][4 * q + u], acc[2 * jj + 1][j][4 * q + u]);
+            uint2 o;
+            o.x = pack_bf16x2(h[0], h[1]);
+            o.y = pack_bf16x2(h[2], h[3]);
+            *reinterpret_cast<uint2*>(crow + jj * 32 + 8 * q) = o;
+          }
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < MB; ++j) {
+      const int p = p_begin + wm * WTM + j * 32 + tok_l;
+      if (p < p_end) {
+        uint16_t* crow = args.C + int64_t(p) * args.ldc + n0 + wn * WTN + col4;
+#pragma unroll
+        for (int i = 0; i < NB; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            uint2 o;
+            o.x = pack_bf16x2(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]);
+            o.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+            *reinterpret_cast<uint2*>(crow + i * 32 + 8 * q) = o;
+          }
+        }
+      }
+    }
+  }
+}
+
 // Upper bound on the number of tiles: sum_e ceil(cnt_e / BM) <= ceil(Nk / BM) + E.
 template <int BM, int BN>
 unsigned grid_bound(int64_t nk, int n_experts, int nout) {
@@ -267,7 +576,20 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
   reinterpret_cast<uint2*>(xb)[i] = o;
 }
 
-// Tile configurations.
+// Tile configurations (the k depth and LDS stage count can be overridden at
+// build time for tuning).
+#ifndef G5_GU_BK
+#define G5_GU_BK 64
+#endif
+#ifndef G5_GU_STAGES
+#define G5_GU_STAGES 2
+#endif
+#ifndef G5_DN_BK
+#define G5_DN_BK 64
+#endif
+#ifndef G5_DN_STAGES
+#define G5_DN_STAGES 2
+#endif
 constexpr int kGuBM = 256, kGuBN = 256, kGuWM = 2, kGuWN = 4;
 constexpr int kDnBM = 256, kDnBN = 128, kDnWM = 4, kDnWN = 2;
 
@@ -289,9 +611,15 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.K = s.d_model;
   a.Nout = 2 * s.d_ff;
   a.ldc = s.d_ff;
+#ifdef G5MOE_GEMM_V1
   const unsigned grid = grid_bound<kGuBM, kGuBN>(nk, s.n_experts, a.Nout);
   hipLaunchKernelGGL((grouped_gemm_kernel<kGuBM, kGuBN, kGuWM, kGuWN, true>), dim3(grid),
                      dim3(kGuWM * kGuWN * 64), 0, st, a);
+#else
+  const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+  hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_GU_BK, G5_GU_STAGES, true>), dim3(grid),
+                     dim3(256), 0, st, a);
+#endif
   return hipGetLastError();
 }
 
@@ -310,9 +638,21 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.K = s.d_ff;
   a.Nout = s.d_model;
   a.ldc = s.d_model;
+#ifdef G5MOE_GEMM_V1
   const unsigned grid = grid_bound<kDnBM, kDnBN>(nk, s.n_experts, a.Nout);
   hipLaunchKernelGGL((grouped_gemm_kernel<kDnBM, kDnBN, kDnWM, kDnWN, false>), dim3(grid),
                      dim3(kDnWM * kDnWN * 64), 0, st, a);
+#else
+  if (a.Nout % 256 == 0) {
+    const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+    hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_DN_BK, G5_DN_STAGES, false>),
+                       dim3(grid), dim3(256), 0, st, a);
+  } else {
+    const unsigned grid = grid_bound<256, 128>(nk, s.n_experts, a.Nout);
+    hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 128, G5_DN_BK, G5_DN_STAGES, false>),
+                       dim3(grid), dim3(256), 0, st, a);
+  }
+#endif
   return hipGetLastError();
 }
 

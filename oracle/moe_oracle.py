@@ -29,7 +29,8 @@ expert_forward
     h = silu(X Wg^T) * (X Wu^T), y = h Wd^T per expert over its rows —
     FeedForward.forward (lib/blocks/_component.py:48-52, 'silu' at :31); with
     storage="bf16" h and y are rounded to bf16 where the bf16 dataflow stores
-    them (round_bf16 is pinned against torch's bf16 cast).  Pins:
+    them, and moe_forward rounds an fp32 x to bf16 on its way into the expert
+    products (round_bf16 is pinned against torch's bf16 cast).  Pins:
     float64 brute force on tiny inputs; upcycling invariant (all experts equal
     one dense FeedForward => MoE output == dense output, since the k gates sum
     to 1); zero down weights => zero output; E = 1, k = 1 reduces to dense.
@@ -268,6 +269,8 @@ def moe_forward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: n
     idx, w = topk_gates_c(logits, top_k)
     counts, offsets, perm, inv_pos = dispatch_c(idx, E)
     xf = widen(x)
+    if storage == "bf16" and x.dtype != np.uint16:
+        xf = round_bf16(xf)  # an fp32 x enters the bf16 expert GEMMs rounded to bf16
     res = expert_forward(xf, perm, offsets, top_k, w_gate, w_up, w_down, dtype=dtype,
                          return_h=return_h, storage=storage)
     y_perm, h = res if return_h else (res, None)
