@@ -1,0 +1,177 @@
+"""GeneT5-shaped encoder with the HIP MoE in every layer, and the MDLM unmasking driver
+(BASELINE config 5).
+
+Reference shapes followed:
+  * GeneT5.forward (lib/model/genet5.py:49-59): embed -> Encoder -> tied lm_head,
+    returning {"logits": ...}; vocab 4,096, d 768, 12 layers, 12 heads; depth
+    scaling off (genet5.py:22).
+  * EncoderBlock.forward (lib/blocks/encoder.py:73-90), non-fused path:
+    h = h + attn(norm1(h)); h = h + ff(norm2(h)); Encoder adds a final norm
+    (encoder.py:148).  Here ff is MoEFeedForward (HIP) and attention stays in
+    PyTorch.
+  * Attention projections q/k/v/o bias-free (lib/blocks/_sdpa_att.py:68-71),
+    bidirectional, scale 1/sqrt(head_dim).  No reference backend adds a
+    positional bias; following the DNABERT-2 lineage this one adds
+    symmetric ALiBi, bias[h, i, j] = -slope_h * |i - j|, with the slopes of
+    Press et al. (2022), "Train Short, Test Long".  Packed inputs with
+    cu_seqlens attend within each sequence only (a block-diagonal mask per
+    row, unlike the reference SDPA fallback's global-offset mask).
+  * diffusion_generate (lib/inference/diffusion_engine.py:18-95): linear unmask
+    schedule, mask/pad logits suppressed, argmax (temperature 0) or sampling,
+    confidence = log-prob of the prediction, per-sample top-n unmasking of the
+    most confident masked positions, final fill pass.  The per-sample Python
+    loop with host syncs (diffusion_engine.py:69-82) is replaced by one
+    sort-based selection on the device; among equal confidences the lower
+    position is unmasked first.
+"""
+from __future__ import annotations
+
+import math
+from typing import Dict, List, Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ..moe import MoEFeedForward
+from .blocks import RMSNorm
+
+
+def alibi_slopes(n_heads: int) -> List[float]:
+    """Head slopes of Press et al. (2022): a geometric sequence starting at
+    2^(-8/n) for n a power of two; otherwise the slopes of the nearest lower power
+    of two followed by every other slope of twice that count."""
+    def pow2(n):
+        start = 2.0 ** (-8.0 / n)
+        return [start ** (i + 1) for i in range(n)]
+    if n_heads & (n_heads - 1) == 0:
+        return pow2(n_heads)
+    m = 1 << int(math.floor(math.log2(n_heads)))
+    return pow2(m) + pow2(2 * m)[0::2][: n_heads - m]
+
+
+class ALiBiSelfAttention(nn.Module):
+    def __init__(self, embed_dim: int, num_heads: int):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = embed_dim // num_heads
+        self.q = nn.Linear(embed_dim, embed_dim, bias=False)
+        self.k = nn.Linear(embed_dim, embed_dim, bias=False)
+        self.v = nn.Linear(embed_dim, embed_dim, bias=False)
+        self.o = nn.Linear(embed_dim, embed_dim, bias=False)
+        self.register_buffer("slopes", torch.tensor(alibi_slopes(num_heads)), persistent=False)
+        self._bias_cache: Dict[tuple, torch.Tensor] = {}
+
+    def alibi_bias(self, L: int, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+        key = (L, dtype, device)
+        b = self._bias_cache.get(key)
+        if b is None:
+            pos = torch.arange(L, device=device, dtype=torch.float32)
+            dist = (pos[None, :] - pos[:, None]).abs()
+            b = (-self.slopes.to(device)[:, None, None] * dist[None]).to(dtype).unsqueeze(0)
+            self._bias_cache = {key: b}  # keep only the latest length
+        return b
+
+    def _attend(self, h: torch.Tensor) -> torch.Tensor:
+        B, L, D = h.shape
+        q = self.q(h).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        k = self.k(h).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        v = self.v(h).view(B, L, self.num_heads, self.head_dim).transpose(1, 2)
+        out = F.scaled_dot_product_attention(q, k, v, attn_mask=self.alibi_bias(L, q.dtype, q.device),
+                                             scale=1.0 / math.sqrt(self.head_dim))
+        return self.o(out.transpose(1, 2).reshape(B, L, D))
+
+    def forward(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if cu_seqlens is None:
+            return self._attend(h)
+        # packed [1, T, D]: attend within each sequence
+        bounds = cu_seqlens.tolist()
+        parts = [self._attend(h[:, a:b]) for a, b in zip(bounds[:-1], bounds[1:])]
+        return torch.cat(parts, dim=1)
+
+
+class MoEEncoderBlock(nn.Module):
+    def __init__(self, embed_dim: int, num_heads: int, ff_dim: int, num_experts: int = 16,
+                 top_k: int = 2):
+        super().__init__()
+        self.norm1 = RMSNorm(embed_dim)
+        self.self_attn = ALiBiSelfAttention(embed_dim, num_heads)
+        self.norm2 = RMSNorm(embed_dim)
+        self.ff = MoEFeedForward(embed_dim, ff_dim, 0.0, "silu", num_experts, top_k)
+
+    def forward(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None) -> torch.Tensor:
+        h = h + self.self_attn(self.norm1(h), cu_seqlens)
+        return h + self.ff(self.norm2(h))
+
+
+class GeneT5MoE(nn.Module):
+    """embed -> 12 x (ALiBi attention + MoE) -> final RMSNorm -> tied lm_head."""
+
+    def __init__(self, vocab_size: int = 4096, embed_dim: int = 768, num_layers: int = 12,
+                 num_heads: int = 12, ff_dim: int = 3072, num_experts: int = 16,
+                 top_k: int = 2):
+        super().__init__()
+        self.embed = nn.Embedding(vocab_size, embed_dim)
+        self.layers = nn.ModuleList([
+            MoEEncoderBlock(embed_dim, num_heads, ff_dim, num_experts, top_k)
+            for _ in range(num_layers)])
+        self.final_norm = RMSNorm(embed_dim)
+        self.lm_head = nn.Linear(embed_dim, vocab_size, bias=False)
+        self.lm_head.weight = self.embed.weight
+
+    def forward(self, input_ids: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None):
+        h = self.embed(input_ids)
+        for layer in self.layers:
+            h = layer(h, cu_seqlens)
+        return {"logits": self.lm_head(self.final_norm(h))}
+
+
+def linear_unmask_schedule(num_steps: int, eps: float = 1e-3) -> List[float]:
+    """Fraction of the target unmasked at each step: differences of linspace(1, eps, T+1)."""
+    t = torch.linspace(1.0, eps, num_steps + 1)
+    return [(t[i] - t[i + 1]).item() for i in range(num_steps)]
+
+
+@torch.no_grad()
+def diffusion_generate(model, prefix_ids: torch.Tensor, target_len: int, mask_token_id: int,
+                       pad_token_id: int, num_steps: int = 16, temperature: float = 0.0,
+                       generator: Optional[torch.Generator] = None,
+                       stats: Optional[dict] = None) -> torch.Tensor:
+    """Iterative unmasking of a fully masked target appended to prefix_ids [B, P]."""
+    device = prefix_ids.device
+    B, P = prefix_ids.shape
+    target = torch.full((B, target_len), mask_token_id, dtype=torch.long, device=device)
+    input_ids = torch.cat([prefix_ids, target], dim=1)
+    is_masked = torch.ones(B, target_len, dtype=torch.bool, device=device)
+    n_forward = 0
+    for frac in linear_unmask_schedule(num_steps):
+        logits = model(input_ids)["logits"][:, P:].float()
+        n_forward += 1
+        logits[:, :, mask_token_id] = float("-inf")
+        logits[:, :, pad_token_id] = float("-inf")
+        if temperature > 0:
+            probs = F.softmax(logits / temperature, dim=-1)
+            preds = torch.multinomial(probs.view(-1, probs.size(-1)), 1,
+                                      generator=generator).view(B, target_len)
+        else:
+            preds = logits.argmax(dim=-1)
+        conf = F.log_softmax(logits, dim=-1).gather(-1, preds.unsqueeze(-1)).squeeze(-1)
+        conf = conf.masked_fill(~is_masked, float("-inf"))
+        # same float32 product and truncation as diffusion_engine.py:63-64
+        n_unmask = torch.minimum(
+            (frac * target_len * torch.ones(B, device=device)).long(), is_masked.sum(dim=1))
+        order = torch.sort(conf, dim=1, descending=True, stable=True).indices
+        rank = torch.empty_like(order)
+        rank.scatter_(1, order, torch.arange(target_len, device=device).expand(B, -1))
+        unmask = (rank < n_unmask[:, None]) & is_masked
+        input_ids[:, P:] = torch.where(unmask, preds, input_ids[:, P:])
+        is_masked &= ~unmask
+    if bool(is_masked.any()):
+        logits = model(input_ids)["logits"][:, P:].float()
+        n_forward += 1
+        logits[:, :, mask_token_id] = float("-inf")
+        final = logits.argmax(dim=-1)
+        input_ids[:, P:] = torch.where(is_masked, final, input_ids[:, P:])
+    if stats is not None:
+        stats["forwards"] = n_forward
+    return input_ids

@@ -43,6 +43,26 @@ def _(x, w_router, bias, w_gate_up, w_down, top_k):
     return torch.empty_like(x)
 
 
+@torch.library.custom_op("g5moe::pack_gate_up", mutates_args=())
+def _pack_gate_up_op(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
+    return ops.pack_gate_up(w_gate, w_up)
+
+
+@_pack_gate_up_op.register_fake
+def _(w_gate, w_up):
+    E, F, d = w_gate.shape
+    return w_gate.new_empty((E, 2 * F, d))
+
+
+def _no_backward(ctx, grad):
+    raise NotImplementedError(
+        "g5moe::moe_forward is forward-only (no MoE backward is built); run the layer "
+        "under torch.no_grad() / inference_mode or detach its inputs")
+
+
+_moe_forward_op.register_autograd(_no_backward)
+
+
 class MoEFeedForward(nn.Module):
     """Top-k routed mixture of SwiGLU experts (forward only)."""
 
@@ -93,7 +113,12 @@ class MoEFeedForward(nn.Module):
         self.w_down.copy_(wo.unsqueeze(0).expand_as(self.w_down))
 
     def _expert_weights(self):
-        """bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F], cached by version."""
+        """bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F], cached by version.
+        Under torch.compile the cache (Python-side state) is bypassed and the packing
+        runs as its own custom op on every call."""
+        if torch.compiler.is_compiling():
+            return (_pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16)),
+                    self.w_down.to(torch.bfloat16))
         key = (self.w_gate.data_ptr(), self.w_gate._version, self.w_up.data_ptr(),
                self.w_up._version, self.w_down.data_ptr(), self.w_down._version,
                self.w_gate.device, self.w_gate.dtype)

@@ -1,0 +1,198 @@
+"""GPU checks of the module and the reference-shaped callers (configs 4 and 5).
+
+* MoEFeedForward: upcycling invariant on the GPU (identical experts == the dense
+  FeedForward computed by a plain PyTorch fp32 reference), shape/dtype contract,
+  torch.compile traceability.
+* Config 4 (12 stacked RMSNorm -> MoE -> residual blocks, 45,500 packed tokens):
+  teacher-forced per layer — each layer's routing on the GPU's own RMSNorm output
+  is bit-exact against the oracle; the MoE output of the first and last layers is
+  within the bf16 tolerance of the oracle in its bf16-storage mode.
+* Config 5 (encoder with ALiBi attention + MoE, MDLM unmasking): in a reduced
+  model every layer's MoE, on the inputs the forward actually produced, routes
+  bit-exactly and stays within the bf16 tolerance; the unmasking loop fills every
+  mask deterministically.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from genet5_amd import ops, synth
+from genet5_amd.harness import blocks, encoder
+from genet5_amd.moe import MoEFeedForward
+
+pytestmark = pytest.mark.gpu
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def normwise(got, ref):
+    err = np.abs(got.astype(np.float64) - ref.astype(np.float64))
+    return err.max() / np.abs(ref).max(), err.mean() / np.abs(ref).mean()
+
+
+def torch_moe_fp32(m: MoEFeedForward, x: torch.Tensor, bf16_experts: bool = False) -> torch.Tensor:
+    """Plain PyTorch fp32 MoE of the same parameters (routing by fp32 matmul).  With
+    bf16_experts it follows the module's storage contract: the expert inputs and
+    weights are rounded to bf16 (its expert compute dtype), and h and each
+    expert's output are rounded to bf16 where the kernels store them; the
+    products themselves are fp32."""
+    xf = x.reshape(-1, m.embed_dim).float()
+    r = (lambda t: t.to(torch.bfloat16).float()) if bf16_experts else (lambda t: t.float())
+    logits = xf @ m.router.weight.float().T
+    if m.router_bias is not None:
+        logits = logits + m.router_bias
+    vals, idx = torch.topk(logits, m.top_k, dim=-1)
+    w = torch.softmax(vals, dim=-1)
+    y = torch.zeros_like(xf)
+    for e in range(m.num_experts):
+        for s in range(m.top_k):
+            sel = idx[:, s] == e
+            if sel.any():
+                xe = r(xf[sel])
+                h = r(torch.nn.functional.silu(xe @ r(m.w_gate[e]).T) * (xe @ r(m.w_up[e]).T))
+                y[sel] += w[sel, s:s + 1] * r(h @ r(m.w_down[e]).T)
+    return y.view(x.shape)
+
+
+def test_module_upcycled_equals_dense(cuda_device):
+    torch.manual_seed(0)
+    d, F, E = 768, 3072, 16
+    m = MoEFeedForward(d, F, 0.0).to(cuda_device).to(torch.bfloat16)
+    wi0 = (torch.randn(F, d) * 0.02).to(cuda_device, torch.bfloat16)
+    wi1 = (torch.randn(F, d) * 0.02).to(cuda_device, torch.bfloat16)
+    wo = (torch.randn(d, F) * 0.02).to(cuda_device, torch.bfloat16)
+    m.load_dense(wi0, wi1, wo)
+    x = torch.randn(2, 300, d, device=cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        y = m(x)
+    assert y.shape == x.shape and y.dtype == x.dtype
+    xf = x.float()
+    dense = (torch.nn.functional.silu(xf @ wi0.float().T) * (xf @ wi1.float().T)) @ wo.float().T
+    mx, mean = normwise(y.float().cpu().numpy(), dense.cpu().numpy())
+    assert mx <= 2e-2 and mean <= 4e-3, (mx, mean)
+
+
+def test_module_matches_torch_fp32_reference(cuda_device):
+    torch.manual_seed(1)
+    m = MoEFeedForward(256, 512, 0.0, num_experts=8, top_k=2, router_bias=True).to(cuda_device)
+    with torch.no_grad():
+        for p in (m.w_gate, m.w_up, m.w_down):
+            p.normal_(0, 0.05)
+        m.router_bias.copy_(torch.linspace(-1, 1, 8))
+    x = torch.randn(700, 256, device=cuda_device)
+    with torch.no_grad():
+        y = m(x)  # fp32 activations: fp32 router, bf16 experts, fp32 output
+        ref_b = torch_moe_fp32(m, x, bf16_experts=True)
+        ref_f = torch_moe_fp32(m, x)
+    assert y.dtype == torch.float32
+    mx, mean = normwise(y.cpu().numpy(), ref_b.cpu().numpy())
+    assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
+    # against an all-fp32 expert computation the bf16 rounding of x and of the
+    # weights shows: about 4.5e-3 mean here
+    mx, mean = normwise(y.cpu().numpy(), ref_f.cpu().numpy())
+    assert mx <= 2e-2 and mean <= 1e-2, (mx, mean)
+
+
+def test_module_traces_under_torch_compile(cuda_device):
+    """The custom op's fake implementation lets dynamo + AOT autograd trace the module
+    (aot_eager: no code generation, the traced graph runs the same HIP op)."""
+    m = MoEFeedForward(128, 256, 0.0, num_experts=4).to(cuda_device).to(torch.bfloat16)
+    x = torch.randn(64, 128, device=cuda_device).to(torch.bfloat16)
+    f = torch.compile(lambda t: m(t) * 2.0, fullgraph=True, backend="aot_eager")
+    with torch.no_grad():
+        torch.testing.assert_close(f(x), m(x) * 2.0, rtol=0, atol=0)
+
+
+def test_backward_raises_clearly(cuda_device):
+    m = MoEFeedForward(128, 256, 0.0, num_experts=4).to(cuda_device)
+    y = m(torch.randn(8, 128, device=cuda_device))
+    with pytest.raises(NotImplementedError, match="forward-only"):
+        y.sum().backward()
+
+
+def test_config4_teacher_forced(cuda_device):
+    cfg = blocks.make_config4()
+    stack = blocks.MoEStack(12, 768, 3072).to(cuda_device).to(torch.bfloat16)
+    blocks.load_layer_weights(stack, cfg.layer_seeds, 3072)
+    x = torch.from_numpy(cfg.x).view(torch.bfloat16).to(cuda_device)
+    with torch.no_grad():
+        hs = stack(x, return_all=True)
+    assert len(hs) == 13 and torch.isfinite(hs[-1].float()).all()
+    for li, layer in enumerate(stack.layers):
+        print(f"config4 layer {li}", flush=True)
+        with torch.no_grad():
+            normed = layer.norm(hs[li]).reshape(-1, 768)
+            y, r = layer.ff.forward_with_routing(normed)
+        nb = bits(normed)
+        wr = bits(layer.ff.router.weight)
+        ref_l = oracle.router_logits(nb, wr)
+        ref_i, ref_w = oracle.topk_gates_c(ref_l, 2)
+        np.testing.assert_array_equal(r.topk_idx.cpu().numpy(), ref_i)
+        rc, ro, rp, ri = oracle.dispatch(ref_i, 16)
+        np.testing.assert_array_equal(r.perm.cpu().numpy(), rp)
+        # the stack's residual update is exactly this layer's MoE output
+        torch.testing.assert_close(hs[li + 1], hs[li] + y.view_as(hs[li]), rtol=0, atol=0)
+        if li in (0, 11):
+            ref = oracle.moe_forward(nb, wr, bits(layer.ff.w_gate), bits(layer.ff.w_up),
+                                     bits(layer.ff.w_down), 2, storage="bf16")
+            mx, mean = normwise(y.float().cpu().numpy(), ref["y"])
+            print(f"config4 layer {li}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+            assert mx <= 2e-2 and mean <= 2e-3, (li, mx, mean)
+
+
+def small_encoder(device, layers=2):
+    torch.manual_seed(3)
+    model = encoder.GeneT5MoE(vocab_size=4096, embed_dim=768, num_layers=layers, num_heads=12,
+                              ff_dim=3072).to(device)
+    with torch.no_grad():
+        for n, p in model.named_parameters():
+            if p.dim() >= 2:
+                p.normal_(0, 0.02)
+    return model.to(torch.bfloat16).eval()
+
+
+def test_config5_encoder_teacher_forced(cuda_device):
+    """Capture every layer's MoE input/output in one encoder forward; on those exact
+    inputs the routing is bit-exact against the oracle and the outputs are within the
+    bf16 tolerance of the oracle's bf16-storage mode.  (End-to-end logit comparisons
+    against a differently-rounded reference are not meaningful through several MoE
+    layers: bf16-level differences flip near-tie routing decisions downstream.)"""
+    model = small_encoder(cuda_device)
+    ids = torch.randint(0, 4096, (2, 384), device=cuda_device)
+    seen = []
+    hooks = [layer.ff.register_forward_hook(lambda mod, inp, out: seen.append((mod, inp[0], out)))
+             for layer in model.layers]
+    with torch.no_grad():
+        logits = model(ids)["logits"]
+    for h in hooks:
+        h.remove()
+    assert logits.shape == (2, 384, 4096) and torch.isfinite(logits.float()).all()
+    assert len(seen) == len(model.layers)
+    for li, (ff, xin, yout) in enumerate(seen):
+        x2 = xin.reshape(-1, 768)
+        nb = bits(x2)
+        ref = oracle.moe_forward(nb, bits(ff.router.weight), bits(ff.w_gate), bits(ff.w_up),
+                                 bits(ff.w_down), 2, storage="bf16")
+        with torch.no_grad():
+            _, r = ff.forward_with_routing(x2)
+        np.testing.assert_array_equal(r.topk_idx.cpu().numpy(), ref["topk_idx"])
+        mx, mean = normwise(yout.reshape(-1, 768).float().cpu().numpy(), ref["y"])
+        print(f"config5 layer {li}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+        assert mx <= 2e-2 and mean <= 2e-3, (li, mx, mean)
+
+
+def test_config5_unmasking_loop(cuda_device):
+    model = small_encoder(cuda_device)
+    mask_id, pad_id = 4095, 0
+    g = torch.Generator(device="cpu").manual_seed(5)
+    prefix = torch.randint(1, 4095, (2, 128), generator=g).to(cuda_device)
+    st1, st2 = {}, {}
+    out1 = encoder.diffusion_generate(model, prefix, 128, mask_id, pad_id, num_steps=4, stats=st1)
+    out2 = encoder.diffusion_generate(model, prefix, 128, mask_id, pad_id, num_steps=4, stats=st2)
+    assert torch.equal(out1, out2)
+    assert torch.equal(out1[:, :128], prefix)
+    assert not (out1[:, 128:] == mask_id).any() and not (out1[:, 128:] == pad_id).any()
+    assert st1["forwards"] == 5
