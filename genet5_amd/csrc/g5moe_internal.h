@@ -5,7 +5,7 @@
 #include <stddef.h>
 #include <stdint.h>
 
-#include "../../include/g5moe.h"
+#include "g5moe.h"
 
 namespace g5moe {
 

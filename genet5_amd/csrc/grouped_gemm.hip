@@ -11,25 +11,32 @@
 // (x rows are gathered straight into the A tile, no permuted copy of x) and p
 // itself for the down GEMM.
 //
-// Tiles.  A workgroup computes a BM x BN tile with BK = 64; its waves form a
-// WM x WN grid, each wave a (BM/WM) x (BN/WN) sub-tile of 32x32 blocks built
-// with v_mfma_f32_32x32x16_bf16.  Both operands are K-contiguous, so one MFMA
-// operand is a 16-byte read of 8 consecutive k for one row.  Tiles are staged
-// through LDS, double-buffered, one barrier per BK step; each 128-byte row of a
-// tile is stored with its 16-byte chunks XOR-swizzled by the row index so the
-// 32 rows an MFMA operand read touches fall in distinct banks.
+// Tile: BM x BN x 64 per workgroup of 4 waves in a 2 x 2 grid; each wave owns a
+// (BM/2) x (BN/2) block of 32x32 v_mfma_f32_32x32x16_bf16 tiles (128 x 128 =
+// 256 fp32 accumulators per lane in AGPRs at BM = BN = 256).  The MFMA takes the
+// weight block as its A operand and the token block as its B operand, so each
+// lane ends up holding four consecutive output columns of one token.
 //
-// Scheduling.  Expert row counts live on the device (offsets[]), so the grid is
+// Data movement: global tiles go straight to LDS with global_load_lds_dwordx4
+// (one instruction moves 64 x 16 bytes into 1 KB of LDS, lane l at byte 16*l);
+// each 128-byte LDS row keeps logical chunk c at c ^ ((row >> 1) & 7), chosen
+// by picking each lane's global source chunk, so that 16-lane groups of the
+// fragment reads hit 16 distinct bank groups of the 64-bank LDS.  Two LDS
+// stages; fragment reads for the next 16-k substep are interleaved one by one
+// with the current substep's MFMAs, and the stage barrier sits inside the MFMA
+// stream.
+//
+// Scheduling: expert row counts live on the device (offsets[]), so the grid is
 // an upper bound and every workgroup derives its tile from offsets[]: tiles are
 // numbered expert-major, inside an expert in groups of kGroupM m-tiles swept
 // across all n-tiles (neighbouring tiles share A rows or B columns).  Block ids
 // are remapped so each of the 8 XCDs (which receive blocks round-robin) runs a
 // contiguous range of that numbering and its L2 sees the reuse.
 //
-// SwiGLU epilogue.  The packed gate|up weight interleaves 32-row groups (gate
-// rows of f in [32g, 32g+32), then the matching up rows), so a wave's n-blocks
-// 2j and 2j+1 hold gate and up for the same 32 columns in the same lanes;
-// silu(g) * u is formed in registers and only h is stored (bf16).
+// SwiGLU epilogue: the packed gate|up weight interleaves 32-row groups (gate
+// rows of f in [32g, 32g+32), then the matching up rows), so the wave's
+// feature blocks 2j and 2j+1 hold gate and up of the same 32 h columns in the
+// same lanes; silu(g) * u is formed in registers and only h is stored (bf16).
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -54,7 +61,10 @@ struct GemmArgs {
   int ldc;
 };
 
-__device__ __forceinline__ int swz(int r, int c) { return c ^ (r & 7); }
+// 8-byte output store (four bf16).
+__device__ __forceinline__ void store8(uint16_t* dst, uint2 v) {
+  *reinterpret_cast<uint2*>(dst) = v;
+}
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
 // below the bf16 rounding of the result).
@@ -62,189 +72,6 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
-template <int BM, int BN, int WM, int WN, bool SWIGLU>
-__global__ __launch_bounds__(WM* WN * 64) void grouped_gemm_kernel(GemmArgs args) {
-  constexpr int NT = WM * WN * 64;
-  constexpr int ROWS_PER_PASS = NT / 8;  // 8 chunks of 16 B per 128-byte row
-  constexpr int PA = BM / ROWS_PER_PASS;
-  constexpr int PB = BN / ROWS_PER_PASS;
-  constexpr int WTM = BM / WM;
-  constexpr int WTN = BN / WN;
-  constexpr int MB = WTM / 32;
-  constexpr int NB = WTN / 32;
-  static_assert(BM % ROWS_PER_PASS == 0 && BN % ROWS_PER_PASS == 0, "tile/threads");
-  static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
-  constexpr int A_STAGE = BM * kBK;  // bf16 elements
-  constexpr int B_STAGE = BN * kBK;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2 * (A_STAGE + B_STAGE)];
-
-  // ---- tile decode from device-side offsets --------------------------------
-  const int ntn = args.Nout / BN;
-  int total = 0;
-  for (int e = 0; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
-    total += ((cnt + BM - 1) / BM) * ntn;
-  }
-  const int b = blockIdx.x;
-  if (b >= total) return;
-  const int q = total >> 3, rem = total & 7, xcd = b & 7;
-  int u = xcd * q + min(xcd, rem) + (b >> 3);
-  int e = 0, mt_e = 0;
-  for (; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
-    mt_e = (cnt + BM - 1) / BM;
-    const int t = mt_e * ntn;
-    if (u < t) break;
-    u -= t;
-  }
-  const int g = u / (kGroupM * ntn);
-  const int first_m = g * kGroupM;
-  const int gs = min(kGroupM, mt_e - first_m);
-  const int rr = u - g * kGroupM * ntn;
-  const int mt = first_m + rr % gs;
-  const int nt = rr / gs;
-  const int p_begin = args.offsets[e] + mt * BM;
-  const int p_end = args.offsets[e + 1];
-  const int n0 = nt * BN;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-
-  // ---- global row pointers for this thread's load slots --------------------
-  const int chunk = tid & 7;
-  const int prow = tid >> 3;
-  const uint16_t* pa[PA];
-  const uint16_t* pb[PB];
-#pragma unroll
-  for (int i = 0; i < PA; ++i) {
-    const int r = i * ROWS_PER_PASS + prow;
-    const int p = min(p_begin + r, p_end - 1);
-    const int64_t row = args.perm ? int64_t(args.perm[p] / args.topk) : int64_t(p);
-    pa[i] = args.A + row * args.K + chunk * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < PB; ++i) {
-    const int r = i * ROWS_PER_PASS + prow;
-    pb[i] = args.B + (int64_t(e) * args.Nout + n0 + r) * args.K + chunk * 8;
-  }
-
-  uint4 ra[PA], rb[PB];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int i = 0; i < PA; ++i) ra[i] = *reinterpret_cast<const uint4*>(pa[i] + k0);
-#pragma unroll
-    for (int i = 0; i < PB; ++i) rb[i] = *reinterpret_cast<const uint4*>(pb[i] + k0);
-  };
-  auto sstore = [&](int stage) {
-    uint16_t* As = smem + stage * (A_STAGE + B_STAGE);
-    uint16_t* Bs = As + A_STAGE;
-#pragma unroll
-    for (int i = 0; i < PA; ++i) {
-      const int r = i * ROWS_PER_PASS + prow;
-      *reinterpret_cast<uint4*>(As + (r * 8 + swz(r, chunk)) * 8) = ra[i];
-    }
-#pragma unroll
-    for (int i = 0; i < PB; ++i) {
-      const int r = i * ROWS_PER_PASS + prow;
-      *reinterpret_cast<uint4*>(Bs + (r * 8 + swz(r, chunk)) * 8) = rb[i];
-    }
-  };
-
-  f32x16 acc[MB][NB];
-#pragma unroll
-  for (int i = 0; i < MB; ++i)
-#pragma unroll
-    for (int j = 0; j < NB; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  const int nk = args.K / kBK;
-  gload(0);
-  sstore(0);
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    if (kt + 1 < nk) gload((kt + 1) * kBK);
-    const uint16_t* As = smem + (kt & 1) * (A_STAGE + B_STAGE);
-    const uint16_t* Bs = As + A_STAGE;
-#pragma unroll
-    for (int ks = 0; ks < kBK / 16; ++ks) {
-      const int c = ks * 2 + (lane >> 5);
-      bf16x8 af[MB], bfr[NB];
-#pragma unroll
-      for (int i = 0; i < MB; ++i) {
-        const int r = wm * WTM + i * 32 + (lane & 31);
-        af[i] = *reinterpret_cast<const bf16x8*>(As + (r * 8 + swz(r, c)) * 8);
-      }
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int r = wn * WTN + j * 32 + (lane & 31);
-        bfr[j] = *reinterpret_cast<const bf16x8*>(Bs + (r * 8 + swz(r, c)) * 8);
-      }
-#pragma unroll
-      for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int j = 0; j < NB; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
-    }
-    if (kt + 1 < nk) sstore((kt + 1) & 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue ---------------------------------------------------------------
-  // acc[i][j][v] is row wm*WTM + i*32 + 8*(v/4) + 4*(lane/32) + v%4 and column
-  // wn*WTN + j*32 + lane%32 of the tile.
-  const int col_l = lane & 31;
-  const int row_hi = (lane >> 5) * 4;
-  if constexpr (SWIGLU) {
-    const int f_base = (n0 + wn * WTN) / 2;
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-#pragma unroll
-      for (int jj = 0; jj < NB / 2; ++jj) {
-        const int f = f_base + jj * 32 + col_l;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = wm * WTM + i * 32 + 8 * (v >> 2) + row_hi + (v & 3);
-          const int p = p_begin + row;
-          if (p < p_end) {
-            const float h = silu_mul(acc[i][2 * jj][v], acc[i][2 * jj + 1][v]);
-            args.C[int64_t(p) * args.ldc + f] = f32_to_bf16_bits(h);
-          }
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < MB; ++i) {
-#pragma unroll
-      for (int j = 0; j < NB; ++j) {
-        const int n = n0 + wn * WTN + j * 32 + col_l;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int row = wm * WTM + i * 32 + 8 * (v >> 2) + row_hi + (v & 3);
-          const int p = p_begin + row;
-          if (p < p_end) args.C[int64_t(p) * args.ldc + n] = f32_to_bf16_bits(acc[i][j][v]);
-        }
-      }
-    }
-  }
-}
-
-// ---- v2: 4 waves of 128x128, direct global->LDS loads ------------------------
-//
-// 256 threads; the waves form a 2 x 2 grid and each owns a (BM/2) x (BN/2)
-// sub-tile, so a 256 x 256 tile keeps 256 fp32 accumulators per lane (in
-// AGPRs).  Per BK = 64 step a wave reads 32 KB of fragments from LDS for 64
-// MFMAs (2048 cycles of one SIMD's matrix core); with the 64 KB the step writes,
-// LDS carries 192 KB per 2048 cycles.  Global tiles go straight to LDS with
-// global_load_lds_dwordx4: one instruction moves 64 x 16 bytes into a
-// contiguous 1 KB of LDS (8 rows of 128 bytes), lane l landing at byte 16*l, so
-// the XOR swizzle is applied by choosing each lane's global source chunk.  Two
-// LDS stages in separate arrays, prefetch distance one step; the k-loop is
-// unrolled by two so every LDS access names its stage statically.
 struct TileCoord {
   int e, p_begin, p_end, n0;
 };
@@ -370,25 +197,6 @@ __global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
 #pragma unroll
     for (int j = 0; j < BI; ++j) lds_dma16(b_src[j] + k0, Bs + (wave * BI + j) * 1024);
   };
-  // VGPR-staged alternative: global loads into registers, stored to LDS later
-  // (same LDS layout as the DMA path: lane l of block blk at blk*1024 + 16*l).
-  uint4 stg[AI + BI];
-  auto gload = [&](int k0) {
-#pragma unroll
-    for (int j = 0; j < AI; ++j) stg[j] = *reinterpret_cast<const uint4*>(a_src[j] + k0);
-#pragma unroll
-    for (int j = 0; j < BI; ++j) stg[AI + j] = *reinterpret_cast<const uint4*>(b_src[j] + k0);
-  };
-  auto sstore = [&](int stage) {
-    char* As = smem + stage * STAGE;
-    char* Bs = As + A_BYTES;
-#pragma unroll
-    for (int j = 0; j < AI; ++j)
-      *reinterpret_cast<uint4*>(As + (wave * AI + j) * 1024 + lane * 16) = stg[j];
-#pragma unroll
-    for (int j = 0; j < BI; ++j)
-      *reinterpret_cast<uint4*>(Bs + (wave * BI + j) * 1024 + lane * 16) = stg[AI + j];
-  };
 
   // acc[i][j] = D of the MFMA with the weight block as the A operand and the
   // token block as the B operand: D[feature][token] for feature block i and
@@ -430,21 +238,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
   static_assert(KS % 2 == 0, "even substeps per stage");
   constexpr int PER = AI + BI;  // DMA instructions per thread per stage
   const int nk = K / BK;
-#ifdef G5_STAGE_VGPR
-  static_assert(STAGES == 2, "VGPR staging uses two LDS buffers");
-  gload(0);
-  wait_vmcnt<0>();
-  sstore(0);
-  if (nk > 1) gload(BK);
-  __syncthreads();
-#else
 #pragma unroll
   for (int s = 0; s < STAGES; ++s)
     if (s < nk) issue(s, s * BK);
   // stage 0 landed; min(STAGES, nk) - 1 later stages may still be in flight
   wait_vmcnt_upto<STAGES - 1, PER>(min(STAGES, nk) - 1);
   __syncthreads();
-#endif
 #pragma unroll
   for (int f = 0; f < MB + NB; ++f) load_frag(smem, smem + A_BYTES, 0, 0, f);
   for (int kt = 0; kt < nk; ++kt) {
@@ -459,19 +258,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
     for (int ks = 0; ks < KS; ++ks) {
       if (ks == KS - 1) {
         __builtin_amdgcn_sched_barrier(0);
-#ifdef G5_STAGE_VGPR
-        if (more) {
-          wait_vmcnt<0>();
-          sstore(nxt);
-        }
-        __syncthreads();
-        if (kt + 2 < nk) gload((kt + 2) * BK);
-#else
         // stage kt+1 landed; stages kt+2 .. min(kt+STAGES-1, nk-1) may be in flight
         wait_vmcnt_upto<STAGES - 2, PER>(max(0, min(kt + STAGES - 1, nk - 1) - (kt + 1)));
         __syncthreads();
         if (kt + STAGES < nk) issue(cur, (kt + STAGES) * BK);
-#endif
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
@@ -514,7 +304,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
             uint2 o;
             o.x = pack_bf16x2(h[0], h[1]);
             o.y = pack_bf16x2(h[2], h[3]);
-            *reinterpret_cast<uint2*>(crow + jj * 32 + 8 * q) = o;
+            store8(crow + jj * 32 + 8 * q, o);
           }
         }
       }
@@ -532,7 +322,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
             uint2 o;
             o.x = pack_bf16x2(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]);
             o.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-            *reinterpret_cast<uint2*>(crow + i * 32 + 8 * q) = o;
+            store8(crow + i * 32 + 8 * q, o);
           }
         }
       }
@@ -590,8 +380,6 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #ifndef G5_DN_STAGES
 #define G5_DN_STAGES 2
 #endif
-constexpr int kGuBM = 256, kGuBN = 256, kGuWM = 2, kGuWN = 4;
-constexpr int kDnBM = 256, kDnBN = 128, kDnWM = 4, kDnWN = 2;
 
 }  // namespace
 
@@ -611,15 +399,9 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.K = s.d_model;
   a.Nout = 2 * s.d_ff;
   a.ldc = s.d_ff;
-#ifdef G5MOE_GEMM_V1
-  const unsigned grid = grid_bound<kGuBM, kGuBN>(nk, s.n_experts, a.Nout);
-  hipLaunchKernelGGL((grouped_gemm_kernel<kGuBM, kGuBN, kGuWM, kGuWN, true>), dim3(grid),
-                     dim3(kGuWM * kGuWN * 64), 0, st, a);
-#else
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_GU_BK, G5_GU_STAGES, true>), dim3(grid),
                      dim3(256), 0, st, a);
-#endif
   return hipGetLastError();
 }
 
@@ -638,11 +420,6 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.K = s.d_ff;
   a.Nout = s.d_model;
   a.ldc = s.d_model;
-#ifdef G5MOE_GEMM_V1
-  const unsigned grid = grid_bound<kDnBM, kDnBN>(nk, s.n_experts, a.Nout);
-  hipLaunchKernelGGL((grouped_gemm_kernel<kDnBM, kDnBN, kDnWM, kDnWN, false>), dim3(grid),
-                     dim3(kDnWM * kDnWN * 64), 0, st, a);
-#else
   if (a.Nout % 256 == 0) {
     const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_DN_BK, G5_DN_STAGES, false>),
@@ -652,7 +429,6 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 128, G5_DN_BK, G5_DN_STAGES, false>),
                        dim3(grid), dim3(256), 0, st, a);
   }
-#endif
   return hipGetLastError();
 }
 
