@@ -4,31 +4,39 @@
 // top-2"); the logit is nn.Linear(d, E, bias=False) in the orientation of
 // lib/blocks/_component.py:42-44.
 //
-// Mapping.  One wavefront owns one token at a time.  Lane c holds, in
-// registers, the fp32 slice W[e][c*L .. c*L+L) of every expert (L = d/64), so
-// the router weight is read once per block and never from LDS.  For each token
-// lane c loads its L contiguous columns of x (the wave reads the whole row,
-// coalesced), forms E partial sums with a fused multiply-add chain, and the
-// wave reduces the E x 64 partials with a reduce-scatter butterfly: at the
-// xor-32 step each lane keeps half of the experts and receives the partner's
-// copy of that half, and so on down to xor-4; xor-2 and xor-1 finish a plain
-// butterfly.  Every expert's sum is thus the pairwise tree that pairs lanes
-// differing in bit 5, then 4, 3, 2, 1, 0 — the order the C ABI specifies.
-// Lane c then holds expert c>>2.  The block's logits go through LDS and one
-// thread per token does the top-k scan and the gates.
+// Reduction order (the bit-exact contract, include/g5moe.h): lane c in [0, 64)
+// forms a fused multiply-add chain over columns [c*L, c*L + L), L = d/64, from
+// 0 upward; the 64 partial sums are added pairwise, pairing lanes that differ
+// in bit 5, then 4, 3, 2, 1, 0; the bias is added last.
+//
+// Mapping.  A workgroup has 4 waves; waves 2h and 2h+1 work on the same tokens,
+// wave 2h+q owning experts [8q, 8q+8).  Lane c of a wave keeps, in fp32
+// registers, its L-column slice of its 8 experts' weights (8L registers), and
+// processes 4 tokens at a time: it loads its L columns of each token (a wave
+// reads whole rows, coalesced), forms 4 x 8 = 32 partial sums, and the wave
+// reduces them with a reduce-scatter butterfly — at the xor-32 step every lane
+// keeps 16 of its 32 values and adds the partner's copy of those 16, then
+// 16 -> 8 at xor-16, ..., 2 -> 1 at xor-2, and a plain xor-1 butterfly.  Each
+// sum is therefore the pairwise tree of the contract; lanes 2m and 2m+1 end up
+// holding the logit of (token m >> 3, expert m & 7).  Each level's shuffles are
+// independent of each other, so the exchange latency overlaps; per token a wave
+// spends 8 exchanges instead of 17.  Logits go through LDS; one thread per token
+// does the top-k scan and the gates.
 //
 // Cost.  The E*d fused multiply-adds per token are the floor: N*E*d = 447M
-// FMAs at N = 36,400, about 11 us of VALU time on 256 CUs; the 55.9 MB read of
-// x would take about 7 us at 8 TB/s, so the kernel is VALU-bound, not HBM-bound.
+// FMAs at N = 36,400, about 11-14 us of VALU time on 256 CUs at 2.0-2.4 GHz;
+// reading x (55.9 MB) takes about 7 us at 8 TB/s, so the kernel is VALU-bound.
 #include "g5moe_internal.h"
 
 namespace g5moe {
 namespace {
 
 constexpr int kRouterThreads = 256;
-constexpr int kRouterWaves = kRouterThreads / 64;
-constexpr int kTokensPerWave = 8;
-constexpr int kTokensPerBlock = kRouterWaves * kTokensPerWave;
+constexpr int kHalfExperts = 8;           // experts per wave
+constexpr int kTokBatch = 4;              // tokens reduced together
+constexpr int kPairBatches = 4;           // batches per wave pair
+constexpr int kTokensPerPair = kTokBatch * kPairBatches;
+constexpr int kTokensPerBlock = 2 * kTokensPerPair;
 
 template <typename XT, int L>
 struct RowLoader;
@@ -85,21 +93,16 @@ struct RowLoader<float, L> {
   }
 };
 
-__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
-}
-
-// One reduce-scatter level: lanes with `bit` set keep the upper half of p.
+// One reduce-scatter level over V values: lanes with `bit` set keep the upper
+// half.  p[i] and the partner's p[i] (same index) hold the same (token, expert).
 template <int HALF>
 __device__ __forceinline__ void rs_level(float* p, int lane, int bit) {
   const bool hi = (lane & bit) != 0;
+  float recv[HALF];
 #pragma unroll
-  for (int i = 0; i < HALF; ++i) {
-    float send = hi ? p[i] : p[HALF + i];
-    float keep = hi ? p[HALF + i] : p[i];
-    float recv = shfl_xor_f(send, bit);
-    p[i] = keep + recv;
-  }
+  for (int i = 0; i < HALF; ++i) recv[i] = __shfl_xor(hi ? p[i] : p[HALF + i], bit, 64);
+#pragma unroll
+  for (int i = 0; i < HALF; ++i) p[i] = (hi ? p[HALF + i] : p[i]) + recv[i];
 }
 
 template <typename XT, int L>
@@ -112,61 +115,61 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int64_t tok0 = int64_t(blockIdx.x) * kTokensPerBlock;
+  const int half = wave & 1;      // experts [8*half, 8*half + 8)
+  const int pair = wave >> 1;     // token group of the block
+  const int e0 = half * kHalfExperts;
+  const int64_t tok0 = int64_t(blockIdx.x) * kTokensPerBlock + pair * kTokensPerPair;
 
-  // Router weight slice for this lane, all experts, in fp32 registers.
-  float w[kMaxExperts][L];
+  // This lane's weight slice for its wave's 8 experts (0 for experts >= E).
+  float w[kHalfExperts][L];
 #pragma unroll
-  for (int e = 0; e < kMaxExperts; ++e) {
-    if (e < n_experts) {
-      RowLoader<XT, L>::load(wr + size_t(e) * D + lane * L, w[e]);
+  for (int e = 0; e < kHalfExperts; ++e) {
+    if (e0 + e < n_experts) {
+      RowLoader<XT, L>::load(wr + size_t(e0 + e) * D + lane * L, w[e]);
     } else {
 #pragma unroll
       for (int i = 0; i < L; ++i) w[e][i] = 0.f;
     }
   }
 
-  // Tokens of this wave: tok0 + wave*kTokensPerWave + j.
-  const int64_t wtok0 = tok0 + wave * kTokensPerWave;
-  float xv[L];
-  if (wtok0 < n_tokens) RowLoader<XT, L>::load(x + size_t(wtok0) * D + lane * L, xv);
-  for (int j = 0; j < kTokensPerWave; ++j) {
-    const int64_t t = wtok0 + j;
-    if (t >= n_tokens) break;
-    float xn[L];
-    const bool more = (j + 1 < kTokensPerWave) && (t + 1 < n_tokens);
-    if (more) RowLoader<XT, L>::load(x + size_t(t + 1) * D + lane * L, xn);
-
-    float p[kMaxExperts];
+  for (int b = 0; b < kPairBatches; ++b) {
+    const int64_t tb = tok0 + b * kTokBatch;
+    if (tb >= n_tokens) break;
+    float p[kTokBatch * kHalfExperts];
 #pragma unroll
-    for (int e = 0; e < kMaxExperts; ++e) {
-      float acc = 0.f;
+    for (int m = 0; m < kTokBatch; ++m) {
+      float xv[L];
+      const int64_t t = min(tb + m, n_tokens - 1);  // rows past the end are computed, not stored
+      RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv);
 #pragma unroll
-      for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[i], w[e][i], acc);
-      p[e] = acc;
+      for (int e = 0; e < kHalfExperts; ++e) {
+        float acc = 0.f;
+#pragma unroll
+        for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[i], w[e][i], acc);
+        p[m * kHalfExperts + e] = acc;
+      }
     }
-    rs_level<8>(p, lane, 32);
-    rs_level<4>(p, lane, 16);
-    rs_level<2>(p, lane, 8);
-    rs_level<1>(p, lane, 4);
-    p[0] = p[0] + shfl_xor_f(p[0], 2);
-    p[0] = p[0] + shfl_xor_f(p[0], 1);
-    const int e = lane >> 2;
-    if ((lane & 3) == 0 && e < n_experts) {
-      float v = p[0];
-      if (bias != nullptr) v = v + bias[e];
-      lg[wave * kTokensPerWave + j][e] = v;
-    }
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < L; ++i) xv[i] = xn[i];
+    rs_level<16>(p, lane, 32);
+    rs_level<8>(p, lane, 16);
+    rs_level<4>(p, lane, 8);
+    rs_level<2>(p, lane, 4);
+    rs_level<1>(p, lane, 2);
+    p[0] = p[0] + __shfl_xor(p[0], 1, 64);
+    // lane holds value index v = 16*b5 + 8*b4 + 4*b3 + 2*b2 + b1 of its bits,
+    // i.e. token m = v >> 3, expert e0 + (v & 7).
+    const int v = lane >> 1;
+    const int m = v >> 3, e = e0 + (v & 7);
+    if ((lane & 1) == 0 && e < n_experts && tb + m < n_tokens) {
+      float val = p[0];
+      if (bias != nullptr) val = val + bias[e];
+      lg[pair * kTokensPerPair + b * kTokBatch + m][e] = val;
     }
   }
   __syncthreads();
 
   // Top-k scan and gates: one thread per token.
   const int tl = threadIdx.x;
-  const int64_t t = tok0 + tl;
+  const int64_t t = int64_t(blockIdx.x) * kTokensPerBlock + tl;
   if (tl < kTokensPerBlock && t < n_tokens) {
     float l[kMaxExperts];
 #pragma unroll
