@@ -47,6 +47,10 @@ g5moe_status check_shape(const g5moe_shape* s) {
   if (s->n_tokens * s->top_k > int64_t(INT32_MAX) / 2)
     return fail(G5MOE_ERR_UNSUPPORTED, "n_tokens * top_k = %lld exceeds the int32 index range",
                 (long long)(s->n_tokens * s->top_k));
+  // The gate|up GEMM addresses gathered rows of x with 32-bit byte offsets.
+  if (s->n_tokens * int64_t(d) * 2 > int64_t(UINT32_MAX))
+    return fail(G5MOE_ERR_UNSUPPORTED, "x holds %lld bf16 values, beyond the 4 GiB the "
+                "row gather addresses", (long long)(s->n_tokens * d));
   return G5MOE_OK;
 }
 

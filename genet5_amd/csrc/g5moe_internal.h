@@ -12,6 +12,7 @@ namespace g5moe {
 constexpr int kMaxExperts = 16;
 constexpr int kMaxTopK = 4;
 constexpr int kDispatchBlock = 256;  // assignments per dispatch block
+constexpr int kGemmRowPad = 256;     // rows of padding after h (one GEMM m-tile)
 
 // Byte offsets of the workspace regions (each 256-byte aligned).
 struct WorkspaceLayout {
@@ -41,7 +42,9 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   w.rank = off;
   off += align256(size_t(nk) * 4);
   w.h = off;
-  off += align256(size_t(nk) * s.d_ff * 2);
+  // kGemmRowPad rows of padding: the down GEMM reads whole 256-row tiles of h
+  // without clamping (rows past the end are computed and never stored).
+  off += align256(size_t(nk + kGemmRowPad) * s.d_ff * 2);
   w.y_perm = off;
   off += align256(size_t(nk) * s.d_model * 2);
   w.total = off;

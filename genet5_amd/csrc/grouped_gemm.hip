@@ -37,6 +37,9 @@
 // rows of f in [32g, 32g+32), then the matching up rows), so the wave's
 // feature blocks 2j and 2j+1 hold gate and up of the same 32 h columns in the
 // same lanes; silu(g) * u is formed in registers and only h is stored (bf16).
+#include <algorithm>
+#include <type_traits>
+
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -330,6 +333,341 @@ __global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Persistent variant: one workgroup per CU walks a list of tiles.
+//
+// The tiles of the launch (same numbering as decode_tile) are cut into 8
+// contiguous ranges, one per XCD (workgroup b runs on XCD b % 8); workgroup
+// slot s of an XCD takes tiles lo + s, lo + s + nslot, ... of its range, so at
+// any time the XCD's CUs work on consecutive tiles that share A rows and B
+// columns in its L2.
+//
+// The k-steps of all of a workgroup's tiles form one pipelined stream: the
+// DMA of step g + 2 is issued while step g computes, so the first two stages
+// of tile i + 1 land during the last two k-steps and the epilogue of tile i.
+// The epilogue goes through a wave-private 8 KB LDS region (after the two
+// stage buffers) so that every global store instruction writes whole 128-byte
+// row segments: 8 lanes per 128 bytes of one output row.
+constexpr int kEpiBytesPerWave = 8192;
+
+template <int BM, int BN, int GM>
+__device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileCoord& tc) {
+  const int ntn = args.Nout / BN;
+  int e = 0, mt_e = 0;
+  for (; e < args.n_experts; ++e) {
+    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    mt_e = (cnt + BM - 1) / BM;
+    const int t = mt_e * ntn;
+    if (u < t) break;
+    u -= t;
+  }
+  const int g = u / (GM * ntn);
+  const int first_m = g * GM;
+  const int gs = min(GM, mt_e - first_m);
+  const int rr = u - g * GM * ntn;
+  const int mt = first_m + rr % gs;
+  const int nt = rr / gs;
+  tc.e = e;
+  tc.p_begin = args.offsets[e] + mt * BM;
+  tc.p_end = args.offsets[e + 1];
+  tc.n0 = nt * BN;
+}
+
+template <int BM, int BN, int GM, bool SWIGLU>
+__global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
+  constexpr int BK = 64;
+  constexpr int WTM = BM / 2, WTN = BN / 2;
+  constexpr int MB = WTM / 32, NB = WTN / 32;
+  constexpr int RB = BK * 2;          // 128 bytes per tile row
+  constexpr int CPR = RB / 16;        // 8 chunks of 16 bytes per row
+  constexpr int RPB = 1024 / RB;      // 8 rows per 1 KB DMA block
+  constexpr int G = 256 / RB;         // 2 rows per 256-byte bank line
+  constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int AI = A_BYTES / 1024 / 4;
+  constexpr int BI = B_BYTES / 1024 / 4;
+  constexpr int KS = BK / 16;
+  static_assert(2 * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
+  static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
+  static_assert(KS % 2 == 0, "even substeps per stage");
+  // The swizzle of DMA slot j's rows depends only on j % 2 (see lane offsets).
+  static_assert((AI * RPB / G) % CPR == 0 && (BI * RPB / G) % CPR == 0 &&
+                    (RPB / G) * 2 == CPR,
+                "slot swizzle period");
+  // The gate|up GEMM gathers token rows through perm; the down GEMM reads the
+  // expert-contiguous h rows in place.
+  constexpr bool GATHER = SWIGLU;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE + 4 * kEpiBytesPerWave];
+
+  const int ntn = args.Nout / BN;
+  int total = 0;
+  for (int e = 0; e < args.n_experts; ++e) {
+    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    total += ((cnt + BM - 1) / BM) * ntn;
+  }
+  // This workgroup's share: XCD x owns tiles [lo, hi), slot s takes every
+  // nslot-th of them.
+  const int ng = gridDim.x;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  int before = 0;
+  for (int y = 0; y < xcd; ++y) before += (ng - y + 7) >> 3;
+  const int nslot = (ng - xcd + 7) >> 3;
+  const int lo = int(int64_t(total) * before / ng);
+  const int hi = int(int64_t(total) * (before + nslot) / ng);
+  int u = lo + slot;
+  if (u >= hi) return;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int K = args.K;
+  const int nk = K / BK;  // >= 2 (checked by the launcher)
+  const int64_t kslot = int64_t(RPB) * K * 2;  // bytes between DMA slots' first rows
+
+  auto sw = [](int r) { return (r / G) % CPR; };
+  const int lrow = lane / CPR;
+  const int lpc = lane % CPR;
+  // DMA slot j of a wave fills rows (wave * SLOTS + j) * RPB + lrow with the
+  // lane's 16-byte chunk lpc ^ sw(row); sw(row) = (4 j + lrow / 2) % 8, so the
+  // byte offset of a lane inside its slot takes two values, by j % 2.
+  uint32_t lane_off[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par)
+    lane_off[par] = uint32_t(lrow * K * 2 + (lpc ^ sw(par * RPB + lrow)) * 16);
+
+  // Gathered rows: fetch_rows issues the perm loads of a tile (no wait);
+  // finish_rows turns the fetched assignments into byte offsets of token rows
+  // of x once they are needed.  Positions past the expert's end repeat its
+  // last row.
+  uint32_t rows_cur[GATHER ? AI : 1], rows_nxt[GATHER ? AI : 1];
+  auto fetch_rows = [&](const TileCoord& tc, uint32_t* rows) {
+    if constexpr (GATHER) {
+#pragma unroll
+      for (int j = 0; j < AI; ++j) {
+        const int p = min(tc.p_begin + (wave * AI + j) * RPB + lrow, tc.p_end - 1);
+        rows[j] = uint32_t(__builtin_nontemporal_load(args.perm + p));
+      }
+    }
+  };
+  auto finish_rows = [&](uint32_t* rows) {
+    if constexpr (GATHER) {
+      const uint32_t tk = uint32_t(args.topk);
+#pragma unroll
+      for (int j = 0; j < AI; ++j)
+        rows[j] = (rows[j] / tk) * uint32_t(K * 2) + (lane_off[j & 1] - uint32_t(lrow * K * 2));
+    }
+  };
+  auto issue = [&](int buf, const uint32_t* rows, const TileCoord& tc, int k0) {
+    char* As = smem + buf * STAGE;
+    char* Bs = As + A_BYTES;
+    if constexpr (GATHER) {
+      const char* ab = reinterpret_cast<const char*>(args.A + k0);
+#pragma unroll
+      for (int j = 0; j < AI; ++j) lds_dma16(ab + rows[j], As + (wave * AI + j) * 1024);
+    } else {
+      // Rows p_begin .. p_begin + BM - 1: the h buffer has BM rows of padding
+      // after its last row, so no clamping is needed (padding rows are never
+      // stored).
+      const char* ab = reinterpret_cast<const char*>(
+          args.A + (int64_t(tc.p_begin) + wave * AI * RPB) * K + k0);
+#pragma unroll
+      for (int j = 0; j < AI; ++j)
+        lds_dma16(ab + j * kslot + lane_off[j & 1], As + (wave * AI + j) * 1024);
+    }
+    const char* bb = reinterpret_cast<const char*>(
+        args.B + (int64_t(tc.e) * args.Nout + tc.n0 + wave * BI * RPB) * K + k0);
+#pragma unroll
+    for (int j = 0; j < BI; ++j)
+      lds_dma16(bb + j * kslot + lane_off[j & 1], Bs + (wave * BI + j) * 1024);
+  };
+
+  TileCoord cur, nxt;
+  decode_tile_u<BM, BN, GM>(args, u, cur);
+  fetch_rows(cur, rows_cur);
+  bool has_nxt = u + nslot < hi;
+  if (has_nxt) {
+    decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
+    fetch_rows(nxt, rows_nxt);
+  }
+  finish_rows(rows_cur);
+
+  // acc[i][j]: feature block i x token block j (see grouped_gemm_dma_kernel);
+  // the first MFMA of every tile takes a zero accumulator input.
+  f32x16 acc[NB][MB];
+  const f32x16 zero16 = {};
+
+  const int a_row = (wm * WTM + (lane & 31)) * RB;
+  const int b_row = (wn * WTN + (lane & 31)) * RB;
+  const int khalf = lane >> 5;
+  const int rsw = sw(lane & 31);
+  bf16x8 af[2][MB], bfr[2][NB];
+  auto load_frag = [&](const char* As, const char* Bs, int ks, int slot_, int f) {
+    const int pc = ((ks * 2 + khalf) ^ rsw) * 16;
+    if (f < MB)
+      af[slot_][f] = *reinterpret_cast<const bf16x8*>(As + a_row + f * 32 * RB + pc);
+    else
+      bfr[slot_][f - MB] =
+          *reinterpret_cast<const bf16x8*>(Bs + b_row + (f - MB) * 32 * RB + pc);
+  };
+
+  issue(0, rows_cur, cur, 0);
+  issue(1, rows_cur, cur, BK);
+  wait_vmcnt<AI + BI>();  // stage 0 landed
+  __syncthreads();
+#pragma unroll
+  for (int f = 0; f < MB + NB; ++f) load_frag(smem, smem + A_BYTES, 0, 0, f);
+
+  char* epi = smem + 2 * STAGE + wave * kEpiBytesPerWave;
+  const int tok_l = lane & 31;
+  const int half = lane >> 5;
+  int gstep = 0;  // k-step counter over all tiles of this workgroup; buffer = gstep & 1
+
+  // One k-step (KS substeps of 16 k) of the current tile.  FIRST: the tile's
+  // first step (zero accumulator input); LAST: its last step (the next step's
+  // first fragments are read after the epilogue instead).
+  auto kstep = [&](auto first_c, auto last_c, int kt) {
+    constexpr bool FIRST = decltype(first_c)::value;
+    constexpr bool LAST = decltype(last_c)::value;
+    const int cb = gstep & 1;
+    const char* As = smem + cb * STAGE;
+    const char* Bs = As + A_BYTES;
+    const char* As_n = smem + (cb ^ 1) * STAGE;
+    const char* Bs_n = As_n + A_BYTES;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks == KS - 1) {
+        __builtin_amdgcn_sched_barrier(0);
+        // step g + 1 landed (and the stores of the last epilogue drained)
+        wait_vmcnt<0>();
+        __syncthreads();
+        if (kt + 2 < nk) {
+          issue(cb, rows_cur, cur, (kt + 2) * BK);
+        } else if (has_nxt) {
+          if (kt + 2 == nk) finish_rows(rows_nxt);  // fetched a tile ago; landed
+          issue(cb, rows_nxt, nxt, (kt + 2 - nk) * BK);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int t = 0; t < MB * NB; ++t) {
+        const int i = t / MB, j = t % MB;
+        if (FIRST && ks == 0)
+          acc[i][j] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[0][i], af[0][j], zero16, 0, 0, 0);
+        else
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][i], af[ks & 1][j],
+                                                              acc[i][j], 0, 0, 0);
+        if (t < MB + NB) {
+          if (ks + 1 < KS)
+            load_frag(As, Bs, ks + 1, (ks + 1) & 1, t);
+          else if (!LAST)
+            load_frag(As_n, Bs_n, 0, 0, t);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    ++gstep;
+  };
+
+  using T_ = std::true_type;
+  using F_ = std::false_type;
+  for (;;) {
+    kstep(T_{}, F_{}, 0);
+    for (int kt = 1; kt + 1 < nk; ++kt) kstep(F_{}, F_{}, kt);
+    kstep(F_{}, T_{}, nk - 1);
+
+    // Epilogue of `cur` through the wave's LDS region.  The wave's output is
+    // OB blocks of 32 columns (SwiGLU: h columns, half the feature columns) of
+    // bf16, RBY bytes per token row; a pass stages ROWS token rows, chunk c of
+    // row r at c ^ ((r / (256 / RBY)) % CR), then writes them back as 16-byte
+    // stores, CR lanes per row.
+    {
+      constexpr int OB = SWIGLU ? NB / 2 : NB;
+      constexpr int RBY = OB * 64;
+      constexpr int CR = RBY / 16;
+      constexpr int ROWS = kEpiBytesPerWave / RBY;
+      constexpr int JP = ROWS / 32;  // token blocks per pass
+      constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
+      static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+      const int col0 = SWIGLU ? (cur.n0 + wn * WTN) / 2 : cur.n0 + wn * WTN;
+#pragma unroll
+      for (int pass = 0; pass < MB / JP; ++pass) {
+#pragma unroll
+        for (int jl = 0; jl < JP; ++jl) {
+          const int j = pass * JP + jl;
+          const int row = jl * 32 + tok_l;
+          const int swz = (row / LPR) % CR;
+#pragma unroll
+          for (int ob = 0; ob < OB; ++ob) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float h[4];
+#pragma unroll
+              for (int uu = 0; uu < 4; ++uu) {
+                if constexpr (SWIGLU)
+                  h[uu] = silu_mul(acc[2 * ob][j][4 * q + uu], acc[2 * ob + 1][j][4 * q + uu]);
+                else
+                  h[uu] = acc[ob][j][4 * q + uu];
+              }
+              uint2 o;
+              o.x = pack_bf16x2(h[0], h[1]);
+              o.y = pack_bf16x2(h[2], h[3]);
+              const int c = ob * 4 + q;
+              *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+              // keep only one group's accumulators in VGPRs at a time
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < ROWS * RBY / 1024; ++it) {
+          const int row = it * (1024 / RBY) + lane / CR;
+          const int c = lane % CR;
+          const uint4 v = *reinterpret_cast<const uint4*>(
+              epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
+          const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
+          if (p < cur.p_end)
+            *reinterpret_cast<uint4*>(args.C + int64_t(p) * args.ldc + col0 + c * 8) = v;
+        }
+      }
+    }
+
+    if (!has_nxt) break;
+    cur = nxt;
+    if constexpr (GATHER) {
+#pragma unroll
+      for (int j = 0; j < AI; ++j) rows_cur[j] = rows_nxt[j];
+    }
+    u += nslot;
+    has_nxt = u + nslot < hi;
+    if (has_nxt) {
+      decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
+      fetch_rows(nxt, rows_nxt);
+    }
+    // first substep's fragments of the new tile (its stage 0 landed at the
+    // last stage barrier)
+    {
+      const char* As = smem + (gstep & 1) * STAGE;
+#pragma unroll
+      for (int f = 0; f < MB + NB; ++f) load_frag(As, As + A_BYTES, 0, 0, f);
+    }
+  }
+}
+
+int device_cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
 // Upper bound on the number of tiles: sum_e ceil(cnt_e / BM) <= ceil(Nk / BM) + E.
 template <int BM, int BN>
 unsigned grid_bound(int64_t nk, int n_experts, int nout) {
@@ -380,6 +718,15 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #ifndef G5_DN_STAGES
 #define G5_DN_STAGES 2
 #endif
+#ifndef G5_GEMM_PERSIST
+#define G5_GEMM_PERSIST 1
+#endif
+#ifndef G5_GU_GM
+#define G5_GU_GM 4
+#endif
+#ifndef G5_DN_GM
+#define G5_DN_GM 4
+#endif
 
 }  // namespace
 
@@ -400,8 +747,14 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.Nout = 2 * s.d_ff;
   a.ldc = s.d_ff;
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+#if G5_GEMM_PERSIST
+  const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
+  hipLaunchKernelGGL((grouped_gemm_persist_kernel<256, 256, G5_GU_GM, true>), dim3(pgrid),
+                     dim3(256), 0, st, a);
+#else
   hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_GU_BK, G5_GU_STAGES, true>), dim3(grid),
                      dim3(256), 0, st, a);
+#endif
   return hipGetLastError();
 }
 
@@ -420,6 +773,18 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.K = s.d_ff;
   a.Nout = s.d_model;
   a.ldc = s.d_model;
+#if G5_GEMM_PERSIST
+  const unsigned ncu = unsigned(device_cu_count());
+  if (a.Nout % 256 == 0) {
+    const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout), ncu);
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<256, 256, G5_DN_GM, false>), dim3(grid),
+                       dim3(256), 0, st, a);
+  } else {
+    const unsigned grid = std::min(grid_bound<256, 128>(nk, s.n_experts, a.Nout), ncu);
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<256, 128, G5_DN_GM, false>), dim3(grid),
+                       dim3(256), 0, st, a);
+  }
+#else
   if (a.Nout % 256 == 0) {
     const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_DN_BK, G5_DN_STAGES, false>),
@@ -429,6 +794,7 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
     hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 128, G5_DN_BK, G5_DN_STAGES, false>),
                        dim3(grid), dim3(256), 0, st, a);
   }
+#endif
   return hipGetLastError();
 }
 

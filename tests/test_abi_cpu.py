@@ -50,7 +50,8 @@ def test_workspace_size_layout(g5lib):
     nk = 36400 * 2
     a = lambda v: (v + 255) // 256 * 256
     nblk = (nk + 255) // 256
-    assert n == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4) + a(nk * 3072 * 2) + a(nk * 768 * 2)
+    # h carries one 256-row GEMM tile of padding after its last row
+    assert n == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4) + a((nk + 256) * 3072 * 2) + a(nk * 768 * 2)
     n32 = _lib.workspace_size(shape(x_dtype=1))
     assert n32 == n + a(36400 * 768 * 2)
     assert ops._h_offset(s) == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4)
@@ -67,6 +68,7 @@ def test_workspace_size_layout(g5lib):
     (dict(x_dtype=7), 1, "x_dtype"),
     (dict(n_tokens=-1), 1, "n_tokens"),
     (dict(n_tokens=2 ** 31), 2, "int32"),
+    (dict(n_tokens=2 ** 22), 2, "4 GiB"),
 ])
 def test_invalid_shapes_rejected(g5lib, kw, code, msg):
     n = ctypes.c_size_t(0)
