@@ -119,6 +119,22 @@ __device__ __forceinline__ void lds_dma16(const void* src, char* lds_base) {
                                    0);
 }
 
+// The same DMA with an explicit scalar base and a 32-bit per-lane byte offset
+// (global_load_lds_dwordx4 voff, sbase), M0 = LDS byte address of the 1 KB
+// block.  The compiler never holds M0 in the kernels that use these helpers:
+// every LDS DMA there goes through them and sets M0 itself.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
+}
+__device__ __forceinline__ void lds_dma16_s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+__device__ __forceinline__ void lds_dma4_s(const void* sbase, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
+               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -373,31 +389,40 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileC
   tc.n0 = nt * BN;
 }
 
-template <int BM, int BN, int GM, bool SWIGLU>
+template <int BM, int BN, int BK, int S, int NSLOT, int GM, bool SWIGLU>
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
-  constexpr int BK = 64;
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int MB = WTM / 32, NB = WTN / 32;
-  constexpr int RB = BK * 2;          // 128 bytes per tile row
-  constexpr int CPR = RB / 16;        // 8 chunks of 16 bytes per row
-  constexpr int RPB = 1024 / RB;      // 8 rows per 1 KB DMA block
-  constexpr int G = 256 / RB;         // 2 rows per 256-byte bank line
+  constexpr int RB = BK * 2;          // bytes per tile row in LDS
+  constexpr int CPR = RB / 16;        // 16-byte chunks per row
+  constexpr int RPB = 1024 / RB;      // rows per 1 KB DMA block
+  constexpr int G = 256 / RB;         // rows per 256-byte bank line
   constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int AI = A_BYTES / 1024 / 4;
+  constexpr int AI = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage
   constexpr int BI = B_BYTES / 1024 / 4;
-  constexpr int KS = BK / 16;
-  static_assert(2 * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
+  constexpr int PER = AI + BI;
+  constexpr int KS = BK / 16;             // 16-k substeps per stage
+  // Fragment registers: NSLOT slots; the fragments of substep q + NSLOT - 1
+  // are read while substep q computes.  With NSLOT = 3 the stage buffer is
+  // free two substeps before the step ends, so its refill spreads over those
+  // substeps' MFMAs (the k-step loop is unrolled by 3: nk % 3 == 0, nk >= 6).
+  constexpr int LA = NSLOT - 1;           // substeps read ahead
+  constexpr int BS = KS - LA;             // substep at which the stage barrier sits
+  static_assert(NSLOT == 2 || (NSLOT == 3 && KS == 4), "fragment slots");
+  static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(S >= 2 && S * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
+  static_assert((S - 2) * PER < 64, "vmcnt range");
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
-  static_assert(KS % 2 == 0, "even substeps per stage");
-  // The swizzle of DMA slot j's rows depends only on j % 2 (see lane offsets).
+  constexpr int NT = MB * NB;             // MFMAs per substep
+  // The swizzle of DMA slot j's rows depends only on j % 2 (see lane_off).
   static_assert((AI * RPB / G) % CPR == 0 && (BI * RPB / G) % CPR == 0 &&
-                    (RPB / G) * 2 == CPR,
+                    (2 * RPB / G) % CPR == 0,
                 "slot swizzle period");
   // The gate|up GEMM gathers token rows through perm; the down GEMM reads the
   // expert-contiguous h rows in place.
   constexpr bool GATHER = SWIGLU;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE + 4 * kEpiBytesPerWave];
+  __shared__ __attribute__((aligned(1024))) char smem[S * STAGE + 4 * kEpiBytesPerWave];
 
   const int ntn = args.Nout / BN;
   int total = 0;
@@ -418,78 +443,97 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   if (u >= hi) return;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform (scalar) so every wave-dependent address term stays in SGPRs
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int K = args.K;
-  const int nk = K / BK;  // >= 2 (checked by the launcher)
-  const int64_t kslot = int64_t(RPB) * K * 2;  // bytes between DMA slots' first rows
+  const int nk = K / BK;  // >= S (checked by the launcher)
 
   auto sw = [](int r) { return (r / G) % CPR; };
   const int lrow = lane / CPR;
   const int lpc = lane % CPR;
   // DMA slot j of a wave fills rows (wave * SLOTS + j) * RPB + lrow with the
-  // lane's 16-byte chunk lpc ^ sw(row); sw(row) = (4 j + lrow / 2) % 8, so the
-  // byte offset of a lane inside its slot takes two values, by j % 2.
+  // lane's 16-byte chunk lpc ^ sw(row); sw(row) depends on j only through
+  // j % 2, so a lane's byte offset inside its slot takes two values.
   uint32_t lane_off[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par)
     lane_off[par] = uint32_t(lrow * K * 2 + (lpc ^ sw(par * RPB + lrow)) * 16);
 
-  // Gathered rows: fetch_rows issues the perm loads of a tile (no wait);
-  // finish_rows turns the fetched assignments into byte offsets of token rows
-  // of x once they are needed.  Positions past the expert's end repeat its
-  // last row.
+  // Gathered rows.  The rows of the first tile are loaded directly; those of
+  // every later tile travel by LDS DMA (one dword per lane, the wave's 64
+  // rows) into the wave's epilogue region a tile ahead, where the stage waits
+  // cover them, and become byte offsets of token rows of x when the tile's
+  // first stage is issued.  Positions past the expert's end repeat its last
+  // row.  Wave w reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile: slot j's
+  // rows (w * AI + j) * RPB + lrow.
+  static_assert(AI * RPB == 64, "one 64-row perm block per wave");
+  char* epi = smem + S * STAGE + wave * kEpiBytesPerWave;
   uint32_t rows_cur[GATHER ? AI : 1], rows_nxt[GATHER ? AI : 1];
-  auto fetch_rows = [&](const TileCoord& tc, uint32_t* rows) {
+  auto to_offset = [&](uint32_t assignment, int j) -> uint32_t {
+    return (assignment / uint32_t(args.topk)) * uint32_t(K * 2) +
+           (lane_off[j & 1] - uint32_t(lrow * K * 2));
+  };
+  auto load_rows_now = [&](const TileCoord& tc, uint32_t* rows) {
     if constexpr (GATHER) {
+      uint32_t v[AI];
 #pragma unroll
       for (int j = 0; j < AI; ++j) {
         const int p = min(tc.p_begin + (wave * AI + j) * RPB + lrow, tc.p_end - 1);
-        rows[j] = uint32_t(__builtin_nontemporal_load(args.perm + p));
+        v[j] = uint32_t(__builtin_nontemporal_load(args.perm + p));
       }
+#pragma unroll
+      for (int j = 0; j < AI; ++j) rows[j] = to_offset(v[j], j);
+    }
+  };
+  auto dma_rows = [&](const TileCoord& tc) {
+    if constexpr (GATHER) {
+      const int p = min(tc.p_begin + wave * 64 + lane, tc.p_end - 1);
+      lds_dma4_s(args.perm, uint32_t(p) * 4u, lds_addr(epi));
     }
   };
   auto finish_rows = [&](uint32_t* rows) {
     if constexpr (GATHER) {
-      const uint32_t tk = uint32_t(args.topk);
+      const uint32_t* pr = reinterpret_cast<const uint32_t*>(epi);
 #pragma unroll
-      for (int j = 0; j < AI; ++j)
-        rows[j] = (rows[j] / tk) * uint32_t(K * 2) + (lane_off[j & 1] - uint32_t(lrow * K * 2));
+      for (int j = 0; j < AI; ++j) rows[j] = to_offset(pr[j * RPB + lrow], j);
     }
   };
-  auto issue = [&](int buf, const uint32_t* rows, const TileCoord& tc, int k0) {
+  // DMA instruction q (q < AI: A slot q, else B slot q - AI) of a stage of the
+  // tile (e, n0, p_begin); row_off is the gathered row's byte offset (GATHER).
+  auto issue_one = [&](int buf, uint32_t row_off, int e, int n0, int p_begin, int k0, int q) {
     char* As = smem + buf * STAGE;
     char* Bs = As + A_BYTES;
-    if constexpr (GATHER) {
-      const char* ab = reinterpret_cast<const char*>(args.A + k0);
-#pragma unroll
-      for (int j = 0; j < AI; ++j) lds_dma16(ab + rows[j], As + (wave * AI + j) * 1024);
+    if (q < AI) {
+      if constexpr (GATHER) {
+        lds_dma16_s(args.A + k0, row_off, lds_addr(As + (wave * AI + q) * 1024));
+      } else {
+        // Rows p_begin .. p_begin + BM - 1: h has BM rows of padding after its
+        // last row, so no clamping is needed (padding rows are never stored).
+        const char* ab = reinterpret_cast<const char*>(
+            args.A + (int64_t(p_begin) + (wave * AI + q) * RPB) * K + k0);
+        lds_dma16_s(ab, lane_off[q & 1], lds_addr(As + (wave * AI + q) * 1024));
+      }
     } else {
-      // Rows p_begin .. p_begin + BM - 1: the h buffer has BM rows of padding
-      // after its last row, so no clamping is needed (padding rows are never
-      // stored).
-      const char* ab = reinterpret_cast<const char*>(
-          args.A + (int64_t(tc.p_begin) + wave * AI * RPB) * K + k0);
-#pragma unroll
-      for (int j = 0; j < AI; ++j)
-        lds_dma16(ab + j * kslot + lane_off[j & 1], As + (wave * AI + j) * 1024);
+      const int j = q - AI;
+      const char* bb = reinterpret_cast<const char*>(
+          args.B + (int64_t(e) * args.Nout + n0 + (wave * BI + j) * RPB) * K + k0);
+      lds_dma16_s(bb, lane_off[j & 1], lds_addr(Bs + (wave * BI + j) * 1024));
     }
-    const char* bb = reinterpret_cast<const char*>(
-        args.B + (int64_t(tc.e) * args.Nout + tc.n0 + wave * BI * RPB) * K + k0);
-#pragma unroll
-    for (int j = 0; j < BI; ++j)
-      lds_dma16(bb + j * kslot + lane_off[j & 1], Bs + (wave * BI + j) * 1024);
+  };
+  auto row_of = [&](const uint32_t* rows, int q) -> uint32_t {
+    if constexpr (GATHER) return q < AI ? rows[q < AI ? q : 0] : 0u;
+    return 0u;
   };
 
   TileCoord cur, nxt;
   decode_tile_u<BM, BN, GM>(args, u, cur);
-  fetch_rows(cur, rows_cur);
+  load_rows_now(cur, rows_cur);
   bool has_nxt = u + nslot < hi;
   if (has_nxt) {
     decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
-    fetch_rows(nxt, rows_nxt);
+    dma_rows(nxt);
   }
-  finish_rows(rows_cur);
 
   // acc[i][j]: feature block i x token block j (see grouped_gemm_dma_kernel);
   // the first MFMA of every tile takes a zero accumulator input.
@@ -500,7 +544,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   const int b_row = (wn * WTN + (lane & 31)) * RB;
   const int khalf = lane >> 5;
   const int rsw = sw(lane & 31);
-  bf16x8 af[2][MB], bfr[2][NB];
+  bf16x8 af[NSLOT][MB], bfr[NSLOT][NB];
   auto load_frag = [&](const char* As, const char* Bs, int ks, int slot_, int f) {
     const int pc = ((ks * 2 + khalf) ^ rsw) * 16;
     if (f < MB)
@@ -510,71 +554,125 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
           *reinterpret_cast<const bf16x8*>(Bs + b_row + (f - MB) * 32 * RB + pc);
   };
 
-  issue(0, rows_cur, cur, 0);
-  issue(1, rows_cur, cur, BK);
-  wait_vmcnt<AI + BI>();  // stage 0 landed
-  __syncthreads();
+  // Prologue: stages 0 .. S-1 of the first tile (nk >= S).
 #pragma unroll
-  for (int f = 0; f < MB + NB; ++f) load_frag(smem, smem + A_BYTES, 0, 0, f);
+  for (int st = 0; st < S; ++st)
+#pragma unroll
+    for (int q = 0; q < PER; ++q)
+      issue_one(st, row_of(rows_cur, q), cur.e, cur.n0, cur.p_begin, st * BK, q);
+  int issued = S;  // stages issued so far (global step numbering)
+  wait_vmcnt<(S - 1) * PER>();  // stage 0 landed
+  __syncthreads();
+  // fragments of the tile's first LA substeps (slots 0 .. LA - 1)
+  auto load_first_frags = [&](const char* As) {
+#pragma unroll
+    for (int ks = 0; ks < LA; ++ks)
+#pragma unroll
+      for (int f = 0; f < MB + NB; ++f) load_frag(As, As + A_BYTES, ks, ks, f);
+  };
+  load_first_frags(smem);
 
-  char* epi = smem + 2 * STAGE + wave * kEpiBytesPerWave;
   const int tok_l = lane & 31;
   const int half = lane >> 5;
-  int gstep = 0;  // k-step counter over all tiles of this workgroup; buffer = gstep & 1
+  int gstep = 0;  // k-step counter over all tiles of this workgroup; buffer = gstep % S
 
   // One k-step (KS substeps of 16 k) of the current tile.  FIRST: the tile's
   // first step (zero accumulator input); LAST: its last step (the next step's
-  // first fragments are read after the epilogue instead).
-  auto kstep = [&](auto first_c, auto last_c, int kt) {
+  // first fragments are read after the epilogue instead).  At the start of the
+  // last substep the wave waits for step g + 1's stage, syncs (every wave is
+  // done reading buffer g % S), and then refills that buffer with stage g + S,
+  // one DMA instruction after every other MFMA of the substep.
+  auto kstep = [&](auto first_c, auto last_c, auto phase_c, int kt) {
     constexpr bool FIRST = decltype(first_c)::value;
     constexpr bool LAST = decltype(last_c)::value;
-    const int cb = gstep & 1;
+    constexpr int PHASE = decltype(phase_c)::value;  // gstep % 3 when NSLOT == 3
+    auto slot = [](int ks) { return NSLOT == 2 ? (ks & 1) : (PHASE * KS + ks) % 3; };
+    const int cb = gstep % S;
+    const int nb = (gstep + 1) % S;
     const char* As = smem + cb * STAGE;
     const char* Bs = As + A_BYTES;
-    const char* As_n = smem + (cb ^ 1) * STAGE;
+    const char* As_n = smem + nb * STAGE;
     const char* Bs_n = As_n + A_BYTES;
+    // the stage that refills buffer cb: tile-relative k-step kt + S
+    const int ks_fill = kt + S;
+    const bool fill_cur = ks_fill < nk;
+    const bool fill = fill_cur || has_nxt;
+    const int k0_fill = (fill_cur ? ks_fill : ks_fill - nk) * BK;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
-      if (ks == KS - 1) {
+      if (ks == BS) {
         __builtin_amdgcn_sched_barrier(0);
-        // step g + 1 landed (and the stores of the last epilogue drained)
-        wait_vmcnt<0>();
+        // stage g + 1 landed; stages g + 2 .. issued - 1 may still be in flight
+        // (epilogue stores issued after them only make this wait longer)
+        wait_vmcnt_upto<S - 2, PER>(min(S - 2, max(0, issued - (gstep + 2))));
         __syncthreads();
-        if (kt + 2 < nk) {
-          issue(cb, rows_cur, cur, (kt + 2) * BK);
-        } else if (has_nxt) {
-          if (kt + 2 == nk) finish_rows(rows_nxt);  // fetched a tile ago; landed
-          issue(cb, rows_nxt, nxt, (kt + 2 - nk) * BK);
+        if (fill && !fill_cur && ks_fill == nk) {
+          // the next tile's perm block went out at this tile's start, before
+          // stage kt + 1 when nk >= 2S - 1; otherwise wait for it explicitly
+          if (nk < 2 * S - 1) wait_vmcnt<0>();
+          finish_rows(rows_nxt);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
 #pragma unroll
       for (int t = 0; t < MB * NB; ++t) {
         const int i = t / MB, j = t % MB;
+        const int sl = slot(ks);
         if (FIRST && ks == 0)
           acc[i][j] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[0][i], af[0][j], zero16, 0, 0, 0);
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[sl][i], af[sl][j], zero16, 0, 0, 0);
         else
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][i], af[ks & 1][j],
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[sl][i], af[sl][j],
                                                               acc[i][j], 0, 0, 0);
         if (t < MB + NB) {
-          if (ks + 1 < KS)
-            load_frag(As, Bs, ks + 1, (ks + 1) & 1, t);
+          if (ks + LA < KS)
+            load_frag(As, Bs, ks + LA, slot(ks + LA), t);
           else if (!LAST)
-            load_frag(As_n, Bs_n, 0, 0, t);
+            load_frag(As_n, Bs_n, ks + LA - KS, slot(ks + LA), t);
+        }
+        if (ks >= BS && fill) {
+          // DMA instructions q in [w * PER / W, (w + 1) * PER / W) go out after
+          // the w-th MFMA since the barrier: the stage's PER instructions
+          // spread over the substeps from BS on.
+          constexpr int W = (KS - BS) * NT;
+          const int w = (ks - BS) * NT + t;
+#pragma unroll
+          for (int q = (w * PER) / W; q < ((w + 1) * PER) / W; ++q)
+            issue_one(cb, fill_cur ? row_of(rows_cur, q) : row_of(rows_nxt, q),
+                      fill_cur ? cur.e : nxt.e, fill_cur ? cur.n0 : nxt.n0,
+                      fill_cur ? cur.p_begin : nxt.p_begin, k0_fill, q);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
+    if (fill) ++issued;
     ++gstep;
   };
 
   using T_ = std::true_type;
   using F_ = std::false_type;
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  using P2 = std::integral_constant<int, 2>;
   for (;;) {
-    kstep(T_{}, F_{}, 0);
-    for (int kt = 1; kt + 1 < nk; ++kt) kstep(F_{}, F_{}, kt);
-    kstep(F_{}, T_{}, nk - 1);
+    if constexpr (NSLOT == 2) {
+      kstep(T_{}, F_{}, P0{}, 0);
+      for (int kt = 1; kt + 1 < nk; ++kt) kstep(F_{}, F_{}, P0{}, kt);
+      kstep(F_{}, T_{}, P0{}, nk - 1);
+    } else {
+      // nk % 3 == 0 and nk >= 6, so every tile starts at gstep % 3 == 0
+      kstep(T_{}, F_{}, P0{}, 0);
+      kstep(F_{}, F_{}, P1{}, 1);
+      kstep(F_{}, F_{}, P2{}, 2);
+      for (int kt = 3; kt + 3 < nk; kt += 3) {
+        kstep(F_{}, F_{}, P0{}, kt);
+        kstep(F_{}, F_{}, P1{}, kt + 1);
+        kstep(F_{}, F_{}, P2{}, kt + 2);
+      }
+      kstep(F_{}, F_{}, P0{}, nk - 3);
+      kstep(F_{}, F_{}, P1{}, nk - 2);
+      kstep(F_{}, T_{}, P2{}, nk - 1);
+    }
 
     // Epilogue of `cur` through the wave's LDS region.  The wave's output is
     // OB blocks of 32 columns (SwiGLU: h columns, half the feature columns) of
@@ -642,15 +740,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
     has_nxt = u + nslot < hi;
     if (has_nxt) {
       decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
-      fetch_rows(nxt, rows_nxt);
+      // the epilogue's LDS reads of this region completed before its stores
+      dma_rows(nxt);
     }
-    // first substep's fragments of the new tile (its stage 0 landed at the
+    // first substeps' fragments of the new tile (its stage 0 landed at the
     // last stage barrier)
-    {
-      const char* As = smem + (gstep & 1) * STAGE;
-#pragma unroll
-      for (int f = 0; f < MB + NB; ++f) load_frag(As, As + A_BYTES, 0, 0, f);
-    }
+    load_first_frags(smem + (gstep % S) * STAGE);
   }
 }
 
@@ -706,20 +801,22 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 
 // Tile configurations (the k depth and LDS stage count can be overridden at
 // build time for tuning).
-#ifndef G5_GU_BK
-#define G5_GU_BK 64
-#endif
-#ifndef G5_GU_STAGES
-#define G5_GU_STAGES 2
-#endif
-#ifndef G5_DN_BK
-#define G5_DN_BK 64
-#endif
-#ifndef G5_DN_STAGES
-#define G5_DN_STAGES 2
-#endif
 #ifndef G5_GEMM_PERSIST
 #define G5_GEMM_PERSIST 1
+#endif
+#define G5_DEF_BK 64
+#define G5_DEF_STAGES 2
+#ifndef G5_GU_BK
+#define G5_GU_BK G5_DEF_BK
+#endif
+#ifndef G5_GU_STAGES
+#define G5_GU_STAGES G5_DEF_STAGES
+#endif
+#ifndef G5_DN_BK
+#define G5_DN_BK G5_DEF_BK
+#endif
+#ifndef G5_DN_STAGES
+#define G5_DN_STAGES G5_DEF_STAGES
 #endif
 #ifndef G5_GU_GM
 #define G5_GU_GM 4
@@ -727,6 +824,18 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #ifndef G5_DN_GM
 #define G5_DN_GM 4
 #endif
+
+// Persistent launch: three fragment slots when the k-step count allows it.
+template <int BM, int BN, int BK, int S, int GM, bool SWIGLU>
+void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
+  const int nk = a.K / BK;
+  if (nk % 3 == 0 && nk >= 6)
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, SWIGLU>), dim3(grid),
+                       dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, SWIGLU>), dim3(grid),
+                       dim3(256), 0, st, a);
+}
 
 }  // namespace
 
@@ -747,10 +856,10 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.Nout = 2 * s.d_ff;
   a.ldc = s.d_ff;
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+  if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
 #if G5_GEMM_PERSIST
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  hipLaunchKernelGGL((grouped_gemm_persist_kernel<256, 256, G5_GU_GM, true>), dim3(pgrid),
-                     dim3(256), 0, st, a);
+  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, true>(pgrid, a, st);
 #else
   hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_GU_BK, G5_GU_STAGES, true>), dim3(grid),
                      dim3(256), 0, st, a);
@@ -773,16 +882,15 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.K = s.d_ff;
   a.Nout = s.d_model;
   a.ldc = s.d_model;
+  if (a.K < G5_DN_STAGES * G5_DN_BK) return hipErrorInvalidValue;
 #if G5_GEMM_PERSIST
   const unsigned ncu = unsigned(device_cu_count());
   if (a.Nout % 256 == 0) {
     const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout), ncu);
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<256, 256, G5_DN_GM, false>), dim3(grid),
-                       dim3(256), 0, st, a);
+    launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false>(grid, a, st);
   } else {
     const unsigned grid = std::min(grid_bound<256, 128>(nk, s.n_experts, a.Nout), ncu);
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<256, 128, G5_DN_GM, false>), dim3(grid),
-                       dim3(256), 0, st, a);
+    launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false>(grid, a, st);
   }
 #else
   if (a.Nout % 256 == 0) {
