@@ -469,7 +469,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   // rows (w * AI + j) * RPB + lrow.
   static_assert(AI * RPB == 64, "one 64-row perm block per wave");
   char* epi = smem + S * STAGE + wave * kEpiBytesPerWave;
-  uint32_t rows_cur[GATHER ? AI : 1], rows_nxt[GATHER ? AI : 1];
+  // rows_fill: byte offsets of the gathered rows of the tile whose stages
+  // the refills load (the current tile, then the next from its first stage).
+  uint32_t rows_fill[GATHER ? AI : 1];
   auto to_offset = [&](uint32_t assignment, int j) -> uint32_t {
     return (assignment / uint32_t(args.topk)) * uint32_t(K * 2) +
            (lane_off[j & 1] - uint32_t(lrow * K * 2));
@@ -499,26 +501,37 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
       for (int j = 0; j < AI; ++j) rows[j] = to_offset(pr[j * RPB + lrow], j);
     }
   };
-  // DMA instruction q (q < AI: A slot q, else B slot q - AI) of a stage of the
-  // tile (e, n0, p_begin); row_off is the gathered row's byte offset (GATHER).
-  auto issue_one = [&](int buf, uint32_t row_off, int e, int n0, int p_begin, int k0, int q) {
+  // Scalar source bases of a tile's DMA slot 0 (A and B), in bytes: slot q of
+  // a stage adds q * slot_bytes and the stage's k offset.
+  const uint32_t slot_bytes = uint32_t(RPB * K * 2);
+  auto a_base_of = [&](const TileCoord& tc) -> const char* {
+    if constexpr (GATHER)
+      return reinterpret_cast<const char*>(args.A);
+    else  // rows p_begin ..: h has BM rows of padding after its last row, so a
+          // partial tile reads padding (never stored) instead of clamping
+      return reinterpret_cast<const char*>(args.A +
+                                           (int64_t(tc.p_begin) + wave * AI * RPB) * K);
+  };
+  auto b_base_of = [&](const TileCoord& tc) -> const char* {
+    return reinterpret_cast<const char*>(
+        args.B + (int64_t(tc.e) * args.Nout + tc.n0 + wave * BI * RPB) * K);
+  };
+  // DMA instruction q (q < AI: A slot q, else B slot q - AI) of the stage at
+  // element offset k0; row_off is the gathered row's byte offset (GATHER).
+  auto issue_one = [&](int buf, uint32_t row_off, const char* a_base, const char* b_base,
+                       int k0, int q) {
     char* As = smem + buf * STAGE;
     char* Bs = As + A_BYTES;
     if (q < AI) {
-      if constexpr (GATHER) {
-        lds_dma16_s(args.A + k0, row_off, lds_addr(As + (wave * AI + q) * 1024));
-      } else {
-        // Rows p_begin .. p_begin + BM - 1: h has BM rows of padding after its
-        // last row, so no clamping is needed (padding rows are never stored).
-        const char* ab = reinterpret_cast<const char*>(
-            args.A + (int64_t(p_begin) + (wave * AI + q) * RPB) * K + k0);
-        lds_dma16_s(ab, lane_off[q & 1], lds_addr(As + (wave * AI + q) * 1024));
-      }
+      if constexpr (GATHER)
+        lds_dma16_s(a_base + 2 * k0, row_off, lds_addr(As + (wave * AI + q) * 1024));
+      else
+        lds_dma16_s(a_base + 2 * k0 + size_t(q) * slot_bytes, lane_off[q & 1],
+                    lds_addr(As + (wave * AI + q) * 1024));
     } else {
       const int j = q - AI;
-      const char* bb = reinterpret_cast<const char*>(
-          args.B + (int64_t(e) * args.Nout + n0 + (wave * BI + j) * RPB) * K + k0);
-      lds_dma16_s(bb, lane_off[j & 1], lds_addr(Bs + (wave * BI + j) * 1024));
+      lds_dma16_s(b_base + 2 * k0 + size_t(j) * slot_bytes, lane_off[j & 1],
+                  lds_addr(Bs + (wave * BI + j) * 1024));
     }
   };
   auto row_of = [&](const uint32_t* rows, int q) -> uint32_t {
@@ -528,12 +541,17 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
 
   TileCoord cur, nxt;
   decode_tile_u<BM, BN, GM>(args, u, cur);
-  load_rows_now(cur, rows_cur);
+  load_rows_now(cur, rows_fill);
   bool has_nxt = u + nslot < hi;
+  nxt = cur;
   if (has_nxt) {
     decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
     dma_rows(nxt);
   }
+  const char* a_cur = a_base_of(cur);
+  const char* b_cur = b_base_of(cur);
+  const char* a_nxt = a_base_of(nxt);
+  const char* b_nxt = b_base_of(nxt);
 
   // acc[i][j]: feature block i x token block j (see grouped_gemm_dma_kernel);
   // the first MFMA of every tile takes a zero accumulator input.
@@ -558,8 +576,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
 #pragma unroll
   for (int st = 0; st < S; ++st)
 #pragma unroll
-    for (int q = 0; q < PER; ++q)
-      issue_one(st, row_of(rows_cur, q), cur.e, cur.n0, cur.p_begin, st * BK, q);
+    for (int q = 0; q < PER; ++q) issue_one(st, row_of(rows_fill, q), a_cur, b_cur, st * BK, q);
   int issued = S;  // stages issued so far (global step numbering)
   wait_vmcnt<(S - 1) * PER>();  // stage 0 landed
   __syncthreads();
@@ -593,11 +610,17 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
     const char* Bs = As + A_BYTES;
     const char* As_n = smem + nb * STAGE;
     const char* Bs_n = As_n + A_BYTES;
-    // the stage that refills buffer cb: tile-relative k-step kt + S
+    // the stage that refills buffer cb: tile-relative k-step kt + S of this
+    // tile or of the next.  Past the end of the tile list the refill still
+    // goes out (stage 0 of the current tile again, into a buffer no later
+    // step reads), so the MFMA stream carries no branches.
     const int ks_fill = kt + S;
     const bool fill_cur = ks_fill < nk;
     const bool fill = fill_cur || has_nxt;
-    const int k0_fill = (fill_cur ? ks_fill : ks_fill - nk) * BK;
+    const bool use_nxt = !fill_cur && has_nxt;
+    const int k0_fill = fill_cur ? ks_fill * BK : (has_nxt ? (ks_fill - nk) * BK : 0);
+    const char* a_fill = use_nxt ? a_nxt : a_cur;
+    const char* b_fill = use_nxt ? b_nxt : b_cur;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks == BS) {
@@ -610,7 +633,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
           // the next tile's perm block went out at this tile's start, before
           // stage kt + 1 when nk >= 2S - 1; otherwise wait for it explicitly
           if (nk < 2 * S - 1) wait_vmcnt<0>();
-          finish_rows(rows_nxt);
+          finish_rows(rows_fill);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -630,7 +653,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
           else if (!LAST)
             load_frag(As_n, Bs_n, ks + LA - KS, slot(ks + LA), t);
         }
-        if (ks >= BS && fill) {
+        if (ks >= BS) {
           // DMA instructions q in [w * PER / W, (w + 1) * PER / W) go out after
           // the w-th MFMA since the barrier: the stage's PER instructions
           // spread over the substeps from BS on.
@@ -638,14 +661,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
           const int w = (ks - BS) * NT + t;
 #pragma unroll
           for (int q = (w * PER) / W; q < ((w + 1) * PER) / W; ++q)
-            issue_one(cb, fill_cur ? row_of(rows_cur, q) : row_of(rows_nxt, q),
-                      fill_cur ? cur.e : nxt.e, fill_cur ? cur.n0 : nxt.n0,
-                      fill_cur ? cur.p_begin : nxt.p_begin, k0_fill, q);
+            issue_one(cb, row_of(rows_fill, q), a_fill, b_fill, k0_fill, q);
         }
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (fill) ++issued;
+    (void)fill;
+    ++issued;
     ++gstep;
   };
 
@@ -730,18 +752,22 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
       }
     }
 
-    if (!has_nxt) break;
-    cur = nxt;
-    if constexpr (GATHER) {
-#pragma unroll
-      for (int j = 0; j < AI; ++j) rows_cur[j] = rows_nxt[j];
+    if (!has_nxt) {
+      // refills past the end may still be landing in this workgroup's LDS
+      wait_vmcnt<0>();
+      break;
     }
+    cur = nxt;
     u += nslot;
+    a_cur = a_nxt;
+    b_cur = b_nxt;
     has_nxt = u + nslot < hi;
     if (has_nxt) {
       decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
       // the epilogue's LDS reads of this region completed before its stores
       dma_rows(nxt);
+      a_nxt = a_base_of(nxt);
+      b_nxt = b_base_of(nxt);
     }
     // first substeps' fragments of the new tile (its stage 0 landed at the
     // last stage barrier)
