@@ -3,14 +3,14 @@
     python bench.py [--steps K] [--warmup W] [--config 2|3] [--no-cpu-baseline]
 
 A step is one whole layer forward (router -> dispatch -> gate|up GEMM + SwiGLU
--> down GEMM -> combine) through the C ABI's g5moe_forward, on synthetic
+-> down GEMM -> combine) through the C ABI's stage entry points, on synthetic
 inputs already resident in HBM (config 2: 36,400 tokens bf16, uniform routing).
 Prints ONE JSON line.  `value` is tokens/s of the whole layer; `roofline` is
 for the dominant kernel (the grouped gate|up GEMM), its average launch time
-taken from HIP events recorded around that kernel on the stream it runs on, in
-a second timed loop that enqueues the stages one by one.  `cpu_baseline` times
-the CPU oracle (fp32, numpy/BLAS) on a bounded token sample of the same
-workload on this host's cores.
+taken from HIP events recorded between the stages, on the stream they run on,
+inside the timed loop.  `cpu_baseline` times the CPU oracle (fp32,
+numpy/BLAS) on a bounded token sample of the same workload on this host's
+cores.
 """
 from __future__ import annotations
 
@@ -35,6 +35,10 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the benchmark, run a 256 MiB elementwise copy (read 256 MiB, "
+                         "write 256 MiB) whose FETCH_SIZE / WRITE_SIZE counters scale the "
+                         "GEMM's counters to bytes")
     return ap.parse_args()
 
 
@@ -189,60 +193,53 @@ def main():
     buf = ops.ForwardBuffers(N, d, F, E, k, x.dtype, dev)
     torch.cuda.synchronize()
 
-    def step():
-        ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf)
-
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms = (t1 - t0) * 1e3 / args.steps
-
-    # Per-stage times: same kernels enqueued stage by stage with events between.
+    # One step = the whole layer through the C ABI's stage entry points (the
+    # same kernels g5moe_forward enqueues), with HIP events recorded between
+    # the stages on the stream they run on, so the per-stage averages come from
+    # the timed region itself.  No host synchronisation inside the loop.
+    import ctypes
+    from genet5_amd import _lib
     r = buf.routing
     y_perm = torch.empty((N * k, d), dtype=torch.bfloat16, device=dev)
     stream = torch.cuda.current_stream(dev)
     names = ["router", "dispatch", "gate_up", "down", "combine"]
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-    acc = {n: 0.0 for n in names}
-    import ctypes
-    from genet5_amd import _lib
     P = ops._ptr
     shape = buf.shape
     S = ops._stream(dev)
     ws = buf.ws
 
-    def staged():
-        ev[0].record(stream)
+    def step(ev=None):
+        rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
+        rec(0)
         _lib.call("g5moe_router_topk", P(x), P(wr), P(bias), P(r.topk_idx), P(r.topk_w), None,
                   ctypes.byref(shape), S)
-        ev[1].record(stream)
+        rec(1)
         _lib.call("g5moe_dispatch", P(r.topk_idx), P(r.counts), P(r.offsets), P(r.perm),
                   P(r.inv_pos), P(ws), ctypes.byref(shape), S)
-        ev[2].record(stream)
+        rec(2)
         _lib.call("g5moe_expert_gate_up", P(x), P(r.perm), P(r.offsets), P(wgu), P(ws),
                   ctypes.byref(shape), S)
-        ev[3].record(stream)
-        _lib.call("g5moe_expert_down", P(r.offsets), P(wd), P(y_perm), P(ws), ctypes.byref(shape), S)
-        ev[4].record(stream)
+        rec(3)
+        _lib.call("g5moe_expert_down", P(r.offsets), P(wd), P(y_perm), P(ws),
+                  ctypes.byref(shape), S)
+        rec(4)
         _lib.call("g5moe_combine", P(y_perm), P(r.inv_pos), P(r.topk_w), P(buf.y),
                   ctypes.byref(shape), S)
-        ev[5].record(stream)
+        rec(5)
 
-    for _ in range(3):
-        staged()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+              for _ in range(args.steps)]
+    for _ in range(args.warmup):
+        step()
     torch.cuda.synchronize()
-    n_staged = max(10, args.steps)
-    for _ in range(n_staged):
-        staged()
-        torch.cuda.synchronize()
-        for i, n in enumerate(names):
-            acc[n] += ev[i].elapsed_time(ev[i + 1])
-    stage_ms = {n: acc[n] / n_staged for n in names}
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms = (t1 - t0) * 1e3 / args.steps
+    stage_ms = {n: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
+                for j, n in enumerate(names)}
 
     flops_gu = 4 * d * F * N * k
     flops_dn = 2 * d * F * N * k
@@ -258,7 +255,7 @@ def main():
     ref_l = oracle.router_logits(inp.x, inp.w_router, inp.bias)
     ref_i, _ = oracle.topk_gates_c(ref_l, k)
     rc, ro, rp, ri = oracle.dispatch(ref_i, E)
-    step()
+    ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf)
     torch.cuda.synchronize()
     routing_exact = bool(
         np.array_equal(r.topk_idx.cpu().numpy(), ref_i)
@@ -301,7 +298,7 @@ def main():
             "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
         },
         "roofline": {
-            "kernel": "grouped_gemm_dma_kernel<256,256,64,2,true> (gate|up + SwiGLU)",
+            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,true> (gate|up + SwiGLU)",
             "bound": "mfma",
             "achieved": gu_tflops,
             "peak": PEAK_BF16_TFLOPS,
@@ -312,6 +309,13 @@ def main():
         },
         "routing_bit_exact_vs_oracle": routing_exact,
     }
+    if args.calibrate_copy:
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(inp, min(args.cpu_sample_tokens, N))
     print(json.dumps(out), flush=True)
