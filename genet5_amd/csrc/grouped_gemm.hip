@@ -5,33 +5,36 @@
 // `wo(act(wi_0 x, wi_1 x))` with act = silu(a) * b (_FUSED_ACT['silu'], :31),
 // evaluated per expert on the rows routed to it.
 //
-// One kernel template serves both GEMMs.  C[p, :] = A[row(p), :] . B_e^T for
-// the sorted positions p of expert e, where B_e is [Nout, K] (nn.Linear
-// orientation, K contiguous) and row(p) is perm[p] / k for the gate|up GEMM
-// (x rows are gathered straight into the A tile, no permuted copy of x) and p
-// itself for the down GEMM.
+// One persistent kernel template serves both GEMMs.  C[p, :] = A[row(p), :] .
+// B_e^T for the sorted positions p of expert e, where B_e is [Nout, K]
+// (nn.Linear orientation, K contiguous) and row(p) is perm[p] / k for the
+// gate|up GEMM (x rows are gathered straight into the A tile, no permuted copy
+// of x) and p itself for the down GEMM.
 //
-// Tile: BM x BN x 64 per workgroup of 4 waves in a 2 x 2 grid; each wave owns a
-// (BM/2) x (BN/2) block of 32x32 v_mfma_f32_32x32x16_bf16 tiles (128 x 128 =
-// 256 fp32 accumulators per lane in AGPRs at BM = BN = 256).  The MFMA takes the
-// weight block as its A operand and the token block as its B operand, so each
-// lane ends up holding four consecutive output columns of one token.
+// Tile: 256 x 256 (x 64 k per LDS stage) per workgroup of 4 waves in a 2 x 2
+// grid; each wave owns a 128 x 128 block of 32x32 v_mfma_f32_32x32x16_bf16
+// tiles (256 fp32 accumulators per lane in AGPRs).  The MFMA takes the weight
+// block as its A operand and the token block as its B operand, so each lane
+// ends up holding four consecutive output columns of one token.
 //
 // Data movement: global tiles go straight to LDS with global_load_lds_dwordx4
-// (one instruction moves 64 x 16 bytes into 1 KB of LDS, lane l at byte 16*l);
-// each 128-byte LDS row keeps logical chunk c at c ^ ((row >> 1) & 7), chosen
-// by picking each lane's global source chunk, so that 16-lane groups of the
-// fragment reads hit 16 distinct bank groups of the 64-bank LDS.  Two LDS
-// stages; fragment reads for the next 16-k substep are interleaved one by one
-// with the current substep's MFMAs, and the stage barrier sits inside the MFMA
-// stream.
+// issued with a scalar base and a 32-bit lane offset (one instruction moves 64
+// x 16 bytes into 1 KB of LDS, lane l at byte 16*l); each 128-byte LDS row keeps
+// logical chunk c at c ^ ((row >> 1) & 7), chosen by picking each lane's global
+// source chunk, so that 16-lane groups of the fragment reads hit 16 distinct
+// bank groups of the 64-bank LDS.  Two LDS stages.  Fragments are read two
+// substeps ahead into three register slots, so a stage buffer is free two
+// substeps before its k-step ends; its refill (the stage two k-steps ahead) is
+// issued one DMA instruction after every other MFMA over those substeps, which
+// keeps the texture path busy without stalling the matrix core (issuing a
+// stage's 16 instructions in one burst stalled the MFMA stream for about as
+// long as the DMA took).
 //
-// Scheduling: expert row counts live on the device (offsets[]), so the grid is
-// an upper bound and every workgroup derives its tile from offsets[]: tiles are
-// numbered expert-major, inside an expert in groups of kGroupM m-tiles swept
-// across all n-tiles (neighbouring tiles share A rows or B columns).  Block ids
-// are remapped so each of the 8 XCDs (which receive blocks round-robin) runs a
-// contiguous range of that numbering and its L2 sees the reuse.
+// Scheduling: expert row counts live on the device (offsets[]); the grid is
+// one workgroup per CU, and each workgroup walks a list of tiles derived from
+// offsets[] (see the persistent section below).  Tiles are numbered
+// expert-major, inside an expert in groups of GM m-tiles swept across all
+// n-tiles (neighbouring tiles share A rows or B columns).
 //
 // SwiGLU epilogue: the packed gate|up weight interleaves 32-row groups (gate
 // rows of f in [32g, 32g+32), then the matching up rows), so the wave's
@@ -48,9 +51,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int kBK = 64;       // k per LDS stage (one 128-byte row segment)
-constexpr int kGroupM = 4;    // m-tiles per raster group
-
 struct GemmArgs {
   const uint16_t* A;      // gate|up: x (bf16) [N, K]; down: h [N*k, K]
   const int32_t* perm;    // gate|up: sorted position -> assignment; down: nullptr
@@ -64,11 +64,6 @@ struct GemmArgs {
   int ldc;
 };
 
-// 8-byte output store (four bf16).
-__device__ __forceinline__ void store8(uint16_t* dst, uint2 v) {
-  *reinterpret_cast<uint2*>(dst) = v;
-}
-
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
 // below the bf16 rounding of the result).
 __device__ __forceinline__ float silu_mul(float g, float u) {
@@ -78,46 +73,6 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 struct TileCoord {
   int e, p_begin, p_end, n0;
 };
-
-template <int BM, int BN>
-__device__ __forceinline__ bool decode_tile(const GemmArgs& args, TileCoord& tc) {
-  const int ntn = args.Nout / BN;
-  int total = 0;
-  for (int e = 0; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
-    total += ((cnt + BM - 1) / BM) * ntn;
-  }
-  const int b = blockIdx.x;
-  if (b >= total) return false;
-  const int q = total >> 3, rem = total & 7, xcd = b & 7;
-  int u = xcd * q + min(xcd, rem) + (b >> 3);
-  int e = 0, mt_e = 0;
-  for (; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
-    mt_e = (cnt + BM - 1) / BM;
-    const int t = mt_e * ntn;
-    if (u < t) break;
-    u -= t;
-  }
-  const int g = u / (kGroupM * ntn);
-  const int first_m = g * kGroupM;
-  const int gs = min(kGroupM, mt_e - first_m);
-  const int rr = u - g * kGroupM * ntn;
-  const int mt = first_m + rr % gs;
-  const int nt = rr / gs;
-  tc.e = e;
-  tc.p_begin = args.offsets[e] + mt * BM;
-  tc.p_end = args.offsets[e + 1];
-  tc.n0 = nt * BN;
-  return true;
-}
-
-// 16 bytes per lane from global memory straight into LDS: lane l of the wave
-// writes lds_base + 16*l (lds_base must be wave-uniform).
-__device__ __forceinline__ void lds_dma16(const void* src, char* lds_base) {
-  __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)lds_base, 16, 0,
-                                   0);
-}
 
 // The same DMA with an explicit scalar base and a 32-bit per-lane byte offset
 // (global_load_lds_dwordx4 voff, sbase), M0 = LDS byte address of the 1 KB
@@ -156,203 +111,10 @@ __device__ __forceinline__ void wait_vmcnt_upto(int n) {
   }
 }
 
-template <int BM, int BN, int BK, int STAGES, bool SWIGLU>
-__global__ __launch_bounds__(256) void grouped_gemm_dma_kernel(GemmArgs args) {
-  constexpr int WTM = BM / 2, WTN = BN / 2;
-  constexpr int MB = WTM / 32, NB = WTN / 32;
-  constexpr int RB = BK * 2;          // bytes per tile row
-  constexpr int CPR = RB / 16;        // 16-byte chunks per row
-  constexpr int RPB = 1024 / RB;      // rows per 1 KB DMA block
-  constexpr int G = 256 / RB;         // rows sharing one 256-byte line of the 64 banks
-  constexpr int A_BYTES = BM * RB, B_BYTES = BN * RB;
-  constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int AI = A_BYTES / 1024 / 4;  // DMA instructions per wave per stage
-  constexpr int BI = B_BYTES / 1024 / 4;
-  constexpr int KS = BK / 16;
-  static_assert(BK == 32 || BK == 64, "BK");
-  static_assert(STAGES >= 2 && STAGES * STAGE <= 160 * 1024, "LDS");
-  static_assert((STAGES - 1) * (AI + BI) < 64, "vmcnt");
-  static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE];
-
-  TileCoord tc;
-  if (!decode_tile<BM, BN>(args, tc)) return;
-  const int e = tc.e, p_begin = tc.p_begin, p_end = tc.p_end, n0 = tc.n0;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int K = args.K;
-
-  // LDS layout: tile row r holds RB bytes; logical 16-byte chunk c sits at
-  // physical chunk c ^ sw(r), sw(r) = (r / G) % CPR.  The 64 banks span 256
-  // bytes = G rows, so a 16-lane group reading 16 consecutive rows at one
-  // logical chunk lands in 16 distinct 16-byte bank groups.
-  auto sw = [](int r) { return (r / G) % CPR; };
-  // DMA slots: wave w, instruction j fills block blk = w*AI + j (rows
-  // blk*RPB ..); lane l lands in row l / CPR of it at physical chunk l % CPR.
-  const int lrow = lane / CPR;
-  const int lpc = lane % CPR;
-  const uint16_t* a_src[AI];
-#pragma unroll
-  for (int j = 0; j < AI; ++j) {
-    const int r = (wave * AI + j) * RPB + lrow;
-    const int p = min(p_begin + r, p_end - 1);
-    const int64_t row = args.perm ? int64_t(args.perm[p] / args.topk) : int64_t(p);
-    a_src[j] = args.A + row * K + (lpc ^ sw(r)) * 8;
-  }
-  const uint16_t* b_src[BI];
-#pragma unroll
-  for (int j = 0; j < BI; ++j) {
-    const int r = (wave * BI + j) * RPB + lrow;
-    b_src[j] = args.B + (int64_t(e) * args.Nout + n0 + r) * K + (lpc ^ sw(r)) * 8;
-  }
-
-  auto issue = [&](int stage, int k0) {
-    char* As = smem + stage * STAGE;
-    char* Bs = As + A_BYTES;
-#pragma unroll
-    for (int j = 0; j < AI; ++j) lds_dma16(a_src[j] + k0, As + (wave * AI + j) * 1024);
-#pragma unroll
-    for (int j = 0; j < BI; ++j) lds_dma16(b_src[j] + k0, Bs + (wave * BI + j) * 1024);
-  };
-
-  // acc[i][j] = D of the MFMA with the weight block as the A operand and the
-  // token block as the B operand: D[feature][token] for feature block i and
-  // token block j, so lane l holds token 32j + l%32 and, in acc[i][j][4q + u],
-  // feature 32i + 8q + 4(l/32) + u — four consecutive output columns.
-  f32x16 acc[NB][MB];
-#pragma unroll
-  for (int i = 0; i < NB; ++i)
-#pragma unroll
-    for (int j = 0; j < MB; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.f;
-
-  // Fragment reads: row r = 32*m + (lane & 31), so sw(r) = sw(lane & 31).
-  const int a_row = (wm * WTM + (lane & 31)) * RB;
-  const int b_row = (wn * WTN + (lane & 31)) * RB;
-  const int khalf = lane >> 5;
-  const int rsw = sw(lane & 31);
-  bf16x8 af[2][MB], bfr[2][NB];
-  // Fragment f of substep ks: f < MB is A block f, otherwise B block f - MB.
-  auto load_frag = [&](const char* As, const char* Bs, int ks, int slot, int f) {
-    const int pc = ((ks * 2 + khalf) ^ rsw) * 16;
-    if (f < MB)
-      af[slot][f] = *reinterpret_cast<const bf16x8*>(As + a_row + f * 32 * RB + pc);
-    else
-      bfr[slot][f - MB] =
-          *reinterpret_cast<const bf16x8*>(Bs + b_row + (f - MB) * 32 * RB + pc);
-  };
-
-  // Pipeline (STAGES LDS buffers, KS substeps of 16 k per stage).  Substep g
-  // of the whole k range uses fragment slot g & 1; while its MFMAs run, the
-  // reads for substep g + 1 go out.  The stage barrier sits inside the MFMA
-  // stream: once the last substep's fragments of stage kt are in registers (all
-  // reads of that buffer are done), the wave waits for stage kt+1's DMA, syncs,
-  // refills the drained buffer with stage kt+STAGES, and runs the last
-  // substep's MFMAs interleaved with the reads of stage kt+1's first substep —
-  // the matrix core keeps its queue across the barrier, and every stage's DMA
-  // has STAGES-1 k-steps to land.
-  static_assert(KS % 2 == 0, "even substeps per stage");
-  constexpr int PER = AI + BI;  // DMA instructions per thread per stage
-  const int nk = K / BK;
-#pragma unroll
-  for (int s = 0; s < STAGES; ++s)
-    if (s < nk) issue(s, s * BK);
-  // stage 0 landed; min(STAGES, nk) - 1 later stages may still be in flight
-  wait_vmcnt_upto<STAGES - 1, PER>(min(STAGES, nk) - 1);
-  __syncthreads();
-#pragma unroll
-  for (int f = 0; f < MB + NB; ++f) load_frag(smem, smem + A_BYTES, 0, 0, f);
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt % STAGES;
-    const int nxt = (kt + 1) % STAGES;
-    const char* As = smem + cur * STAGE;
-    const char* Bs = As + A_BYTES;
-    const char* As_next = smem + nxt * STAGE;
-    const char* Bs_next = As_next + A_BYTES;
-    const bool more = kt + 1 < nk;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      if (ks == KS - 1) {
-        __builtin_amdgcn_sched_barrier(0);
-        // stage kt+1 landed; stages kt+2 .. min(kt+STAGES-1, nk-1) may be in flight
-        wait_vmcnt_upto<STAGES - 2, PER>(max(0, min(kt + STAGES - 1, nk - 1) - (kt + 1)));
-        __syncthreads();
-        if (kt + STAGES < nk) issue(cur, (kt + STAGES) * BK);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-#pragma unroll
-      for (int t = 0; t < MB * NB; ++t) {
-        const int i = t / MB, j = t % MB;  // feature block i, token block j
-        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(bfr[ks & 1][i], af[ks & 1][j],
-                                                            acc[i][j], 0, 0, 0);
-        if (t < MB + NB) {
-          if (ks + 1 < KS)
-            load_frag(As, Bs, ks + 1, (ks + 1) & 1, t);
-          else if (more)
-            load_frag(As_next, Bs_next, 0, 0, t);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-  }
-
-  // Epilogue: lane l owns token row p = p_begin + wm*WTM + 32j + l%32 and, per
-  // q, four consecutive output columns, stored as one 8-byte write.
-  const int tok_l = lane & 31;
-  const int col4 = (lane >> 5) * 4;
-  if constexpr (SWIGLU) {
-    // Feature blocks 2jj / 2jj+1 of the packed gate|up weight are gate / up of
-    // the same 32 h columns.
-    const int f_base = (n0 + wn * WTN) / 2;
-#pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      const int p = p_begin + wm * WTM + j * 32 + tok_l;
-      if (p < p_end) {
-        uint16_t* crow = args.C + int64_t(p) * args.ldc + f_base + col4;
-#pragma unroll
-        for (int jj = 0; jj < NB / 2; ++jj) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            float h[4];
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-              h[u] = silu_mul(acc[2 * jj][j][4 * q + u], acc[2 * jj + 1][j][4 * q + u]);
-            uint2 o;
-            o.x = pack_bf16x2(h[0], h[1]);
-            o.y = pack_bf16x2(h[2], h[3]);
-            store8(crow + jj * 32 + 8 * q, o);
-          }
-        }
-      }
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < MB; ++j) {
-      const int p = p_begin + wm * WTM + j * 32 + tok_l;
-      if (p < p_end) {
-        uint16_t* crow = args.C + int64_t(p) * args.ldc + n0 + wn * WTN + col4;
-#pragma unroll
-        for (int i = 0; i < NB; ++i) {
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            uint2 o;
-            o.x = pack_bf16x2(acc[i][j][4 * q + 0], acc[i][j][4 * q + 1]);
-            o.y = pack_bf16x2(acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
-            store8(crow + i * 32 + 8 * q, o);
-          }
-        }
-      }
-    }
-  }
-}
-
 // ---------------------------------------------------------------------------
-// Persistent variant: one workgroup per CU walks a list of tiles.
+// Persistent schedule: one workgroup per CU walks a list of tiles.
 //
-// The tiles of the launch (same numbering as decode_tile) are cut into 8
+// The tiles of the launch (numbered as decode_tile_u reads them) are cut into 8
 // contiguous ranges, one per XCD (workgroup b runs on XCD b % 8); workgroup
 // slot s of an XCD takes tiles lo + s, lo + s + nslot, ... of its range, so at
 // any time the XCD's CUs work on consecutive tiles that share A rows and B
@@ -553,8 +315,10 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   const char* a_nxt = a_base_of(nxt);
   const char* b_nxt = b_base_of(nxt);
 
-  // acc[i][j]: feature block i x token block j (see grouped_gemm_dma_kernel);
-  // the first MFMA of every tile takes a zero accumulator input.
+  // acc[i][j] = D of the MFMA with the weight block as the A operand and the
+  // token block as the B operand: lane l holds token 32j + l%32 and, in
+  // acc[i][j][4q + u], feature 32i + 8q + 4(l/32) + u.  The first MFMA of
+  // every tile takes a zero accumulator input.
   f32x16 acc[NB][MB];
   const f32x16 zero16 = {};
 
@@ -827,22 +591,17 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 
 // Tile configurations (the k depth and LDS stage count can be overridden at
 // build time for tuning).
-#ifndef G5_GEMM_PERSIST
-#define G5_GEMM_PERSIST 1
-#endif
-#define G5_DEF_BK 64
-#define G5_DEF_STAGES 2
 #ifndef G5_GU_BK
-#define G5_GU_BK G5_DEF_BK
+#define G5_GU_BK 64
 #endif
 #ifndef G5_GU_STAGES
-#define G5_GU_STAGES G5_DEF_STAGES
+#define G5_GU_STAGES 2
 #endif
 #ifndef G5_DN_BK
-#define G5_DN_BK G5_DEF_BK
+#define G5_DN_BK 64
 #endif
 #ifndef G5_DN_STAGES
-#define G5_DN_STAGES G5_DEF_STAGES
+#define G5_DN_STAGES 2
 #endif
 #ifndef G5_GU_GM
 #define G5_GU_GM 4
@@ -883,13 +642,8 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.ldc = s.d_ff;
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
-#if G5_GEMM_PERSIST
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
   launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, true>(pgrid, a, st);
-#else
-  hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_GU_BK, G5_GU_STAGES, true>), dim3(grid),
-                     dim3(256), 0, st, a);
-#endif
   return hipGetLastError();
 }
 
@@ -909,7 +663,6 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.Nout = s.d_model;
   a.ldc = s.d_model;
   if (a.K < G5_DN_STAGES * G5_DN_BK) return hipErrorInvalidValue;
-#if G5_GEMM_PERSIST
   const unsigned ncu = unsigned(device_cu_count());
   if (a.Nout % 256 == 0) {
     const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout), ncu);
@@ -918,17 +671,6 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
     const unsigned grid = std::min(grid_bound<256, 128>(nk, s.n_experts, a.Nout), ncu);
     launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false>(grid, a, st);
   }
-#else
-  if (a.Nout % 256 == 0) {
-    const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
-    hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 256, G5_DN_BK, G5_DN_STAGES, false>),
-                       dim3(grid), dim3(256), 0, st, a);
-  } else {
-    const unsigned grid = grid_bound<256, 128>(nk, s.n_experts, a.Nout);
-    hipLaunchKernelGGL((grouped_gemm_dma_kernel<256, 128, G5_DN_BK, G5_DN_STAGES, false>),
-                       dim3(grid), dim3(256), 0, st, a);
-  }
-#endif
   return hipGetLastError();
 }
 
