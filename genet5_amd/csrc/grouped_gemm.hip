@@ -151,8 +151,23 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileC
   tc.n0 = nt * BN;
 }
 
-template <int BM, int BN, int BK, int S, int NSLOT, int GM, bool SWIGLU>
-__global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
+// The tiles one workgroup runs in one pass of the tile loop.  Unit i < count
+// is h = first + i * stride: full tile h of the launch, or, in a half pass,
+// the n-half (h & 1) of full tile base + h / 2.
+struct Units {
+  int first, stride, count, base;
+};
+
+// LDS bytes of the persistent kernel for a BM x BN tile (stages + epilogue).
+template <int BM, int BN, int BK, int S>
+constexpr int persist_smem_bytes() {
+  return S * (BM + BN) * BK * 2 + 4 * kEpiBytesPerWave;
+}
+
+// One pass of the persistent tile loop over the units `un` (BN = BNF for full
+// tiles, BNF / 2 for half tiles, decoded in the full-tile numbering).
+template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, bool SWIGLU, bool HALF>
+__device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, const Units un) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int MB = WTM / 32, NB = WTN / 32;
   constexpr int RB = BK * 2;          // bytes per tile row in LDS
@@ -173,9 +188,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   constexpr int BS = KS - LA;             // substep at which the stage barrier sits
   static_assert(NSLOT == 2 || (NSLOT == 3 && KS == 4), "fragment slots");
   static_assert(BK == 32 || BK == 64, "BK");
+  static_assert(HALF ? 2 * BN == BNF : BN == BNF, "tile width");
   static_assert(S >= 2 && S * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
   static_assert((S - 2) * PER < 64, "vmcnt range");
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
+  // Fragment f of the next substeps is read after the f-th MFMA of a substep,
+  // so a substep must hold at least as many MFMAs as fragments.
+  static_assert(MB * NB >= MB + NB, "fragment prefetch needs MB * NB >= MB + NB");
   constexpr int NT = MB * NB;             // MFMAs per substep
   // The swizzle of DMA slot j's rows depends only on j % 2 (see lane_off).
   static_assert((AI * RPB / G) % CPR == 0 && (BI * RPB / G) % CPR == 0 &&
@@ -184,25 +203,15 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   // The gate|up GEMM gathers token rows through perm; the down GEMM reads the
   // expert-contiguous h rows in place.
   constexpr bool GATHER = SWIGLU;
-  __shared__ __attribute__((aligned(1024))) char smem[S * STAGE + 4 * kEpiBytesPerWave];
-
-  const int ntn = args.Nout / BN;
-  int total = 0;
-  for (int e = 0; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
-    total += ((cnt + BM - 1) / BM) * ntn;
-  }
-  // This workgroup's share: XCD x owns tiles [lo, hi), slot s takes every
-  // nslot-th of them.
-  const int ng = gridDim.x;
-  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
-  int before = 0;
-  for (int y = 0; y < xcd; ++y) before += (ng - y + 7) >> 3;
-  const int nslot = (ng - xcd + 7) >> 3;
-  const int lo = int(int64_t(total) * before / ng);
-  const int hi = int(int64_t(total) * (before + nslot) / ng);
-  int u = lo + slot;
-  if (u >= hi) return;
+  auto decode_unit = [&](int i, TileCoord& tc) {
+    const int h = un.first + i * un.stride;
+    if constexpr (HALF) {
+      decode_tile_u<BM, BNF, GM>(args, un.base + (h >> 1), tc);
+      tc.n0 += (h & 1) * BN;
+    } else {
+      decode_tile_u<BM, BNF, GM>(args, h, tc);
+    }
+  };
 
   const int lane = threadIdx.x & 63;
   // wave-uniform (scalar) so every wave-dependent address term stays in SGPRs
@@ -302,12 +311,13 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   };
 
   TileCoord cur, nxt;
-  decode_tile_u<BM, BN, GM>(args, u, cur);
+  int ui = 0;
+  decode_unit(0, cur);
   load_rows_now(cur, rows_fill);
-  bool has_nxt = u + nslot < hi;
+  bool has_nxt = un.count > 1;
   nxt = cur;
   if (has_nxt) {
-    decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
+    decode_unit(1, nxt);
     dma_rows(nxt);
   }
   const char* a_cur = a_base_of(cur);
@@ -522,12 +532,12 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
       break;
     }
     cur = nxt;
-    u += nslot;
+    ++ui;
     a_cur = a_nxt;
     b_cur = b_nxt;
-    has_nxt = u + nslot < hi;
+    has_nxt = ui + 1 < un.count;
     if (has_nxt) {
-      decode_tile_u<BM, BN, GM>(args, u + nslot, nxt);
+      decode_unit(ui + 1, nxt);
       // the epilogue's LDS reads of this region completed before its stores
       dma_rows(nxt);
       a_nxt = a_base_of(nxt);
@@ -536,6 +546,52 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
     // first substeps' fragments of the new tile (its stage 0 landed at the
     // last stage barrier)
     load_first_frags(smem + (gstep % S) * STAGE);
+  }
+}
+
+// Persistent grouped GEMM: one workgroup per CU.  XCD x owns the contiguous
+// tile range [lo, hi) of the launch; each of its nslot workgroups runs q =
+// (hi - lo) / nslot tiles (slot s: lo + s, lo + s + nslot, ...).  The r tiles
+// left over run either whole, one each on slots 0 .. r - 1, or (HALF_TAIL, the
+// down GEMM) as 2r n-halves spread over the slots, so that no workgroup runs
+// more than q tiles plus one half while r <= nslot / 2.  A tile's time is
+// dominated by its A rows and its MFMAs scale with its width, so a half takes
+// about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
+// the gate|up GEMM (K = 768), which therefore keeps whole tiles.
+template <int BM, int BN, int BK, int S, int NSLOT, int GM, bool SWIGLU, bool HALF_TAIL>
+__global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
+  __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
+  const int ntn = args.Nout / BN;
+  int total = 0;
+  for (int e = 0; e < args.n_experts; ++e) {
+    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    total += ((cnt + BM - 1) / BM) * ntn;
+  }
+  const int ng = gridDim.x;
+  const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+  int before = 0;
+  for (int y = 0; y < xcd; ++y) before += (ng - y + 7) >> 3;
+  const int nslot = (ng - xcd + 7) >> 3;
+  const int lo = int(int64_t(total) * before / ng);
+  const int hi = int(int64_t(total) * (before + nslot) / ng);
+  const int q = (hi - lo) / nslot, r = (hi - lo) % nslot;
+  if constexpr (HALF_TAIL) {
+    if (q > 0)
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, SWIGLU, false>(args, smem,
+                                                           Units{lo + slot, nslot, q, 0});
+    if (slot < 2 * r) {
+      // every wave's DMAs of the full pass have landed (each waited for its
+      // own) before the half pass refills the stage buffers
+      if (q > 0) __syncthreads();
+      tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, SWIGLU, true>(
+          args, smem, Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
+    }
+  } else {
+    // one pass: the remainder tile of slots s < r is lo + s + q * nslot
+    const int cnt = q + (slot < r ? 1 : 0);
+    if (cnt > 0)
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, SWIGLU, false>(args, smem,
+                                                           Units{lo + slot, nslot, cnt, 0});
   }
 }
 
@@ -611,15 +667,15 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #endif
 
 // Persistent launch: three fragment slots when the k-step count allows it.
-template <int BM, int BN, int BK, int S, int GM, bool SWIGLU>
+template <int BM, int BN, int BK, int S, int GM, bool SWIGLU, bool HALF_TAIL>
 void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
   const int nk = a.K / BK;
   if (nk % 3 == 0 && nk >= 6)
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, SWIGLU>), dim3(grid),
-                       dim3(256), 0, st, a);
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, SWIGLU, HALF_TAIL>),
+                       dim3(grid), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, SWIGLU>), dim3(grid),
-                       dim3(256), 0, st, a);
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, SWIGLU, HALF_TAIL>),
+                       dim3(grid), dim3(256), 0, st, a);
 }
 
 }  // namespace
@@ -643,7 +699,7 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, true>(pgrid, a, st);
+  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, true, false>(pgrid, a, st);
   return hipGetLastError();
 }
 
@@ -666,10 +722,10 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   const unsigned ncu = unsigned(device_cu_count());
   if (a.Nout % 256 == 0) {
     const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout), ncu);
-    launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false>(grid, a, st);
+    launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false, true>(grid, a, st);
   } else {
     const unsigned grid = std::min(grid_bound<256, 128>(nk, s.n_experts, a.Nout), ncu);
-    launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false>(grid, a, st);
+    launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false, false>(grid, a, st);
   }
   return hipGetLastError();
 }
