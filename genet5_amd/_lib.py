@@ -30,6 +30,8 @@ EXPORTED = (
     "g5moe_expert_down",
     "g5moe_expert_swiglu",
     "g5moe_combine",
+    "g5moe_add_rmsnorm_router",
+    "g5moe_combine_residual",
     "g5moe_forward",
 )
 
@@ -69,6 +71,10 @@ _SIGS = {
     "g5moe_expert_down": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_swiglu": ([_P, _P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_combine": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_add_rmsnorm_router": ([_P, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _P, _P,
+                                  _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_combine_residual": ([_P, _P, _P, _P, ctypes.c_float, _P, _SHAPE_P, _P],
+                               ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
 }
 

@@ -84,7 +84,7 @@ extern "C" {
 
 const char* g5moe_last_error(void) { return g_err; }
 
-int32_t g5moe_version(void) { return (1 << 16) | 0; }
+int32_t g5moe_version(void) { return (1 << 16) | 1; }
 
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes) {
   G5_CHECK(check_shape(shape));
@@ -191,6 +191,44 @@ g5moe_status g5moe_combine(const void* y_perm, const int32_t* inv_pos, const flo
   return hip_status(launch_combine(static_cast<const uint16_t*>(y_perm), inv_pos, topk_w, y,
                                    *shape, as_stream(stream)),
                     "g5moe_combine");
+}
+
+g5moe_status g5moe_add_rmsnorm_router(const void* x_add, const void* residual,
+                                      const float* norm_weight, float eps,
+                                      const void* w_router, const float* bias, void* sum_out,
+                                      void* normed_out, int32_t* topk_idx, float* topk_w,
+                                      float* logits, const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (!(eps >= 0.0f)) return fail(G5MOE_ERR_INVALID_ARG, "eps must be >= 0 (got %g)", eps);
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(residual);
+  G5_NONNULL(norm_weight);
+  G5_NONNULL(w_router);
+  G5_NONNULL(normed_out);
+  G5_NONNULL(topk_idx);
+  G5_NONNULL(topk_w);
+  if (sum_out != nullptr && x_add == nullptr)
+    return fail(G5MOE_ERR_INVALID_ARG, "sum_out needs x_add (without it the sum is residual)");
+  return hip_status(launch_norm_router(x_add, residual, norm_weight, eps, w_router, bias,
+                                       sum_out, normed_out, topk_idx, topk_w, logits, *shape,
+                                       as_stream(stream)),
+                    "g5moe_add_rmsnorm_router");
+}
+
+g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
+                                    const float* topk_w, const void* residual, float alpha,
+                                    void* out, const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(y_perm);
+  G5_NONNULL(inv_pos);
+  G5_NONNULL(topk_w);
+  G5_NONNULL(residual);
+  G5_NONNULL(out);
+  return hip_status(launch_combine_residual(static_cast<const uint16_t*>(y_perm), inv_pos,
+                                            topk_w, residual, alpha, out, *shape,
+                                            as_stream(stream)),
+                    "g5moe_combine_residual");
 }
 
 g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bias,

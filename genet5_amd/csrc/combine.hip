@@ -8,17 +8,30 @@
 // One thread produces 8 consecutive outputs (16 bytes of bf16 input per slot),
 // so a wavefront reads and writes contiguous 1 KB row segments.  HBM-bound:
 // N*k*d*2 + N*k*8 + N*d*2 bytes (168.3 MB at N = 36,400, k = 2, d = 768).
+//
+// Residual variant: the encoder block's `hidden_states + dropout(ff_output) *
+// alpha` (lib/blocks/encoder.py:89, dropout the identity in inference) folded
+// into the combine, with the roundings of that composition in the activation
+// dtype T: y = T(acc), t = T(y * alpha), out = T(residual + t).  The MoE
+// output never goes to memory: it saves writing and re-reading [N, d].  The
+// output may alias the residual (each thread reads its 8 residual values
+// before it writes them).
 #include "g5moe_internal.h"
 
 namespace g5moe {
 namespace {
 
-template <bool OUT_F32>
+__device__ __forceinline__ float round_bf16(float v) {
+  return __uint_as_float(uint32_t(f32_to_bf16_bits(v)) << 16);
+}
+
+template <bool OUT_F32, bool RESID>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y_perm,
                                                       const int32_t* __restrict__ inv_pos,
                                                       const float* __restrict__ w,
-                                                      void* __restrict__ y, int64_t n_tokens,
-                                                      int d, int topk) {
+                                                      void* y, int64_t n_tokens, int d,
+                                                      int topk, const void* residual,
+                                                      float alpha) {
   const int cpr = d / 8;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n_tokens * cpr) return;
@@ -39,6 +52,36 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
       acc[2 * j + 1] = __builtin_fmaf(ws, __uint_as_float(vv[j] & 0xffff0000u), acc[2 * j + 1]);
     }
   }
+  if constexpr (RESID) {
+    float r[8];
+    if constexpr (OUT_F32) {
+      const float4* q =
+          reinterpret_cast<const float4*>(static_cast<const float*>(residual) + t * d + ch * 8);
+      const float4 a = q[0], b = q[1];
+      r[0] = a.x, r[1] = a.y, r[2] = a.z, r[3] = a.w, r[4] = b.x, r[5] = b.y, r[6] = b.z,
+      r[7] = b.w;
+    } else {
+      const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(residual) +
+                                                      t * d + ch * 8);
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        r[2 * j] = __uint_as_float(vv[j] << 16);
+        r[2 * j + 1] = __uint_as_float(vv[j] & 0xffff0000u);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (OUT_F32) {
+        // two roundings, as the unfused product then sum (no fma contraction)
+#pragma clang fp contract(off)
+        acc[j] = r[j] + acc[j] * alpha;
+      } else {
+        const float yt = round_bf16(acc[j]);
+        acc[j] = r[j] + round_bf16(yt * alpha);
+      }
+    }
+  }
   if constexpr (OUT_F32) {
     float4* o = reinterpret_cast<float4*>(static_cast<float*>(y) + t * d + ch * 8);
     o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
@@ -55,18 +98,33 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
 
 }  // namespace
 
-hipError_t launch_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
-                          void* y, const g5moe_shape& s, hipStream_t st) {
+namespace {
+template <bool RESID>
+hipError_t launch_combine_impl(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
+                               const void* residual, float alpha, void* y,
+                               const g5moe_shape& s, hipStream_t st) {
   const int64_t work = s.n_tokens * (s.d_model / 8);
   if (work == 0) return hipSuccess;
   const unsigned grid = unsigned((work + 255) / 256);
   if (s.x_dtype == G5MOE_DTYPE_F32)
-    hipLaunchKernelGGL(combine_kernel<true>, dim3(grid), dim3(256), 0, st, y_perm, inv_pos, w,
-                       y, s.n_tokens, s.d_model, s.top_k);
+    hipLaunchKernelGGL((combine_kernel<true, RESID>), dim3(grid), dim3(256), 0, st, y_perm,
+                       inv_pos, w, y, s.n_tokens, s.d_model, s.top_k, residual, alpha);
   else
-    hipLaunchKernelGGL(combine_kernel<false>, dim3(grid), dim3(256), 0, st, y_perm, inv_pos, w,
-                       y, s.n_tokens, s.d_model, s.top_k);
+    hipLaunchKernelGGL((combine_kernel<false, RESID>), dim3(grid), dim3(256), 0, st, y_perm,
+                       inv_pos, w, y, s.n_tokens, s.d_model, s.top_k, residual, alpha);
   return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
+                          void* y, const g5moe_shape& s, hipStream_t st) {
+  return launch_combine_impl<false>(y_perm, inv_pos, w, nullptr, 1.0f, y, s, st);
+}
+
+hipError_t launch_combine_residual(const uint16_t* y_perm, const int32_t* inv_pos,
+                                   const float* w, const void* residual, float alpha, void* out,
+                                   const g5moe_shape& s, hipStream_t st) {
+  return launch_combine_impl<true>(y_perm, inv_pos, w, residual, alpha, out, s, st);
 }
 
 }  // namespace g5moe

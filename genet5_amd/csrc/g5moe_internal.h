@@ -54,6 +54,13 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
 // ---- kernel launchers (each returns hipSuccess or the launch error) -------
 hipError_t launch_router(const void* x, const void* wr, const float* bias, int32_t* idx,
                          float* w, float* logits, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_norm_router(const void* x_add, const void* residual, const float* norm_w,
+                              float eps, const void* wr, const float* bias, void* sum_out,
+                              void* normed_out, int32_t* idx, float* w, float* logits,
+                              const g5moe_shape& s, hipStream_t st);
+hipError_t launch_combine_residual(const uint16_t* y_perm, const int32_t* inv_pos,
+                                   const float* w, const void* residual, float alpha, void* out,
+                                   const g5moe_shape& s, hipStream_t st);
 hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets,
                            int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                            hipStream_t st);

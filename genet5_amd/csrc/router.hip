@@ -26,6 +26,23 @@
 // Cost.  The E*d fused multiply-adds per token are the floor: N*E*d = 447M
 // FMAs at N = 36,400, about 11-14 us of VALU time on 256 CUs at 2.0-2.4 GHz;
 // reading x (55.9 MB) takes about 7 us at 8 TB/s, so the kernel is VALU-bound.
+//
+// Fused pre-norm variant (MODE 1: RMSNorm, MODE 2: residual add + RMSNorm),
+// the step before the MoE in GeneT5's encoder block: fused_add_rmsnorm
+// (lib/blocks/_component.py:17-20) called at lib/blocks/encoder.py:80-83, or
+// `hidden_states + attn_output` then norm2 at :84-86.  Per token row, in x's
+// dtype T (bf16 or fp32):
+//   s_j    = T(x_j + r_j)                       (MODE 2; s = r in MODE 1)
+//   ss     = sum_j s_j^2 in the router's order: lane c forms the fma chain
+//            over its columns [c*L, c*L + L) from 0, the 64 partials are added
+//            pairwise over lane bits 5, 4, ..., 0 (a xor butterfly gives every
+//            lane that same tree, fp addition being commutative)
+//   rstd   = 1 / sqrt(ss / d + eps)             (correctly rounded / and sqrt)
+//   n_j    = T((s_j * rstd) * w_j)              (two fp32 products)
+// and the router then runs on the stored values n_j, so its logits are the
+// ones g5moe_router_topk gives on the written normed rows.  Both waves of a
+// pair compute the row (the second one's loads hit the L2); the even wave
+// stores s and n.
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -93,6 +110,53 @@ struct RowLoader<float, L> {
   }
 };
 
+// Round an fp32 value to the activation dtype and back (exact widening).
+template <typename XT>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (sizeof(XT) == 2)
+    return __uint_as_float(uint32_t(f32_to_bf16_bits(v)) << 16);
+  else
+    return v;
+}
+
+template <typename XT, int L>
+__device__ __forceinline__ void store_row(XT* p, const float (&v)[L]) {
+  if constexpr (sizeof(XT) == 2) {
+    uint32_t u[L / 2];
+#pragma unroll
+    for (int i = 0; i < L / 2; ++i)
+      u[i] = (__float_as_uint(v[2 * i + 1]) & 0xffff0000u) | (__float_as_uint(v[2 * i]) >> 16);
+    if constexpr (L % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < L / 4; ++i)
+        reinterpret_cast<uint2*>(p)[i] = make_uint2(u[2 * i], u[2 * i + 1]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < L / 2; ++i) reinterpret_cast<uint32_t*>(p)[i] = u[i];
+    }
+  } else {
+    if constexpr (L % 4 == 0) {
+#pragma unroll
+      for (int i = 0; i < L / 4; ++i)
+        reinterpret_cast<float4*>(p)[i] =
+            make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < L / 2; ++i)
+        reinterpret_cast<float2*>(p)[i] = make_float2(v[2 * i], v[2 * i + 1]);
+    }
+  }
+}
+
+// Pre-norm inputs of the fused variant (unused in MODE 0).
+struct NormArgs {
+  const void* x_add;   // MODE 2: added to the residual rows
+  const float* weight; // RMSNorm weight [d], fp32
+  float eps;
+  void* sum_out;       // MODE 2: s rows, or nullptr
+  void* normed_out;    // normed rows (the MoE input)
+};
+
 // One reduce-scatter level over V values: lanes with `bit` set keep the upper
 // half.  p[i] and the partner's p[i] (same index) hold the same (token, expert).
 template <int HALF>
@@ -105,11 +169,13 @@ __device__ __forceinline__ void rs_level(float* p, int lane, int bit) {
   for (int i = 0; i < HALF; ++i) p[i] = (hi ? p[HALF + i] : p[i]) + recv[i];
 }
 
-template <typename XT, int L>
+// MODE 0: router on x.  MODE 1 / 2: x is the residual stream, normalised
+// (after adding na.x_add in MODE 2) on the way in; see the header comment.
+template <typename XT, int L, int MODE>
 __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     const XT* __restrict__ x, const XT* __restrict__ wr, const float* __restrict__ bias,
     int64_t n_tokens, int n_experts, int top_k, int32_t* __restrict__ topk_idx,
-    float* __restrict__ topk_w, float* __restrict__ logits_out) {
+    float* __restrict__ topk_w, float* __restrict__ logits_out, NormArgs na) {
   constexpr int D = 64 * L;
   __shared__ float lg[kTokensPerBlock][kMaxExperts + 1];
 
@@ -132,21 +198,74 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     }
   }
 
+  // This lane's columns of the RMSNorm weight.
+  float nw[MODE == 0 ? 1 : L];
+  if constexpr (MODE != 0) {
+#pragma unroll
+    for (int i = 0; i < L; ++i) nw[i] = na.weight[lane * L + i];
+  }
+
   for (int b = 0; b < kPairBatches; ++b) {
     const int64_t tb = tok0 + b * kTokBatch;
     if (tb >= n_tokens) break;
     float p[kTokBatch * kHalfExperts];
+    if constexpr (MODE == 0) {
 #pragma unroll
-    for (int m = 0; m < kTokBatch; ++m) {
-      float xv[L];
-      const int64_t t = min(tb + m, n_tokens - 1);  // rows past the end are computed, not stored
-      RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv);
+      for (int m = 0; m < kTokBatch; ++m) {
+        float xv[L];
+        const int64_t t = min(tb + m, n_tokens - 1);  // rows past the end are computed, not stored
+        RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv);
 #pragma unroll
-      for (int e = 0; e < kHalfExperts; ++e) {
+        for (int e = 0; e < kHalfExperts; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[i], w[e][i], acc);
+          p[m * kHalfExperts + e] = acc;
+        }
+      }
+    } else {
+      float xv[kTokBatch][L], ss[kTokBatch];
+#pragma unroll
+      for (int m = 0; m < kTokBatch; ++m) {
+        const int64_t t = min(tb + m, n_tokens - 1);
+        RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv[m]);
+        if constexpr (MODE == 2) {
+          float xa[L];
+          RowLoader<XT, L>::load(static_cast<const XT*>(na.x_add) + size_t(t) * D + lane * L,
+                                 xa);
+#pragma unroll
+          for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>(xv[m][i] + xa[i]);
+        }
         float acc = 0.f;
 #pragma unroll
-        for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[i], w[e][i], acc);
-        p[m * kHalfExperts + e] = acc;
+        for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], xv[m][i], acc);
+        ss[m] = acc;
+      }
+#pragma unroll
+      for (int bit = 32; bit >= 1; bit >>= 1)
+#pragma unroll
+        for (int m = 0; m < kTokBatch; ++m) ss[m] = ss[m] + __shfl_xor(ss[m], bit, 64);
+#pragma unroll
+      for (int m = 0; m < kTokBatch; ++m) {
+        const float rstd = 1.0f / __builtin_sqrtf(ss[m] / float(D) + na.eps);
+        const bool store = half == 0 && tb + m < n_tokens;
+        if constexpr (MODE == 2) {
+          if (store && na.sum_out != nullptr)
+            store_row<XT, L>(static_cast<XT*>(na.sum_out) + size_t(tb + m) * D + lane * L,
+                             xv[m]);
+        }
+#pragma unroll
+        for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>((xv[m][i] * rstd) * nw[i]);
+        if (store)
+          store_row<XT, L>(static_cast<XT*>(na.normed_out) + size_t(tb + m) * D + lane * L,
+                           xv[m]);
+#pragma unroll
+        for (int e = 0; e < kHalfExperts; ++e) {
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], w[e][i], acc);
+          p[m * kHalfExperts + e] = acc;
+        }
       }
     }
     rs_level<16>(p, lane, 32);
@@ -218,16 +337,17 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
   }
 }
 
-template <typename XT>
+template <typename XT, int MODE>
 hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* idx, float* w,
-                        float* logits, const g5moe_shape& s, hipStream_t st) {
+                        float* logits, const NormArgs& na, const g5moe_shape& s,
+                        hipStream_t st) {
   const int64_t n = s.n_tokens;
   const unsigned grid = unsigned((n + kTokensPerBlock - 1) / kTokensPerBlock);
   const int L = s.d_model / 64;
-#define G5_ROUTER_CASE(LL)                                                              \
-  case LL:                                                                              \
-    hipLaunchKernelGGL((router_topk_kernel<XT, LL>), dim3(grid), dim3(kRouterThreads), \
-                       0, st, x, wr, bias, n, s.n_experts, s.top_k, idx, w, logits);    \
+#define G5_ROUTER_CASE(LL)                                                                  \
+  case LL:                                                                                  \
+    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE>), dim3(grid), dim3(kRouterThreads), \
+                       0, st, x, wr, bias, n, s.n_experts, s.top_k, idx, w, logits, na);    \
     break;
   switch (L) {
     G5_ROUTER_CASE(2)
@@ -241,16 +361,35 @@ hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* i
   return hipGetLastError();
 }
 
+template <int MODE>
+hipError_t launch_mode(const void* x, const void* wr, const float* bias, int32_t* idx,
+                       float* w, float* logits, const NormArgs& na, const g5moe_shape& s,
+                       hipStream_t st) {
+  if (s.x_dtype == G5MOE_DTYPE_BF16)
+    return launch_typed<uint16_t, MODE>(static_cast<const uint16_t*>(x),
+                                        static_cast<const uint16_t*>(wr), bias, idx, w,
+                                        logits, na, s, st);
+  return launch_typed<float, MODE>(static_cast<const float*>(x), static_cast<const float*>(wr),
+                                   bias, idx, w, logits, na, s, st);
+}
+
 }  // namespace
 
 hipError_t launch_router(const void* x, const void* wr, const float* bias, int32_t* idx,
                          float* w, float* logits, const g5moe_shape& s, hipStream_t st) {
   if (s.n_tokens == 0) return hipSuccess;
-  if (s.x_dtype == G5MOE_DTYPE_BF16)
-    return launch_typed(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(wr),
-                        bias, idx, w, logits, s, st);
-  return launch_typed(static_cast<const float*>(x), static_cast<const float*>(wr), bias, idx,
-                      w, logits, s, st);
+  return launch_mode<0>(x, wr, bias, idx, w, logits, NormArgs{}, s, st);
+}
+
+hipError_t launch_norm_router(const void* x_add, const void* residual, const float* norm_w,
+                              float eps, const void* wr, const float* bias, void* sum_out,
+                              void* normed_out, int32_t* idx, float* w, float* logits,
+                              const g5moe_shape& s, hipStream_t st) {
+  if (s.n_tokens == 0) return hipSuccess;
+  const NormArgs na{x_add, norm_w, eps, sum_out, normed_out};
+  if (x_add != nullptr)
+    return launch_mode<2>(residual, wr, bias, idx, w, logits, na, s, st);
+  return launch_mode<1>(residual, wr, bias, idx, w, logits, na, s, st);
 }
 
 }  // namespace g5moe

@@ -37,7 +37,12 @@ class RMSNorm(nn.Module):
 
 
 class MoEBlock(nn.Module):
-    """h <- h + alpha * MoE(RMSNorm(h))."""
+    """h <- h + alpha * MoE(RMSNorm(h)).
+
+    fused (default): MoEFeedForward.residual_block — the RMSNorm and the router in
+    one pass (g5moe_add_rmsnorm_router) and the residual add inside the combine
+    (g5moe_combine_residual).  fused = False: the reference-shaped composition of
+    this module's torch RMSNorm, the MoE module and a torch residual add."""
 
     def __init__(self, embed_dim: int, ff_dim: int, num_experts: int = 16, top_k: int = 2,
                  residual_scale: float = 1.0, eps: float = 1e-6):
@@ -45,8 +50,12 @@ class MoEBlock(nn.Module):
         self.norm = RMSNorm(embed_dim, eps)
         self.ff = MoEFeedForward(embed_dim, ff_dim, 0.0, "silu", num_experts, top_k)
         self.residual_scale = residual_scale
+        self.fused = True
 
     def forward(self, h: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            return self.ff.residual_block(h, self.norm.weight, self.norm.variance_epsilon,
+                                          alpha=self.residual_scale)
         return h + self.ff(self.norm(h)) * self.residual_scale
 
 
@@ -58,6 +67,11 @@ class MoEStack(nn.Module):
             MoEBlock(embed_dim, ff_dim, num_experts, top_k,
                      (1.0 / math.sqrt(i + 1)) if depth_scaling else 1.0)
             for i in range(num_layers)])
+
+    def set_fused(self, fused: bool) -> "MoEStack":
+        for layer in self.layers:
+            layer.fused = fused
+        return self
 
     def forward(self, h: torch.Tensor, return_all: bool = False):
         outs = [h]

@@ -91,6 +91,11 @@ class ALiBiSelfAttention(nn.Module):
 
 
 class MoEEncoderBlock(nn.Module):
+    """fused (default): the attention output, the residual add, norm2, the router and
+    the MoE's own residual add run as MoEFeedForward.residual_block (the
+    fused_add_norm path of encoder.py:80-83).  fused = False: the non-fused path of
+    encoder.py:84-89 in torch around the MoE module."""
+
     def __init__(self, embed_dim: int, num_heads: int, ff_dim: int, num_experts: int = 16,
                  top_k: int = 2):
         super().__init__()
@@ -98,9 +103,14 @@ class MoEEncoderBlock(nn.Module):
         self.self_attn = ALiBiSelfAttention(embed_dim, num_heads)
         self.norm2 = RMSNorm(embed_dim)
         self.ff = MoEFeedForward(embed_dim, ff_dim, 0.0, "silu", num_experts, top_k)
+        self.fused = True
 
     def forward(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None) -> torch.Tensor:
-        h = h + self.self_attn(self.norm1(h), cu_seqlens)
+        a = self.self_attn(self.norm1(h), cu_seqlens)
+        if self.fused:
+            return self.ff.residual_block(h, self.norm2.weight, self.norm2.variance_epsilon,
+                                          x_add=a)
+        h = h + a
         return h + self.ff(self.norm2(h))
 
 
@@ -118,6 +128,11 @@ class GeneT5MoE(nn.Module):
         self.final_norm = RMSNorm(embed_dim)
         self.lm_head = nn.Linear(embed_dim, vocab_size, bias=False)
         self.lm_head.weight = self.embed.weight
+
+    def set_fused(self, fused: bool) -> "GeneT5MoE":
+        for layer in self.layers:
+            layer.fused = fused
+        return self
 
     def forward(self, input_ids: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None):
         h = self.embed(input_ids)

@@ -149,6 +149,42 @@ class MoEFeedForward(nn.Module):
         y = _moe_forward_op(x2, w_router.contiguous(), self.router_bias, wgu, wd, self.top_k)
         return y.view(*lead, self.embed_dim)
 
+    def residual_block(self, residual: torch.Tensor, norm_weight: torch.Tensor,
+                       eps: float = 1e-6, x_add: Optional[torch.Tensor] = None,
+                       alpha: float = 1.0) -> torch.Tensor:
+        """The MoE half of GeneT5's encoder block, fused around the experts:
+
+            h = residual + x_add                 (or residual alone)
+            return h + alpha * self(rmsnorm(h) * norm_weight)
+
+        i.e. `fused_add_rmsnorm(x_add, residual, norm2.weight, eps)` then
+        `hidden + ff(normed) * alpha` (lib/blocks/encoder.py:80-89,
+        lib/blocks/_component.py:17-20), as g5moe_add_rmsnorm_router ->
+        g5moe_dispatch -> g5moe_expert_swiglu -> g5moe_combine_residual: the
+        normalised rows feed the router in the same pass, and the layer output is
+        added into the residual inside the combine.  The RMSNorm follows the C
+        ABI's reduction order (fp32, correctly rounded sqrt and division)."""
+        if self.training and self.dropout > 0.0:
+            raise NotImplementedError(
+                "MoEFeedForward is forward-only: dropout on the expert hidden state in "
+                "training mode is not implemented")
+        d = self.embed_dim
+        if residual.shape[-1] != d:
+            raise ValueError(f"last dim {residual.shape[-1]} != embed_dim {d}")
+        lead = residual.shape[:-1]
+        r2 = residual.reshape(-1, d).contiguous()
+        xa2 = None if x_add is None else x_add.reshape(-1, d).to(r2.dtype).contiguous()
+        w_router = self.router.weight.to(r2.dtype).contiguous()
+        nw = norm_weight.detach().to(torch.float32).contiguous()
+        normed, ssum, idx, w = ops.add_rmsnorm_router(r2, nw, eps, w_router, self.top_k,
+                                                      x_add=xa2, bias=self.router_bias)
+        base = ssum if xa2 is not None else r2
+        _, offsets, perm, inv_pos = ops.dispatch(idx, self.num_experts, d)
+        wgu, wd = self._expert_weights()
+        y_perm = ops.expert_swiglu(normed, perm, offsets, wgu, wd, self.top_k)
+        out = ops.combine_residual(y_perm, inv_pos, w, base, alpha)
+        return out.view(*lead, d)
+
     def forward_with_routing(self, x: torch.Tensor):
         """Forward that also returns the routing tensors (ops.Routing)."""
         lead = x.shape[:-1]

@@ -166,6 +166,64 @@ def combine(y_perm: torch.Tensor, inv_pos: torch.Tensor, topk_w: torch.Tensor,
     return y
 
 
+def add_rmsnorm_router(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                       w_router: torch.Tensor, top_k: int,
+                       x_add: Optional[torch.Tensor] = None,
+                       bias: Optional[torch.Tensor] = None, return_logits: bool = False):
+    """Residual add + RMSNorm + router on [N, d] rows (g5moe_add_rmsnorm_router).
+
+    Mirrors fused_add_rmsnorm(X, R, W, eps) (lib/blocks/_component.py:17-20), which
+    returns (rmsnorm(X + R), X + R), followed by the router on the normed rows.
+    Returns (normed, sum_or_None, topk_idx, topk_w[, logits]); sum is x_add + residual
+    (None without x_add: the residual itself is the sum)."""
+    dev = _check_device(residual)
+    N, d = residual.shape
+    E = w_router.shape[0]
+    dt = residual.dtype
+    _require(residual, "residual", (N, d), dt, dev)
+    if x_add is not None:
+        _require(x_add, "x_add", (N, d), dt, dev)
+    _require(norm_weight, "norm_weight", (d,), torch.float32, dev)
+    _require(w_router, "w_router", (E, d), dt, dev)
+    if bias is not None:
+        _require(bias, "bias", (E,), torch.float32, dev)
+    shape = _lib.make_shape(N, d, 128, E, top_k, _dtype_code(dt))
+    normed = torch.empty((N, d), dtype=dt, device=dev)
+    ssum = torch.empty((N, d), dtype=dt, device=dev) if x_add is not None else None
+    idx = torch.empty((N, top_k), dtype=torch.int32, device=dev)
+    w = torch.empty((N, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((N, E), dtype=torch.float32, device=dev) if return_logits else None
+    _lib.call("g5moe_add_rmsnorm_router", _ptr(x_add), _ptr(residual), _ptr(norm_weight),
+              ctypes.c_float(eps), _ptr(w_router), _ptr(bias), _ptr(ssum), _ptr(normed),
+              _ptr(idx), _ptr(w), _ptr(logits), ctypes.byref(shape), _stream(dev))
+    out = (normed, ssum, idx, w)
+    return out + (logits,) if return_logits else out
+
+
+def combine_residual(y_perm: torch.Tensor, inv_pos: torch.Tensor, topk_w: torch.Tensor,
+                     residual: torch.Tensor, alpha: float = 1.0,
+                     out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """residual + alpha * combine(...) with the roundings of that composition in the
+    residual's dtype (g5moe_combine_residual); `out` may be `residual` itself."""
+    dev = _check_device(y_perm)
+    N, k = topk_w.shape
+    d = y_perm.shape[1]
+    dt = residual.dtype
+    _require(y_perm, "y_perm", (N * k, d), torch.bfloat16, dev)
+    _require(inv_pos, "inv_pos", (N * k,), torch.int32, dev)
+    _require(topk_w, "topk_w", (N, k), torch.float32, dev)
+    _require(residual, "residual", (N, d), dt, dev)
+    if out is None:
+        out = torch.empty((N, d), dtype=dt, device=dev)
+    else:
+        _require(out, "out", (N, d), dt, dev)
+    shape = _lib.make_shape(N, d, 128, max(k, 1), k, _dtype_code(dt))
+    _lib.call("g5moe_combine_residual", _ptr(y_perm), _ptr(inv_pos), _ptr(topk_w),
+              _ptr(residual), ctypes.c_float(alpha), _ptr(out), ctypes.byref(shape),
+              _stream(dev))
+    return out
+
+
 @dataclass
 class Routing:
     topk_idx: torch.Tensor  # int32 [N, k]

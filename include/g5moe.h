@@ -142,6 +142,43 @@ g5moe_status g5moe_expert_swiglu(const void* x, const int32_t* perm, const int32
 g5moe_status g5moe_combine(const void* y_perm, const int32_t* inv_pos, const float* topk_w,
                            void* y, const g5moe_shape* shape, void* stream);
 
+/* Residual add + RMSNorm + router in one pass over each row: the step that
+ * feeds the MoE in GeneT5's encoder block.  Replaces
+ * `normed, hidden = fused_add_rmsnorm(attn * alpha, hidden, norm2.weight, eps)`
+ * (lib/blocks/_component.py:17-20, called at lib/blocks/encoder.py:80-83; or
+ * the unfused `hidden + attn * alpha` then `norm2(hidden)` at :84-86, LigerRMSNorm
+ * at _component.py:14) followed by g5moe_router_topk on the normed rows.
+ *   x_add       : [N, d] in x_dtype, or NULL (plain RMSNorm of `residual`)
+ *   residual    : [N, d] in x_dtype
+ *   norm_weight : fp32 [d];  eps >= 0 (GeneT5 uses 1e-6)
+ *   w_router, bias, topk_idx, topk_w, logits : as g5moe_router_topk
+ *   sum_out     : [N, d] in x_dtype out (x_add + residual), or NULL; needs x_add
+ *   normed_out  : [N, d] in x_dtype out (the MoE input)
+ * Per row, with T the activation dtype and every step in fp32:
+ *   s_j = T(x_j + r_j) (s = r without x_add);
+ *   ss  = sum_j s_j * s_j in the router's order (lane c: fused multiply-add
+ *         chain over columns [c*d/64, (c+1)*d/64) from 0; partials added
+ *         pairwise over lane bits 5, 4, 3, 2, 1, 0);
+ *   rstd = 1 / sqrt(ss / d + eps), correctly rounded division and sqrt;
+ *   normed_j = T((s_j * rstd) * norm_weight_j).
+ * Routing is then exactly g5moe_router_topk applied to normed_out. */
+g5moe_status g5moe_add_rmsnorm_router(const void* x_add, const void* residual,
+                                      const float* norm_weight, float eps,
+                                      const void* w_router, const float* bias, void* sum_out,
+                                      void* normed_out, int32_t* topk_idx, float* topk_w,
+                                      float* logits, const g5moe_shape* shape, void* stream);
+
+/* Gated combine added into the residual stream: the encoder block's
+ * `hidden_states + dropout(ff_output) * alpha` (lib/blocks/encoder.py:89;
+ * alpha = 1/sqrt(i+1) under depth_scaling, :118) with ff_output = the MoE
+ * layer output, so the layer output never goes to memory.  With T the
+ * activation dtype: y = T(sum over s of topk_w[t, s] * y_perm[inv_pos[t, s]])
+ * (fp32, slot order, as g5moe_combine), out = T(residual + T(y * alpha)).
+ *   residual, out : [N, d] in x_dtype (out may alias residual). */
+g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
+                                    const float* topk_w, const void* residual, float alpha,
+                                    void* out, const g5moe_shape* shape, void* stream);
+
 /* The whole layer forward, enqueued as router -> dispatch -> gate|up ->
  * down -> combine.  Replaces FeedForward.forward (lib/blocks/_component.py:48-52)
  * when the module is the MoE.  Routing outputs are written to the caller's

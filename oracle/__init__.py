@@ -12,7 +12,10 @@ up = wi_1 (:42-43, split order lib/model/build.py:30-34) — and the router is
 pin.
 """
 from .moe_oracle import (  # noqa: F401
+    add_rmsnorm,
+    add_rmsnorm_np,
     combine,
+    combine_c,
     dispatch,
     dispatch_c,
     expert_forward,

@@ -15,6 +15,13 @@
  *                   added last.
  *   top-k         : increasing-expert scan, replace on strictly greater.
  *   dispatch      : stable counting sort of the flattened assignments.
+ *   add + RMSNorm : s = T(x + r), ss in the router's lane/tree order with
+ *                   fmaf, rstd = 1 / sqrtf(ss / d + eps), n = T((s * rstd) * w)
+ *                   (include/g5moe.h, g5moe_add_rmsnorm_router; the step of
+ *                   lib/blocks/_component.py:17-20 / lib/blocks/encoder.py:80-86).
+ *   combine       : fmaf in slot order from 0, one rounding to T; with a
+ *                   residual, out = T(r + T(T(acc) * alpha))
+ *                   (g5moe_combine / g5moe_combine_residual; encoder.py:89).
  *
  * Build: oracle/build.py (gcc -O2 -ffp-contract=off, so only the explicit
  * fmaf calls fuse).
@@ -129,6 +136,81 @@ int g5o_dispatch(const int32_t* idx, int64_t nk, int E, int32_t* counts, int32_t
     const int32_t p = fill[e]++;
     perm[p] = (int32_t)a;
     inv_pos[a] = p;
+  }
+  return 0;
+}
+
+static inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+/* Round to the activation dtype (0 = bf16, 1 = fp32) and widen back. */
+static inline float round_to(float v, int dtype) {
+  return dtype == 0 ? bf16_to_f32(f32_to_bf16(v)) : v;
+}
+
+static inline float load_elem(const void* p, int dtype, size_t i) {
+  return dtype == 0 ? bf16_to_f32(((const uint16_t*)p)[i]) : ((const float*)p)[i];
+}
+
+static inline void store_elem(void* p, int dtype, size_t i, float v) {
+  if (dtype == 0)
+    ((uint16_t*)p)[i] = f32_to_bf16(v);
+  else
+    ((float*)p)[i] = v;
+}
+
+/* Residual add + RMSNorm.  x_add and sum_out may be NULL; scratch: d floats. */
+int g5o_add_rmsnorm(const void* x_add, const void* res, int dtype, const float* w, float eps,
+                    int64_t n, int d, void* sum_out, void* normed_out, float* scratch) {
+  if (d % 64 != 0 || d <= 0 || (dtype != 0 && dtype != 1)) return 1;
+  const int L = d / 64;
+  float p[64];
+  for (int64_t t = 0; t < n; ++t) {
+    const size_t base = (size_t)t * d;
+    for (int j = 0; j < d; ++j) {
+      float v = load_elem(res, dtype, base + j);
+      if (x_add) v = round_to(load_elem(x_add, dtype, base + j) + v, dtype);
+      scratch[j] = v;
+      if (sum_out) store_elem(sum_out, dtype, base + j, v);
+    }
+    for (int c = 0; c < 64; ++c) {
+      float acc = 0.0f;
+      for (int i = 0; i < L; ++i) acc = fmaf(scratch[c * L + i], scratch[c * L + i], acc);
+      p[c] = acc;
+    }
+    const float ss = tree64(p);
+    const float rstd = 1.0f / sqrtf(ss / (float)d + eps);
+    for (int j = 0; j < d; ++j) store_elem(normed_out, dtype, base + j, (scratch[j] * rstd) * w[j]);
+  }
+  return 0;
+}
+
+/* Combine (residual == NULL) or combine added into the residual stream.
+ * y_perm: bf16 bits [N*k, d]; inv_pos int32 [N*k]; w fp32 [N, k]. */
+int g5o_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
+                const void* residual, float alpha, int dtype, int64_t n, int d, int k,
+                void* out) {
+  if (dtype != 0 && dtype != 1) return 1;
+  for (int64_t t = 0; t < n; ++t) {
+    for (int j = 0; j < d; ++j) {
+      float acc = 0.0f;
+      for (int s = 0; s < k; ++s) {
+        const int32_t p = inv_pos[(size_t)t * k + s];
+        if (p < 0) continue;
+        acc = fmaf(w[(size_t)t * k + s], bf16_to_f32(y_perm[(size_t)p * d + j]), acc);
+      }
+      if (residual) {
+        const float y = round_to(acc, dtype);
+        const float tt = round_to(y * alpha, dtype);
+        acc = load_elem(residual, dtype, (size_t)t * d + j) + tt;
+      }
+      store_elem(out, dtype, (size_t)t * d + j, acc);
+    }
   }
   return 0;
 }

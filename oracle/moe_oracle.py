@@ -38,6 +38,24 @@ combine
     y[t] = sum_s w[t, s] * y_perm[inv_pos[t, s]], fp32, slot order.  Pins: a
     permutation-equivariance check (permuting tokens permutes y) and the
     upcycling invariant above.
+combine_c
+    The C restatement of the combine as the C ABI fixes it (fmaf in slot order
+    from 0, one rounding to the activation dtype) and of the residual variant
+    out = T(r + T(T(acc) * alpha)) — the encoder block's
+    `hidden_states + ff_output * alpha` (lib/blocks/encoder.py:89).  Pins:
+    exact-rational fma restatement; k = 1, w = 1 returns y_perm bit for bit;
+    the residual composition equals torch's own bf16 ops (CPU) on y_moe.
+add_rmsnorm / add_rmsnorm_np
+    s = T(x + r); ss = sum s^2 in the router's lane/tree order; rstd =
+    1 / sqrt(ss / d + eps); normed = T((s * rstd) * w) — fused_add_rmsnorm /
+    RMSNorm (lib/blocks/_component.py:14, :17-20; eps 1e-6) in the order the C
+    ABI fixes (g5moe_add_rmsnorm_router).  add_rmsnorm is C, add_rmsnorm_np an
+    independent numpy restatement (bf16 rows, where s*s is exact in fp32).
+    Pins: C == numpy bit for bit; C == exact-rational restatement on fp32 rows;
+    power-of-two constant rows with eps = 0 give T(sign * w) exactly; the bf16
+    add equals torch's bf16 add; within fp32 rounding of a float64 RMSNorm.
+    Liger's own casting (LigerRMSNorm) stays unpinned: this is the contract's
+    order, not Liger's.
 """
 from __future__ import annotations
 
@@ -65,7 +83,12 @@ def _clib():
                                              P, P]
         L.g5o_topk.argtypes = [P, ctypes.c_int64, ctypes.c_int, ctypes.c_int, P, P]
         L.g5o_dispatch.argtypes = [P, ctypes.c_int64, ctypes.c_int, P, P, P, P]
-        for f in (L.g5o_router_logits_f32, L.g5o_router_logits_bf16, L.g5o_topk, L.g5o_dispatch):
+        L.g5o_add_rmsnorm.argtypes = [P, P, ctypes.c_int, P, ctypes.c_float, ctypes.c_int64,
+                                      ctypes.c_int, P, P, P]
+        L.g5o_combine.argtypes = [P, P, P, P, ctypes.c_float, ctypes.c_int, ctypes.c_int64,
+                                  ctypes.c_int, ctypes.c_int, P]
+        for f in (L.g5o_router_logits_f32, L.g5o_router_logits_bf16, L.g5o_topk, L.g5o_dispatch,
+                  L.g5o_add_rmsnorm, L.g5o_combine):
             f.restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -279,4 +302,82 @@ def moe_forward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: n
                perm=perm, inv_pos=inv_pos, y_perm=y_perm, y=y)
     if return_h:
         out["h"] = h
+    return out
+
+
+# ---- pre-norm (residual add + RMSNorm) and combine in the C ABI's order ------------
+
+def _rows(a: np.ndarray):
+    """-> (contiguous array, dtype code 0 = bf16 bits, 1 = fp32)."""
+    if a.dtype == np.uint16:
+        return np.ascontiguousarray(a), 0
+    return np.ascontiguousarray(a, np.float32), 1
+
+
+def add_rmsnorm(residual: np.ndarray, weight: np.ndarray, eps: float,
+                x_add: Optional[np.ndarray] = None):
+    """C implementation.  Rows as uint16 bf16 bits or fp32 (x_add of the same kind).
+    -> (normed, sum) in the input's representation; sum is None without x_add."""
+    r, code = _rows(residual)
+    N, d = r.shape
+    xa = None
+    if x_add is not None:
+        xa, c2 = _rows(x_add)
+        if c2 != code or xa.shape != r.shape:
+            raise ValueError("x_add must match residual")
+    w = np.ascontiguousarray(weight, np.float32)
+    normed = np.empty_like(r)
+    ssum = np.empty_like(r) if xa is not None else None
+    scratch = np.empty(d, np.float32)
+    if _clib().g5o_add_rmsnorm(_p(xa), _p(r), code, _p(w), float(eps), N, d, _p(ssum),
+                               _p(normed), _p(scratch)) != 0:
+        raise ValueError("d must be a positive multiple of 64")
+    return normed, ssum
+
+
+def add_rmsnorm_np(residual_f32: np.ndarray, weight: np.ndarray, eps: float,
+                   x_add_f32: Optional[np.ndarray] = None):
+    """Vectorised numpy restatement for bf16 rows (given widened to fp32): every
+    s * s is exact in fp32, so the lane fma chain is a chain of fp32 adds.
+    -> (normed, sum) as fp32 arrays holding bf16 values."""
+    s = np.asarray(residual_f32, np.float32)
+    if x_add_f32 is not None:
+        s = round_bf16(np.asarray(x_add_f32, np.float32) + s)
+    N, d = s.shape
+    L = d // 64
+    S = s.reshape(N, 64, L)
+    acc = np.zeros((N, 64), np.float32)
+    for i in range(L):
+        acc = acc + S[:, :, i] * S[:, :, i]
+    m = 32
+    while m >= 1:
+        acc = acc[:, :m] + acc[:, m:2 * m]
+        m //= 2
+    ss = acc[:, 0]
+    rstd = np.float32(1.0) / np.sqrt(ss / np.float32(d) + np.float32(eps))
+    normed = round_bf16((s * rstd[:, None]) * np.asarray(weight, np.float32)[None, :])
+    return normed, (s if x_add_f32 is not None else None)
+
+
+def combine_c(y_perm_bits: np.ndarray, inv_pos: np.ndarray, topk_w: np.ndarray,
+              residual: Optional[np.ndarray] = None, alpha: float = 1.0,
+              out_dtype: str = "bf16") -> np.ndarray:
+    """C restatement of g5moe_combine (residual None) / g5moe_combine_residual.
+    y_perm as uint16 bf16 bits; residual and the result in out_dtype's
+    representation (uint16 bits for "bf16", fp32 for "f32")."""
+    N, k = topk_w.shape
+    yp = np.ascontiguousarray(y_perm_bits, np.uint16)
+    d = yp.shape[1]
+    code = 0 if out_dtype == "bf16" else 1
+    out = np.empty((N, d), np.uint16 if code == 0 else np.float32)
+    r = None
+    if residual is not None:
+        r, c2 = _rows(residual)
+        if c2 != code:
+            raise ValueError("residual dtype must match out_dtype")
+    ip = np.ascontiguousarray(inv_pos, np.int32).reshape(-1)
+    w = np.ascontiguousarray(topk_w, np.float32)
+    if _clib().g5o_combine(_p(yp), _p(ip), _p(w), _p(r), float(alpha), code, N, d, k,
+                           _p(out)) != 0:
+        raise ValueError("bad dtype")
     return out

@@ -6,7 +6,10 @@
 * Config 4 (12 stacked RMSNorm -> MoE -> residual blocks, 45,500 packed tokens):
   teacher-forced per layer — each layer's routing on the GPU's own RMSNorm output
   is bit-exact against the oracle; the MoE output of the first and last layers is
-  within the bf16 tolerance of the oracle in its bf16-storage mode.
+  within the bf16 tolerance of the oracle in its bf16-storage mode.  Both the
+  fused blocks (g5moe_add_rmsnorm_router + g5moe_combine_residual: normed rows
+  and every residual update bit-exact against the oracle) and the unfused torch
+  composition.
 * Config 5 (encoder with ALiBi attention + MoE, MDLM unmasking): in a reduced
   model every layer's MoE, on the inputs the forward actually produced, routes
   bit-exactly and stays within the bf16 tolerance; the unmasking loop fills every
@@ -113,9 +116,61 @@ def test_backward_raises_clearly(cuda_device):
         y.sum().backward()
 
 
+def check_fused_layer(ff, h2, nw, x_add2=None, alpha=1.0, out2=None, label="",
+                      tol_check=False):
+    """One fused MoE block on its actual inputs: normed/sum rows bit-exact, routing
+    bit-exact, and (out2 given) the block output == the oracle's residual combine of
+    this layer's expert outputs, bit for bit."""
+    w_np = nw.float().cpu().numpy()
+    normed, ssum, idx, w = ops.add_rmsnorm_router(
+        h2, nw.float().contiguous(), 1e-6, ff.router.weight.contiguous(), ff.top_k, x_add=x_add2)
+    n_ref, s_ref = oracle.add_rmsnorm(bits(h2), w_np, 1e-6,
+                                      None if x_add2 is None else bits(x_add2))
+    np.testing.assert_array_equal(bits(normed), n_ref)
+    base = h2 if x_add2 is None else ssum
+    if x_add2 is not None:
+        np.testing.assert_array_equal(bits(ssum), s_ref)
+    wr = bits(ff.router.weight)
+    ref_l = oracle.router_logits(n_ref, wr)
+    ref_i, _ = oracle.topk_gates_c(ref_l, ff.top_k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_i)
+    _, offsets, perm, inv_pos = ops.dispatch(idx, ff.num_experts, h2.shape[1])
+    wgu, wd = ff._expert_weights()
+    y_perm = ops.expert_swiglu(normed, perm, offsets, wgu, wd, ff.top_k)
+    if out2 is not None:
+        ref_out = oracle.combine_c(bits(y_perm), inv_pos.cpu().numpy(), w.cpu().numpy(),
+                                   bits(base), alpha)
+        np.testing.assert_array_equal(bits(out2), ref_out)
+    if tol_check:
+        ref = oracle.moe_forward(n_ref, wr, bits(ff.w_gate), bits(ff.w_up), bits(ff.w_down),
+                                 ff.top_k, storage="bf16")
+        np.testing.assert_array_equal(ref["topk_idx"], ref_i)
+        y = ops.combine(y_perm, inv_pos, w, torch.bfloat16)
+        mx, mean = normwise(y.float().cpu().numpy(), ref["y"])
+        print(f"{label}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+        assert mx <= 2e-2 and mean <= 2e-3, (label, mx, mean)
+
+
+def test_config4_fused_teacher_forced(cuda_device):
+    cfg = blocks.make_config4()
+    stack = blocks.MoEStack(12, 768, 3072).to(cuda_device).to(torch.bfloat16)
+    blocks.load_layer_weights(stack, cfg.layer_seeds, 3072)
+    x = torch.from_numpy(cfg.x).view(torch.bfloat16).to(cuda_device)
+    with torch.no_grad():
+        hs = stack(x, return_all=True)
+    assert len(hs) == 13 and torch.isfinite(hs[-1].float()).all()
+    for li, layer in enumerate(stack.layers):
+        print(f"config4 fused layer {li}", flush=True)
+        with torch.no_grad():
+            check_fused_layer(layer.ff, hs[li].reshape(-1, 768), layer.norm.weight,
+                              alpha=layer.residual_scale, out2=hs[li + 1].reshape(-1, 768),
+                              label=f"config4 fused layer {li}", tol_check=li in (0, 11))
+
+
 def test_config4_teacher_forced(cuda_device):
     cfg = blocks.make_config4()
     stack = blocks.MoEStack(12, 768, 3072).to(cuda_device).to(torch.bfloat16)
+    stack.set_fused(False)
     blocks.load_layer_weights(stack, cfg.layer_seeds, 3072)
     x = torch.from_numpy(cfg.x).view(torch.bfloat16).to(cuda_device)
     with torch.no_grad():
@@ -160,7 +215,7 @@ def test_config5_encoder_teacher_forced(cuda_device):
     bf16 tolerance of the oracle's bf16-storage mode.  (End-to-end logit comparisons
     against a differently-rounded reference are not meaningful through several MoE
     layers: bf16-level differences flip near-tie routing decisions downstream.)"""
-    model = small_encoder(cuda_device)
+    model = small_encoder(cuda_device).set_fused(False)
     ids = torch.randint(0, 4096, (2, 384), device=cuda_device)
     seen = []
     hooks = [layer.ff.register_forward_hook(lambda mod, inp, out: seen.append((mod, inp[0], out)))
@@ -182,6 +237,33 @@ def test_config5_encoder_teacher_forced(cuda_device):
         mx, mean = normwise(yout.reshape(-1, 768).float().cpu().numpy(), ref["y"])
         print(f"config5 layer {li}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
         assert mx <= 2e-2 and mean <= 2e-3, (li, mx, mean)
+
+
+def test_config5_fused_encoder_teacher_forced(cuda_device):
+    """Fused blocks (attention output + residual add + norm2 + router in one pass,
+    residual add in the combine): on each block's actual input and attention
+    output, the normed and sum rows, the routing and the block output are
+    bit-exact against the oracle."""
+    model = small_encoder(cuda_device)
+    ids = torch.randint(0, 4096, (2, 384), device=cuda_device)
+    ins, attn, outs = [], [], []
+    hooks = []
+    for layer in model.layers:
+        hooks.append(layer.register_forward_pre_hook(lambda mod, a: ins.append(a[0])))
+        hooks.append(layer.self_attn.register_forward_hook(lambda mod, a, o: attn.append(o)))
+        hooks.append(layer.register_forward_hook(lambda mod, a, o: outs.append(o)))
+    with torch.no_grad():
+        logits = model(ids)["logits"]
+    for h in hooks:
+        h.remove()
+    assert torch.isfinite(logits.float()).all() and len(outs) == len(model.layers)
+    for li, layer in enumerate(model.layers):
+        print(f"config5 fused layer {li}", flush=True)
+        with torch.no_grad():
+            check_fused_layer(layer.ff, ins[li].reshape(-1, 768), layer.norm2.weight,
+                              x_add2=attn[li].reshape(-1, 768).contiguous(),
+                              out2=outs[li].reshape(-1, 768), label=f"config5 fused layer {li}",
+                              tol_check=True)
 
 
 def test_config5_unmasking_loop(cuda_device):
