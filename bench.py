@@ -116,6 +116,10 @@ def bench_config4(args) -> dict:
     N = x.shape[1]
     with torch.no_grad():
         t = timed(lambda: stack(x), args.steps, args.warmup)
+        # the same stack as the torch composition RMSNorm -> MoE -> residual add
+        stack.set_fused(False)
+        t_unfused = timed(lambda: stack(x), args.steps, args.warmup)
+        stack.set_fused(True)
     flops = 12 * 6 * 768 * 3072 * N * 2
     return {
         "metric": "12-block RMSNorm->MoE->residual stack tokens/s, 45.5k packed tok, 16e top-2",
@@ -126,6 +130,8 @@ def bench_config4(args) -> dict:
                                "lengths U[1000, 9000], seeded N(0, 0.02) weights per layer",
                    "n_tokens": N, "n_layers": 12, "n_sequences": len(cfg.cu_seqlens) - 1},
         "expert_gemm_tflops_incl_layer_overheads": flops / t / 1e12,
+        "blocks": "fused: g5moe_add_rmsnorm_router + dispatch + experts + g5moe_combine_residual",
+        "unfused_ms_per_step": t_unfused * 1e3,
     }
 
 

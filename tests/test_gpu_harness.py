@@ -278,3 +278,40 @@ def test_config5_unmasking_loop(cuda_device):
     assert torch.equal(out1[:, :128], prefix)
     assert not (out1[:, 128:] == mask_id).any() and not (out1[:, 128:] == pad_id).any()
     assert st1["forwards"] == 5
+
+
+def test_upcycled_checkpoint_layer_equals_dense(cuda_device):
+    """A dense checkpoint loaded through genet5_amd.upcycle: every layer's MoE output
+    equals the dense FeedForward it came from (plain PyTorch fp32), whatever the
+    seeded router picks, because every expert is that FeedForward."""
+    from genet5_amd import upcycle
+    d, F, L = 256, 512, 2
+    g = torch.Generator().manual_seed(11)
+    r = lambda *s: torch.randn(*s, generator=g) * 0.05
+    enc = {}
+    for i in range(L):
+        for p in "qkvo":
+            enc[f"layers.{i}.self_attn.{p}.weight"] = r(d, d)
+        enc[f"layers.{i}.norm1.weight"] = torch.ones(d)
+        enc[f"layers.{i}.norm2.weight"] = torch.ones(d)
+        enc[f"layers.{i}.ff.wi_0.weight"] = r(F, d)
+        enc[f"layers.{i}.ff.wi_1.weight"] = r(F, d)
+        enc[f"layers.{i}.ff.wo.weight"] = r(d, F)
+    enc["final_norm.weight"] = torch.ones(d)
+    emb = r(64, d)
+    m = encoder.GeneT5MoE(vocab_size=64, embed_dim=d, num_layers=L, num_heads=4, ff_dim=F)
+    rep = upcycle.load_upcycled(m, {"embed": {"weight": emb}, "encoder": enc,
+                                    "lm_head": {"weight": emb}})
+    assert rep.clean
+    m = m.to(cuda_device).to(torch.bfloat16)
+    x = torch.randn(500, d, device=cuda_device).to(torch.bfloat16)
+    for i, layer in enumerate(m.layers):
+        with torch.no_grad():
+            y = layer.ff(x).float()
+        xf = x.float()
+        w0, w1, wo = (enc[f"layers.{i}.ff.{n}.weight"].to(cuda_device).to(torch.bfloat16).float()
+                      for n in ("wi_0", "wi_1", "wo"))
+        dense = (torch.nn.functional.silu(xf @ w0.T) * (xf @ w1.T)) @ wo.T
+        mx, mean = normwise(y.cpu().numpy(), dense.cpu().numpy())
+        print(f"upcycled layer {i}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+        assert mx <= 2e-2 and mean <= 4e-3, (i, mx, mean)
