@@ -32,6 +32,13 @@ EXPORTED = (
     "g5moe_combine",
     "g5moe_add_rmsnorm_router",
     "g5moe_combine_residual",
+    "g5moe_transpose_experts",
+    "g5moe_grouped_gemm",
+    "g5moe_gate_grad",
+    "g5moe_router_grad",
+    "g5moe_expert_gate_up_raw",
+    "g5moe_swiglu_backward",
+    "g5moe_input_grad",
     "g5moe_forward",
 )
 
@@ -75,6 +82,15 @@ _SIGS = {
                                   _SHAPE_P, _P], ctypes.c_int),
     "g5moe_combine_residual": ([_P, _P, _P, _P, ctypes.c_float, _P, _SHAPE_P, _P],
                                ctypes.c_int),
+    "g5moe_transpose_experts": ([_P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P],
+                                ctypes.c_int),
+    "g5moe_grouped_gemm": ([_P, _P, _P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
+                           ctypes.c_int32, _P], ctypes.c_int),
+    "g5moe_gate_grad": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_router_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_expert_gate_up_raw": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_swiglu_backward": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_input_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
 }
 

@@ -34,7 +34,8 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     f"-I{INCLUDE_DIR}",
 ]
-SOURCES = ["api.hip", "router.hip", "dispatch.hip", "grouped_gemm.hip", "combine.hip"]
+SOURCES = ["api.hip", "router.hip", "dispatch.hip", "grouped_gemm.hip", "combine.hip",
+           "backward.hip"]
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:

@@ -231,6 +231,124 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
                     "g5moe_combine_residual");
 }
 
+g5moe_status g5moe_transpose_experts(const void* w, void* w_t, int32_t n_experts, int32_t rows,
+                                     int32_t cols, void* stream) {
+  G5_NONNULL(w);
+  G5_NONNULL(w_t);
+  if (n_experts < 0 || rows < 0 || cols < 0 || rows % 64 != 0 || cols % 64 != 0)
+    return fail(G5MOE_ERR_INVALID_ARG, "transpose: [%d, %d, %d] needs non-negative sizes and "
+                "rows, cols multiples of 64", int(n_experts), int(rows), int(cols));
+  return hip_status(launch_transpose_experts(static_cast<const uint16_t*>(w),
+                                             static_cast<uint16_t*>(w_t), n_experts, rows, cols,
+                                             as_stream(stream)),
+                    "g5moe_transpose_experts");
+}
+
+g5moe_status g5moe_grouped_gemm(const void* a, const int32_t* offsets, const void* b, void* c,
+                                int64_t rows, int32_t k, int32_t n_out, int32_t n_experts,
+                                void* stream) {
+  if (rows < 0 || rows > int64_t(INT32_MAX) / 2)
+    return fail(G5MOE_ERR_INVALID_ARG, "grouped_gemm: rows %lld out of range", (long long)rows);
+  if (n_experts < 1 || n_experts > kMaxExperts)
+    return fail(G5MOE_ERR_UNSUPPORTED, "grouped_gemm: n_experts %d not in [1, %d]",
+                int(n_experts), kMaxExperts);
+  if (k < 128 || k % 64 != 0 || n_out < 128 || n_out % 128 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "grouped_gemm: k = %d must be a multiple of 64 >= 128 "
+                "and n_out = %d a multiple of 128", int(k), int(n_out));
+  if (rows == 0) return G5MOE_OK;
+  G5_NONNULL(a);
+  G5_NONNULL(offsets);
+  G5_NONNULL(b);
+  G5_NONNULL(c);
+  return hip_status(launch_grouped_nt(static_cast<const uint16_t*>(a), offsets,
+                                      static_cast<const uint16_t*>(b), static_cast<uint16_t*>(c),
+                                      rows, n_experts, k, n_out, as_stream(stream)),
+                    "g5moe_grouped_gemm");
+}
+
+g5moe_status g5moe_gate_grad(const void* dy, const void* y_perm, const int32_t* inv_pos,
+                             const float* topk_w, float* dw, void* dy_perm,
+                             const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->x_dtype != G5MOE_DTYPE_BF16)
+    return fail(G5MOE_ERR_UNSUPPORTED, "the backward takes bf16 activations");
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(dy);
+  G5_NONNULL(y_perm);
+  G5_NONNULL(inv_pos);
+  G5_NONNULL(topk_w);
+  G5_NONNULL(dw);
+  G5_NONNULL(dy_perm);
+  return hip_status(launch_gate_grad(static_cast<const uint16_t*>(dy),
+                                     static_cast<const uint16_t*>(y_perm), inv_pos, topk_w, dw,
+                                     static_cast<uint16_t*>(dy_perm), *shape, as_stream(stream)),
+                    "g5moe_gate_grad");
+}
+
+g5moe_status g5moe_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
+                               const float* grad_logits, float* dlogits,
+                               const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(dw);
+  G5_NONNULL(topk_w);
+  G5_NONNULL(topk_idx);
+  G5_NONNULL(dlogits);
+  return hip_status(launch_router_grad(dw, topk_w, topk_idx, grad_logits, dlogits, *shape,
+                                       as_stream(stream)),
+                    "g5moe_router_grad");
+}
+
+g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const int32_t* offsets,
+                                      const void* w_gate_up, void* gu, void* ws,
+                                      const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(x);
+  G5_NONNULL(perm);
+  G5_NONNULL(offsets);
+  G5_NONNULL(w_gate_up);
+  G5_NONNULL(gu);
+  G5_NONNULL(ws);
+  const hipStream_t st = as_stream(stream);
+  hipError_t err;
+  const uint16_t* xb = gemm_input(x, static_cast<char*>(ws), *shape, st, &err);
+  G5_CHECK(hip_status(err, "g5moe_expert_gate_up_raw (cast)"));
+  return hip_status(launch_gate_up_raw(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
+                                       static_cast<uint16_t*>(gu), *shape, st),
+                    "g5moe_expert_gate_up_raw");
+}
+
+g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, void* dgu, void* h,
+                                   const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(dh);
+  G5_NONNULL(gu);
+  G5_NONNULL(dgu);
+  G5_NONNULL(h);
+  return hip_status(launch_swiglu_bwd(static_cast<const uint16_t*>(dh),
+                                      static_cast<const uint16_t*>(gu),
+                                      static_cast<uint16_t*>(dgu), static_cast<uint16_t*>(h),
+                                      *shape, as_stream(stream)),
+                    "g5moe_swiglu_backward");
+}
+
+g5moe_status g5moe_input_grad(const void* dx_perm, const int32_t* inv_pos, const float* dlogits,
+                              const void* w_router, void* dx, const g5moe_shape* shape,
+                              void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(dx_perm);
+  G5_NONNULL(inv_pos);
+  G5_NONNULL(dlogits);
+  G5_NONNULL(w_router);
+  G5_NONNULL(dx);
+  return hip_status(launch_input_grad(static_cast<const uint16_t*>(dx_perm), inv_pos, dlogits,
+                                      w_router, dx, *shape, as_stream(stream)),
+                    "g5moe_input_grad");
+}
+
 g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bias,
                            const void* w_gate_up, const void* w_down, void* y,
                            int32_t* topk_idx, float* topk_w, int32_t* counts,

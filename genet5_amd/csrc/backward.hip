@@ -1,0 +1,283 @@
+// Backward of the MoE layer: the elementwise, gather/scatter and reduction
+// stages.  The data-gradient products run on the grouped GEMM kernels
+// (grouped_gemm.hip); the weight-gradient products are plain per-expert GEMMs
+// issued by the host (hipBLASLt through PyTorch).
+//
+// New stage: the reference trains the dense FeedForward through autograd
+// (lib/blocks/_component.py:48-52 under train/diffusion_finet:761's
+// loss.backward()); the MoE layer and hence its backward are new.  With the
+// forward
+//   w[t, s]   = exp(l_{t,i_s}) / sum_j exp(l_{t,i_j})        (top-k renormalised)
+//   y[t]      = sum_s w[t, s] * Y[inv_pos[t, s]],  Y[p] = h[p] Wd_e^T,
+//   h[p]      = silu(g[p]) * u[p],  (g | u)[p] = x[t(p)] Wgu_e^T
+// and dy = dL/dy:
+//   dw[t, s]  = dy[t] . Y[inv_pos[t, s]]                       (gate_grad)
+//   dY[p]     = w[t, s] * dy[t]                                (gate_grad)
+//   dl[t, i_r] = w_r (dw_r - sum_s w_s dw_s), 0 elsewhere      (router_grad)
+//   dh        = dY Wd_e                                        (grouped GEMM)
+//   dg        = dh * u * s(g) (1 + g (1 - s(g))), du = dh * silu(g)   (swiglu_bwd)
+//   dX_perm   = (dg | du) Wgu_e                                (grouped GEMM)
+//   dx[t]     = sum_s dX_perm[inv_pos[t, s]] + sum_e dl[t, e] Wr[e]   (input_grad)
+// with s the logistic sigmoid.
+#include "g5moe_internal.h"
+
+namespace g5moe {
+namespace {
+
+__device__ __forceinline__ float bf_lo(uint32_t u) { return __uint_as_float(u << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 0xffff0000u); }
+
+// One wavefront per assignment a = t * k + s.  Lane c holds columns
+// [c * L, c * L + L); the dot product is an fma chain per lane added over lane
+// bits 5 .. 0, so dw is deterministic.
+template <int L>
+__global__ __launch_bounds__(256) void gate_grad_kernel(
+    const uint16_t* __restrict__ dy, const uint16_t* __restrict__ y_perm,
+    const int32_t* __restrict__ inv_pos, const float* __restrict__ topk_w,
+    float* __restrict__ dw, uint16_t* __restrict__ dyp, int64_t nk, int topk) {
+  constexpr int D = 64 * L;
+  const int lane = threadIdx.x & 63;
+  const int64_t a = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (a >= nk) return;
+  const int64_t t = a / topk;
+  const int32_t p = inv_pos[a];
+  if (p < 0) {
+    if (lane == 0) dw[a] = 0.f;
+    return;
+  }
+  const float w = topk_w[a];
+  const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
+  const uint32_t* yr = reinterpret_cast<const uint32_t*>(y_perm + int64_t(p) * D + lane * L);
+  uint32_t* outr = reinterpret_cast<uint32_t*>(dyp + int64_t(p) * D + lane * L);
+  float acc = 0.f;
+#pragma unroll
+  for (int i = 0; i < L / 2; ++i) {
+    const uint32_t g = dyr[i], y = yr[i];
+    acc = __builtin_fmaf(bf_lo(g), bf_lo(y), acc);
+    acc = __builtin_fmaf(bf_hi(g), bf_hi(y), acc);
+    outr[i] = pack_bf16x2(w * bf_lo(g), w * bf_hi(g));
+  }
+#pragma unroll
+  for (int bit = 32; bit >= 1; bit >>= 1) acc = acc + __shfl_xor(acc, bit, 64);
+  if (lane == 0) dw[a] = acc;
+}
+
+// One thread per token.
+__global__ __launch_bounds__(256) void router_grad_kernel(
+    const float* __restrict__ dw, const float* __restrict__ topk_w,
+    const int32_t* __restrict__ topk_idx, const float* __restrict__ grad_logits,
+    float* __restrict__ dlogits, int64_t n_tokens, int n_experts, int topk) {
+  const int64_t t = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= n_tokens) return;
+  float dl[kMaxExperts];
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; ++e)
+    dl[e] = (e < n_experts && grad_logits != nullptr) ? grad_logits[t * n_experts + e] : 0.f;
+  float sdot = 0.f;
+  for (int s = 0; s < topk; ++s) sdot = __builtin_fmaf(topk_w[t * topk + s], dw[t * topk + s], sdot);
+  for (int s = 0; s < topk; ++s) {
+    const int e = topk_idx[t * topk + s];
+    const float v = topk_w[t * topk + s] * (dw[t * topk + s] - sdot);
+#pragma unroll
+    for (int j = 0; j < kMaxExperts; ++j)
+      if (j == e) dl[j] = dl[j] + v;
+  }
+  for (int e = 0; e < n_experts; ++e) dlogits[t * n_experts + e] = dl[e];
+}
+
+// One thread per 8 consecutive h columns of one row.  gu rows interleave
+// 32-column groups: entries [64q, 64q + 32) are g of columns [32q, 32q + 32),
+// the next 32 the matching u.
+__global__ __launch_bounds__(256) void swiglu_bwd_kernel(
+    const uint16_t* __restrict__ dh, const uint16_t* __restrict__ gu,
+    uint16_t* __restrict__ dgu, uint16_t* __restrict__ h, int64_t rows, int F) {
+  const int cpr = F / 8;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * cpr) return;
+  const int64_t p = i / cpr;
+  const int f0 = int(i - p * cpr) * 8;
+  const int q = f0 >> 5, r = f0 & 31;
+  const int64_t go = p * 2 * F + 64 * q + r;
+  const uint4 vd = *reinterpret_cast<const uint4*>(dh + p * F + f0);
+  const uint4 vg = *reinterpret_cast<const uint4*>(gu + go);
+  const uint4 vu = *reinterpret_cast<const uint4*>(gu + go + 32);
+  const uint32_t ad[4] = {vd.x, vd.y, vd.z, vd.w};
+  const uint32_t ag[4] = {vg.x, vg.y, vg.z, vg.w};
+  const uint32_t au[4] = {vu.x, vu.y, vu.z, vu.w};
+  uint32_t og[4], ou[4], oh[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float rg[2], ru[2], rh[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const float d = hh ? bf_hi(ad[j]) : bf_lo(ad[j]);
+      const float g = hh ? bf_hi(ag[j]) : bf_lo(ag[j]);
+      const float u = hh ? bf_hi(au[j]) : bf_lo(au[j]);
+      const float sg = 1.0f / (1.0f + expf(-g));
+      const float silu = g * sg;
+      rg[hh] = d * u * (sg * (1.0f + g * (1.0f - sg)));
+      ru[hh] = d * silu;
+      rh[hh] = silu * u;
+    }
+    og[j] = pack_bf16x2(rg[0], rg[1]);
+    ou[j] = pack_bf16x2(ru[0], ru[1]);
+    oh[j] = pack_bf16x2(rh[0], rh[1]);
+  }
+  *reinterpret_cast<uint4*>(dgu + go) = make_uint4(og[0], og[1], og[2], og[3]);
+  *reinterpret_cast<uint4*>(dgu + go + 32) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+  *reinterpret_cast<uint4*>(h + p * F + f0) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+}
+
+// One thread per 8 consecutive outputs: dx = sum over slots of dX_perm rows
+// (slot order) + sum over experts of dl * Wr (expert order), fp32, one rounding.
+template <bool OUT_F32>
+__global__ __launch_bounds__(256) void input_grad_kernel(
+    const uint16_t* __restrict__ dxp, const int32_t* __restrict__ inv_pos,
+    const float* __restrict__ dlogits, const void* __restrict__ w_router, void* __restrict__ dx,
+    int64_t n_tokens, int d, int topk, int n_experts) {
+  const int cpr = d / 8;
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n_tokens * cpr) return;
+  const int64_t t = i / cpr;
+  const int c0 = int(i - t * cpr) * 8;
+  float acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+  for (int s = 0; s < topk; ++s) {
+    const int32_t p = inv_pos[t * topk + s];
+    if (p < 0) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(dxp + int64_t(p) * d + c0);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      acc[2 * j] += bf_lo(vv[j]);
+      acc[2 * j + 1] += bf_hi(vv[j]);
+    }
+  }
+  for (int e = 0; e < n_experts; ++e) {
+    const float g = dlogits[t * n_experts + e];
+    float wv[8];
+    if constexpr (OUT_F32) {
+      const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(w_router) +
+                                                        int64_t(e) * d + c0);
+      const float4 a = q[0], b = q[1];
+      wv[0] = a.x, wv[1] = a.y, wv[2] = a.z, wv[3] = a.w;
+      wv[4] = b.x, wv[5] = b.y, wv[6] = b.z, wv[7] = b.w;
+    } else {
+      const uint4 v = *reinterpret_cast<const uint4*>(static_cast<const uint16_t*>(w_router) +
+                                                      int64_t(e) * d + c0);
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        wv[2 * j] = bf_lo(vv[j]);
+        wv[2 * j + 1] = bf_hi(vv[j]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(g, wv[j], acc[j]);
+  }
+  if constexpr (OUT_F32) {
+    float4* o = reinterpret_cast<float4*>(static_cast<float*>(dx) + t * d + c0);
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+  } else {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(dx) + t * d + c0) =
+        make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                   pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
+  }
+}
+
+// W [E, R, C] -> WT [E, C, R] (bf16), 64 x 64 tiles through LDS; R and C are
+// multiples of 64.
+__global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restrict__ w,
+                                                        uint16_t* __restrict__ wt, int R,
+                                                        int C) {
+  __shared__ uint16_t tile[64][66];
+  const int e = blockIdx.z;
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const uint16_t* src = w + int64_t(e) * R * C;
+  uint16_t* dst = wt + int64_t(e) * R * C;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;
+    tile[r][tx] = src[int64_t(r0 + r) * C + c0 + tx];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = ty + 4 * i;
+    dst[int64_t(c0 + c) * R + r0 + tx] = tile[tx][c];
+  }
+}
+
+}  // namespace
+
+hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const int32_t* inv_pos,
+                            const float* topk_w, float* dw, uint16_t* dyp,
+                            const g5moe_shape& s, hipStream_t st) {
+  const int64_t nk = s.n_tokens * s.top_k;
+  if (nk == 0) return hipSuccess;
+  const unsigned grid = unsigned((nk + 3) / 4);
+  switch (s.d_model / 64) {
+#define G5_GG(LL)                                                                          \
+  case LL:                                                                                 \
+    hipLaunchKernelGGL(gate_grad_kernel<LL>, dim3(grid), dim3(256), 0, st, dy, y_perm,    \
+                       inv_pos, topk_w, dw, dyp, nk, s.top_k);                             \
+    break;
+    G5_GG(2)
+    G5_GG(4)
+    G5_GG(8)
+    G5_GG(12)
+#undef G5_GG
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
+                              const float* grad_logits, float* dlogits, const g5moe_shape& s,
+                              hipStream_t st) {
+  if (s.n_tokens == 0) return hipSuccess;
+  hipLaunchKernelGGL(router_grad_kernel, dim3(unsigned((s.n_tokens + 255) / 256)), dim3(256),
+                     0, st, dw, topk_w, topk_idx, grad_logits, dlogits, s.n_tokens,
+                     s.n_experts, s.top_k);
+  return hipGetLastError();
+}
+
+hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, uint16_t* dgu,
+                             uint16_t* h, const g5moe_shape& s, hipStream_t st) {
+  const int64_t rows = s.n_tokens * s.top_k;
+  const int64_t work = rows * (s.d_ff / 8);
+  if (work == 0) return hipSuccess;
+  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, st,
+                     dh, gu, dgu, h, rows, s.d_ff);
+  return hipGetLastError();
+}
+
+hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const float* dlogits,
+                             const void* w_router, void* dx, const g5moe_shape& s,
+                             hipStream_t st) {
+  const int64_t work = s.n_tokens * (s.d_model / 8);
+  if (work == 0) return hipSuccess;
+  const unsigned grid = unsigned((work + 255) / 256);
+  if (s.x_dtype == G5MOE_DTYPE_F32)
+    hipLaunchKernelGGL(input_grad_kernel<true>, dim3(grid), dim3(256), 0, st, dxp, inv_pos,
+                       dlogits, w_router, dx, s.n_tokens, s.d_model, s.top_k, s.n_experts);
+  else
+    hipLaunchKernelGGL(input_grad_kernel<false>, dim3(grid), dim3(256), 0, st, dxp, inv_pos,
+                       dlogits, w_router, dx, s.n_tokens, s.d_model, s.top_k, s.n_experts);
+  return hipGetLastError();
+}
+
+hipError_t launch_transpose_experts(const uint16_t* w, uint16_t* wt, int E, int R, int C,
+                                    hipStream_t st) {
+  if (E == 0 || R == 0 || C == 0) return hipSuccess;
+  if (R % 64 != 0 || C % 64 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(transpose_kernel, dim3(unsigned(C / 64), unsigned(R / 64), unsigned(E)),
+                     dim3(256), 0, st, w, wt, R, C);
+  return hipGetLastError();
+}
+
+}  // namespace g5moe

@@ -69,6 +69,25 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
                           hipStream_t st);
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
+                              const uint16_t* wgu, uint16_t* gu, const g5moe_shape& s,
+                              hipStream_t st);
+hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
+                             uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
+                             hipStream_t st);
+hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const int32_t* inv_pos,
+                            const float* topk_w, float* dw, uint16_t* dyp,
+                            const g5moe_shape& s, hipStream_t st);
+hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
+                              const float* grad_logits, float* dlogits, const g5moe_shape& s,
+                              hipStream_t st);
+hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, uint16_t* dgu,
+                             uint16_t* h, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const float* dlogits,
+                             const void* w_router, void* dx, const g5moe_shape& s,
+                             hipStream_t st);
+hipError_t launch_transpose_experts(const uint16_t* w, uint16_t* wt, int E, int R, int C,
+                                    hipStream_t st);
 hipError_t launch_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,
                           void* y, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_pack_gate_up(const uint16_t* wg, const uint16_t* wu, uint16_t* wgu,

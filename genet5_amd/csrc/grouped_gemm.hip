@@ -166,7 +166,10 @@ constexpr int persist_smem_bytes() {
 
 // One pass of the persistent tile loop over the units `un` (BN = BNF for full
 // tiles, BNF / 2 for half tiles, decoded in the full-tile numbering).
-template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, bool SWIGLU, bool HALF>
+// MODE: 0 = A rows in place (down, and the backward GEMMs), 1 = gathered x
+// rows with the SwiGLU epilogue (gate|up), 2 = gathered x rows, raw outputs
+// (the gate|up recompute of the backward).
+template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF>
 __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, const Units un) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int MB = WTM / 32, NB = WTN / 32;
@@ -191,6 +194,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   static_assert(HALF ? 2 * BN == BNF : BN == BNF, "tile width");
   static_assert(S >= 2 && S * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
   static_assert((S - 2) * PER < 64, "vmcnt range");
+  constexpr bool SWIGLU = MODE == 1;
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
   // Fragment f of the next substeps is read after the f-th MFMA of a substep,
   // so a substep must hold at least as many MFMAs as fragments.
@@ -200,9 +204,9 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   static_assert((AI * RPB / G) % CPR == 0 && (BI * RPB / G) % CPR == 0 &&
                     (2 * RPB / G) % CPR == 0,
                 "slot swizzle period");
-  // The gate|up GEMM gathers token rows through perm; the down GEMM reads the
-  // expert-contiguous h rows in place.
-  constexpr bool GATHER = SWIGLU;
+  // The gate|up GEMMs gather token rows through perm; the others read the
+  // expert-contiguous A rows in place.
+  constexpr bool GATHER = MODE != 0;
   auto decode_unit = [&](int i, TileCoord& tc) {
     const int h = un.first + i * un.stride;
     if constexpr (HALF) {
@@ -558,7 +562,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
 // dominated by its A rows and its MFMAs scale with its width, so a half takes
 // about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
 // the gate|up GEMM (K = 768), which therefore keeps whole tiles.
-template <int BM, int BN, int BK, int S, int NSLOT, int GM, bool SWIGLU, bool HALF_TAIL>
+template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL>
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
   const int ntn = args.Nout / BN;
@@ -577,20 +581,20 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   const int q = (hi - lo) / nslot, r = (hi - lo) % nslot;
   if constexpr (HALF_TAIL) {
     if (q > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, SWIGLU, false>(args, smem,
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, smem,
                                                            Units{lo + slot, nslot, q, 0});
     if (slot < 2 * r) {
       // every wave's DMAs of the full pass have landed (each waited for its
       // own) before the half pass refills the stage buffers
       if (q > 0) __syncthreads();
-      tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, SWIGLU, true>(
+      tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, MODE, true>(
           args, smem, Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
     }
   } else {
     // one pass: the remainder tile of slots s < r is lo + s + q * nslot
     const int cnt = q + (slot < r ? 1 : 0);
     if (cnt > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, SWIGLU, false>(args, smem,
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, smem,
                                                            Units{lo + slot, nslot, cnt, 0});
   }
 }
@@ -667,14 +671,14 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #endif
 
 // Persistent launch: three fragment slots when the k-step count allows it.
-template <int BM, int BN, int BK, int S, int GM, bool SWIGLU, bool HALF_TAIL>
+template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL>
 void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
   const int nk = a.K / BK;
   if (nk % 3 == 0 && nk >= 6)
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, SWIGLU, HALF_TAIL>),
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, MODE, HALF_TAIL>),
                        dim3(grid), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, SWIGLU, HALF_TAIL>),
+    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, MODE, HALF_TAIL>),
                        dim3(grid), dim3(256), 0, st, a);
 }
 
@@ -699,7 +703,7 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, true, false>(pgrid, a, st);
+  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);
   return hipGetLastError();
 }
 
@@ -722,10 +726,60 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   const unsigned ncu = unsigned(device_cu_count());
   if (a.Nout % 256 == 0) {
     const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout), ncu);
-    launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false, true>(grid, a, st);
+    launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, true>(grid, a, st);
   } else {
     const unsigned grid = std::min(grid_bound<256, 128>(nk, s.n_experts, a.Nout), ncu);
-    launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, false, false>(grid, a, st);
+    launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
+                              const uint16_t* wgu, uint16_t* gu, const g5moe_shape& s,
+                              hipStream_t st) {
+  const int64_t nk = s.n_tokens * s.top_k;
+  if (nk == 0) return hipSuccess;
+  GemmArgs a{};
+  a.A = xb;
+  a.perm = perm;
+  a.offsets = offsets;
+  a.B = wgu;
+  a.C = gu;
+  a.topk = s.top_k;
+  a.n_experts = s.n_experts;
+  a.K = s.d_model;
+  a.Nout = 2 * s.d_ff;
+  a.ldc = 2 * s.d_ff;
+  if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
+  const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout),
+                                 unsigned(device_cu_count()));
+  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 2, false>(grid, a, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
+                             uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
+                             hipStream_t st) {
+  if (rows == 0) return hipSuccess;
+  if (K % 64 != 0 || K < 128 || Nout % 128 != 0) return hipErrorInvalidValue;
+  GemmArgs a{};
+  a.A = A;
+  a.perm = nullptr;
+  a.offsets = offsets;
+  a.B = B;
+  a.C = C;
+  a.topk = 1;
+  a.n_experts = n_experts;
+  a.K = K;
+  a.Nout = Nout;
+  a.ldc = Nout;
+  const unsigned ncu = unsigned(device_cu_count());
+  if (Nout % 256 == 0) {
+    const unsigned grid = std::min(grid_bound<256, 256>(rows, n_experts, Nout), ncu);
+    launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, true>(grid, a, st);
+  } else {
+    const unsigned grid = std::min(grid_bound<256, 128>(rows, n_experts, Nout), ncu);
+    launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);
   }
   return hipGetLastError();
 }

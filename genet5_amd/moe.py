@@ -24,7 +24,7 @@ weight changes.
 from __future__ import annotations
 
 import math
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -56,11 +56,61 @@ def _(w_gate, w_up):
 
 def _no_backward(ctx, grad):
     raise NotImplementedError(
-        "g5moe::moe_forward is forward-only (no MoE backward is built); run the layer "
-        "under torch.no_grad() / inference_mode or detach its inputs")
+        "g5moe::moe_forward is the inference op; MoEFeedForward runs "
+        "g5moe::moe_forward_train (which has a backward) whenever gradients are needed")
 
 
 _moe_forward_op.register_autograd(_no_backward)
+
+
+def _pack_backward(ctx, grad):
+    return ops.unpack_gate_up(grad.contiguous())
+
+
+_pack_gate_up_op.register_autograd(_pack_backward)
+
+
+@torch.library.custom_op("g5moe::moe_forward_train", mutates_args=())
+def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
+                          w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int
+                          ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                     torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+    return tuple(t.contiguous() for t in
+                 ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias))
+
+
+@_moe_forward_train_op.register_fake
+def _(x, w_router, bias, w_gate_up, w_down, top_k):
+    N, d = x.shape
+    E = w_router.shape[0]
+    i32 = dict(dtype=torch.int32, device=x.device)
+    f32 = dict(dtype=torch.float32, device=x.device)
+    return (torch.empty_like(x), torch.empty((N, E), **f32), torch.empty((N, top_k), **i32),
+            torch.empty((N, top_k), **f32), torch.empty((E + 1,), **i32),
+            torch.empty((N * top_k,), **i32), torch.empty((N * top_k,), **i32),
+            torch.empty((N * top_k, d), dtype=torch.bfloat16, device=x.device))
+
+
+def _train_setup(ctx, inputs, output):
+    x, w_router, bias, w_gate_up, w_down, top_k = inputs
+    _, _, idx, w, offsets, perm, inv_pos, y_perm = output
+    ctx.top_k = top_k
+    ctx.save_for_backward(x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm)
+    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm)
+
+
+def _train_backward(ctx, dy, dlogits, *unused):
+    x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm = ctx.saved_tensors
+    if dy is None:
+        dy = torch.zeros_like(x)
+    dx, d_wr, d_wgu, d_wd = ops.moe_backward(
+        dy.to(torch.bfloat16).contiguous(), x, w_router, w_gate_up, w_down, ctx.top_k, idx, w,
+        offsets, perm, inv_pos, y_perm,
+        grad_logits=None if dlogits is None else dlogits.float().contiguous())
+    return dx, d_wr, None, d_wgu, d_wd, None
+
+
+_moe_forward_train_op.register_autograd(_train_backward, setup_context=_train_setup)
 
 
 class MoEFeedForward(nn.Module):
@@ -97,6 +147,10 @@ class MoEFeedForward(nn.Module):
         self.reset_parameters()
         self._packed_key = None
         self._packed = None
+        # Switch-style load-balancing loss weight (0 = off); the loss of the last
+        # differentiable forward is left in self.aux_loss.
+        self.aux_loss_coef = 0.0
+        self.aux_loss = None
 
     def reset_parameters(self) -> None:
         # nn.Linear's default init, per expert matrix.
@@ -131,11 +185,16 @@ class MoEFeedForward(nn.Module):
             self._packed_key = key
         return self._packed
 
+    def _needs_grad(self, x: torch.Tensor) -> bool:
+        return torch.is_grad_enabled() and (
+            x.requires_grad or any(p.requires_grad for p in
+                                   (self.router.weight, self.w_gate, self.w_up, self.w_down)))
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.training and self.dropout > 0.0:
             raise NotImplementedError(
-                "MoEFeedForward is forward-only: dropout on the expert hidden state in "
-                "training mode is not implemented")
+                "MoEFeedForward has no dropout on the expert hidden state; construct it "
+                "with dropout=0.0 for training")
         if x.shape[-1] != self.embed_dim:
             raise ValueError(f"last dim {x.shape[-1]} != embed_dim {self.embed_dim}")
         lead = x.shape[:-1]
@@ -145,9 +204,33 @@ class MoEFeedForward(nn.Module):
         w_router = self.router.weight
         if w_router.dtype != x2.dtype:
             w_router = w_router.to(x2.dtype)
+        if self._needs_grad(x2):
+            return self._forward_train(x2, w_router.contiguous()).view(*lead, self.embed_dim)
         wgu, wd = self._expert_weights()
         y = _moe_forward_op(x2, w_router.contiguous(), self.router_bias, wgu, wd, self.top_k)
         return y.view(*lead, self.embed_dim)
+
+    def _forward_train(self, x2: torch.Tensor, w_router: torch.Tensor) -> torch.Tensor:
+        """Differentiable forward (bf16 activations).  The expert weights are packed
+        through the differentiable packing op so their gradients reach w_gate and
+        w_up.  With aux_loss_coef > 0 the Switch-style load-balancing loss
+        coef * E * sum_e f_e * P_e (f_e: share of assignments routed to e, P_e:
+        mean softmax probability of e) is left in self.aux_loss for the caller
+        to add to its loss (the module's output stays one tensor)."""
+        if x2.dtype != torch.bfloat16:
+            raise TypeError("MoEFeedForward trains on bf16 activations (the model's autocast "
+                            "dtype); got " + str(x2.dtype))
+        wgu = _pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16))
+        wd = self.w_down.to(torch.bfloat16)
+        y, logits, idx, _, offsets, _, _, _ = _moe_forward_train_op(
+            x2, w_router, self.router_bias, wgu, wd.contiguous(), self.top_k)
+        self.aux_loss = None
+        if self.aux_loss_coef > 0:
+            counts = (offsets[1:] - offsets[:-1]).float()
+            f = counts / max(1, idx.numel())
+            p_mean = torch.softmax(logits, dim=-1).mean(dim=0)
+            self.aux_loss = self.aux_loss_coef * self.num_experts * (f * p_mean).sum()
+        return y
 
     def residual_block(self, residual: torch.Tensor, norm_weight: torch.Tensor,
                        eps: float = 1e-6, x_add: Optional[torch.Tensor] = None,

@@ -283,3 +283,123 @@ def moe_forward(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tens
               _ptr(r.offsets), _ptr(r.perm), _ptr(r.inv_pos), _ptr(buffers.ws),
               ctypes.byref(buffers.shape), _stream(dev))
     return (buffers.y, r) if return_routing else buffers.y
+
+
+# ---- training: forward that keeps what the backward needs, and the backward -----------
+
+ROW_PAD = 256  # padding rows of buffers read as the A operand of the grouped GEMM
+
+
+def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
+                      w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None):
+    """The layer forward as stage calls, returning what the backward needs:
+    (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm)."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E, F2, _ = w_gate_up.shape
+    idx, w, logits = router_topk(x2d, w_router, top_k, bias=bias, return_logits=True)
+    _, offsets, perm, inv_pos = dispatch(idx, E, d)
+    y_perm = expert_swiglu(x2d, perm, offsets, w_gate_up, w_down, top_k)
+    y = combine(y_perm, inv_pos, w, x2d.dtype)
+    return y, logits, idx, w, offsets, perm, inv_pos, y_perm
+
+
+def transpose_experts(w: torch.Tensor) -> torch.Tensor:
+    """bf16 [E, R, C] -> [E, C, R]."""
+    dev = _check_device(w)
+    E, R, C = w.shape
+    _require(w, "w", (E, R, C), torch.bfloat16, dev)
+    out = torch.empty((E, C, R), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_transpose_experts", _ptr(w), _ptr(out), E, R, C, _stream(dev))
+    return out
+
+
+def grouped_gemm(a_padded: torch.Tensor, rows: int, offsets: torch.Tensor,
+                 b: torch.Tensor) -> torch.Tensor:
+    """c[p] = a[p] . b_e^T over expert-contiguous rows; a carries ROW_PAD padding rows."""
+    dev = _check_device(a_padded)
+    E, n_out, K = b.shape
+    _require(a_padded, "a", (rows + ROW_PAD, K), torch.bfloat16, dev)
+    _require(b, "b", (E, n_out, K), torch.bfloat16, dev)
+    _require(offsets, "offsets", (E + 1,), torch.int32, dev)
+    c = torch.empty((rows, n_out), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_grouped_gemm", _ptr(a_padded), _ptr(offsets), _ptr(b), _ptr(c), rows, K,
+              n_out, E, _stream(dev))
+    return c
+
+
+def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
+                 w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int,
+                 topk_idx: torch.Tensor, topk_w: torch.Tensor, offsets: torch.Tensor,
+                 perm: torch.Tensor, inv_pos: torch.Tensor, y_perm: torch.Tensor,
+                 grad_logits: Optional[torch.Tensor] = None, w_down_t: Optional[torch.Tensor] = None,
+                 w_gate_up_t: Optional[torch.Tensor] = None):
+    """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer.
+
+    HIP stages: gate gradient and dY (g5moe_gate_grad), router-logit gradient
+    (g5moe_router_grad, plus grad_logits), the gate|up recompute
+    (g5moe_expert_gate_up_raw), dh = dY Wd_e (g5moe_grouped_gemm on Wd^T),
+    SwiGLU backward (g5moe_swiglu_backward), dX_perm = dGU Wgu_e (g5moe_grouped_gemm
+    on the packed gate|up's transpose) and dx (g5moe_input_grad).  The weight
+    gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e and dWr = dlogits^T x are
+    plain GEMMs (torch / hipBLASLt), which read the expert row ranges on the host."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E, F2, _ = w_gate_up.shape
+    F = F2 // 2
+    k = top_k
+    if x2d.dtype != torch.bfloat16:
+        raise TypeError("the MoE backward takes bf16 activations")
+    _require(dy, "dy", (N, d), torch.bfloat16, dev)
+    _require(y_perm, "y_perm", (N * k, d), torch.bfloat16, dev)
+    shape = _lib.make_shape(N, d, F, E, k, _lib.DTYPE_BF16)
+    S = _stream(dev)
+    dw = torch.empty((N, k), dtype=torch.float32, device=dev)
+    dyp = torch.empty((N * k + ROW_PAD, d), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_gate_grad", _ptr(dy), _ptr(y_perm), _ptr(inv_pos), _ptr(topk_w), _ptr(dw),
+              _ptr(dyp), ctypes.byref(shape), S)
+    if grad_logits is not None:
+        _require(grad_logits, "grad_logits", (N, E), torch.float32, dev)
+    dlogits = torch.empty((N, E), dtype=torch.float32, device=dev)
+    _lib.call("g5moe_router_grad", _ptr(dw), _ptr(topk_w), _ptr(topk_idx), _ptr(grad_logits),
+              _ptr(dlogits), ctypes.byref(shape), S)
+    gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
+    ws = workspace(shape, dev)
+    _lib.call("g5moe_expert_gate_up_raw", _ptr(x2d), _ptr(perm), _ptr(offsets), _ptr(w_gate_up),
+              _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
+    del ws
+    if w_down_t is None:
+        w_down_t = transpose_experts(w_down)            # [E, F, d]
+    dh = grouped_gemm(dyp, N * k, offsets, w_down_t)    # [N*k, F]
+    dgu = torch.empty((N * k + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
+    h = torch.empty((N * k, F), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(dgu), _ptr(h),
+              ctypes.byref(shape), S)
+    del dh, gu
+    if w_gate_up_t is None:
+        w_gate_up_t = transpose_experts(w_gate_up)      # [E, d, 2F]
+    dxp = grouped_gemm(dgu, N * k, offsets, w_gate_up_t)  # [N*k, d]
+    dx = torch.empty((N, d), dtype=x2d.dtype, device=dev)
+    _require(w_router, "w_router", (E, d), x2d.dtype, dev)
+    _lib.call("g5moe_input_grad", _ptr(dxp), _ptr(inv_pos), _ptr(dlogits), _ptr(w_router),
+              _ptr(dx), ctypes.byref(shape), S)
+    del dxp
+    # weight gradients: per-expert TN products over the expert's rows
+    xperm = x2d.index_select(0, (perm // k).long())
+    d_wd = torch.zeros((E, d, F), dtype=torch.bfloat16, device=dev)
+    d_wgu = torch.zeros((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
+    offs = offsets.tolist()
+    for e in range(E):
+        o0, o1 = offs[e], offs[e + 1]
+        if o1 > o0:
+            torch.matmul(dyp[o0:o1].t(), h[o0:o1], out=d_wd[e])
+            torch.matmul(dgu[o0:o1].t(), xperm[o0:o1], out=d_wgu[e])
+    d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
+    return dx, d_wr, d_wgu, d_wd
+
+
+def unpack_gate_up(w_gate_up: torch.Tensor):
+    """Inverse of pack_gate_up: packed [E, 2F, d] -> (gate [E, F, d], up [E, F, d])."""
+    E, F2, d = w_gate_up.shape
+    v = w_gate_up.view(E, F2 // 64, 2, 32, d)
+    return v[:, :, 0].reshape(E, F2 // 2, d), v[:, :, 1].reshape(E, F2 // 2, d)

@@ -179,6 +179,72 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
                                     const float* topk_w, const void* residual, float alpha,
                                     void* out, const g5moe_shape* shape, void* stream);
 
+/* ---- Backward ---------------------------------------------------------------
+ * The MoE layer's backward, stage by stage.  The reference trains its dense
+ * FeedForward through autograd (lib/blocks/_component.py:48-52; loss.backward()
+ * at train/diffusion_finet:761); the MoE and its backward are new.  The
+ * weight-gradient products (dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e) are plain
+ * per-expert GEMMs left to the caller (hipBLASLt); everything else is here.
+ * Activations are bf16 (x_dtype must be BF16), gradients of the routing fp32.
+ * A row count "+ 256" means the buffer carries 256 rows of padding after its
+ * last row: g5moe_grouped_gemm reads whole 256-row tiles of its A operand. */
+
+/* W [E, rows, cols] bf16 -> W^T [E, cols, rows] (per-expert transpose; the
+ * backward's products need Wd^T [E, F, d] and the packed gate|up's transpose
+ * [E, d, 2F]).  rows and cols are multiples of 64. */
+g5moe_status g5moe_transpose_experts(const void* w, void* w_t, int32_t n_experts, int32_t rows,
+                                     int32_t cols, void* stream);
+
+/* Grouped product over expert-contiguous rows: for sorted position p of expert
+ * e (offsets[e] <= p < offsets[e+1]), c[p] = a[p] . b_e^T, fp32 accumulate,
+ * bf16 out.  a : bf16 [rows + 256, k];  b : bf16 [E, n_out, k];
+ * c : bf16 [rows, n_out].  k multiple of 64, >= 128; n_out multiple of 128.
+ * (The kernel of g5moe_expert_down.) */
+g5moe_status g5moe_grouped_gemm(const void* a, const int32_t* offsets, const void* b, void* c,
+                                int64_t rows, int32_t k, int32_t n_out, int32_t n_experts,
+                                void* stream);
+
+/* Gate gradient and the scaled output gradient in sorted order:
+ *   dw[t, s] = dy[t] . y_perm[inv_pos[t, s]]   (fp32; per lane c an fma chain
+ *              over columns [c*d/64, (c+1)*d/64), lanes added over bits 5..0)
+ *   dy_perm[inv_pos[t, s]] = bf16(topk_w[t, s] * dy[t])
+ *   dy : bf16 [N, d];  y_perm : bf16 [N*k, d] (the forward's expert outputs);
+ *   dw : fp32 [N, k] out;  dy_perm : bf16 [N*k + 256, d] out. */
+g5moe_status g5moe_gate_grad(const void* dy, const void* y_perm, const int32_t* inv_pos,
+                             const float* topk_w, float* dw, void* dy_perm,
+                             const g5moe_shape* shape, void* stream);
+
+/* Router-logit gradient through the renormalised top-k softmax:
+ *   dlogits[t, i_r] = w_r * (dw_r - sum_s w_s dw_s) for the chosen experts,
+ *   0 for the others, plus grad_logits[t, e] (an extra gradient on the logits,
+ *   e.g. from a load-balancing loss; NULL = none).  fp32 [N, E] out. */
+g5moe_status g5moe_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
+                               const float* grad_logits, float* dlogits,
+                               const g5moe_shape* shape, void* stream);
+
+/* The gate|up product without the activation (the backward recomputes it):
+ * gu[p] = x[perm[p] / k] . Wgu_e^T, bf16 [N*k, 2F] in the packed gate|up
+ * column order (32 gate columns, then the matching 32 up columns). */
+g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const int32_t* offsets,
+                                      const void* w_gate_up, void* gu, void* ws,
+                                      const g5moe_shape* shape, void* stream);
+
+/* SwiGLU backward (the derivative of LigerSiLUMulFunction's silu(a) * b,
+ * lib/blocks/_component.py:31, :50): with s = 1 / (1 + exp(-g)),
+ *   dg = dh * u * s * (1 + g * (1 - s)),  du = dh * g * s,  h = g * s * u
+ * (h recomputed for the down weight gradient).  dh : bf16 [N*k, F];
+ * gu : bf16 [N*k, 2F] packed;  dgu : bf16 [N*k + 256, 2F] packed out;
+ * h : bf16 [N*k, F] out. */
+g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, void* dgu, void* h,
+                                   const g5moe_shape* shape, void* stream);
+
+/* Input gradient: dx[t] = sum over s of dx_perm[inv_pos[t, s]] (slot order)
+ * + sum over e of dlogits[t, e] * w_router[e] (expert order), fp32, one
+ * rounding.  dx_perm : bf16 [N*k, d];  w_router, dx : [E, d], [N, d] in x_dtype. */
+g5moe_status g5moe_input_grad(const void* dx_perm, const int32_t* inv_pos, const float* dlogits,
+                              const void* w_router, void* dx, const g5moe_shape* shape,
+                              void* stream);
+
 /* The whole layer forward, enqueued as router -> dispatch -> gate|up ->
  * down -> combine.  Replaces FeedForward.forward (lib/blocks/_component.py:48-52)
  * when the module is the MoE.  Routing outputs are written to the caller's

@@ -19,6 +19,7 @@ from .moe_oracle import (  # noqa: F401
     dispatch,
     dispatch_c,
     expert_forward,
+    moe_backward,
     moe_forward,
     router_logits,
     router_logits_np,

@@ -45,6 +45,14 @@ combine_c
     `hidden_states + ff_output * alpha` (lib/blocks/encoder.py:89).  Pins:
     exact-rational fma restatement; k = 1, w = 1 returns y_perm bit for bit;
     the residual composition equals torch's own bf16 ops (CPU) on y_moe.
+moe_backward
+    Float64 textbook backward of the layer for fixed routing indices: gate
+    gradient dw = dy . Y, dY = w dy, dh = dY Wd_e, SwiGLU derivative
+    dg = dh u s (1 + g (1 - s)), du = dh g s, dx = dg Wg_e + du Wu_e + dlogits Wr,
+    dlogits through the renormalised top-k softmax w_r (dw_r - sum w dw), weight
+    gradients as outer products.  Pins: central finite differences of a
+    scalar loss in random directions (float64), and torch.autograd in float64
+    on a torch restatement of the same forward.
 add_rmsnorm / add_rmsnorm_np
     s = T(x + r); ss = sum s^2 in the router's lane/tree order; rstd =
     1 / sqrt(ss / d + eps); normed = T((s * rstd) * w) — fused_add_rmsnorm /
@@ -381,3 +389,65 @@ def combine_c(y_perm_bits: np.ndarray, inv_pos: np.ndarray, topk_w: np.ndarray,
                            _p(out)) != 0:
         raise ValueError("bad dtype")
     return out
+
+
+# ---- backward ----------------------------------------------------------------------
+
+def moe_backward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray,
+                 w_down: np.ndarray, topk_idx: np.ndarray, dy: np.ndarray,
+                 grad_logits: Optional[np.ndarray] = None,
+                 bias: Optional[np.ndarray] = None) -> dict:
+    """Textbook float64 backward of the layer for the routing indices topk_idx
+    (the top-k choice is piecewise constant in the logits, so it carries no
+    gradient).  Forward: logits = x Wr^T (+ b); w = softmax over the chosen
+    logits; per assignment (t, s) with e = topk_idx[t, s]:
+    h = silu(x Wg_e^T) * (x Wu_e^T), Y = h Wd_e^T; y[t] = sum_s w[t, s] Y[t, s]
+    (FeedForward.forward, lib/blocks/_component.py:48-52, per expert).  The loss
+    is L(y, logits) with dL/dy = dy and an optional dL/dlogits = grad_logits.
+    Inputs: float arrays or uint16 bf16 bits (widened).  Returns dict with dx,
+    d_w_router, d_w_gate, d_w_up, d_w_down, dlogits, dw, y."""
+    f = lambda a: widen(a).astype(np.float64)
+    X, Wr, Wg, Wu, Wd, DY = f(x), f(w_router), f(w_gate), f(w_up), f(w_down), f(dy)
+    N, d = X.shape
+    E, F = Wg.shape[0], Wg.shape[1]
+    idx = np.asarray(topk_idx, np.int64)
+    k = idx.shape[1]
+    logits = X @ Wr.T
+    if bias is not None:
+        logits = logits + np.asarray(bias, np.float64)[None, :]
+    ls = np.take_along_axis(logits, idx, axis=1)
+    ls = ls - ls.max(axis=1, keepdims=True)
+    w = np.exp(ls) / np.exp(ls).sum(axis=1, keepdims=True)
+    dx = np.zeros_like(X)
+    dwg, dwu, dwd = np.zeros_like(Wg), np.zeros_like(Wu), np.zeros_like(Wd)
+    dw = np.zeros((N, k))
+    y = np.zeros_like(X)
+    for s in range(k):
+        for e in range(E):
+            rows = np.nonzero(idx[:, s] == e)[0]
+            if rows.size == 0:
+                continue
+            xe = X[rows]
+            g, u = xe @ Wg[e].T, xe @ Wu[e].T
+            sg = 1.0 / (1.0 + np.exp(-g))
+            h = g * sg * u
+            Y = h @ Wd[e].T
+            we = w[rows, s:s + 1]
+            y[rows] += we * Y
+            dw[rows, s] = (DY[rows] * Y).sum(axis=1)
+            dY = we * DY[rows]
+            dwd[e] += dY.T @ h
+            dh = dY @ Wd[e]
+            dg = dh * u * sg * (1.0 + g * (1.0 - sg))
+            du = dh * g * sg
+            dwg[e] += dg.T @ xe
+            dwu[e] += du.T @ xe
+            dx[rows] += dg @ Wg[e] + du @ Wu[e]
+    dl_sel = w * (dw - (w * dw).sum(axis=1, keepdims=True))
+    dlogits = np.zeros((N, E))
+    np.put_along_axis(dlogits, idx, dl_sel, axis=1)
+    if grad_logits is not None:
+        dlogits = dlogits + np.asarray(grad_logits, np.float64)
+    dx += dlogits @ Wr
+    return dict(dx=dx, d_w_router=dlogits.T @ X, d_w_gate=dwg, d_w_up=dwu, d_w_down=dwd,
+                dlogits=dlogits, dw=dw, y=y)

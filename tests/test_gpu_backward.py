@@ -1,0 +1,141 @@
+"""GPU backward of the MoE layer (through the C ABI and the module's autograd)
+against the float64 oracle backward (oracle.moe_backward, pinned by finite
+differences and float64 torch autograd).
+
+Exact where the contract fixes the arithmetic: dy_perm = bf16(w * dy) bit for bit,
+and the gate gradient dw (bf16 x bf16 products are exact in fp32, so the lane
+chain and tree order reproduce in numpy).  Everything downstream passes through
+bf16 buffers (dY, dh, dGU, h, dX_perm, bf16 weight gradients), so the gradients are
+checked normwise against float64: max|err| / max|ref| <= 1.5e-2 and
+mean|err| / mean|ref| <= 6e-3, about twice the measured error (max 7e-3, mean
+4e-3 at d = 768, F = 3072, E = 16, N = 2048; printed by each test)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import moe_oracle as mo
+from genet5_amd import ops, synth
+from genet5_amd.moe import MoEFeedForward
+from test_gpu_parity import dev_t, host, layer_tensors
+
+pytestmark = pytest.mark.gpu
+
+MAX_REL = 1.5e-2
+MEAN_REL = 6e-3
+
+
+def normwise(got, ref):
+    err = np.abs(np.asarray(got, np.float64) - np.asarray(ref, np.float64))
+    r = np.abs(np.asarray(ref, np.float64))
+    return err.max() / max(r.max(), 1e-30), err.mean() / max(r.mean(), 1e-30)
+
+
+def check(name, got, ref):
+    mx, mean = normwise(got, ref)
+    print(f"  {name}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+    assert mx <= MAX_REL and mean <= MEAN_REL, (name, mx, mean)
+
+
+@pytest.mark.parametrize("n,d,F,E,k", [
+    (2048, 768, 3072, 16, 2),
+    (700, 256, 512, 8, 2),
+    (333, 512, 384, 4, 3),
+])
+def test_backward_stages_vs_oracle(cuda_device, n, d, F, E, k):
+    print(f"backward n={n} d={d} F={F} E={E} k={k}", flush=True)
+    inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=21, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    rng = np.random.default_rng(5)
+    dy_np = synth.f32_to_bf16_bits(rng.standard_normal((n, d)).astype(np.float32))
+    dy = dev_t(dy_np, cuda_device, True)
+    y, logits, idx, w, offsets, perm, inv_pos, y_perm = ops.moe_forward_train(x, wr, wgu, wd, k)
+    torch.cuda.synchronize()
+    ref_i, _ = oracle.topk_gates_c(oracle.router_logits(inp.x, inp.w_router), k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_i)
+
+    # gate gradient: dy_perm exact, dw in the contract's order (exact products)
+    dw = torch.empty((n, k), dtype=torch.float32, device=cuda_device)
+    dyp = torch.empty((n * k + ops.ROW_PAD, d), dtype=torch.bfloat16, device=cuda_device)
+    from genet5_amd import _lib
+    import ctypes
+    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
+    _lib.call("g5moe_gate_grad", ops._ptr(dy), ops._ptr(y_perm), ops._ptr(inv_pos),
+              ops._ptr(w), ops._ptr(dw), ops._ptr(dyp), ctypes.byref(shape),
+              ops._stream(cuda_device))
+    torch.cuda.synchronize()
+    ip = inv_pos.cpu().numpy().reshape(n, k)
+    wn = w.cpu().numpy()
+    dyf = mo.bf16_to_f32(dy_np)
+    exp_dyp = mo.round_bf16(wn[:, :, None] * dyf[:, None, :])
+    got_dyp = host(dyp[: n * k])
+    np.testing.assert_array_equal(got_dyp[ip.reshape(-1)], exp_dyp.reshape(n * k, d))
+    yp = host(y_perm)[ip.reshape(-1)].reshape(n, k, d)
+    L = d // 64
+    prod = (dyf[:, None, :] * yp).reshape(n, k, 64, L)   # exact in fp32
+    acc = np.zeros((n, k, 64), np.float32)
+    for i in range(L):
+        acc = acc + prod[..., i]
+    m = 32
+    while m >= 1:
+        acc = acc[..., :m] + acc[..., m:2 * m]
+        m //= 2
+    np.testing.assert_array_equal(dw.cpu().numpy().view(np.uint32), acc[..., 0].view(np.uint32))
+
+    dx, d_wr, d_wgu, d_wd = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm,
+                                             inv_pos, y_perm)
+    torch.cuda.synchronize()
+    ref = oracle.moe_backward(inp.x, inp.w_router, inp.w_gate, inp.w_up, inp.w_down, ref_i, dy_np)
+    d_wg, d_wu = ops.unpack_gate_up(d_wgu)
+    check("dx", host(dx), ref["dx"])
+    check("d_w_router", host(d_wr), ref["d_w_router"])
+    check("d_w_gate", host(d_wg), ref["d_w_gate"])
+    check("d_w_up", host(d_wu), ref["d_w_up"])
+    check("d_w_down", host(d_wd), ref["d_w_down"])
+
+
+@pytest.mark.parametrize("aux,data_loss", [(0.0, True), (0.01, True), (1.0, False)])
+def test_module_autograd_vs_oracle(cuda_device, aux, data_loss):
+    """loss = sum(y * R) (+ the load-balancing loss).  With data_loss False the loss
+    is the load-balancing term alone, so the router and input gradients come only
+    through the logits and the expert weights get none."""
+    torch.manual_seed(7)
+    d, F, E, k, n = 256, 512, 8, 2, 900
+    m = MoEFeedForward(d, F, 0.0, num_experts=E, top_k=k).to(cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        for p in (m.w_gate, m.w_up, m.w_down):
+            p.normal_(0, 0.05)
+        m.router.weight.normal_(0, 0.05)
+    m.aux_loss_coef = aux
+    x = torch.randn(n, d, device=cuda_device).to(torch.bfloat16).requires_grad_(True)
+    R = torch.randn(n, d, device=cuda_device) if data_loss else torch.zeros(n, d, device=cuda_device)
+    y = m(x)
+    loss = (y.float() * R).sum()
+    if aux > 0:
+        assert m.aux_loss is not None and m.aux_loss.requires_grad
+        loss = loss + m.aux_loss
+    loss.backward()
+    bits = lambda t: t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    xb, wrb = bits(x), bits(m.router.weight)
+    logits = mo.bf16_to_f32(xb).astype(np.float64) @ mo.bf16_to_f32(wrb).astype(np.float64).T
+    idx, _ = oracle.topk_gates_c(oracle.router_logits(xb, wrb), k)
+    grad_logits = None
+    if aux > 0:
+        # d/dlogits of aux * E * sum_e f_e * mean_t softmax(logits_t)_e, f fixed
+        f = np.bincount(idx.reshape(-1), minlength=E) / idx.size
+        p = np.exp(logits - logits.max(axis=1, keepdims=True))
+        p /= p.sum(axis=1, keepdims=True)
+        gp = aux * E * f / n
+        grad_logits = p * (gp[None, :] - (p * gp[None, :]).sum(axis=1, keepdims=True))
+    dy = synth.f32_to_bf16_bits(R.cpu().numpy())  # dL/dy = R, in the bf16 the backward takes
+    ref = oracle.moe_backward(xb, wrb, bits(m.w_gate), bits(m.w_up), bits(m.w_down), idx, dy,
+                              grad_logits=grad_logits)
+    print(f"module aux={aux} data_loss={data_loss}", flush=True)
+    check("x.grad", host(x.grad), ref["dx"])
+    check("router.grad", host(m.router.weight.grad), ref["d_w_router"])
+    for name, p, key in (("w_gate.grad", m.w_gate, "d_w_gate"), ("w_up.grad", m.w_up, "d_w_up"),
+                         ("w_down.grad", m.w_down, "d_w_down")):
+        if data_loss:
+            check(name, host(p.grad), ref[key])
+        else:
+            assert not np.any(ref[key]) and not torch.any(p.grad), name

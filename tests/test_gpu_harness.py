@@ -109,11 +109,27 @@ def test_module_traces_under_torch_compile(cuda_device):
         torch.testing.assert_close(f(x), m(x) * 2.0, rtol=0, atol=0)
 
 
-def test_backward_raises_clearly(cuda_device):
-    m = MoEFeedForward(128, 256, 0.0, num_experts=4).to(cuda_device)
-    y = m(torch.randn(8, 128, device=cuda_device))
-    with pytest.raises(NotImplementedError, match="forward-only"):
-        y.sum().backward()
+def test_grad_mode_selects_the_differentiable_op(cuda_device):
+    """Under no_grad the module runs the inference op (no graph); with gradients
+    enabled it runs the training op, whose backward fills every parameter's grad;
+    the inference op itself refuses a backward."""
+    m = MoEFeedForward(128, 256, 0.0, num_experts=4).to(cuda_device).to(torch.bfloat16)
+    x = torch.randn(64, 128, device=cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        y0 = m(x)
+    assert y0.grad_fn is None
+    y = m(x)
+    assert y.grad_fn is not None
+    torch.testing.assert_close(y.detach(), y0, rtol=0, atol=0)
+    y.float().sum().backward()
+    for p in (m.router.weight, m.w_gate, m.w_up, m.w_down):
+        assert p.grad is not None and torch.isfinite(p.grad.float()).all()
+    from genet5_amd.moe import _moe_forward_op
+    wgu, wd = m._expert_weights()
+    xr = x.clone().requires_grad_(True)
+    out = _moe_forward_op(xr, m.router.weight, None, wgu, wd, 2)
+    with pytest.raises(NotImplementedError, match="inference op"):
+        out.float().sum().backward()
 
 
 def check_fused_layer(ff, h2, nw, x_add2=None, alpha=1.0, out2=None, label="",
