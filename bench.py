@@ -34,6 +34,9 @@ def parse():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5))
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--train", action="store_true",
+                    help="time the training step instead: the forward that keeps the backward's "
+                         "inputs, then every backward stage (HIP events between stages)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the benchmark, run a 256 MiB elementwise copy (read 256 MiB, "
@@ -121,6 +124,43 @@ def bench_config4(args) -> dict:
         t_unfused = timed(lambda: stack(x), args.steps, args.warmup)
         stack.set_fused(True)
     flops = 12 * 6 * 768 * 3072 * N * 2
+    # the two fused memory-bound entry points on this batch (HIP events, 20 calls each)
+    from genet5_amd import ops
+    layer = stack.layers[0]
+    x2 = x.reshape(-1, 768)
+    nw = layer.norm.weight.float().contiguous()
+    wr = layer.ff.router.weight.contiguous()
+    xa = torch.randn_like(x2)
+    with torch.no_grad():
+        normed, _, idx, w = ops.add_rmsnorm_router(x2, nw, 1e-6, wr, 2)
+        _, offsets, perm, inv_pos = ops.dispatch(idx, 16, 768)
+        wgu, wd = layer.ff._expert_weights()
+        y_perm = ops.expert_swiglu(normed, perm, offsets, wgu, wd, 2)
+
+    def ev_time(fn, reps=20):
+        fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps * 1e-3
+    t_norm = ev_time(lambda: ops.add_rmsnorm_router(x2, nw, 1e-6, wr, 2))
+    t_addnorm = ev_time(lambda: ops.add_rmsnorm_router(x2, nw, 1e-6, wr, 2, x_add=xa))
+    t_comb = ev_time(lambda: ops.combine_residual(y_perm, inv_pos, w, x2, 1.0))
+    nd2 = N * 768 * 2
+    kernels = {
+        "rmsnorm_router_us": t_norm * 1e6,
+        "rmsnorm_router_gbs": (2 * nd2 + N * 16) / t_norm / 1e9,
+        "add_rmsnorm_router_us": t_addnorm * 1e6,
+        "add_rmsnorm_router_gbs": (4 * nd2 + N * 16) / t_addnorm / 1e9,
+        "combine_residual_us": t_comb * 1e6,
+        "combine_residual_gbs": (2 * nd2 + N * 2 * 768 * 2 + N * 16) / t_comb / 1e9,
+        "bytes": "rmsnorm_router: read rows, write normed, write idx/w (8 B/token each); "
+                 "add_: + read x_add, write the sum; combine_residual: read y_perm (k rows), "
+                 "residual, write out, read inv_pos/w",
+    }
     return {
         "metric": "12-block RMSNorm->MoE->residual stack tokens/s, 45.5k packed tok, 16e top-2",
         "value": N / t, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
@@ -132,6 +172,7 @@ def bench_config4(args) -> dict:
         "expert_gemm_tflops_incl_layer_overheads": flops / t / 1e12,
         "blocks": "fused: g5moe_add_rmsnorm_router + dispatch + experts + g5moe_combine_residual",
         "unfused_ms_per_step": t_unfused * 1e3,
+        "fused_kernels": kernels,
     }
 
 
@@ -170,6 +211,99 @@ def bench_config5(args) -> dict:
     }
 
 
+def bench_train(args) -> dict:
+    """Training step of the layer at config 2: forward (router with logits, dispatch,
+    experts, combine) + backward (gate/router gradients, gate|up recompute, dh GEMM,
+    SwiGLU backward, dX GEMM, input gradient, weight-gradient GEMMs), one HIP event
+    between consecutive stages on the stream they run on."""
+    import ctypes
+    import torch
+    from genet5_amd import _lib, ops, synth
+    dev = torch.device("cuda:0")
+    inp = synth.make_config(args.config, seed=0)
+    N, d = inp.x.shape
+    E, F = inp.w_gate.shape[0], inp.w_gate.shape[1]
+    k = inp.top_k
+    tt = synth.to_torch(inp, dev)
+    x, wr = tt["x"], tt["w_router"]
+    wgu = ops.pack_gate_up(tt["w_gate"], tt["w_up"])
+    wd = tt["w_down"]
+    wd_t, wgu_t = ops.transpose_experts(wd), ops.transpose_experts(wgu)
+    dy = (torch.randn(N, d, device=dev) * 0.01).to(torch.bfloat16)
+    shape = _lib.make_shape(N, d, F, E, k, _lib.DTYPE_BF16)
+    P, S = ops._ptr, ops._stream(dev)
+    stream = torch.cuda.current_stream(dev)
+    names = ["fwd", "gate_router_grad", "gate_up_recompute", "dh_gemm", "swiglu_bwd",
+             "dx_gemm", "input_grad", "wgrad_gemms"]
+
+    def step(ev=None):
+        rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
+        rec(0)
+        y, logits, idx, w, offsets, perm, inv_pos, y_perm = ops.moe_forward_train(x, wr, wgu, wd, k)
+        rec(1)
+        dw = torch.empty((N, k), dtype=torch.float32, device=dev)
+        dyp = torch.empty((N * k + ops.ROW_PAD, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_gate_grad", P(dy), P(y_perm), P(inv_pos), P(w), P(dw), P(dyp),
+                  ctypes.byref(shape), S)
+        dl = torch.empty((N, E), dtype=torch.float32, device=dev)
+        _lib.call("g5moe_router_grad", P(dw), P(w), P(idx), None, P(dl), ctypes.byref(shape), S)
+        rec(2)
+        gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
+        ws = ops.workspace(shape, dev)
+        _lib.call("g5moe_expert_gate_up_raw", P(x), P(perm), P(offsets), P(wgu), P(gu), P(ws),
+                  ctypes.byref(shape), S)
+        rec(3)
+        dh = ops.grouped_gemm(dyp, N * k, offsets, wd_t)
+        rec(4)
+        dgu = torch.empty((N * k + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
+        h = torch.empty((N * k, F), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(dgu), P(h), ctypes.byref(shape), S)
+        rec(5)
+        dxp = ops.grouped_gemm(dgu, N * k, offsets, wgu_t)
+        rec(6)
+        dx = torch.empty((N, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),
+                  ctypes.byref(shape), S)
+        rec(7)
+        xperm = x.index_select(0, (perm // k).long())
+        offs = offsets.tolist()
+        d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
+        d_wgu = torch.empty((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
+        for e in range(E):
+            o0, o1 = offs[e], offs[e + 1]
+            torch.matmul(dyp[o0:o1].t(), h[o0:o1], out=d_wd[e])
+            torch.matmul(dgu[o0:o1].t(), xperm[o0:o1], out=d_wgu[e])
+        rec(8)
+
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
+              for _ in range(args.steps)]
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step(events[i])
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    st = {n: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
+          for j, n in enumerate(names)}
+    g = 2 * d * F * N * k  # one d x F product over the routed rows
+    flops = {"gate_up_recompute": 2 * g, "dh_gemm": g, "dx_gemm": 2 * g, "wgrad_gemms": 3 * g}
+    return {
+        "metric": "MoE layer training step (forward + backward) tokens/s, 36.4k tok, 16e top-2",
+        "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": synth.CONFIGS[args.config]["name"] + ", training step",
+                   "n_tokens": N, "d_model": d, "d_ff": F, "n_experts": E, "top_k": k},
+        "stage_ms": st,
+        "stage_tflops": {n: flops[n] / (st[n] * 1e-3) / 1e12 for n in flops},
+        "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
+        "note": "weight-gradient GEMMs are per-expert torch.matmul (hipBLASLt) with a host "
+                "read of the expert offsets; all other stages are this library's HIP kernels",
+    }
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -180,6 +314,9 @@ def main():
     if args.config in (4, 5):
         out = bench_config4(args) if args.config == 4 else bench_config5(args)
         print(json.dumps(out), flush=True)
+        return
+    if args.train:
+        print(json.dumps(bench_train(args)), flush=True)
         return
 
     import torch
@@ -304,7 +441,7 @@ def main():
             "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
         },
         "roofline": {
-            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,true> (gate|up + SwiGLU)",
+            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,1,false> (gate|up + SwiGLU)",
             "bound": "mfma",
             "achieved": gu_tflops,
             "peak": PEAK_BF16_TFLOPS,
