@@ -234,7 +234,7 @@ def bench_train(args) -> dict:
     P, S = ops._ptr, ops._stream(dev)
     stream = torch.cuda.current_stream(dev)
     names = ["fwd", "gate_router_grad", "gate_up_recompute", "dh_gemm", "swiglu_bwd",
-             "dx_gemm", "input_grad", "wgrad_gemms"]
+             "dx_gemm", "input_grad", "wgrad_operands", "wgrad_gemms"]
 
     def step(ev=None):
         rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
@@ -255,9 +255,13 @@ def bench_train(args) -> dict:
         rec(3)
         dh = ops.grouped_gemm(dyp, N * k, offsets, wd_t)
         rec(4)
+        offs = offsets.tolist()
+        kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
         dgu = torch.empty((N * k + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
-        h = torch.empty((N * k, F), dtype=torch.bfloat16, device=dev)
-        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(dgu), P(h), ctypes.byref(shape), S)
+        h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
+        dgu_pad = torch.empty((E, kmax, 2 * F), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(offsets), P(dgu), P(h_pad),
+                  P(dgu_pad), kmax, ctypes.byref(shape), S)
         rec(5)
         dxp = ops.grouped_gemm(dgu, N * k, offsets, wgu_t)
         rec(6)
@@ -265,15 +269,16 @@ def bench_train(args) -> dict:
         _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),
                   ctypes.byref(shape), S)
         rec(7)
-        xperm = x.index_select(0, (perm // k).long())
-        offs = offsets.tolist()
-        d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
-        d_wgu = torch.empty((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
-        for e in range(E):
-            o0, o1 = offs[e], offs[e + 1]
-            torch.matmul(dyp[o0:o1].t(), h[o0:o1], out=d_wd[e])
-            torch.matmul(dgu[o0:o1].t(), xperm[o0:o1], out=d_wgu[e])
+        dyT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_pad_transpose", P(dyp), None, P(offsets), P(dyT), d, kmax,
+                  ctypes.byref(shape), S)
+        xT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_pad_transpose", P(x), P(perm), P(offsets), P(xT), d, kmax,
+                  ctypes.byref(shape), S)
         rec(8)
+        torch.bmm(dyT, h_pad)
+        ops.transpose_experts(torch.bmm(xT, dgu_pad))
+        rec(9)
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]
@@ -299,8 +304,10 @@ def bench_train(args) -> dict:
         "stage_ms": st,
         "stage_tflops": {n: flops[n] / (st[n] * 1e-3) / 1e12 for n in flops},
         "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
-        "note": "weight-gradient GEMMs are per-expert torch.matmul (hipBLASLt) with a host "
-                "read of the expert offsets; all other stages are this library's HIP kernels",
+        "note": "weight-gradient GEMMs are two torch.bmm (hipBLASLt) over per-expert operands "
+                "padded to kmax rows (the padding's zero products count in the time, not in the "
+                "FLOP); the host reads the expert offsets once per step; every other stage is "
+                "this library's HIP kernels",
     }
 
 

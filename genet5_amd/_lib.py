@@ -39,6 +39,7 @@ EXPORTED = (
     "g5moe_expert_gate_up_raw",
     "g5moe_swiglu_backward",
     "g5moe_input_grad",
+    "g5moe_pad_transpose",
     "g5moe_forward",
 )
 
@@ -89,7 +90,10 @@ _SIGS = {
     "g5moe_gate_grad": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_router_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up_raw": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
-    "g5moe_swiglu_backward": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_swiglu_backward": ([_P, _P, _P, _P, _P, _P, ctypes.c_int32, _SHAPE_P, _P],
+                              ctypes.c_int),
+    "g5moe_pad_transpose": ([_P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _SHAPE_P, _P],
+                            ctypes.c_int),
     "g5moe_input_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
 }

@@ -319,19 +319,41 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
                     "g5moe_expert_gate_up_raw");
 }
 
-g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, void* dgu, void* h,
+g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* offsets,
+                                   void* dgu, void* h_pad, void* dgu_pad, int32_t kmax,
                                    const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));
-  if (shape->n_tokens == 0) return G5MOE_OK;
+  if (kmax < 0) return fail(G5MOE_ERR_INVALID_ARG, "kmax %d < 0", int(kmax));
+  if (shape->n_tokens == 0 || kmax == 0) return G5MOE_OK;
   G5_NONNULL(dh);
   G5_NONNULL(gu);
+  G5_NONNULL(offsets);
   G5_NONNULL(dgu);
-  G5_NONNULL(h);
+  G5_NONNULL(h_pad);
+  G5_NONNULL(dgu_pad);
   return hip_status(launch_swiglu_bwd(static_cast<const uint16_t*>(dh),
-                                      static_cast<const uint16_t*>(gu),
-                                      static_cast<uint16_t*>(dgu), static_cast<uint16_t*>(h),
-                                      *shape, as_stream(stream)),
+                                      static_cast<const uint16_t*>(gu), offsets,
+                                      static_cast<uint16_t*>(dgu), static_cast<uint16_t*>(h_pad),
+                                      static_cast<uint16_t*>(dgu_pad), kmax, *shape,
+                                      as_stream(stream)),
                     "g5moe_swiglu_backward");
+}
+
+g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int32_t* offsets,
+                                 void* out, int32_t cols, int32_t kmax,
+                                 const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (cols <= 0 || cols % 64 != 0 || kmax < 0)
+    return fail(G5MOE_ERR_INVALID_ARG, "pad_transpose: cols %d must be a positive multiple of "
+                "64 and kmax %d >= 0", int(cols), int(kmax));
+  if (kmax == 0) return G5MOE_OK;
+  G5_NONNULL(src);
+  G5_NONNULL(offsets);
+  G5_NONNULL(out);
+  return hip_status(launch_pad_transpose(static_cast<const uint16_t*>(src), perm, offsets,
+                                         static_cast<uint16_t*>(out), shape->n_experts, cols,
+                                         kmax, shape->top_k, as_stream(stream)),
+                    "g5moe_pad_transpose");
 }
 
 g5moe_status g5moe_input_grad(const void* dx_perm, const int32_t* inv_pos, const float* dlogits,

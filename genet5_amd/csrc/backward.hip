@@ -1,7 +1,7 @@
 // Backward of the MoE layer: the elementwise, gather/scatter and reduction
 // stages.  The data-gradient products run on the grouped GEMM kernels
-// (grouped_gemm.hip); the weight-gradient products are plain per-expert GEMMs
-// issued by the host (hipBLASLt through PyTorch).
+// (grouped_gemm.hip); the weight-gradient products are plain batched GEMMs
+// issued by the host (hipBLASLt through PyTorch) on operands prepared here.
 //
 // New stage: the reference trains the dense FeedForward through autograd
 // (lib/blocks/_component.py:48-52 under train/diffusion_finet:761's
@@ -18,7 +18,10 @@
 //   dg        = dh * u * s(g) (1 + g (1 - s(g))), du = dh * silu(g)   (swiglu_bwd)
 //   dX_perm   = (dg | du) Wgu_e                                (grouped GEMM)
 //   dx[t]     = sum_s dX_perm[inv_pos[t, s]] + sum_e dl[t, e] Wr[e]   (input_grad)
-// with s the logistic sigmoid.
+// with s the logistic sigmoid.  The weight gradients dWd_e = dY_e^T h_e and
+// dWgu_e^T = X_e^T dGU_e are batched products over operands padded per expert
+// to kmax rows (zeros past the expert's own): pad_transpose writes dY^T and
+// X^T as [E, C, kmax], swiglu_bwd writes h and dGU as [E, kmax, .].
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -85,18 +88,34 @@ __global__ __launch_bounds__(256) void router_grad_kernel(
   for (int e = 0; e < n_experts; ++e) dlogits[t * n_experts + e] = dl[e];
 }
 
-// One thread per 8 consecutive h columns of one row.  gu rows interleave
-// 32-column groups: entries [64q, 64q + 32) are g of columns [32q, 32q + 32),
-// the next 32 the matching u.
+// One thread per 8 consecutive h columns of one row of the expert-padded row
+// space: row e * kmax + j is sorted position offsets[e] + j for j < M_e and a
+// padding row (written as zeros in the padded outputs) otherwise.  gu rows
+// interleave 32-column groups: entries [64q, 64q + 32) are g of columns
+// [32q, 32q + 32), the next 32 the matching u.  Outputs: dgu in sorted order
+// (the dX product's A operand), and h and dgu in the padded row layout
+// [E, kmax, .] the weight-gradient batched products read.
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     const uint16_t* __restrict__ dh, const uint16_t* __restrict__ gu,
-    uint16_t* __restrict__ dgu, uint16_t* __restrict__ h, int64_t rows, int F) {
+    const int32_t* __restrict__ offsets, uint16_t* __restrict__ dgu,
+    uint16_t* __restrict__ h_pad, uint16_t* __restrict__ dgu_pad, int n_experts, int kmax,
+    int F) {
   const int cpr = F / 8;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * cpr) return;
-  const int64_t p = i / cpr;
-  const int f0 = int(i - p * cpr) * 8;
+  const int64_t prow = i / cpr;
+  if (prow >= int64_t(n_experts) * kmax) return;
+  const int e = int(prow / kmax), jr = int(prow - int64_t(e) * kmax);
+  const int f0 = int(i - prow * cpr) * 8;
   const int q = f0 >> 5, r = f0 & 31;
+  const int64_t gpo = prow * 2 * F + 64 * q + r;
+  if (jr >= offsets[e + 1] - offsets[e]) {
+    const uint4 z = make_uint4(0, 0, 0, 0);
+    *reinterpret_cast<uint4*>(dgu_pad + gpo) = z;
+    *reinterpret_cast<uint4*>(dgu_pad + gpo + 32) = z;
+    *reinterpret_cast<uint4*>(h_pad + prow * F + f0) = z;
+    return;
+  }
+  const int64_t p = offsets[e] + jr;
   const int64_t go = p * 2 * F + 64 * q + r;
   const uint4 vd = *reinterpret_cast<const uint4*>(dh + p * F + f0);
   const uint4 vg = *reinterpret_cast<const uint4*>(gu + go);
@@ -123,9 +142,48 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     ou[j] = pack_bf16x2(ru[0], ru[1]);
     oh[j] = pack_bf16x2(rh[0], rh[1]);
   }
-  *reinterpret_cast<uint4*>(dgu + go) = make_uint4(og[0], og[1], og[2], og[3]);
-  *reinterpret_cast<uint4*>(dgu + go + 32) = make_uint4(ou[0], ou[1], ou[2], ou[3]);
-  *reinterpret_cast<uint4*>(h + p * F + f0) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+  const uint4 vog = make_uint4(og[0], og[1], og[2], og[3]);
+  const uint4 vou = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+  *reinterpret_cast<uint4*>(dgu + go) = vog;
+  *reinterpret_cast<uint4*>(dgu + go + 32) = vou;
+  *reinterpret_cast<uint4*>(dgu_pad + gpo) = vog;
+  *reinterpret_cast<uint4*>(dgu_pad + gpo + 32) = vou;
+  *reinterpret_cast<uint4*>(h_pad + prow * F + f0) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+}
+
+// out[e][c][j] = src row (expert e's j-th sorted position) column c, zero for
+// j >= M_e: the [E, C, kmax] transposed operand of the weight-gradient batched
+// products.  The source row of sorted position p is p itself (perm == nullptr)
+// or the token perm[p] / topk (a gather of x rows).  64 x 64 tiles through LDS.
+__global__ __launch_bounds__(256) void pad_transpose_kernel(
+    const uint16_t* __restrict__ src, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, uint16_t* __restrict__ out, int C, int kmax,
+    int topk) {
+  __shared__ uint16_t tile[64][66];
+  const int e = blockIdx.z;
+  const int j0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const int m = offsets[e + 1] - offsets[e];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int jj = ty + 4 * i;  // tile row = position j0 + jj
+    const int j = j0 + jj;
+    uint16_t v = 0;
+    if (j < m) {
+      const int64_t p = offsets[e] + j;
+      const int64_t row = perm != nullptr ? int64_t(perm[p] / topk) : p;
+      v = src[row * C + c0 + tx];
+    }
+    tile[jj][tx] = v;
+  }
+  __syncthreads();
+  uint16_t* dst = out + int64_t(e) * C * kmax;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = ty + 4 * i;
+    const int j = j0 + tx;
+    if (j < kmax) dst[int64_t(c0 + c) * kmax + j] = tile[tx][c];
+  }
 }
 
 // One thread per 8 consecutive outputs: dx = sum over slots of dX_perm rows
@@ -246,13 +304,24 @@ hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_
   return hipGetLastError();
 }
 
-hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, uint16_t* dgu,
-                             uint16_t* h, const g5moe_shape& s, hipStream_t st) {
-  const int64_t rows = s.n_tokens * s.top_k;
-  const int64_t work = rows * (s.d_ff / 8);
+hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32_t* offsets,
+                             uint16_t* dgu, uint16_t* h_pad, uint16_t* dgu_pad, int kmax,
+                             const g5moe_shape& s, hipStream_t st) {
+  const int64_t work = int64_t(s.n_experts) * kmax * (s.d_ff / 8);
   if (work == 0) return hipSuccess;
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, st,
-                     dh, gu, dgu, h, rows, s.d_ff);
+                     dh, gu, offsets, dgu, h_pad, dgu_pad, s.n_experts, kmax, s.d_ff);
+  return hipGetLastError();
+}
+
+hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
+                                uint16_t* out, int n_experts, int C, int kmax, int topk,
+                                hipStream_t st) {
+  if (n_experts == 0 || C == 0 || kmax == 0) return hipSuccess;
+  if (C % 64 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pad_transpose_kernel,
+                     dim3(unsigned(C / 64), unsigned((kmax + 63) / 64), unsigned(n_experts)),
+                     dim3(256), 0, st, src, perm, offsets, out, C, kmax, topk);
   return hipGetLastError();
 }
 

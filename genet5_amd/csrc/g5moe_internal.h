@@ -81,8 +81,12 @@ hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const in
 hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
                               const float* grad_logits, float* dlogits, const g5moe_shape& s,
                               hipStream_t st);
-hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, uint16_t* dgu,
-                             uint16_t* h, const g5moe_shape& s, hipStream_t st);
+hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32_t* offsets,
+                             uint16_t* dgu, uint16_t* h_pad, uint16_t* dgu_pad, int kmax,
+                             const g5moe_shape& s, hipStream_t st);
+hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
+                                uint16_t* out, int n_experts, int C, int kmax, int topk,
+                                hipStream_t st);
 hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const float* dlogits,
                              const void* w_router, void* dx, const g5moe_shape& s,
                              hipStream_t st);

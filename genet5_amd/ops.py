@@ -371,10 +371,15 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     if w_down_t is None:
         w_down_t = transpose_experts(w_down)            # [E, F, d]
     dh = grouped_gemm(dyp, N * k, offsets, w_down_t)    # [N*k, F]
+    # every expert's rows padded to kmax (a multiple of 64 >= max M_e) for the
+    # weight-gradient batched products; the host reads the offsets once here
+    offs = offsets.tolist()
+    kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
     dgu = torch.empty((N * k + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
-    h = torch.empty((N * k, F), dtype=torch.bfloat16, device=dev)
-    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(dgu), _ptr(h),
-              ctypes.byref(shape), S)
+    h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
+    dgu_pad = torch.empty((E, kmax, 2 * F), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(offsets), _ptr(dgu),
+              _ptr(h_pad), _ptr(dgu_pad), kmax, ctypes.byref(shape), S)
     del dh, gu
     if w_gate_up_t is None:
         w_gate_up_t = transpose_experts(w_gate_up)      # [E, d, 2F]
@@ -384,16 +389,18 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     _lib.call("g5moe_input_grad", _ptr(dxp), _ptr(inv_pos), _ptr(dlogits), _ptr(w_router),
               _ptr(dx), ctypes.byref(shape), S)
     del dxp
-    # weight gradients: per-expert TN products over the expert's rows
-    xperm = x2d.index_select(0, (perm // k).long())
-    d_wd = torch.zeros((E, d, F), dtype=torch.bfloat16, device=dev)
-    d_wgu = torch.zeros((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
-    offs = offsets.tolist()
-    for e in range(E):
-        o0, o1 = offs[e], offs[e + 1]
-        if o1 > o0:
-            torch.matmul(dyp[o0:o1].t(), h[o0:o1], out=d_wd[e])
-            torch.matmul(dgu[o0:o1].t(), xperm[o0:o1], out=d_wgu[e])
+    # weight gradients: batched products over the per-expert padded operands
+    # (zero rows past each expert's own): dWd_e = dY_e^T h_e, dWgu_e^T = X_e^T dGU_e
+    dyT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_pad_transpose", _ptr(dyp), None, _ptr(offsets), _ptr(dyT), d, kmax,
+              ctypes.byref(shape), S)
+    del dyp
+    xT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_pad_transpose", _ptr(x2d), _ptr(perm), _ptr(offsets), _ptr(xT), d, kmax,
+              ctypes.byref(shape), S)
+    d_wd = torch.bmm(dyT, h_pad)                       # [E, d, F]
+    del dyT, h_pad
+    d_wgu = transpose_experts(torch.bmm(xT, dgu_pad))  # [E, d, 2F] -> [E, 2F, d]
     d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
     return dx, d_wr, d_wgu, d_wd
 

@@ -183,8 +183,9 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
  * The MoE layer's backward, stage by stage.  The reference trains its dense
  * FeedForward through autograd (lib/blocks/_component.py:48-52; loss.backward()
  * at train/diffusion_finet:761); the MoE and its backward are new.  The
- * weight-gradient products (dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e) are plain
- * per-expert GEMMs left to the caller (hipBLASLt); everything else is here.
+ * weight-gradient products (dWd_e = dY_e^T h_e, dWgu_e^T = X_e^T dGU_e) are plain
+ * batched GEMMs over per-expert padded operands, left to the caller (hipBLASLt);
+ * everything else, including those operands, is here.
  * Activations are bf16 (x_dtype must be BF16), gradients of the routing fp32.
  * A row count "+ 256" means the buffer carries 256 rows of padding after its
  * last row: g5moe_grouped_gemm reads whole 256-row tiles of its A operand. */
@@ -233,10 +234,21 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
  * lib/blocks/_component.py:31, :50): with s = 1 / (1 + exp(-g)),
  *   dg = dh * u * s * (1 + g * (1 - s)),  du = dh * g * s,  h = g * s * u
  * (h recomputed for the down weight gradient).  dh : bf16 [N*k, F];
- * gu : bf16 [N*k, 2F] packed;  dgu : bf16 [N*k + 256, 2F] packed out;
- * h : bf16 [N*k, F] out. */
-g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, void* dgu, void* h,
+ * gu : bf16 [N*k, 2F] packed;  dgu : bf16 [N*k + 256, 2F] packed out (sorted
+ * order); h_pad, dgu_pad : bf16 [E, kmax, F], [E, kmax, 2F] out — the same rows
+ * placed per expert, row e*kmax + j = sorted position offsets[e] + j, zero rows
+ * for j >= M_e (kmax >= every M_e): the weight gradients' batched operands. */
+g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* offsets,
+                                   void* dgu, void* h_pad, void* dgu_pad, int32_t kmax,
                                    const g5moe_shape* shape, void* stream);
+
+/* Per-expert padded transpose: out[e][c][j] = column c of the row of expert
+ * e's j-th sorted position, 0 for j >= M_e.  The row of sorted position p is
+ * src row p (perm == NULL: dY) or src row perm[p] / k (the gathered x row).
+ *   src : bf16 [rows, cols];  out : bf16 [E, cols, kmax];  cols multiple of 64. */
+g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int32_t* offsets,
+                                 void* out, int32_t cols, int32_t kmax,
+                                 const g5moe_shape* shape, void* stream);
 
 /* Input gradient: dx[t] = sum over s of dx_perm[inv_pos[t, s]] (slot order)
  * + sum over e of dlogits[t, e] * w_router[e] (expert order), fp32, one

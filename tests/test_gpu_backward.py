@@ -139,3 +139,67 @@ def test_module_autograd_vs_oracle(cuda_device, aux, data_loss):
             check(name, host(p.grad), ref[key])
         else:
             assert not np.any(ref[key]) and not torch.any(p.grad), name
+
+
+def test_padded_weight_gradient_operands(cuda_device):
+    """g5moe_pad_transpose (plain rows and gathered x rows) and the padded outputs
+    of g5moe_swiglu_backward against numpy, with empty experts and ragged counts:
+    the rows land per expert at kmax spacing and every padding entry is zero."""
+    import ctypes
+    from genet5_amd import _lib
+    rng = np.random.default_rng(9)
+    E, k, d, F = 6, 2, 128, 128
+    counts = np.array([0, 70, 5, 0, 130, 35], np.int32)
+    nk = int(counts.sum())
+    n = nk // k
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    perm = rng.permutation(nk).astype(np.int32)
+    kmax = 192
+    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
+    S = ops._stream(cuda_device)
+    rows = synth.f32_to_bf16_bits(rng.standard_normal((nk, d)).astype(np.float32))
+    x = synth.f32_to_bf16_bits(rng.standard_normal((n, d)).astype(np.float32))
+    t_off = dev_t(offsets, cuda_device)
+    t_perm = dev_t(perm, cuda_device)
+    out = torch.full((E, d, kmax), 7, dtype=torch.int16, device=cuda_device).view(torch.bfloat16)
+    outx = torch.full((E, d, kmax), 7, dtype=torch.int16, device=cuda_device).view(torch.bfloat16)
+    _lib.call("g5moe_pad_transpose", ops._ptr(dev_t(rows, cuda_device, True)), None,
+              ops._ptr(t_off), ops._ptr(out), d, kmax, ctypes.byref(shape), S)
+    _lib.call("g5moe_pad_transpose", ops._ptr(dev_t(x, cuda_device, True)), ops._ptr(t_perm),
+              ops._ptr(t_off), ops._ptr(outx), d, kmax, ctypes.byref(shape), S)
+    # swiglu backward on random dh / gu
+    dh = synth.f32_to_bf16_bits(rng.standard_normal((nk, F)).astype(np.float32))
+    gu = synth.f32_to_bf16_bits(rng.standard_normal((nk, 2 * F)).astype(np.float32))
+    dgu = torch.empty((nk + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=cuda_device)
+    h_pad = torch.full((E, kmax, F), 7, dtype=torch.int16, device=cuda_device).view(torch.bfloat16)
+    dgu_pad = torch.full((E, kmax, 2 * F), 7, dtype=torch.int16,
+                         device=cuda_device).view(torch.bfloat16)
+    _lib.call("g5moe_swiglu_backward", ops._ptr(dev_t(dh, cuda_device, True)),
+              ops._ptr(dev_t(gu, cuda_device, True)), ops._ptr(t_off), ops._ptr(dgu),
+              ops._ptr(h_pad), ops._ptr(dgu_pad), kmax, ctypes.byref(shape), S)
+    torch.cuda.synchronize()
+    bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    exp = np.zeros((E, d, kmax), np.uint16)
+    expx = np.zeros((E, d, kmax), np.uint16)
+    exp_h = np.zeros((E, kmax, F), np.uint16)
+    exp_g = np.zeros((E, kmax, 2 * F), np.uint16)
+    g_sorted = bits(dgu)[:nk]
+    # h = silu(g) * u from the packed layout, in float64, compared after rounding below
+    gf = mo.bf16_to_f32(gu).reshape(nk, F // 32, 2, 32)
+    g, u = gf[:, :, 0].reshape(nk, F).astype(np.float64), gf[:, :, 1].reshape(nk, F).astype(np.float64)
+    h_ref = g / (1 + np.exp(-g)) * u
+    for e in range(E):
+        o0, o1 = offsets[e], offsets[e + 1]
+        exp[e, :, : o1 - o0] = rows[o0:o1].T
+        expx[e, :, : o1 - o0] = x[perm[o0:o1] // k].T
+        exp_g[e, : o1 - o0] = g_sorted[o0:o1]
+    np.testing.assert_array_equal(bits(out), exp)
+    np.testing.assert_array_equal(bits(outx), expx)
+    np.testing.assert_array_equal(bits(dgu_pad), exp_g)
+    hp = bits(h_pad)
+    for e in range(E):
+        o0, o1 = offsets[e], offsets[e + 1]
+        assert not hp[e, o1 - o0:].any()
+        got = mo.bf16_to_f32(hp[e, : o1 - o0]).astype(np.float64)
+        np.testing.assert_allclose(got, h_ref[o0:o1], rtol=8e-3, atol=1e-6)
