@@ -41,6 +41,7 @@ EXPORTED = (
     "g5moe_input_grad",
     "g5moe_pad_transpose",
     "g5moe_forward",
+    "g5moe_attn_varlen_fwd",
 )
 
 
@@ -55,6 +56,28 @@ class Shape(ctypes.Structure):
         ("top_k", ctypes.c_int32),
         ("x_dtype", ctypes.c_int32),
         ("reserved", ctypes.c_int32),
+    ]
+
+
+class AttnShape(ctypes.Structure):
+    """Mirror of `g5moe_attn_shape`."""
+
+    _fields_ = [
+        ("n_seqs", ctypes.c_int32),
+        ("max_seqlen", ctypes.c_int32),
+        ("total_tokens", ctypes.c_int64),
+        ("n_heads", ctypes.c_int32),
+        ("n_kv_heads", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("reserved", ctypes.c_int32),
+        ("q_token_stride", ctypes.c_int64),
+        ("q_head_stride", ctypes.c_int64),
+        ("k_token_stride", ctypes.c_int64),
+        ("k_head_stride", ctypes.c_int64),
+        ("v_token_stride", ctypes.c_int64),
+        ("v_head_stride", ctypes.c_int64),
+        ("o_token_stride", ctypes.c_int64),
+        ("o_head_stride", ctypes.c_int64),
     ]
 
 
@@ -96,6 +119,8 @@ _SIGS = {
                             ctypes.c_int),
     "g5moe_input_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
+    "g5moe_attn_varlen_fwd": ([_P, _P, _P, _P, _P, _P, ctypes.c_float, _P,
+                               ctypes.POINTER(AttnShape), _P], ctypes.c_int),
 }
 
 _lock = threading.Lock()

@@ -400,4 +400,52 @@ g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bia
   return g5moe_combine(y_perm, inv_pos, topk_w, y, shape, stream);
 }
 
+g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, void* out,
+                                   const int32_t* cu_seqlens, const float* alibi_slopes,
+                                   float softmax_scale, float* softmax_lse,
+                                   const g5moe_attn_shape* shape, void* stream) {
+  G5_NONNULL(shape);
+  const g5moe_attn_shape& s = *shape;
+  if (s.reserved != 0) return fail(G5MOE_ERR_INVALID_ARG, "attn shape.reserved must be 0");
+  if (s.n_seqs < 0 || s.max_seqlen < 0 || s.total_tokens < 0)
+    return fail(G5MOE_ERR_INVALID_ARG, "n_seqs, max_seqlen and total_tokens must be >= 0");
+  if (s.n_heads < 1 || s.n_kv_heads < 1 || s.n_heads % s.n_kv_heads != 0)
+    return fail(G5MOE_ERR_INVALID_ARG, "n_kv_heads %d must divide n_heads %d (both >= 1)",
+                int(s.n_kv_heads), int(s.n_heads));
+  if (s.head_dim != 64)
+    return fail(G5MOE_ERR_UNSUPPORTED, "head_dim %d: only 64 is supported", int(s.head_dim));
+  if (s.n_heads > 65535 || s.n_seqs > 65535)
+    return fail(G5MOE_ERR_UNSUPPORTED, "n_heads and n_seqs must be <= 65535");
+  if (s.total_tokens > INT32_MAX / 2)
+    return fail(G5MOE_ERR_UNSUPPORTED, "total_tokens %lld beyond the int32 position range",
+                (long long)s.total_tokens);
+  if (!(softmax_scale == softmax_scale) || softmax_scale == __builtin_inff() ||
+      softmax_scale == -__builtin_inff())
+    return fail(G5MOE_ERR_INVALID_ARG, "softmax_scale must be finite");
+  const int64_t strides[8] = {s.q_token_stride, s.q_head_stride, s.k_token_stride,
+                              s.k_head_stride,  s.v_token_stride, s.v_head_stride,
+                              s.o_token_stride, s.o_head_stride};
+  for (int i = 0; i < 8; ++i)
+    if (strides[i] < 0 || strides[i] % 8 != 0)
+      return fail(G5MOE_ERR_UNSUPPORTED,
+                  "every stride must be a non-negative multiple of 8 elements (stride %d = %lld)",
+                  i, (long long)strides[i]);
+  if (s.n_seqs == 0 || s.max_seqlen == 0) return G5MOE_OK;
+  G5_NONNULL(q);
+  G5_NONNULL(k);
+  G5_NONNULL(v);
+  G5_NONNULL(out);
+  G5_NONNULL(cu_seqlens);
+  const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                          reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(out);
+  if (align % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "q, k, v and out must be 16-byte aligned");
+  return hip_status(launch_attn_fwd(static_cast<const uint16_t*>(q),
+                                    static_cast<const uint16_t*>(k),
+                                    static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out),
+                                    cu_seqlens, alibi_slopes, softmax_scale, softmax_lse, s,
+                                    as_stream(stream)),
+                    "g5moe_attn_varlen_fwd");
+}
+
 }  // extern "C"

@@ -1,0 +1,323 @@
+// Varlen bidirectional attention with ALiBi on bf16 MFMA (gfx950).
+//
+// Reference interface: flash_attn_varlen_func(q, k, v, cu_seqlens_q,
+// cu_seqlens_k, max_seqlen_q, max_seqlen_k, dropout_p, softmax_scale,
+// causal=False) as GeneT5's FlashAttention.forward calls it
+// (lib/blocks/_flash_att.py:60-98), with flash-attn's `alibi_slopes` bias
+// bias[h, i, j] = -slope_h * |i - j| (sequence-local positions, non-causal,
+// equal query and key lengths).  Sequences of the packed batch attend only
+// within themselves (cu_seqlens), unlike the reference SDPA fallback's single
+// global mask (lib/blocks/_sdpa_att.py:36-43).
+//
+// Work split: one workgroup of 4 waves per (128-query block, head, sequence);
+// wave w owns queries q0 + 32w .. q0 + 32w + 31.  Keys stream through LDS in
+// blocks of 64 (K row-major, V transposed), double-buffered, one barrier per
+// block.
+//
+// MFMA layout (v_mfma_f32_32x32x16_bf16): scores are formed transposed,
+// S^T = K . Q^T, with the key block as the A operand and the wave's queries as
+// the B operand, so lane l holds query l % 32 and, in element 4q + u of key
+// block b, key 32b + 8q + 4(l / 32) + u.  Every softmax statistic of a query
+// lives in the two lanes l and l ^ 32; one cross-lane exchange per key block
+// shares the block maximum and the row sums are combined once at the end.
+// The output is formed transposed too, O^T += V^T . P^T: P^T needs no data
+// movement (a lane's eight probabilities of a 16-key chunk are its own
+// accumulator elements), provided V^T's key order inside each 16-key chunk is
+// the one those elements carry: key r at position r with bits 2 and 3
+// swapped.  The LDS copy of V is written transposed in that order.
+//
+// Softmax in base 2: t = s * scale * log2(e) + bias * log2(e), p = 2^(t - m).
+// On a key block that lies entirely on one side of every query of the wave
+// and inside the sequence, bias = c_blk +/- c_r with c_r = -slope * log2(e) *
+// (key offset inside the block) held in registers and c_blk a per-lane
+// scalar, so the bias costs nothing beyond the score's own fused
+// multiply-add; blocks that straddle the diagonal or the sequence end take the
+// exact per-element |i - j| path with masking.
+#include "g5moe_internal.h"
+
+namespace g5moe {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kHeadDim = 64;
+constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
+constexpr int kBKV = 64;   // keys per LDS block
+constexpr int kRowBytes = kHeadDim * 2;           // 128 bytes per K row / V^T row
+constexpr int kTileBytes = kBKV * kRowBytes;      // 8 KB
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  uint16_t* o;
+  const int32_t* cu_seqlens;  // [n_seqs + 1]
+  int64_t q_tok, k_tok, v_tok, o_tok;      // element strides between tokens
+  int64_t q_head, k_head, v_head, o_head;  // element strides between heads
+  int group;                  // query heads per key/value head
+  float sc;                   // softmax_scale * log2(e)
+  const float* slopes;        // [n_heads] or nullptr
+  float* lse;                 // [n_heads, total] (natural log) or nullptr
+  int64_t total;
+};
+
+// 16-byte chunk c of a 128-byte LDS row r sits at chunk c ^ ((r >> 1) & 7):
+// a fragment read (32 rows, one chunk per half-wave) then hits 16 distinct
+// 16-byte bank groups in every 16-lane group.
+__device__ __forceinline__ int swz(int row, int chunk) {
+  return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
+}
+
+// Position of key r (0..63) inside V^T's row: bits 2 and 3 swapped.
+__device__ __forceinline__ int vt_pos(int r) {
+  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+}
+
+__global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
+void attn_fwd_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) char smem[2][2][kTileBytes];  // [buffer][K, V^T]
+
+  const int z = blockIdx.z;
+  const int hq = blockIdx.y;
+  // Sequence bounds clamped to [0, total]: a malformed cu_seqlens cannot move
+  // an access outside the q/k/v/out buffers.
+  const int total = int(a.total);
+  const int s0 = min(max(a.cu_seqlens[z], 0), total);
+  const int L = min(max(a.cu_seqlens[z + 1], s0), total) - s0;
+  const int q0 = blockIdx.x * kBQ;
+  if (q0 >= L) return;
+  const int hk = hq / a.group;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = lane >> 5;
+  const int col = lane & 31;
+  const int iq = q0 + wave * 32 + col;       // this lane's query (sequence position)
+  const int wq_lo = q0 + wave * 32;          // the wave's query range
+  const int wq_hi = wq_lo + 31;
+  const float sl = a.slopes != nullptr ? a.slopes[hq] * kLog2e : 0.0f;
+  const float sc = a.sc;
+
+  // Q^T operand: lane holds query iq, head dims 16kc + 8*half .. +8.
+  bf16x8 qf[4];
+  {
+    const bool ok = iq < L;
+    const uint16_t* qp = a.q + int64_t(s0 + (ok ? iq : 0)) * a.q_tok + hq * a.q_head + half * 8;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc) {
+      const u32x4 raw = ok ? *reinterpret_cast<const u32x4*>(qp + 16 * kc) : u32x4{0, 0, 0, 0};
+      qf[kc] = __builtin_bit_cast(bf16x8, raw);
+    }
+  }
+  // c_r = -slope * log2(e) * (offset of element r's key inside the block)
+  float ck[2][16];
+#pragma unroll
+  for (int b = 0; b < 2; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      ck[b][r] = -sl * float(32 * b + 8 * (r >> 2) + 4 * half + (r & 3));
+
+  // Tile loaders.  K: thread t moves rows (t >> 3) and (t >> 3) + 32, chunk t & 7
+  // (eight threads per 128-byte row).  V: thread t moves key t & 63, chunks
+  // (t >> 6) and (t >> 6) + 4, and writes them transposed.  Rows past the
+  // sequence end are zero (masked keys then meet finite values only).
+  const int k_row = tid >> 3, k_chunk = tid & 7;
+  const int v_key = tid & 63, v_chunk = tid >> 6;
+  const uint16_t* kbase = a.k + int64_t(s0) * a.k_tok + hk * a.k_head;
+  const uint16_t* vbase = a.v + int64_t(s0) * a.v_tok + hk * a.v_head;
+  u32x4 kreg[2], vreg[2];
+  auto load_tile = [&](int j0) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kr = j0 + k_row + 32 * i;
+      kreg[i] = kr < L ? *reinterpret_cast<const u32x4*>(kbase + int64_t(kr) * a.k_tok + k_chunk * 8)
+                       : u32x4{0, 0, 0, 0};
+      const int vr = j0 + v_key;
+      vreg[i] = vr < L ? *reinterpret_cast<const u32x4*>(vbase + int64_t(vr) * a.v_tok +
+                                                        (v_chunk + 4 * i) * 8)
+                       : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto store_tile = [&](int buf) {
+    char* Ks = smem[buf][0];
+    char* Vs = smem[buf][1];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kr = k_row + 32 * i;
+      *reinterpret_cast<u32x4*>(Ks + swz(kr, k_chunk)) = kreg[i];
+      const int p = vt_pos(v_key);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = (v_chunk + 4 * i) * 8 + e;
+        const uint16_t val = uint16_t(vreg[i][e >> 1] >> ((e & 1) * 16));
+        *reinterpret_cast<uint16_t*>(Vs + swz(d, p >> 3) + (p & 7) * 2) = val;
+      }
+    }
+  };
+
+  f32x16 o[2];
+  const f32x16 zero16 = {};
+  o[0] = zero16;
+  o[1] = zero16;
+  float m = -__builtin_inff();
+  float l = 0.0f;
+
+  const int nblk = (L + kBKV - 1) / kBKV;
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int n = 0; n < nblk; ++n) {
+    const int buf = n & 1;
+    const int j0 = n * kBKV;
+    if (n + 1 < nblk) load_tile(j0 + kBKV);
+    const char* Ks = smem[buf][0];
+    const char* Vs = smem[buf][1];
+
+    // S^T = K . Q^T for the two 32-key halves of the block
+    f32x16 s[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+#pragma unroll
+      for (int kc = 0; kc < 4; ++kc) {
+        const bf16x8 kf =
+            *reinterpret_cast<const bf16x8*>(Ks + swz(32 * b + col, 2 * kc + half));
+        s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kc], kc == 0 ? zero16 : s[b], 0,
+                                                       0, 0);
+      }
+    }
+
+    // t = s * sc + bias (base 2), block maximum, rescale, probabilities
+    const bool inside = j0 + kBKV <= L;
+    const bool after = inside && j0 > wq_hi;           // every key > every query
+    const bool before = inside && j0 + kBKV - 1 < wq_lo;  // every key < every query
+    float cblk;
+    float t[2][16];
+    if (after) {
+      cblk = -sl * float(j0 - iq);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t[b][r] = __builtin_fmaf(s[b][r], sc, ck[b][r]);
+    } else if (before) {
+      cblk = -sl * float(iq - j0);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) t[b][r] = __builtin_fmaf(s[b][r], sc, -ck[b][r]);
+    } else {
+      cblk = 0.0f;
+      const float di = float(iq - j0);
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kr = 32 * b + 8 * (r >> 2) + 4 * half + (r & 3);
+          const float bias = -sl * __builtin_fabsf(di - float(kr));
+          t[b][r] = j0 + kr < L ? __builtin_fmaf(s[b][r], sc, bias) : -__builtin_inff();
+        }
+    }
+    float mx = t[0][0];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, t[b][r]);
+    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = __builtin_fmaxf(m, mx + cblk);
+    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+    m = m_new;
+    const float mm = m_new - cblk;
+    float psum = 0.0f;
+    uint32_t pk[2][8];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(t[b][r] - mm);
+        const float p1 = __builtin_amdgcn_exp2f(t[b][r + 1] - mm);
+        psum += p0;
+        psum += p1;
+        pk[b][r >> 1] = pack_bf16x2(p0, p1);
+      }
+    l = l * alpha + psum;
+    if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[mb][r] *= alpha;
+    }
+
+    // O^T += V^T . P^T over the four 16-key chunks (chunk c = key block c / 2,
+    // elements 8 (c % 2) .. +8)
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 praw = {pk[c >> 1][4 * (c & 1) + 0], pk[c >> 1][4 * (c & 1) + 1],
+                          pk[c >> 1][4 * (c & 1) + 2], pk[c >> 1][4 * (c & 1) + 3]};
+      const bf16x8 pf = __builtin_bit_cast(bf16x8, praw);
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const bf16x8 vf =
+            *reinterpret_cast<const bf16x8*>(Vs + swz(32 * mb + col, 2 * c + half));
+        o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[mb], 0, 0, 0);
+      }
+    }
+
+    if (n + 1 < nblk) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  // normalise and store: lane holds query iq, dims 32mb + 8q + 4half + u
+  const float l_tot = l + __shfl_xor(l, 32, 64);
+  if (iq < L) {
+    const float inv = 1.0f / l_tot;
+    uint16_t* op = a.o + int64_t(s0 + iq) * a.o_tok + hq * a.o_head + 4 * half;
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint2 w;
+        w.x = pack_bf16x2(o[mb][4 * q] * inv, o[mb][4 * q + 1] * inv);
+        w.y = pack_bf16x2(o[mb][4 * q + 2] * inv, o[mb][4 * q + 3] * inv);
+        *reinterpret_cast<uint2*>(op + 32 * mb + 8 * q) = w;
+      }
+    if (a.lse != nullptr && half == 0)
+      a.lse[int64_t(hq) * a.total + s0 + iq] = (m + __builtin_log2f(l_tot)) * kLn2;
+  }
+}
+
+}  // namespace
+
+hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
+                           const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
+                           float* lse, const g5moe_attn_shape& s, hipStream_t st) {
+  AttnArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.cu_seqlens = cu_seqlens;
+  a.q_tok = s.q_token_stride;
+  a.k_tok = s.k_token_stride;
+  a.v_tok = s.v_token_stride;
+  a.o_tok = s.o_token_stride;
+  a.q_head = s.q_head_stride;
+  a.k_head = s.k_head_stride;
+  a.v_head = s.v_head_stride;
+  a.o_head = s.o_head_stride;
+  a.group = s.n_heads / s.n_kv_heads;
+  a.sc = softmax_scale * kLog2e;
+  a.slopes = slopes;
+  a.lse = lse;
+  a.total = s.total_tokens;
+  const dim3 grid(unsigned((s.max_seqlen + kBQ - 1) / kBQ), unsigned(s.n_heads),
+                  unsigned(s.n_seqs));
+  hipLaunchKernelGGL(attn_fwd_kernel, grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace g5moe

@@ -7,8 +7,9 @@ Reference shapes followed:
     scaling off (genet5.py:22).
   * EncoderBlock.forward (lib/blocks/encoder.py:73-90), non-fused path:
     h = h + attn(norm1(h)); h = h + ff(norm2(h)); Encoder adds a final norm
-    (encoder.py:148).  Here ff is MoEFeedForward (HIP) and attention stays in
-    PyTorch.
+    (encoder.py:148).  Here ff is MoEFeedForward (HIP) and attention is the
+    HIP varlen ALiBi kernel (genet5_amd.attention); backend "torch" keeps the
+    PyTorch SDPA composition as the reference.
   * Attention projections q/k/v/o bias-free (lib/blocks/_sdpa_att.py:68-71),
     bidirectional, scale 1/sqrt(head_dim).  No reference backend adds a
     positional bias; following the DNABERT-2 lineage this one adds
@@ -33,34 +34,49 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .. import attention
+from ..attention import alibi_slopes  # noqa: F401  (re-exported for the harness)
 from ..moe import MoEFeedForward
 from .blocks import RMSNorm
 
 
-def alibi_slopes(n_heads: int) -> List[float]:
-    """Head slopes of Press et al. (2022): a geometric sequence starting at
-    2^(-8/n) for n a power of two; otherwise the slopes of the nearest lower power
-    of two followed by every other slope of twice that count."""
-    def pow2(n):
-        start = 2.0 ** (-8.0 / n)
-        return [start ** (i + 1) for i in range(n)]
-    if n_heads & (n_heads - 1) == 0:
-        return pow2(n_heads)
-    m = 1 << int(math.floor(math.log2(n_heads)))
-    return pow2(m) + pow2(2 * m)[0::2][: n_heads - m]
-
-
 class ALiBiSelfAttention(nn.Module):
-    def __init__(self, embed_dim: int, num_heads: int):
+    """Bidirectional self-attention with symmetric ALiBi, bias-free q/k/v/o.
+
+    backend "hip" (default): the HIP kernel through genet5_amd.attention's
+    flash_attn_varlen_func (the call GeneT5's FlashAttention makes,
+    lib/blocks/_flash_att.py:76-88), forward-only, head_dim 64.
+    backend "torch": the reference composition in PyTorch, SDPA with the ALiBi
+    bias as an explicit mask, one call per packed sequence."""
+
+    def __init__(self, embed_dim: int, num_heads: int, backend: str = "hip"):
         super().__init__()
+        if backend not in ("hip", "torch"):
+            raise ValueError(f"attention backend {backend!r} is neither 'hip' nor 'torch'")
+        self.backend = backend
         self.num_heads = num_heads
         self.head_dim = embed_dim // num_heads
         self.q = nn.Linear(embed_dim, embed_dim, bias=False)
         self.k = nn.Linear(embed_dim, embed_dim, bias=False)
         self.v = nn.Linear(embed_dim, embed_dim, bias=False)
         self.o = nn.Linear(embed_dim, embed_dim, bias=False)
-        self.register_buffer("slopes", torch.tensor(alibi_slopes(num_heads)), persistent=False)
+        # fp32 slopes outside the module's buffers (a bf16 cast of the model must
+        # not round them)
+        self._slopes = alibi_slopes(num_heads)
+        self._slopes_dev: Dict[torch.device, torch.Tensor] = {}
         self._bias_cache: Dict[tuple, torch.Tensor] = {}
+        self._cu_cache: Dict[tuple, torch.Tensor] = {}
+
+    @property
+    def slopes(self) -> torch.Tensor:
+        return torch.tensor(self._slopes, dtype=torch.float32)
+
+    def slopes_on(self, device: torch.device) -> torch.Tensor:
+        t = self._slopes_dev.get(device)
+        if t is None:
+            t = torch.tensor(self._slopes, dtype=torch.float32, device=device)
+            self._slopes_dev[device] = t
+        return t
 
     def alibi_bias(self, L: int, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
         key = (L, dtype, device)
@@ -68,7 +84,7 @@ class ALiBiSelfAttention(nn.Module):
         if b is None:
             pos = torch.arange(L, device=device, dtype=torch.float32)
             dist = (pos[None, :] - pos[:, None]).abs()
-            b = (-self.slopes.to(device)[:, None, None] * dist[None]).to(dtype).unsqueeze(0)
+            b = (-self.slopes_on(device)[:, None, None] * dist[None]).to(dtype).unsqueeze(0)
             self._bias_cache = {key: b}  # keep only the latest length
         return b
 
@@ -81,7 +97,31 @@ class ALiBiSelfAttention(nn.Module):
                                              scale=1.0 / math.sqrt(self.head_dim))
         return self.o(out.transpose(1, 2).reshape(B, L, D))
 
+    def _attend_hip(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor]) -> torch.Tensor:
+        B, L, D = h.shape
+        H, hd = self.num_heads, self.head_dim
+        q = self.q(h).view(B * L, H, hd)
+        k = self.k(h).view(B * L, H, hd)
+        v = self.v(h).view(B * L, H, hd)
+        if cu_seqlens is None:
+            key = (B, L, h.device)
+            cu = self._cu_cache.get(key)
+            if cu is None:
+                cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=h.device)
+                self._cu_cache = {key: cu}
+            max_len = L
+        else:
+            bounds = cu_seqlens.tolist()
+            cu = torch.tensor(bounds, dtype=torch.int32, device=h.device)
+            max_len = max((b - a for a, b in zip(bounds[:-1], bounds[1:])), default=0)
+        out = attention.flash_attn_varlen_func(q, k, v, cu, cu, max_len, max_len,
+                                               softmax_scale=1.0 / math.sqrt(hd),
+                                               alibi_slopes=self.slopes_on(h.device))
+        return self.o(out.view(B, L, D))
+
     def forward(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.backend == "hip":
+            return self._attend_hip(h, cu_seqlens)
         if cu_seqlens is None:
             return self._attend(h)
         # packed [1, T, D]: attend within each sequence
@@ -97,10 +137,10 @@ class MoEEncoderBlock(nn.Module):
     encoder.py:84-89 in torch around the MoE module."""
 
     def __init__(self, embed_dim: int, num_heads: int, ff_dim: int, num_experts: int = 16,
-                 top_k: int = 2):
+                 top_k: int = 2, attention_backend: str = "hip"):
         super().__init__()
         self.norm1 = RMSNorm(embed_dim)
-        self.self_attn = ALiBiSelfAttention(embed_dim, num_heads)
+        self.self_attn = ALiBiSelfAttention(embed_dim, num_heads, attention_backend)
         self.norm2 = RMSNorm(embed_dim)
         self.ff = MoEFeedForward(embed_dim, ff_dim, 0.0, "silu", num_experts, top_k)
         self.fused = True
@@ -119,11 +159,11 @@ class GeneT5MoE(nn.Module):
 
     def __init__(self, vocab_size: int = 4096, embed_dim: int = 768, num_layers: int = 12,
                  num_heads: int = 12, ff_dim: int = 3072, num_experts: int = 16,
-                 top_k: int = 2):
+                 top_k: int = 2, attention_backend: str = "hip"):
         super().__init__()
         self.embed = nn.Embedding(vocab_size, embed_dim)
         self.layers = nn.ModuleList([
-            MoEEncoderBlock(embed_dim, num_heads, ff_dim, num_experts, top_k)
+            MoEEncoderBlock(embed_dim, num_heads, ff_dim, num_experts, top_k, attention_backend)
             for _ in range(num_layers)])
         self.final_norm = RMSNorm(embed_dim)
         self.lm_head = nn.Linear(embed_dim, vocab_size, bias=False)
@@ -132,6 +172,13 @@ class GeneT5MoE(nn.Module):
     def set_fused(self, fused: bool) -> "GeneT5MoE":
         for layer in self.layers:
             layer.fused = fused
+        return self
+
+    def set_attention_backend(self, backend: str) -> "GeneT5MoE":
+        if backend not in ("hip", "torch"):
+            raise ValueError(f"attention backend {backend!r} is neither 'hip' nor 'torch'")
+        for layer in self.layers:
+            layer.self_attn.backend = backend
         return self
 
     def forward(self, input_ids: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None):

@@ -267,6 +267,51 @@ g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bia
                            int32_t* offsets, int32_t* perm, int32_t* inv_pos, void* ws,
                            const g5moe_shape* shape, void* stream);
 
+/* ---- Attention ----------------------------------------------------------------
+ * Varlen bidirectional attention with ALiBi: the encoder block's self-attention
+ * core in front of the MoE.  Replaces flash_attn_varlen_func(q, k, v,
+ * cu_seqlens, cu_seqlens, max_seqlen, max_seqlen, dropout_p=0,
+ * softmax_scale, causal=False) as FlashAttention.forward calls it
+ * (lib/blocks/_flash_att.py:76-88; fixed-length flash_attn_func at :90-96 is
+ * the case of equal-length sequences), with flash-attn's alibi_slopes bias.
+ *
+ * Shape of one call.  Element (token t, head h, dim j) of q sits at
+ * q + t * q_token_stride + h * q_head_stride + j (likewise k, v, out); head
+ * dims are contiguous, every stride is in elements and a multiple of 8.
+ *   n_seqs >= 0; max_seqlen >= every cu_seqlens[i+1] - cu_seqlens[i] (as
+ *   flash-attn requires; longer sequences are not computed past it);
+ *   total_tokens = cu_seqlens[n_seqs] (rows of softmax_lse);
+ *   n_heads >= 1, n_kv_heads >= 1 dividing n_heads (query head h reads key/
+ *   value head h / (n_heads / n_kv_heads)); head_dim = 64. */
+typedef struct g5moe_attn_shape {
+  int32_t n_seqs;
+  int32_t max_seqlen;
+  int64_t total_tokens;
+  int32_t n_heads;
+  int32_t n_kv_heads;
+  int32_t head_dim;
+  int32_t reserved; /* must be 0 */
+  int64_t q_token_stride, q_head_stride;
+  int64_t k_token_stride, k_head_stride;
+  int64_t v_token_stride, v_head_stride;
+  int64_t o_token_stride, o_head_stride;
+} g5moe_attn_shape;
+
+/* out[t, h] = sum_j softmax_j(q[t,h] . k[j,h'] * softmax_scale
+ *                             - alibi_slopes[h] * |i - j|) v[j, h']
+ * over the keys j of t's own sequence (i, j sequence-local positions).
+ *   q, k, v, out : bf16 (layout above);  cu_seqlens : int32 [n_seqs + 1],
+ *   non-decreasing from 0;  alibi_slopes : fp32 [n_heads] or NULL (no bias);
+ *   softmax_lse : fp32 [n_heads, total_tokens] out (natural-log sum of the
+ *   exponentials of each row, flash-attn's softmax_lse), or NULL.
+ * Scores, softmax and the output sum are fp32; the probabilities enter the
+ * output product as bf16 (as in flash-attn); one rounding to bf16 at the end.
+ * The summation order is fixed, so results are deterministic. */
+g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, void* out,
+                                   const int32_t* cu_seqlens, const float* alibi_slopes,
+                                   float softmax_scale, float* softmax_lse,
+                                   const g5moe_attn_shape* shape, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -9,8 +9,10 @@ benchmark names: the expert body is FeedForward.forward
 (lib/blocks/_component.py:48-52) with activation 'silu' (:31) — gate = wi_0,
 up = wi_1 (:42-43, split order lib/model/build.py:30-34) — and the router is
 16 experts top-2 (README.md:12).  See oracle/moe_oracle.py for each function's
-pin.
+pin.  oracle/attn_oracle.py restates the encoder's varlen ALiBi attention
+(flash_attn_varlen_func as lib/blocks/_flash_att.py:76-88 calls it).
 """
+from .attn_oracle import attention_varlen  # noqa: F401
 from .moe_oracle import (  # noqa: F401
     add_rmsnorm,
     add_rmsnorm_np,

@@ -36,7 +36,7 @@ def explicit_attention(x, attn):
 
 def test_alibi_attention_matches_explicit_softmax():
     torch.manual_seed(0)
-    attn = encoder.ALiBiSelfAttention(32, 4)
+    attn = encoder.ALiBiSelfAttention(32, 4, backend="torch")
     x = torch.randn(2, 9, 32)
     got = attn(x)
     ref = explicit_attention(x, attn)
@@ -48,7 +48,7 @@ def test_alibi_attention_matches_explicit_softmax():
 
 def test_packed_attention_is_block_diagonal():
     torch.manual_seed(1)
-    attn = encoder.ALiBiSelfAttention(32, 4)
+    attn = encoder.ALiBiSelfAttention(32, 4, backend="torch")
     a, b = torch.randn(1, 5, 32), torch.randn(1, 7, 32)
     packed = attn(torch.cat([a, b], 1), torch.tensor([0, 5, 12]))
     assert torch.allclose(packed[:, :5], attn(a), atol=1e-6)
@@ -107,3 +107,21 @@ def test_config4_packing():
     assert c.cu_seqlens[-1] == 45500 and c.x.shape == (1, 45500, 768)
     assert (lens[:-1] >= 1000).all() and (lens <= 9000).all()
     assert c.layer_seeds == list(range(12))
+
+
+def test_attention_backend_choice_is_explicit():
+    import pytest
+    with pytest.raises(ValueError, match="backend"):
+        encoder.ALiBiSelfAttention(32, 4, backend="eager")
+    m = encoder.GeneT5MoE(vocab_size=64, embed_dim=128, num_layers=2, num_heads=2, ff_dim=256)
+    assert all(l.self_attn.backend == "hip" for l in m.layers)
+    m.set_attention_backend("torch")
+    assert all(l.self_attn.backend == "torch" for l in m.layers)
+    # the HIP backend never runs on CPU tensors (no silent fallback)
+    m.set_attention_backend("hip")
+    with pytest.raises(RuntimeError, match="GPU only"), torch.no_grad():
+        m.layers[0].self_attn(torch.zeros(1, 4, 128))
+    # slopes stay fp32 through a bf16 cast of the model
+    m = m.to(torch.bfloat16)
+    assert m.layers[0].self_attn.slopes.dtype == torch.float32
+    assert m.layers[0].self_attn.slopes[1].item() == 2.0 ** -8
