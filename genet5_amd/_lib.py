@@ -41,6 +41,7 @@ EXPORTED = (
     "g5moe_input_grad",
     "g5moe_pad_transpose",
     "g5moe_forward",
+    "g5moe_attn_workspace_size",
     "g5moe_attn_varlen_fwd",
 )
 
@@ -119,7 +120,9 @@ _SIGS = {
                             ctypes.c_int),
     "g5moe_input_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
-    "g5moe_attn_varlen_fwd": ([_P, _P, _P, _P, _P, _P, ctypes.c_float, _P,
+    "g5moe_attn_workspace_size": ([ctypes.POINTER(AttnShape), ctypes.POINTER(ctypes.c_size_t)],
+                                  ctypes.c_int),
+    "g5moe_attn_varlen_fwd": ([_P, _P, _P, _P, _P, _P, ctypes.c_float, _P, _P,
                                ctypes.POINTER(AttnShape), _P], ctypes.c_int),
 }
 

@@ -66,11 +66,16 @@ def _check_qkv(t: torch.Tensor, name: str, total: int, heads: int, dev: torch.de
 
 def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     cu_seqlens: torch.Tensor, max_seqlen: int, softmax_scale: float,
-                    alibi_slopes: Optional[torch.Tensor] = None, return_lse: bool = False):
+                    alibi_slopes: Optional[torch.Tensor] = None, return_lse: bool = False,
+                    skip_negligible: bool = True):
     """g5moe_attn_varlen_fwd on the current stream.  q [T, H, 64], k/v [T, Hkv, 64]
     bf16 (head dims contiguous, other strides free); cu_seqlens int32 [n + 1] on
     the GPU; alibi_slopes fp32 [H] or None.  Returns out [T, H, 64] (and the
-    natural-log softmax_lse [H, T] fp32 when return_lse)."""
+    natural-log softmax_lse [H, T] fp32 when return_lse).
+
+    skip_negligible (with ALiBi): leave out the key blocks whose probabilities are
+    provably below 2^-64 of each row's largest (a key-norm bound against the ALiBi
+    distance); the result equals the dense computation to fp32 rounding."""
     dev = _check_device(q)
     T, H = q.shape[0], q.shape[1]
     Hkv = k.shape[1] if k.dim() == 3 else -1
@@ -93,9 +98,14 @@ def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         cu_seqlens.numel() - 1, int(max_seqlen), T, H, Hkv, HEAD_DIM, 0,
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1))
+    ws = None
+    if skip_negligible and alibi_slopes is not None:
+        n = ctypes.c_size_t(0)
+        _lib.call("g5moe_attn_workspace_size", ctypes.byref(shape), ctypes.byref(n))
+        ws = torch.empty(int(n.value), dtype=torch.uint8, device=dev)
     _lib.call("g5moe_attn_varlen_fwd", _ptr(q), _ptr(k), _ptr(v), _ptr(out), _ptr(cu_seqlens),
-              _ptr(alibi_slopes), ctypes.c_float(softmax_scale), _ptr(lse), ctypes.byref(shape),
-              _stream(dev))
+              _ptr(alibi_slopes), ctypes.c_float(softmax_scale), _ptr(lse), _ptr(ws),
+              ctypes.byref(shape), _stream(dev))
     return (out, lse) if return_lse else out
 
 

@@ -400,10 +400,7 @@ g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bia
   return g5moe_combine(y_perm, inv_pos, topk_w, y, shape, stream);
 }
 
-g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, void* out,
-                                   const int32_t* cu_seqlens, const float* alibi_slopes,
-                                   float softmax_scale, float* softmax_lse,
-                                   const g5moe_attn_shape* shape, void* stream) {
+static g5moe_status check_attn_shape(const g5moe_attn_shape* shape) {
   G5_NONNULL(shape);
   const g5moe_attn_shape& s = *shape;
   if (s.reserved != 0) return fail(G5MOE_ERR_INVALID_ARG, "attn shape.reserved must be 0");
@@ -419,9 +416,6 @@ g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, 
   if (s.total_tokens > INT32_MAX / 2)
     return fail(G5MOE_ERR_UNSUPPORTED, "total_tokens %lld beyond the int32 position range",
                 (long long)s.total_tokens);
-  if (!(softmax_scale == softmax_scale) || softmax_scale == __builtin_inff() ||
-      softmax_scale == -__builtin_inff())
-    return fail(G5MOE_ERR_INVALID_ARG, "softmax_scale must be finite");
   const int64_t strides[8] = {s.q_token_stride, s.q_head_stride, s.k_token_stride,
                               s.k_head_stride,  s.v_token_stride, s.v_head_stride,
                               s.o_token_stride, s.o_head_stride};
@@ -430,6 +424,25 @@ g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, 
       return fail(G5MOE_ERR_UNSUPPORTED,
                   "every stride must be a non-negative multiple of 8 elements (stride %d = %lld)",
                   i, (long long)strides[i]);
+  return G5MOE_OK;
+}
+
+g5moe_status g5moe_attn_workspace_size(const g5moe_attn_shape* shape, size_t* bytes) {
+  G5_CHECK(check_attn_shape(shape));
+  G5_NONNULL(bytes);
+  *bytes = align256(size_t(shape->n_seqs) * size_t(shape->n_kv_heads) * 4);
+  return G5MOE_OK;
+}
+
+g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, void* out,
+                                   const int32_t* cu_seqlens, const float* alibi_slopes,
+                                   float softmax_scale, float* softmax_lse, void* ws,
+                                   const g5moe_attn_shape* shape, void* stream) {
+  G5_CHECK(check_attn_shape(shape));
+  const g5moe_attn_shape& s = *shape;
+  if (!(softmax_scale == softmax_scale) || softmax_scale == __builtin_inff() ||
+      softmax_scale == -__builtin_inff())
+    return fail(G5MOE_ERR_INVALID_ARG, "softmax_scale must be finite");
   if (s.n_seqs == 0 || s.max_seqlen == 0) return G5MOE_OK;
   G5_NONNULL(q);
   G5_NONNULL(k);
@@ -443,8 +456,8 @@ g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, 
   return hip_status(launch_attn_fwd(static_cast<const uint16_t*>(q),
                                     static_cast<const uint16_t*>(k),
                                     static_cast<const uint16_t*>(v), static_cast<uint16_t*>(out),
-                                    cu_seqlens, alibi_slopes, softmax_scale, softmax_lse, s,
-                                    as_stream(stream)),
+                                    cu_seqlens, alibi_slopes, softmax_scale, softmax_lse,
+                                    static_cast<float*>(ws), s, as_stream(stream)),
                     "g5moe_attn_varlen_fwd");
 }
 

@@ -26,6 +26,21 @@
 // the one those elements carry: key r at position r with bits 2 and 3
 // swapped.  The LDS copy of V is written transposed in that order.
 //
+// LDS rows are padded to 144 bytes (K rows and V^T rows of 64 bf16): the 16
+// rows a 16-lane group of a fragment read touches then start 36 banks apart
+// (mod 64), which covers all 64 banks with 16-byte reads, and every tile write
+// is a base address plus an immediate offset.
+//
+// Block skipping under ALiBi: with key norms bounded by KM (per sequence and
+// key/value head, from a pre-pass) and the query norms of the workgroup by NQ,
+// every score obeys |s| <= NQ * KM (Cauchy-Schwarz), so a key at distance
+// > W = (2 * scale * log2(e) * NQ * KM + 64) / (slope * log2(e)) from every
+// query of the workgroup has p < 2^-64 relative to the row's largest term
+// (the diagonal key is always computed and bounds the row maximum from
+// below).  The workgroup therefore visits only the key blocks within W of its
+// queries; the skipped probability mass is below 2^-51 of each row's sum, so
+// the result equals the dense computation to fp32 rounding.
+//
 // Softmax in base 2: t = s * scale * log2(e) + bias * log2(e), p = 2^(t - m).
 // On a key block that lies entirely on one side of every query of the wave
 // and inside the sequence, bias = c_blk +/- c_r with c_r = -slope * log2(e) *
@@ -45,8 +60,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kHeadDim = 64;
 constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
 constexpr int kBKV = 64;   // keys per LDS block
-constexpr int kRowBytes = kHeadDim * 2;           // 128 bytes per K row / V^T row
-constexpr int kTileBytes = kBKV * kRowBytes;      // 8 KB
+constexpr int kRowBytes = kHeadDim * 2 + 16;      // 144: padded K row / V^T row
+constexpr int kTileBytes = kBKV * kRowBytes;      // 9 KB
+constexpr float kSkipMargin = 64.0f;              // skipped keys have p < 2^-64
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -62,15 +78,13 @@ struct AttnArgs {
   float sc;                   // softmax_scale * log2(e)
   const float* slopes;        // [n_heads] or nullptr
   float* lse;                 // [n_heads, total] (natural log) or nullptr
+  const float* kmax;          // [n_seqs, n_kv_heads] largest key norm, or nullptr (dense)
+  int n_kv_heads;
   int64_t total;
 };
 
-// 16-byte chunk c of a 128-byte LDS row r sits at chunk c ^ ((r >> 1) & 7):
-// a fragment read (32 rows, one chunk per half-wave) then hits 16 distinct
-// 16-byte bank groups in every 16-lane group.
-__device__ __forceinline__ int swz(int row, int chunk) {
-  return row * kRowBytes + ((chunk ^ ((row >> 1) & 7)) << 4);
-}
+// Byte offset of 16-byte chunk c of LDS row r.
+__device__ __forceinline__ int lds_off(int row, int chunk) { return row * kRowBytes + chunk * 16; }
 
 // Position of key r (0..63) inside V^T's row: bits 2 and 3 swapped.
 __device__ __forceinline__ int vt_pos(int r) {
@@ -114,6 +128,37 @@ void attn_fwd_kernel(AttnArgs a) {
       qf[kc] = __builtin_bit_cast(bf16x8, raw);
     }
   }
+  // Key blocks this workgroup visits: [n_lo, n_hi] (all of them without ALiBi
+  // or without key norms).
+  const int nblk = (L + kBKV - 1) / kBKV;
+  int n_lo = 0, n_hi = nblk - 1;
+  if (a.kmax != nullptr && sl > 0.0f) {
+    __shared__ float nq_wave[4];
+    float ss = 0.0f;
+#pragma unroll
+    for (int kc = 0; kc < 4; ++kc)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float x = float(qf[kc][e]);
+        ss = __builtin_fmaf(x, x, ss);
+      }
+    ss += __shfl_xor(ss, 32, 64);
+#pragma unroll
+    for (int bit = 16; bit >= 1; bit >>= 1) ss = __builtin_fmaxf(ss, __shfl_xor(ss, bit, 64));
+    if (lane == 0) nq_wave[wave] = ss;
+    __syncthreads();
+    const float nq2 = __builtin_fmaxf(__builtin_fmaxf(nq_wave[0], nq_wave[1]),
+                                      __builtin_fmaxf(nq_wave[2], nq_wave[3]));
+    const float km = a.kmax[int64_t(z) * a.n_kv_heads + hk];
+    const float w = (2.0f * sc * __builtin_sqrtf(nq2) * km + kSkipMargin) / sl;
+    if (w < 1.0e9f) {  // false for inf / NaN: visit every block
+      const int wi = int(w);
+      const int q_hi = min(q0 + kBQ, L) - 1;
+      n_lo = max(0, (q0 - wi) / kBKV);
+      n_hi = min(nblk - 1, (q_hi + wi) / kBKV);
+    }
+  }
+
   // c_r = -slope * log2(e) * (offset of element r's key inside the block)
   float ck[2][16];
 #pragma unroll
@@ -146,16 +191,15 @@ void attn_fwd_kernel(AttnArgs a) {
   auto store_tile = [&](int buf) {
     char* Ks = smem[buf][0];
     char* Vs = smem[buf][1];
+    char* vrow = Vs + v_chunk * 8 * kRowBytes + vt_pos(v_key) * 2;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int kr = k_row + 32 * i;
-      *reinterpret_cast<u32x4*>(Ks + swz(kr, k_chunk)) = kreg[i];
-      const int p = vt_pos(v_key);
+      *reinterpret_cast<u32x4*>(Ks + lds_off(kr, k_chunk)) = kreg[i];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = (v_chunk + 4 * i) * 8 + e;
         const uint16_t val = uint16_t(vreg[i][e >> 1] >> ((e & 1) * 16));
-        *reinterpret_cast<uint16_t*>(Vs + swz(d, p >> 3) + (p & 7) * 2) = val;
+        *reinterpret_cast<uint16_t*>(vrow + (32 * i + e) * kRowBytes) = val;
       }
     }
   };
@@ -167,15 +211,14 @@ void attn_fwd_kernel(AttnArgs a) {
   float m = -__builtin_inff();
   float l = 0.0f;
 
-  const int nblk = (L + kBKV - 1) / kBKV;
-  load_tile(0);
-  store_tile(0);
+  load_tile(n_lo * kBKV);
+  store_tile(n_lo & 1);
   __syncthreads();
 
-  for (int n = 0; n < nblk; ++n) {
+  for (int n = n_lo; n <= n_hi; ++n) {
     const int buf = n & 1;
     const int j0 = n * kBKV;
-    if (n + 1 < nblk) load_tile(j0 + kBKV);
+    if (n < n_hi) load_tile(j0 + kBKV);
     const char* Ks = smem[buf][0];
     const char* Vs = smem[buf][1];
 
@@ -186,7 +229,7 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int kc = 0; kc < 4; ++kc) {
         const bf16x8 kf =
-            *reinterpret_cast<const bf16x8*>(Ks + swz(32 * b + col, 2 * kc + half));
+            *reinterpret_cast<const bf16x8*>(Ks + lds_off(32 * b + col, 2 * kc + half));
         s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kc], kc == 0 ? zero16 : s[b], 0,
                                                        0, 0);
       }
@@ -262,12 +305,12 @@ void attn_fwd_kernel(AttnArgs a) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         const bf16x8 vf =
-            *reinterpret_cast<const bf16x8*>(Vs + swz(32 * mb + col, 2 * c + half));
+            *reinterpret_cast<const bf16x8*>(Vs + lds_off(32 * mb + col, 2 * c + half));
         o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[mb], 0, 0, 0);
       }
     }
 
-    if (n + 1 < nblk) store_tile(buf ^ 1);
+    if (n < n_hi) store_tile(buf ^ 1);
     __syncthreads();
   }
 
@@ -290,11 +333,62 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
+// Largest key norm of each (sequence, key/value head): kmax[z * Hkv + h] =
+// max_j ||k[j, h]|| over the sequence's tokens (fp32).  One workgroup per
+// (sequence, head); eight lanes per 128-byte key row.
+__global__ __launch_bounds__(256) void key_norm_max_kernel(const uint16_t* __restrict__ k,
+                                                           const int32_t* cu_seqlens,
+                                                           int64_t k_tok, int64_t k_head,
+                                                           int64_t total, int n_kv_heads,
+                                                           float* kmax) {
+  __shared__ float red[4];
+  const int z = blockIdx.y, h = blockIdx.x;
+  const int tot = int(total);
+  const int s0 = min(max(cu_seqlens[z], 0), tot);
+  const int L = min(max(cu_seqlens[z + 1], s0), tot) - s0;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int chunk = tid & 7;
+  float best = 0.0f;
+  for (int r = tid >> 3; r < L; r += 32) {
+    const u32x4 raw = *reinterpret_cast<const u32x4*>(k + int64_t(s0 + r) * k_tok + h * k_head +
+                                                      chunk * 8);
+    float ss = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float lo = bf16_bits_to_f32(raw[w] & 0xffffu);
+      const float hi = bf16_bits_to_f32(raw[w] >> 16);
+      ss = __builtin_fmaf(lo, lo, ss);
+      ss = __builtin_fmaf(hi, hi, ss);
+    }
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    ss += __shfl_xor(ss, 4, 64);
+    best = __builtin_fmaxf(best, ss);
+  }
+#pragma unroll
+  for (int bit = 8; bit <= 32; bit <<= 1) best = __builtin_fmaxf(best, __shfl_xor(best, bit, 64));
+  if (lane == 0) red[tid >> 6] = best;
+  __syncthreads();
+  if (tid == 0) {
+    const float m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    kmax[int64_t(z) * n_kv_heads + h] = __builtin_sqrtf(m);
+  }
+}
+
 }  // namespace
 
 hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
-                           float* lse, const g5moe_attn_shape& s, hipStream_t st) {
+                           float* lse, float* kmax_ws, const g5moe_attn_shape& s,
+                           hipStream_t st) {
+  const bool skip = kmax_ws != nullptr && slopes != nullptr;
+  if (skip) {
+    hipLaunchKernelGGL(key_norm_max_kernel, dim3(unsigned(s.n_kv_heads), unsigned(s.n_seqs)),
+                       dim3(256), 0, st, k, cu_seqlens, s.k_token_stride, s.k_head_stride,
+                       s.total_tokens, int(s.n_kv_heads), kmax_ws);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   AttnArgs a;
   a.q = q;
   a.k = k;
@@ -313,6 +407,8 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
   a.sc = softmax_scale * kLog2e;
   a.slopes = slopes;
   a.lse = lse;
+  a.kmax = skip ? kmax_ws : nullptr;
+  a.n_kv_heads = s.n_kv_heads;
   a.total = s.total_tokens;
   const dim3 grid(unsigned((s.max_seqlen + kBQ - 1) / kBQ), unsigned(s.n_heads),
                   unsigned(s.n_seqs));

@@ -99,7 +99,8 @@ hipError_t launch_pack_gate_up(const uint16_t* wg, const uint16_t* wu, uint16_t*
 hipError_t launch_cast_f32_bf16(const float* x, uint16_t* xb, int64_t n, hipStream_t st);
 hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
-                           float* lse, const g5moe_attn_shape& s, hipStream_t st);
+                           float* lse, float* kmax_ws, const g5moe_attn_shape& s,
+                           hipStream_t st);
 
 // ---- device helpers -------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {

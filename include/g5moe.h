@@ -297,19 +297,30 @@ typedef struct g5moe_attn_shape {
   int64_t o_token_stride, o_head_stride;
 } g5moe_attn_shape;
 
+/* Bytes of workspace g5moe_attn_varlen_fwd uses for block skipping
+ * (n_seqs * n_kv_heads fp32 key-norm bounds, 256-byte aligned). */
+g5moe_status g5moe_attn_workspace_size(const g5moe_attn_shape* shape, size_t* bytes);
+
 /* out[t, h] = sum_j softmax_j(q[t,h] . k[j,h'] * softmax_scale
  *                             - alibi_slopes[h] * |i - j|) v[j, h']
  * over the keys j of t's own sequence (i, j sequence-local positions).
  *   q, k, v, out : bf16 (layout above);  cu_seqlens : int32 [n_seqs + 1],
- *   non-decreasing from 0;  alibi_slopes : fp32 [n_heads] or NULL (no bias);
+ *   non-decreasing from 0 (entries are clamped to [0, total_tokens]);
+ *   alibi_slopes : fp32 [n_heads] or NULL (no bias);
  *   softmax_lse : fp32 [n_heads, total_tokens] out (natural-log sum of the
- *   exponentials of each row, flash-attn's softmax_lse), or NULL.
+ *   exponentials of each row, flash-attn's softmax_lse), or NULL;
+ *   ws : g5moe_attn_workspace_size() bytes, or NULL.  With ALiBi and a
+ *   workspace, key blocks whose every probability is provably below 2^-64 of
+ *   the row's largest (Cauchy-Schwarz on the key and query norms against the
+ *   ALiBi distance) are not computed: the skipped mass is below 2^-51 of each
+ *   row's sum, so the result equals the dense computation (ws = NULL) to fp32
+ *   rounding.
  * Scores, softmax and the output sum are fp32; the probabilities enter the
  * output product as bf16 (as in flash-attn); one rounding to bf16 at the end.
  * The summation order is fixed, so results are deterministic. */
 g5moe_status g5moe_attn_varlen_fwd(const void* q, const void* k, const void* v, void* out,
                                    const int32_t* cu_seqlens, const float* alibi_slopes,
-                                   float softmax_scale, float* softmax_lse,
+                                   float softmax_scale, float* softmax_lse, void* ws,
                                    const g5moe_attn_shape* shape, void* stream);
 
 #ifdef __cplusplus

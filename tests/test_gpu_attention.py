@@ -209,3 +209,22 @@ def test_harness_attention_backends_agree(cuda_device):
         mx, mean = errs(got, ref.double().cpu().numpy())
         print(f"harness attention hip vs torch: max_rel={mx:.2e} mean_rel={mean:.2e}", flush=True)
         assert mx <= 2e-2 and mean <= 8e-3, (mx, mean)
+
+
+@pytest.mark.parametrize("scale", [0.3, 1.0])
+def test_block_skipping_equals_dense(cuda_device, scale):
+    """With ALiBi, the blocks the key-norm bound leaves out carry less than 2^-51 of
+    each row's probability mass: outputs and lse equal the dense computation bit for
+    bit on config-5-shaped inputs (and the oracle within the tolerance)."""
+    B, L, H = 8, 4550, 12
+    cu = [i * L for i in range(B + 1)]
+    q, k, v = make(cu, H, H, seed=21, scale=scale)
+    cu_t = torch.tensor(cu, dtype=torch.int32, device=cuda_device)
+    sl = torch.tensor(alibi_slopes(H), dtype=torch.float32, device=cuda_device)
+    out_s, lse_s = attention.attn_varlen_fwd(q, k, v, cu_t, L, 0.125, sl, return_lse=True,
+                                             skip_negligible=True)
+    out_d, lse_d = attention.attn_varlen_fwd(q, k, v, cu_t, L, 0.125, sl, return_lse=True,
+                                             skip_negligible=False)
+    torch.cuda.synchronize()
+    assert torch.equal(out_s, out_d)
+    assert torch.equal(lse_s, lse_d)

@@ -159,28 +159,33 @@ def attn_shape(**kw):
 def test_attn_invalid_shapes_rejected(g5lib, kw, code, msg):
     s = attn_shape(**kw)
     st = g5lib.g5moe_attn_varlen_fwd(None, None, None, None, None, None, ctypes.c_float(0.125),
-                                     None, ctypes.byref(s), None)
+                                     None, None, ctypes.byref(s), None)
     err = g5lib.g5moe_last_error().decode()
     assert st == code and msg in err, (st, err)
+    n = ctypes.c_size_t(0)
+    assert g5lib.g5moe_attn_workspace_size(ctypes.byref(s), ctypes.byref(n)) == code
 
 
 def test_attn_null_and_misaligned_pointers_rejected(g5lib):
     s = attn_shape()
     st = g5lib.g5moe_attn_varlen_fwd(None, None, None, None, None, None, ctypes.c_float(0.125),
-                                     None, ctypes.byref(s), None)
+                                     None, None, ctypes.byref(s), None)
     assert st == 1 and "NULL" in g5lib.g5moe_last_error().decode()
+    n = ctypes.c_size_t(0)
+    assert g5lib.g5moe_attn_workspace_size(ctypes.byref(s), ctypes.byref(n)) == 0
+    assert n.value == 256  # 2 sequences x 12 heads x 4 bytes, 256-byte aligned
     p = ctypes.c_void_p(0x1000)
     bad = ctypes.c_void_p(0x1008)
-    st = g5lib.g5moe_attn_varlen_fwd(p, p, bad, p, p, None, ctypes.c_float(0.125), None,
+    st = g5lib.g5moe_attn_varlen_fwd(p, p, bad, p, p, None, ctypes.c_float(0.125), None, None,
                                      ctypes.byref(s), None)
     assert st == 2 and "aligned" in g5lib.g5moe_last_error().decode()
     st = g5lib.g5moe_attn_varlen_fwd(p, p, p, p, p, None, ctypes.c_float(float("nan")), None,
-                                     ctypes.byref(s), None)
+                                     None, ctypes.byref(s), None)
     assert st == 1 and "finite" in g5lib.g5moe_last_error().decode()
     # nothing to do: no pointer is touched
     s0 = attn_shape(n_seqs=0)
     assert g5lib.g5moe_attn_varlen_fwd(None, None, None, None, None, None, ctypes.c_float(1.0),
-                                       None, ctypes.byref(s0), None) == 0
+                                       None, None, ctypes.byref(s0), None) == 0
 
 
 def test_attn_wrappers_refuse_cpu_and_unsupported_modes():
