@@ -430,7 +430,7 @@ static g5moe_status check_attn_shape(const g5moe_attn_shape* shape) {
 g5moe_status g5moe_attn_workspace_size(const g5moe_attn_shape* shape, size_t* bytes) {
   G5_CHECK(check_attn_shape(shape));
   G5_NONNULL(bytes);
-  *bytes = align256(size_t(shape->n_seqs) * size_t(shape->n_kv_heads) * 4);
+  *bytes = align256(size_t((shape->total_tokens + 63) / 64) * size_t(shape->n_kv_heads) * 4);
   return G5MOE_OK;
 }
 

@@ -31,8 +31,9 @@
 // (mod 64), which covers all 64 banks with 16-byte reads, and every tile write
 // is a base address plus an immediate offset.
 //
-// Block skipping under ALiBi: with key norms bounded by KM (per sequence and
-// key/value head, from a pre-pass) and the query norms of the workgroup by NQ,
+// Block skipping under ALiBi: with key norms bounded by KM (the largest of the
+// per-64-token-block maxima a pre-pass writes, over the blocks that cover the
+// sequence) and the query norms of the workgroup by NQ,
 // every score obeys |s| <= NQ * KM (Cauchy-Schwarz), so a key at distance
 // > W = (2 * scale * log2(e) * NQ * KM + 64) / (slope * log2(e)) from every
 // query of the workgroup has p < 2^-64 relative to the row's largest term
@@ -78,8 +79,9 @@ struct AttnArgs {
   float sc;                   // softmax_scale * log2(e)
   const float* slopes;        // [n_heads] or nullptr
   float* lse;                 // [n_heads, total] (natural log) or nullptr
-  const float* kmax;          // [n_seqs, n_kv_heads] largest key norm, or nullptr (dense)
-  int n_kv_heads;
+  const float* kmax;          // [n_kv_heads, ceil(total / 64)] largest key norm of each
+                              // 64-token block, or nullptr (dense)
+  int n_kblk;                 // ceil(total / 64)
   int64_t total;
 };
 
@@ -133,7 +135,13 @@ void attn_fwd_kernel(AttnArgs a) {
   const int nblk = (L + kBKV - 1) / kBKV;
   int n_lo = 0, n_hi = nblk - 1;
   if (a.kmax != nullptr && sl > 0.0f) {
-    __shared__ float nq_wave[4];
+    __shared__ float red[8];
+    // largest key norm over the 64-token blocks that cover the sequence
+    float km = 0.0f;
+    const float* bm = a.kmax + int64_t(hk) * a.n_kblk;
+    for (int i = (s0 >> 6) + tid; i <= ((s0 + L - 1) >> 6); i += 256) km = __builtin_fmaxf(km, bm[i]);
+#pragma unroll
+    for (int bit = 32; bit >= 1; bit >>= 1) km = __builtin_fmaxf(km, __shfl_xor(km, bit, 64));
     float ss = 0.0f;
 #pragma unroll
     for (int kc = 0; kc < 4; ++kc)
@@ -145,12 +153,14 @@ void attn_fwd_kernel(AttnArgs a) {
     ss += __shfl_xor(ss, 32, 64);
 #pragma unroll
     for (int bit = 16; bit >= 1; bit >>= 1) ss = __builtin_fmaxf(ss, __shfl_xor(ss, bit, 64));
-    if (lane == 0) nq_wave[wave] = ss;
+    if (lane == 0) {
+      red[wave] = ss;
+      red[4 + wave] = km;
+    }
     __syncthreads();
-    const float nq2 = __builtin_fmaxf(__builtin_fmaxf(nq_wave[0], nq_wave[1]),
-                                      __builtin_fmaxf(nq_wave[2], nq_wave[3]));
-    const float km = a.kmax[int64_t(z) * a.n_kv_heads + hk];
-    const float w = (2.0f * sc * __builtin_sqrtf(nq2) * km + kSkipMargin) / sl;
+    const float nq2 = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
+    const float kmx = __builtin_fmaxf(__builtin_fmaxf(red[4], red[5]), __builtin_fmaxf(red[6], red[7]));
+    const float w = (2.0f * sc * __builtin_sqrtf(nq2) * kmx + kSkipMargin) / sl;
     if (w < 1.0e9f) {  // false for inf / NaN: visit every block
       const int wi = int(w);
       const int q_hi = min(q0 + kBQ, L) - 1;
@@ -333,32 +343,31 @@ void attn_fwd_kernel(AttnArgs a) {
   }
 }
 
-// Largest key norm of each (sequence, key/value head): kmax[z * Hkv + h] =
-// max_j ||k[j, h]|| over the sequence's tokens (fp32).  One workgroup per
-// (sequence, head); eight lanes per 128-byte key row.
+// Largest key norm of each 64-token block of each key/value head:
+// kmax[h * n_kblk + b] = max over tokens t in [64b, 64b + 64) of ||k[t, h]||
+// (fp32).  One workgroup per (block, head); eight lanes per 128-byte key row.
 __global__ __launch_bounds__(256) void key_norm_max_kernel(const uint16_t* __restrict__ k,
-                                                           const int32_t* cu_seqlens,
                                                            int64_t k_tok, int64_t k_head,
-                                                           int64_t total, int n_kv_heads,
+                                                           int64_t total, int n_kblk,
                                                            float* kmax) {
   __shared__ float red[4];
-  const int z = blockIdx.y, h = blockIdx.x;
-  const int tot = int(total);
-  const int s0 = min(max(cu_seqlens[z], 0), tot);
-  const int L = min(max(cu_seqlens[z + 1], s0), tot) - s0;
+  const int b = blockIdx.x, h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63;
   const int chunk = tid & 7;
   float best = 0.0f;
-  for (int r = tid >> 3; r < L; r += 32) {
-    const u32x4 raw = *reinterpret_cast<const u32x4*>(k + int64_t(s0 + r) * k_tok + h * k_head +
-                                                      chunk * 8);
-    float ss = 0.0f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) {
-      const float lo = bf16_bits_to_f32(raw[w] & 0xffffu);
-      const float hi = bf16_bits_to_f32(raw[w] >> 16);
-      ss = __builtin_fmaf(lo, lo, ss);
-      ss = __builtin_fmaf(hi, hi, ss);
+  for (int pass = 0; pass < 2; ++pass) {
+    const int64_t t = int64_t(b) * 64 + pass * 32 + (tid >> 3);
+    float ss = 0.0f;
+    if (t < total) {
+      const u32x4 raw = *reinterpret_cast<const u32x4*>(k + t * k_tok + h * k_head + chunk * 8);
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float lo = bf16_bits_to_f32(raw[w] & 0xffffu);
+        const float hi = bf16_bits_to_f32(raw[w] >> 16);
+        ss = __builtin_fmaf(lo, lo, ss);
+        ss = __builtin_fmaf(hi, hi, ss);
+      }
     }
     ss += __shfl_xor(ss, 1, 64);
     ss += __shfl_xor(ss, 2, 64);
@@ -371,7 +380,7 @@ __global__ __launch_bounds__(256) void key_norm_max_kernel(const uint16_t* __res
   __syncthreads();
   if (tid == 0) {
     const float m = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
-    kmax[int64_t(z) * n_kv_heads + h] = __builtin_sqrtf(m);
+    kmax[int64_t(h) * n_kblk + b] = __builtin_sqrtf(m);
   }
 }
 
@@ -381,11 +390,12 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
                            float* lse, float* kmax_ws, const g5moe_attn_shape& s,
                            hipStream_t st) {
-  const bool skip = kmax_ws != nullptr && slopes != nullptr;
+  const bool skip = kmax_ws != nullptr && slopes != nullptr && s.total_tokens > 0;
+  const int n_kblk = int((s.total_tokens + 63) / 64);
   if (skip) {
-    hipLaunchKernelGGL(key_norm_max_kernel, dim3(unsigned(s.n_kv_heads), unsigned(s.n_seqs)),
-                       dim3(256), 0, st, k, cu_seqlens, s.k_token_stride, s.k_head_stride,
-                       s.total_tokens, int(s.n_kv_heads), kmax_ws);
+    hipLaunchKernelGGL(key_norm_max_kernel, dim3(unsigned(n_kblk), unsigned(s.n_kv_heads)),
+                       dim3(256), 0, st, k, s.k_token_stride, s.k_head_stride, s.total_tokens,
+                       n_kblk, kmax_ws);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
@@ -408,7 +418,7 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
   a.slopes = slopes;
   a.lse = lse;
   a.kmax = skip ? kmax_ws : nullptr;
-  a.n_kv_heads = s.n_kv_heads;
+  a.n_kblk = n_kblk;
   a.total = s.total_tokens;
   const dim3 grid(unsigned((s.max_seqlen + kBQ - 1) / kBQ), unsigned(s.n_heads),
                   unsigned(s.n_seqs));

@@ -298,7 +298,8 @@ typedef struct g5moe_attn_shape {
 } g5moe_attn_shape;
 
 /* Bytes of workspace g5moe_attn_varlen_fwd uses for block skipping
- * (n_seqs * n_kv_heads fp32 key-norm bounds, 256-byte aligned). */
+ * (n_kv_heads * ceil(total_tokens / 64) fp32 key-norm maxima, 256-byte
+ * aligned). */
 g5moe_status g5moe_attn_workspace_size(const g5moe_attn_shape* shape, size_t* bytes);
 
 /* out[t, h] = sum_j softmax_j(q[t,h] . k[j,h'] * softmax_scale

@@ -173,7 +173,10 @@ def test_attn_null_and_misaligned_pointers_rejected(g5lib):
     assert st == 1 and "NULL" in g5lib.g5moe_last_error().decode()
     n = ctypes.c_size_t(0)
     assert g5lib.g5moe_attn_workspace_size(ctypes.byref(s), ctypes.byref(n)) == 0
-    assert n.value == 256  # 2 sequences x 12 heads x 4 bytes, 256-byte aligned
+    assert n.value == 256  # 12 heads x ceil(200 / 64) blocks x 4 bytes, 256-byte aligned
+    s_big = attn_shape(total_tokens=36400)
+    assert g5lib.g5moe_attn_workspace_size(ctypes.byref(s_big), ctypes.byref(n)) == 0
+    assert n.value == (12 * 569 * 4 + 255) // 256 * 256
     p = ctypes.c_void_p(0x1000)
     bad = ctypes.c_void_p(0x1008)
     st = g5lib.g5moe_attn_varlen_fwd(p, p, bad, p, p, None, ctypes.c_float(0.125), None, None,
