@@ -297,13 +297,13 @@ def bench_train(args) -> dict:
         rec(4)
         offs = offsets.tolist()
         kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
-        dgu = torch.empty((N * k + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
         h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
-        dgu_pad = torch.empty((E, kmax, 2 * F), dtype=torch.bfloat16, device=dev)
-        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(offsets), P(dgu), P(h_pad),
-                  P(dgu_pad), kmax, ctypes.byref(shape), S)
+        dgu_buf = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
+        dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
+        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(offsets), None, P(h_pad),
+                  P(dgu_buf), kmax, ctypes.byref(shape), S)
         rec(5)
-        dxp = ops.grouped_gemm(dgu, N * k, offsets, wgu_t)
+        dxp = ops.grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, wgu_t)
         rec(6)
         dx = torch.empty((N, d), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),

@@ -34,6 +34,7 @@ EXPORTED = (
     "g5moe_combine_residual",
     "g5moe_transpose_experts",
     "g5moe_grouped_gemm",
+    "g5moe_grouped_gemm_padded",
     "g5moe_gate_grad",
     "g5moe_router_grad",
     "g5moe_expert_gate_up_raw",
@@ -111,6 +112,9 @@ _SIGS = {
                                 ctypes.c_int),
     "g5moe_grouped_gemm": ([_P, _P, _P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,
                            ctypes.c_int32, _P], ctypes.c_int),
+    "g5moe_grouped_gemm_padded": ([_P, ctypes.c_int32, _P, _P, _P, ctypes.c_int64,
+                                   ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P],
+                                  ctypes.c_int),
     "g5moe_gate_grad": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_router_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up_raw": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),

@@ -262,8 +262,33 @@ g5moe_status g5moe_grouped_gemm(const void* a, const int32_t* offsets, const voi
   G5_NONNULL(c);
   return hip_status(launch_grouped_nt(static_cast<const uint16_t*>(a), offsets,
                                       static_cast<const uint16_t*>(b), static_cast<uint16_t*>(c),
-                                      rows, n_experts, k, n_out, as_stream(stream)),
+                                      rows, n_experts, k, n_out, 0, as_stream(stream)),
                     "g5moe_grouped_gemm");
+}
+
+g5moe_status g5moe_grouped_gemm_padded(const void* a, int32_t kmax, const int32_t* offsets,
+                                       const void* b, void* c, int64_t rows, int32_t k,
+                                       int32_t n_out, int32_t n_experts, void* stream) {
+  if (kmax < 1 || int64_t(kmax) * kMaxExperts > int64_t(INT32_MAX) / 2)
+    return fail(G5MOE_ERR_INVALID_ARG, "grouped_gemm_padded: kmax %d out of range", int(kmax));
+  if (rows < 0 || rows > int64_t(INT32_MAX) / 2)
+    return fail(G5MOE_ERR_INVALID_ARG, "grouped_gemm_padded: rows %lld out of range",
+                (long long)rows);
+  if (n_experts < 1 || n_experts > kMaxExperts)
+    return fail(G5MOE_ERR_UNSUPPORTED, "grouped_gemm_padded: n_experts %d not in [1, %d]",
+                int(n_experts), kMaxExperts);
+  if (k < 128 || k % 64 != 0 || n_out < 128 || n_out % 128 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "grouped_gemm_padded: k = %d must be a multiple of 64 "
+                ">= 128 and n_out = %d a multiple of 128", int(k), int(n_out));
+  if (rows == 0) return G5MOE_OK;
+  G5_NONNULL(a);
+  G5_NONNULL(offsets);
+  G5_NONNULL(b);
+  G5_NONNULL(c);
+  return hip_status(launch_grouped_nt(static_cast<const uint16_t*>(a), offsets,
+                                      static_cast<const uint16_t*>(b), static_cast<uint16_t*>(c),
+                                      rows, n_experts, k, n_out, kmax, as_stream(stream)),
+                    "g5moe_grouped_gemm_padded");
 }
 
 g5moe_status g5moe_gate_grad(const void* dy, const void* y_perm, const int32_t* inv_pos,
@@ -328,7 +353,6 @@ g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t
   G5_NONNULL(dh);
   G5_NONNULL(gu);
   G5_NONNULL(offsets);
-  G5_NONNULL(dgu);
   G5_NONNULL(h_pad);
   G5_NONNULL(dgu_pad);
   return hip_status(launch_swiglu_bwd(static_cast<const uint16_t*>(dh),

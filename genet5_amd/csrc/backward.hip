@@ -92,9 +92,9 @@ __global__ __launch_bounds__(256) void router_grad_kernel(
 // space: row e * kmax + j is sorted position offsets[e] + j for j < M_e and a
 // padding row (written as zeros in the padded outputs) otherwise.  gu rows
 // interleave 32-column groups: entries [64q, 64q + 32) are g of columns
-// [32q, 32q + 32), the next 32 the matching u.  Outputs: dgu in sorted order
-// (the dX product's A operand), and h and dgu in the padded row layout
-// [E, kmax, .] the weight-gradient batched products read.
+// [32q, 32q + 32), the next 32 the matching u.  Outputs: h and dgu in the
+// padded row layout [E, kmax, .] the weight-gradient batched products and the
+// padded dX product read, and optionally (dgu != nullptr) dgu in sorted order.
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     const uint16_t* __restrict__ dh, const uint16_t* __restrict__ gu,
     const int32_t* __restrict__ offsets, uint16_t* __restrict__ dgu,
@@ -144,8 +144,10 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   }
   const uint4 vog = make_uint4(og[0], og[1], og[2], og[3]);
   const uint4 vou = make_uint4(ou[0], ou[1], ou[2], ou[3]);
-  *reinterpret_cast<uint4*>(dgu + go) = vog;
-  *reinterpret_cast<uint4*>(dgu + go + 32) = vou;
+  if (dgu != nullptr) {
+    *reinterpret_cast<uint4*>(dgu + go) = vog;
+    *reinterpret_cast<uint4*>(dgu + go + 32) = vou;
+  }
   *reinterpret_cast<uint4*>(dgu_pad + gpo) = vog;
   *reinterpret_cast<uint4*>(dgu_pad + gpo + 32) = vou;
   *reinterpret_cast<uint4*>(h_pad + prow * F + f0) = make_uint4(oh[0], oh[1], oh[2], oh[3]);

@@ -74,7 +74,7 @@ hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int
                               hipStream_t st);
 hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
                              uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
-                             hipStream_t st);
+                             int a_rows_per_expert, hipStream_t st);
 hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const int32_t* inv_pos,
                             const float* topk_w, float* dw, uint16_t* dyp,
                             const g5moe_shape& s, hipStream_t st);

@@ -62,6 +62,9 @@ struct GemmArgs {
   int K;
   int Nout;
   int ldc;
+  int a_rows_per_expert;  // 0: A row of sorted position p is p; > 0: expert e's j-th
+                          // row is A row e * a_rows_per_expert + j (per-expert padded
+                          // layout; at most a_rows_per_expert rows of each expert are used)
 };
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
@@ -72,7 +75,15 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
 
 struct TileCoord {
   int e, p_begin, p_end, n0;
+  int a_row;  // A row of position p_begin (non-gathered A)
 };
+
+// Rows of expert e the GEMM computes: its sorted positions, capped at the padded
+// layout's per-expert row count.
+__device__ __forceinline__ int expert_rows(const GemmArgs& args, int e) {
+  const int cnt = args.offsets[e + 1] - args.offsets[e];
+  return args.a_rows_per_expert > 0 ? min(cnt, args.a_rows_per_expert) : cnt;
+}
 
 // The same DMA with an explicit scalar base and a 32-bit per-lane byte offset
 // (global_load_lds_dwordx4 voff, sbase), M0 = LDS byte address of the 1 KB
@@ -133,7 +144,7 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileC
   const int ntn = args.Nout / BN;
   int e = 0, mt_e = 0;
   for (; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    const int cnt = expert_rows(args, e);
     mt_e = (cnt + BM - 1) / BM;
     const int t = mt_e * ntn;
     if (u < t) break;
@@ -147,7 +158,8 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileC
   const int nt = rr / gs;
   tc.e = e;
   tc.p_begin = args.offsets[e] + mt * BM;
-  tc.p_end = args.offsets[e + 1];
+  tc.p_end = args.offsets[e] + expert_rows(args, e);
+  tc.a_row = args.a_rows_per_expert > 0 ? e * args.a_rows_per_expert + mt * BM : tc.p_begin;
   tc.n0 = nt * BN;
 }
 
@@ -282,10 +294,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   auto a_base_of = [&](const TileCoord& tc) -> const char* {
     if constexpr (GATHER)
       return reinterpret_cast<const char*>(args.A);
-    else  // rows p_begin ..: h has BM rows of padding after its last row, so a
+    else  // rows a_row ..: A has BM rows of padding after its last row, so a
           // partial tile reads padding (never stored) instead of clamping
       return reinterpret_cast<const char*>(args.A +
-                                           (int64_t(tc.p_begin) + wave * AI * RPB) * K);
+                                           (int64_t(tc.a_row) + wave * AI * RPB) * K);
   };
   auto b_base_of = [&](const TileCoord& tc) -> const char* {
     return reinterpret_cast<const char*>(
@@ -568,7 +580,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   const int ntn = args.Nout / BN;
   int total = 0;
   for (int e = 0; e < args.n_experts; ++e) {
-    const int cnt = args.offsets[e + 1] - args.offsets[e];
+    const int cnt = expert_rows(args, e);
     total += ((cnt + BM - 1) / BM) * ntn;
   }
   const int ng = gridDim.x;
@@ -759,10 +771,12 @@ hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int
 
 hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
                              uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
-                             hipStream_t st) {
+                             int a_rows_per_expert, hipStream_t st) {
   if (rows == 0) return hipSuccess;
-  if (K % 64 != 0 || K < 128 || Nout % 128 != 0) return hipErrorInvalidValue;
+  if (K % 64 != 0 || K < 128 || Nout % 128 != 0 || a_rows_per_expert < 0)
+    return hipErrorInvalidValue;
   GemmArgs a{};
+  a.a_rows_per_expert = a_rows_per_expert;
   a.A = A;
   a.perm = nullptr;
   a.offsets = offsets;

@@ -328,6 +328,21 @@ def grouped_gemm(a_padded: torch.Tensor, rows: int, offsets: torch.Tensor,
     return c
 
 
+def grouped_gemm_padded(a_pad: torch.Tensor, kmax: int, rows: int, offsets: torch.Tensor,
+                        b: torch.Tensor) -> torch.Tensor:
+    """c[offsets[e] + j] = a[e * kmax + j] . b_e^T for j < M_e: the grouped product over
+    a per-expert padded A ([E * kmax + ROW_PAD, K]; kmax >= every M_e)."""
+    dev = _check_device(a_pad)
+    E, n_out, K = b.shape
+    _require(a_pad, "a", (E * kmax + ROW_PAD, K), torch.bfloat16, dev)
+    _require(b, "b", (E, n_out, K), torch.bfloat16, dev)
+    _require(offsets, "offsets", (E + 1,), torch.int32, dev)
+    c = torch.empty((rows, n_out), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_grouped_gemm_padded", _ptr(a_pad), kmax, _ptr(offsets), _ptr(b), _ptr(c),
+              rows, K, n_out, E, _stream(dev))
+    return c
+
+
 def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
                  w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int,
                  topk_idx: torch.Tensor, topk_w: torch.Tensor, offsets: torch.Tensor,
@@ -339,8 +354,9 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     HIP stages: gate gradient and dY (g5moe_gate_grad), router-logit gradient
     (g5moe_router_grad, plus grad_logits), the gate|up recompute
     (g5moe_expert_gate_up_raw), dh = dY Wd_e (g5moe_grouped_gemm on Wd^T),
-    SwiGLU backward (g5moe_swiglu_backward), dX_perm = dGU Wgu_e (g5moe_grouped_gemm
-    on the packed gate|up's transpose) and dx (g5moe_input_grad).  The weight
+    SwiGLU backward (g5moe_swiglu_backward, dGU written once, per expert padded),
+    dX_perm = dGU Wgu_e (g5moe_grouped_gemm_padded on the packed gate|up's
+    transpose) and dx (g5moe_input_grad).  The weight
     gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e and dWr = dlogits^T x are
     plain GEMMs (torch / hipBLASLt), which read the expert row ranges on the host."""
     dev = _check_device(x2d)
@@ -375,15 +391,16 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     # weight-gradient batched products; the host reads the offsets once here
     offs = offsets.tolist()
     kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
-    dgu = torch.empty((N * k + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
     h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
-    dgu_pad = torch.empty((E, kmax, 2 * F), dtype=torch.bfloat16, device=dev)
-    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(offsets), _ptr(dgu),
-              _ptr(h_pad), _ptr(dgu_pad), kmax, ctypes.byref(shape), S)
+    # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
+    dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
+    dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
+    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(offsets), None,
+              _ptr(h_pad), _ptr(dgu_buf), kmax, ctypes.byref(shape), S)
     del dh, gu
     if w_gate_up_t is None:
         w_gate_up_t = transpose_experts(w_gate_up)      # [E, d, 2F]
-    dxp = grouped_gemm(dgu, N * k, offsets, w_gate_up_t)  # [N*k, d]
+    dxp = grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, w_gate_up_t)  # [N*k, d]
     dx = torch.empty((N, d), dtype=x2d.dtype, device=dev)
     _require(w_router, "w_router", (E, d), x2d.dtype, dev)
     _lib.call("g5moe_input_grad", _ptr(dxp), _ptr(inv_pos), _ptr(dlogits), _ptr(w_router),

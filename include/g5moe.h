@@ -205,6 +205,16 @@ g5moe_status g5moe_grouped_gemm(const void* a, const int32_t* offsets, const voi
                                 int64_t rows, int32_t k, int32_t n_out, int32_t n_experts,
                                 void* stream);
 
+/* g5moe_grouped_gemm over the per-expert padded row layout: expert e's j-th
+ * sorted position (offsets[e] + j, j < min(M_e, kmax)) reads A row
+ * e*kmax + j and writes c row offsets[e] + j.  a : bf16 [E*kmax + 256, k]
+ * (e.g. the SwiGLU backward's dgu_pad);  b, c, k, n_out as g5moe_grouped_gemm.
+ * The backward's dX product reads dGU this way, so the SwiGLU backward writes
+ * dGU once. */
+g5moe_status g5moe_grouped_gemm_padded(const void* a, int32_t kmax, const int32_t* offsets,
+                                       const void* b, void* c, int64_t rows, int32_t k,
+                                       int32_t n_out, int32_t n_experts, void* stream);
+
 /* Gate gradient and the scaled output gradient in sorted order:
  *   dw[t, s] = dy[t] . y_perm[inv_pos[t, s]]   (fp32; per lane c an fma chain
  *              over columns [c*d/64, (c+1)*d/64), lanes added over bits 5..0)
@@ -234,10 +244,12 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
  * lib/blocks/_component.py:31, :50): with s = 1 / (1 + exp(-g)),
  *   dg = dh * u * s * (1 + g * (1 - s)),  du = dh * g * s,  h = g * s * u
  * (h recomputed for the down weight gradient).  dh : bf16 [N*k, F];
- * gu : bf16 [N*k, 2F] packed;  dgu : bf16 [N*k + 256, 2F] packed out (sorted
- * order); h_pad, dgu_pad : bf16 [E, kmax, F], [E, kmax, 2F] out — the same rows
- * placed per expert, row e*kmax + j = sorted position offsets[e] + j, zero rows
- * for j >= M_e (kmax >= every M_e): the weight gradients' batched operands. */
+ * gu : bf16 [N*k, 2F] packed;  h_pad, dgu_pad : bf16 [E, kmax, F],
+ * [E, kmax, 2F] out — rows placed per expert, row e*kmax + j = sorted position
+ * offsets[e] + j, zero rows for j >= M_e (kmax >= every M_e): the weight
+ * gradients' batched operands and g5moe_grouped_gemm_padded's A operand (give
+ * dgu_pad 256 rows of padding after row E*kmax for that);  dgu : bf16
+ * [N*k + 256, 2F] packed out in sorted order, or NULL (not written). */
 g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* offsets,
                                    void* dgu, void* h_pad, void* dgu_pad, int32_t kmax,
                                    const g5moe_shape* shape, void* stream);

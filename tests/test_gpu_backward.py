@@ -203,3 +203,50 @@ def test_padded_weight_gradient_operands(cuda_device):
         assert not hp[e, o1 - o0:].any()
         got = mo.bf16_to_f32(hp[e, : o1 - o0]).astype(np.float64)
         np.testing.assert_allclose(got, h_ref[o0:o1], rtol=8e-3, atol=1e-6)
+
+
+def test_padded_dx_product_equals_sorted(cuda_device):
+    """g5moe_grouped_gemm_padded over the SwiGLU backward's per-expert padded dGU
+    equals g5moe_grouped_gemm over the sorted dGU bit for bit (same rows, same
+    kernel), with empty experts, ragged counts and a partial last tile; the SwiGLU
+    backward writes the same padded outputs whether or not it also writes the
+    sorted copy."""
+    import ctypes
+    from genet5_amd import _lib
+    rng = np.random.default_rng(12)
+    E, k, d, F = 5, 2, 256, 256
+    counts = np.array([300, 0, 41, 513, 2], np.int32)
+    nk = int(counts.sum())
+    n = nk // k
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    kmax = 576
+    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
+    S = ops._stream(cuda_device)
+    t_off = dev_t(offsets, cuda_device)
+    dh = dev_t(synth.f32_to_bf16_bits(rng.standard_normal((nk, F)).astype(np.float32)),
+               cuda_device, True)
+    gu = dev_t(synth.f32_to_bf16_bits(rng.standard_normal((nk, 2 * F)).astype(np.float32)),
+               cuda_device, True)
+    dgu = torch.empty((nk + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=cuda_device)
+    h1 = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=cuda_device)
+    p1 = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=cuda_device)
+    h2 = torch.empty_like(h1)
+    p2 = torch.empty_like(p1)
+    _lib.call("g5moe_swiglu_backward", ops._ptr(dh), ops._ptr(gu), ops._ptr(t_off),
+              ops._ptr(dgu), ops._ptr(h1), ops._ptr(p1), kmax, ctypes.byref(shape), S)
+    _lib.call("g5moe_swiglu_backward", ops._ptr(dh), ops._ptr(gu), ops._ptr(t_off), None,
+              ops._ptr(h2), ops._ptr(p2), kmax, ctypes.byref(shape), S)
+    wt = (torch.randn(E, d, 2 * F, device=cuda_device) * 0.05).to(torch.bfloat16)
+    ref = ops.grouped_gemm(dgu, nk, t_off, wt)
+    got = ops.grouped_gemm_padded(p1, kmax, nk, t_off, wt)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2) and torch.equal(p1[:E * kmax], p2[:E * kmax])
+    assert torch.equal(got, ref)
+    # and against an fp32 product of the same bf16 rows
+    dg = dgu[:nk].float()
+    for e in range(E):
+        o0, o1 = offsets[e], offsets[e + 1]
+        if o1 > o0:
+            exp = dg[o0:o1] @ wt[e].float().T
+            torch.testing.assert_close(got[o0:o1].float(), exp, rtol=2e-2, atol=2e-2)
