@@ -32,6 +32,7 @@ EXPORTED = (
     "g5moe_combine",
     "g5moe_add_rmsnorm_router",
     "g5moe_combine_residual",
+    "g5moe_rmsnorm",
     "g5moe_transpose_experts",
     "g5moe_grouped_gemm",
     "g5moe_grouped_gemm_padded",
@@ -108,6 +109,8 @@ _SIGS = {
                                   _SHAPE_P, _P], ctypes.c_int),
     "g5moe_combine_residual": ([_P, _P, _P, _P, ctypes.c_float, _P, _SHAPE_P, _P],
                                ctypes.c_int),
+    "g5moe_rmsnorm": ([_P, _P, _P, ctypes.c_float, _P, _P, ctypes.c_int64, ctypes.c_int32,
+                       ctypes.c_int32, _P], ctypes.c_int),
     "g5moe_transpose_experts": ([_P, _P, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P],
                                 ctypes.c_int),
     "g5moe_grouped_gemm": ([_P, _P, _P, _P, ctypes.c_int64, ctypes.c_int32, ctypes.c_int32,

@@ -215,6 +215,28 @@ g5moe_status g5moe_add_rmsnorm_router(const void* x_add, const void* residual,
                     "g5moe_add_rmsnorm_router");
 }
 
+g5moe_status g5moe_rmsnorm(const void* x_add, const void* residual, const float* norm_weight,
+                           float eps, void* sum_out, void* normed_out, int64_t n_rows,
+                           int32_t d_model, int32_t dtype, void* stream) {
+  if (n_rows < 0) return fail(G5MOE_ERR_INVALID_ARG, "rmsnorm: n_rows < 0");
+  if (dtype != G5MOE_DTYPE_BF16 && dtype != G5MOE_DTYPE_F32)
+    return fail(G5MOE_ERR_INVALID_ARG, "rmsnorm: dtype %d is neither bf16 (0) nor f32 (1)",
+                int(dtype));
+  if (d_model != 128 && d_model != 256 && d_model != 512 && d_model != 768)
+    return fail(G5MOE_ERR_UNSUPPORTED, "rmsnorm: d_model %d not in {128, 256, 512, 768}",
+                int(d_model));
+  if (!(eps >= 0.0f)) return fail(G5MOE_ERR_INVALID_ARG, "rmsnorm: eps must be >= 0");
+  if (sum_out != nullptr && x_add == nullptr)
+    return fail(G5MOE_ERR_INVALID_ARG, "rmsnorm: sum_out needs x_add");
+  if (n_rows == 0) return G5MOE_OK;
+  G5_NONNULL(residual);
+  G5_NONNULL(norm_weight);
+  G5_NONNULL(normed_out);
+  return hip_status(launch_rmsnorm(x_add, residual, norm_weight, eps, sum_out, normed_out, n_rows,
+                                   d_model, dtype, as_stream(stream)),
+                    "g5moe_rmsnorm");
+}
+
 g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
                                     const float* topk_w, const void* residual, float alpha,
                                     void* out, const g5moe_shape* shape, void* stream) {

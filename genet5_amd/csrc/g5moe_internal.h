@@ -58,6 +58,9 @@ hipError_t launch_norm_router(const void* x_add, const void* residual, const flo
                               float eps, const void* wr, const float* bias, void* sum_out,
                               void* normed_out, int32_t* idx, float* w, float* logits,
                               const g5moe_shape& s, hipStream_t st);
+hipError_t launch_rmsnorm(const void* x_add, const void* residual, const float* norm_w, float eps,
+                          void* sum_out, void* normed_out, int64_t n, int d, int dtype,
+                          hipStream_t st);
 hipError_t launch_combine_residual(const uint16_t* y_perm, const int32_t* inv_pos,
                                    const float* w, const void* residual, float alpha, void* out,
                                    const g5moe_shape& s, hipStream_t st);

@@ -169,6 +169,59 @@ __device__ __forceinline__ void rs_level(float* p, int lane, int bit) {
   for (int i = 0; i < HALF; ++i) p[i] = (hi ? p[HALF + i] : p[i]) + recv[i];
 }
 
+// Plain (residual add +) RMSNorm with the fused variant's arithmetic, so its
+// normed rows equal the ones g5moe_add_rmsnorm_router writes bit for bit: one
+// wave per row, lane c holding columns [c*L, c*L + L), kRowsPerWave rows per
+// wave (their loads in flight together).
+constexpr int kRowsPerWave = 4;
+
+template <typename XT, int L, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ x,
+                                                      const XT* __restrict__ x_add,
+                                                      const float* __restrict__ weight,
+                                                      float eps, XT* __restrict__ sum_out,
+                                                      XT* __restrict__ normed_out,
+                                                      int64_t n_rows) {
+  constexpr int D = 64 * L;
+  const int lane = threadIdx.x & 63;
+  const int64_t row0 = (int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6)) * kRowsPerWave;
+  if (row0 >= n_rows) return;
+  float nw[L];
+#pragma unroll
+  for (int i = 0; i < L; ++i) nw[i] = weight[lane * L + i];
+  float xv[kRowsPerWave][L], ss[kRowsPerWave];
+#pragma unroll
+  for (int m = 0; m < kRowsPerWave; ++m) {
+    const int64_t t = min(row0 + m, n_rows - 1);  // rows past the end: computed, not stored
+    RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv[m]);
+    if constexpr (ADD) {
+      float xa[L];
+      RowLoader<XT, L>::load(x_add + size_t(t) * D + lane * L, xa);
+#pragma unroll
+      for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>(xv[m][i] + xa[i]);
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], xv[m][i], acc);
+    ss[m] = acc;
+  }
+#pragma unroll
+  for (int bit = 32; bit >= 1; bit >>= 1)
+#pragma unroll
+    for (int m = 0; m < kRowsPerWave; ++m) ss[m] = ss[m] + __shfl_xor(ss[m], bit, 64);
+#pragma unroll
+  for (int m = 0; m < kRowsPerWave; ++m) {
+    if (row0 + m >= n_rows) break;
+    const float rstd = 1.0f / __builtin_sqrtf(ss[m] / float(D) + eps);
+    if constexpr (ADD) {
+      if (sum_out != nullptr) store_row<XT, L>(sum_out + size_t(row0 + m) * D + lane * L, xv[m]);
+    }
+#pragma unroll
+    for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>((xv[m][i] * rstd) * nw[i]);
+    store_row<XT, L>(normed_out + size_t(row0 + m) * D + lane * L, xv[m]);
+  }
+}
+
 // MODE 0: router on x.  MODE 1 / 2: x is the residual stream, normalised
 // (after adding na.x_add in MODE 2) on the way in; see the header comment.
 template <typename XT, int L, int MODE>
@@ -390,6 +443,50 @@ hipError_t launch_norm_router(const void* x_add, const void* residual, const flo
   if (x_add != nullptr)
     return launch_mode<2>(residual, wr, bias, idx, w, logits, na, s, st);
   return launch_mode<1>(residual, wr, bias, idx, w, logits, na, s, st);
+}
+
+
+namespace {
+template <typename XT, bool ADD>
+hipError_t launch_rmsnorm_typed(const XT* x, const XT* xa, const float* w, float eps, XT* sum_out,
+                                XT* normed, int64_t n, int d, hipStream_t st) {
+  const unsigned grid = unsigned((n + 4 * kRowsPerWave - 1) / (4 * kRowsPerWave));
+  switch (d) {
+#define G5_RMSNORM_CASE(LL)                                                                  \
+  case 64 * LL:                                                                              \
+    hipLaunchKernelGGL((rmsnorm_kernel<XT, LL, ADD>), dim3(grid), dim3(256), 0, st, x, xa, w,  \
+                       eps, sum_out, normed, n);                                             \
+    break;
+    G5_RMSNORM_CASE(2)
+    G5_RMSNORM_CASE(4)
+    G5_RMSNORM_CASE(8)
+    G5_RMSNORM_CASE(12)
+#undef G5_RMSNORM_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+}  // namespace
+
+hipError_t launch_rmsnorm(const void* x_add, const void* residual, const float* norm_w, float eps,
+                          void* sum_out, void* normed_out, int64_t n, int d, int dtype,
+                          hipStream_t st) {
+  if (n == 0) return hipSuccess;
+  if (dtype == G5MOE_DTYPE_BF16) {
+    auto* r = static_cast<const uint16_t*>(residual);
+    auto* xa = static_cast<const uint16_t*>(x_add);
+    auto* so = static_cast<uint16_t*>(sum_out);
+    auto* no = static_cast<uint16_t*>(normed_out);
+    return xa ? launch_rmsnorm_typed<uint16_t, true>(r, xa, norm_w, eps, so, no, n, d, st)
+              : launch_rmsnorm_typed<uint16_t, false>(r, xa, norm_w, eps, so, no, n, d, st);
+  }
+  auto* r = static_cast<const float*>(residual);
+  auto* xa = static_cast<const float*>(x_add);
+  auto* so = static_cast<float*>(sum_out);
+  auto* no = static_cast<float*>(normed_out);
+  return xa ? launch_rmsnorm_typed<float, true>(r, xa, norm_w, eps, so, no, n, d, st)
+            : launch_rmsnorm_typed<float, false>(r, xa, norm_w, eps, so, no, n, d, st);
 }
 
 }  // namespace g5moe

@@ -23,14 +23,25 @@ from ..moe import MoEFeedForward
 
 
 class RMSNorm(nn.Module):
-    """y = x * rsqrt(mean(x^2) + eps) * weight, computed in fp32, returned in x's dtype."""
+    """y = x * rsqrt(mean(x^2) + eps) * weight, computed in fp32, returned in x's dtype.
+
+    hip = True: the HIP kernel g5moe_rmsnorm (the fused norm+router kernel's
+    arithmetic: fixed reduction order, correctly rounded sqrt and division);
+    otherwise the torch composition."""
 
     def __init__(self, dim: int, eps: float = 1e-6):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(dim))
         self.variance_epsilon = eps
+        self.hip = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.hip:
+            from .. import ops
+            d = x.shape[-1]
+            w = self.weight.detach().to(torch.float32).contiguous()
+            return ops.rmsnorm(x.reshape(-1, d).contiguous(), w,
+                               self.variance_epsilon).view(x.shape)
         xf = x.float()
         y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
         return (y * self.weight.float()).to(x.dtype)

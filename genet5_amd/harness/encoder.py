@@ -168,10 +168,16 @@ class GeneT5MoE(nn.Module):
         self.final_norm = RMSNorm(embed_dim)
         self.lm_head = nn.Linear(embed_dim, vocab_size, bias=False)
         self.lm_head.weight = self.embed.weight
+        self.set_fused(True)
 
     def set_fused(self, fused: bool) -> "GeneT5MoE":
+        """fused: every block's MoE half as MoEFeedForward.residual_block, and the
+        attention pre-norms and the final norm as the HIP RMSNorm; otherwise the
+        torch composition around the MoE module."""
         for layer in self.layers:
             layer.fused = fused
+            layer.norm1.hip = fused
+        self.final_norm.hip = fused
         return self
 
     def set_attention_backend(self, backend: str) -> "GeneT5MoE":

@@ -200,6 +200,27 @@ def add_rmsnorm_router(residual: torch.Tensor, norm_weight: torch.Tensor, eps: f
     return out + (logits,) if return_logits else out
 
 
+def rmsnorm(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+            x_add: Optional[torch.Tensor] = None, return_sum: bool = False):
+    """(Residual add +) RMSNorm of [N, d] rows (g5moe_rmsnorm), the same arithmetic as
+    add_rmsnorm_router's normed rows.  Returns normed, or (normed, x_add + residual)
+    with return_sum (x_add given)."""
+    dev = _check_device(residual)
+    N, d = residual.shape
+    dt = residual.dtype
+    _require(residual, "residual", (N, d), dt, dev)
+    if x_add is not None:
+        _require(x_add, "x_add", (N, d), dt, dev)
+    elif return_sum:
+        raise ValueError("return_sum needs x_add")
+    _require(norm_weight, "norm_weight", (d,), torch.float32, dev)
+    normed = torch.empty((N, d), dtype=dt, device=dev)
+    ssum = torch.empty((N, d), dtype=dt, device=dev) if return_sum else None
+    _lib.call("g5moe_rmsnorm", _ptr(x_add), _ptr(residual), _ptr(norm_weight), ctypes.c_float(eps),
+              _ptr(ssum), _ptr(normed), N, d, _dtype_code(dt), _stream(dev))
+    return (normed, ssum) if return_sum else normed
+
+
 def combine_residual(y_perm: torch.Tensor, inv_pos: torch.Tensor, topk_w: torch.Tensor,
                      residual: torch.Tensor, alpha: float = 1.0,
                      out: Optional[torch.Tensor] = None) -> torch.Tensor:

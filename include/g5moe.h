@@ -168,6 +168,17 @@ g5moe_status g5moe_add_rmsnorm_router(const void* x_add, const void* residual,
                                       void* normed_out, int32_t* topk_idx, float* topk_w,
                                       float* logits, const g5moe_shape* shape, void* stream);
 
+/* Residual add + RMSNorm alone, with g5moe_add_rmsnorm_router's arithmetic (its
+ * normed rows bit for bit): the encoder block's attention pre-norm
+ * `norm1(hidden)` (lib/blocks/encoder.py:76-78, LigerRMSNorm at
+ * lib/blocks/_component.py:14) and the encoder's final norm (encoder.py:148).
+ *   x_add : [n_rows, d] or NULL;  residual : [n_rows, d];  norm_weight : fp32 [d]
+ *   sum_out : [n_rows, d] or NULL (needs x_add);  normed_out : [n_rows, d]
+ *   d_model in {128, 256, 512, 768};  dtype : G5MOE_DTYPE_BF16 or _F32 (all rows). */
+g5moe_status g5moe_rmsnorm(const void* x_add, const void* residual, const float* norm_weight,
+                           float eps, void* sum_out, void* normed_out, int64_t n_rows,
+                           int32_t d_model, int32_t dtype, void* stream);
+
 /* Gated combine added into the residual stream: the encoder block's
  * `hidden_states + dropout(ff_output) * alpha` (lib/blocks/encoder.py:89;
  * alpha = 1/sqrt(i+1) under depth_scaling, :118) with ff_output = the MoE

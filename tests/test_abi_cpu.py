@@ -146,3 +146,20 @@ def test_fake_impl_traces_shape():
                             torch.empty(16, 6144, 768, dtype=torch.bfloat16),
                             torch.empty(16, 768, 3072, dtype=torch.bfloat16), 2)
         assert y.shape == x.shape and y.dtype == x.dtype
+
+
+@pytest.mark.parametrize("args,code,msg", [
+    (dict(n=-1), 1, "n_rows"),
+    (dict(dtype=3), 1, "dtype"),
+    (dict(d=640), 2, "d_model"),
+    (dict(eps=-1.0), 1, "eps"),
+    (dict(sum_out=True), 1, "x_add"),
+    (dict(), 1, "NULL"),
+])
+def test_rmsnorm_argument_checks(g5lib, args, code, msg):
+    a = dict(n=4, d=768, dtype=0, eps=1e-6, sum_out=False)
+    a.update(args)
+    so = ctypes.c_void_p(0x1000) if a["sum_out"] else None
+    st = g5lib.g5moe_rmsnorm(None, None, None, ctypes.c_float(a["eps"]), so, None, a["n"],
+                             a["d"], a["dtype"], None)
+    assert st == code and msg in g5lib.g5moe_last_error().decode()

@@ -77,6 +77,39 @@ def test_add_rmsnorm_router_bit_exact(cuda_device, n, d, E, k, dtype, add):
     assert torch.equal(idx2, idx) and torch.equal(w2, w)
 
 
+@pytest.mark.parametrize("n,d,dtype,add", [
+    (36400, 768, "bf16", False),
+    (2049, 768, "bf16", True),
+    (1000, 512, "f32", True),
+    (17, 256, "f32", False),
+    (1, 128, "bf16", True),
+])
+def test_rmsnorm_bit_exact(cuda_device, n, d, dtype, add):
+    """g5moe_rmsnorm: normed and sum rows bit-exact against the C oracle's add_rmsnorm
+    and equal to the fused norm+router kernel's normed rows."""
+    print(f"rmsnorm n={n} d={d} {dtype} add={add}", flush=True)
+    rng = np.random.default_rng(n * 7 + d)
+    res = act(rng, (n, d), dtype)
+    xa = act(rng, (n, d), dtype, 0.5) if add else None
+    nw = (1.0 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    dev = cuda_device
+    r_t, nw_t = as_dev(res, dev), as_dev(nw, dev)
+    xa_t = None if xa is None else as_dev(xa, dev)
+    if add:
+        normed, ssum = ops.rmsnorm(r_t, nw_t, 1e-6, x_add=xa_t, return_sum=True)
+    else:
+        normed, ssum = ops.rmsnorm(r_t, nw_t, 1e-6), None
+    wr = as_dev(act(rng, (4, d), dtype, 0.02), dev)
+    fused, fsum, _, _ = ops.add_rmsnorm_router(r_t, nw_t, 1e-6, wr, 1, x_add=xa_t)
+    torch.cuda.synchronize()
+    n_ref, s_ref = oracle.add_rmsnorm(res, nw, 1e-6, xa)
+    np.testing.assert_array_equal(bits(normed), n_ref.view(bits(normed).dtype))
+    assert torch.equal(normed, fused)
+    if add:
+        np.testing.assert_array_equal(bits(ssum), s_ref.view(bits(ssum).dtype))
+        assert torch.equal(ssum, fsum)
+
+
 def test_add_rmsnorm_router_rejects_sum_without_add(cuda_device):
     from genet5_amd import _lib
     import ctypes
