@@ -38,6 +38,11 @@ def parse():
                     help="time the training step instead: the forward that keeps the backward's "
                          "inputs, then every backward stage (HIP events between stages)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
+    ap.add_argument("--shard", choices=("dp8", "ep8"), default=None,
+                    help="one GPU's share of config 2 sharded over 8 GPUs: dp8 = 4,550 tokens "
+                         "with all 16 experts (about 569 rows per expert), ep8 = the 2 experts "
+                         "one GPU owns with their 4,550 rows each (4,550 tokens routed top-2 of "
+                         "2); the layer's kernels at those shapes, no exchange")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the benchmark, run a 256 MiB elementwise copy (read 256 MiB, "
                          "write 256 MiB) whose FETCH_SIZE / WRITE_SIZE counters scale the "
@@ -371,7 +376,11 @@ def main():
 
     dev = torch.device("cuda:0")
     cfg = args.config
-    inp = synth.make_config(cfg, seed=0)
+    if args.shard is None:
+        inp = synth.make_config(cfg, seed=0)
+    else:
+        inp = synth.make_layer(4550, n_experts=16 if args.shard == "dp8" else 2, top_k=2,
+                               seed=0, dtype="bf16")
     N, d = inp.x.shape
     E, F = inp.w_gate.shape[0], inp.w_gate.shape[1]
     k = inp.top_k
@@ -474,7 +483,10 @@ def main():
         "dtype": "bf16",
         "data": "synthetic",
         "config": {
-            "workload": synth.CONFIGS[cfg]["name"],
+            "workload": synth.CONFIGS[cfg]["name"] if args.shard is None else
+            ("cfg2 DP-8 shard: 4,550 tok bf16, E=16, top-2 (about 569 rows per expert)"
+             if args.shard == "dp8" else
+             "cfg2 EP-8 shard: 2 local experts x 4,550 rows (4,550 tok, top-2 of 2)"),
             "n_tokens": N, "d_model": d, "d_ff": F, "n_experts": E, "top_k": k,
             "seed": 0,
         },

@@ -25,7 +25,10 @@ __device__ __forceinline__ float round_bf16(float v) {
   return __uint_as_float(uint32_t(f32_to_bf16_bits(v)) << 16);
 }
 
-template <bool OUT_F32, bool RESID>
+// TOPK > 0: the slot count as a constant, so every slot's index and row loads
+// are in flight together (the same fma order as the generic loop); TOPK == 0:
+// the slot count `topk` at run time.
+template <bool OUT_F32, bool RESID, int TOPK>
 __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict__ y_perm,
                                                       const int32_t* __restrict__ inv_pos,
                                                       const float* __restrict__ w,
@@ -40,16 +43,35 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s = 0; s < topk; ++s) {
-    const int32_t p = inv_pos[t * topk + s];
-    if (p < 0) continue;
-    const float ws = w[t * topk + s];
-    const uint4 v = *reinterpret_cast<const uint4*>(y_perm + int64_t(p) * d + ch * 8);
+  auto accumulate = [&](float ws, const uint4 v) {
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       acc[2 * j] = __builtin_fmaf(ws, __uint_as_float(vv[j] << 16), acc[2 * j]);
       acc[2 * j + 1] = __builtin_fmaf(ws, __uint_as_float(vv[j] & 0xffff0000u), acc[2 * j + 1]);
+    }
+  };
+  if constexpr (TOPK > 0) {
+    int32_t p[TOPK];
+    float ws[TOPK];
+    uint4 v[TOPK];
+#pragma unroll
+    for (int s = 0; s < TOPK; ++s) {
+      p[s] = inv_pos[t * TOPK + s];
+      ws[s] = w[t * TOPK + s];
+    }
+#pragma unroll
+    for (int s = 0; s < TOPK; ++s)
+      v[s] = p[s] >= 0 ? *reinterpret_cast<const uint4*>(y_perm + int64_t(p[s]) * d + ch * 8)
+                       : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < TOPK; ++s)
+      if (p[s] >= 0) accumulate(ws[s], v[s]);
+  } else {
+    for (int s = 0; s < topk; ++s) {
+      const int32_t p = inv_pos[t * topk + s];
+      if (p < 0) continue;
+      accumulate(w[t * topk + s], *reinterpret_cast<const uint4*>(y_perm + int64_t(p) * d + ch * 8));
     }
   }
   if constexpr (RESID) {
@@ -106,12 +128,18 @@ hipError_t launch_combine_impl(const uint16_t* y_perm, const int32_t* inv_pos, c
   const int64_t work = s.n_tokens * (s.d_model / 8);
   if (work == 0) return hipSuccess;
   const unsigned grid = unsigned((work + 255) / 256);
-  if (s.x_dtype == G5MOE_DTYPE_F32)
-    hipLaunchKernelGGL((combine_kernel<true, RESID>), dim3(grid), dim3(256), 0, st, y_perm,
-                       inv_pos, w, y, s.n_tokens, s.d_model, s.top_k, residual, alpha);
-  else
-    hipLaunchKernelGGL((combine_kernel<false, RESID>), dim3(grid), dim3(256), 0, st, y_perm,
-                       inv_pos, w, y, s.n_tokens, s.d_model, s.top_k, residual, alpha);
+#define G5_COMBINE(F32, K)                                                                   \
+  hipLaunchKernelGGL((combine_kernel<F32, RESID, K>), dim3(grid), dim3(256), 0, st, y_perm,   \
+                     inv_pos, w, y, s.n_tokens, s.d_model, s.top_k, residual, alpha)
+  const bool f32 = s.x_dtype == G5MOE_DTYPE_F32;
+  if (s.top_k == 2) {
+    if (f32) G5_COMBINE(true, 2); else G5_COMBINE(false, 2);
+  } else if (s.top_k == 1) {
+    if (f32) G5_COMBINE(true, 1); else G5_COMBINE(false, 1);
+  } else {
+    if (f32) G5_COMBINE(true, 0); else G5_COMBINE(false, 0);
+  }
+#undef G5_COMBINE
   return hipGetLastError();
 }
 }  // namespace

@@ -4,18 +4,19 @@
 // a = t*k + s of topk_idx, the sorted order is expert-major and, inside an
 // expert, increasing a — a stable argsort of topk_idx.flatten().
 //
-// Three launches, all integer work bound by launch latency at these sizes
-// (72,800 assignments, about 0.9 MB of metadata at N = 36,400, k = 2):
-//   1. rank:    256 assignments per block; for each expert a wavefront
-//               ballot gives every lane its rank among equal lanes below it,
-//               popcounts give per-wave counts, and a pass over the 4 waves'
-//               counts in LDS turns them into a stable rank inside the block
-//               plus the block's per-expert count.
-//   2. scan:    one workgroup, one wavefront per expert, exclusive scan of the
-//               block counts down each expert's column; then counts[] and the
-//               exclusive offsets[] over experts.
-//   3. scatter: position = offsets[e] + column prefix + rank; writes perm and
-//               inv_pos.
+// Two launches, integer work bound by launch latency at these sizes (72,800
+// assignments, about 0.9 MB of metadata at N = 36,400, k = 2):
+//   1. rank:  256 assignments per block; for each expert a wavefront ballot
+//             gives every lane its rank among equal lanes below it, popcounts
+//             give per-wave counts, and a pass over the 4 waves' counts in LDS
+//             turns them into a stable rank inside the block plus the block's
+//             per-expert count.
+//   2. place: every block sums the block counts of the blocks before it and of
+//             all blocks, per expert (the whole [nblk, E] array is 18 KB at
+//             N = 36,400: each block reads it from L2), forms the exclusive
+//             offsets over experts, and writes position = offsets[e] + prefix +
+//             rank into perm and inv_pos; block 0 also writes counts[] and
+//             offsets[].  Integer sums are exact in any order.
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -51,54 +52,81 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
   }
 }
 
-// One workgroup of 64*kMaxExperts threads; wave e scans expert e's column.
-__global__ __launch_bounds__(64 * kMaxExperts) void dispatch_scan_kernel(
-    const int32_t* __restrict__ blk_counts, int64_t nblk, int n_experts,
-    int32_t* __restrict__ colprefix, int32_t* __restrict__ counts,
+__global__ __launch_bounds__(kDispatchBlock) void dispatch_place_kernel(
+    const int32_t* __restrict__ idx, const int32_t* __restrict__ rank,
+    const int32_t* __restrict__ blk_counts, int64_t nblk, int64_t nk, int n_experts,
+    int32_t* __restrict__ perm, int32_t* __restrict__ inv_pos, int32_t* __restrict__ counts,
     int32_t* __restrict__ offsets) {
-  __shared__ int32_t tot[kMaxExperts];
-  const int lane = threadIdx.x & 63;
-  const int e = threadIdx.x >> 6;
-  if (e < n_experts) {
-    int run = 0;
-    for (int64_t b0 = 0; b0 < nblk; b0 += 64) {
-      const int64_t b = b0 + lane;
-      const int v = (b < nblk) ? blk_counts[b * n_experts + e] : 0;
-      int inc = v;
+  static_assert(kMaxExperts == 16 && kDispatchBlock == 256, "16 experts x 16 block groups");
+  __shared__ int32_t part[kWaves][2][kMaxExperts];
+  __shared__ int32_t base[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.x;
+  // thread (g, ex) sums column ex over the blocks g, g + 16, ...
+  const int ex = tid & 15, g = tid >> 4;
+  int below = 0, total = 0;
+  if (ex < n_experts) {
+    // eight loads in flight per pass (nblk is 285 at N = 36,400, k = 2)
+    constexpr int U = 8;
+    for (int64_t bb0 = g; bb0 < nblk; bb0 += 16 * U) {
+      int c[U];
 #pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += o;
+      for (int u = 0; u < U; ++u) {
+        const int64_t bb = bb0 + 16 * u;
+        c[u] = bb < nblk ? blk_counts[bb * n_experts + ex] : 0;
       }
-      if (b < nblk) colprefix[b * n_experts + e] = run + inc - v;
-      run += __shfl(inc, 63, 64);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        total += c[u];
+        if (bb0 + 16 * u < b) below += c[u];
+      }
     }
-    if (lane == 0) tot[e] = run;
+  }
+  below += __shfl_xor(below, 16, 64);
+  below += __shfl_xor(below, 32, 64);
+  total += __shfl_xor(total, 16, 64);
+  total += __shfl_xor(total, 32, 64);
+  if (lane < kMaxExperts) {
+    part[wave][0][lane] = below;
+    part[wave][1][lane] = total;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int off = 0;
-    for (int ex = 0; ex < n_experts; ++ex) {
-      offsets[ex] = off;
-      counts[ex] = tot[ex];
-      off += tot[ex];
+  if (wave == 0) {
+    // lane e < 16: expert e's prefix and total; exclusive scan of the totals
+    // over lanes 0..15 (experts >= n_experts contribute 0)
+    int pre = 0, tot = 0;
+    if (lane < kMaxExperts) {
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        pre += part[w][0][lane];
+        tot += part[w][1][lane];
+      }
     }
-    offsets[n_experts] = off;
+    int inc = tot;
+#pragma unroll
+    for (int dd = 1; dd < kMaxExperts; dd <<= 1) {
+      const int o = __shfl_up(inc, dd, 64);
+      if (lane >= dd) inc += o;
+    }
+    const int off = inc - tot;
+    if (lane < n_experts) {
+      base[lane] = off + pre;
+      if (b == 0) {
+        offsets[lane] = off;
+        counts[lane] = tot;
+      }
+    }
+    if (b == 0 && lane == n_experts - 1) offsets[n_experts] = inc;
   }
-}
-
-__global__ __launch_bounds__(kDispatchBlock) void dispatch_scatter_kernel(
-    const int32_t* __restrict__ idx, const int32_t* __restrict__ rank,
-    const int32_t* __restrict__ colprefix, const int32_t* __restrict__ offsets, int64_t nk,
-    int n_experts, int32_t* __restrict__ perm, int32_t* __restrict__ inv_pos) {
-  const int64_t a = int64_t(blockIdx.x) * kDispatchBlock + threadIdx.x;
+  __syncthreads();
+  const int64_t a = b * kDispatchBlock + tid;
   if (a >= nk) return;
   const int e = idx[a];
   if (e < 0 || e >= n_experts) {
     inv_pos[a] = -1;
     return;
   }
-  const int32_t pos = offsets[e] + colprefix[int64_t(blockIdx.x) * n_experts + e] + rank[a];
+  const int32_t pos = base[e] + rank[a];
   perm[pos] = int32_t(a);
   inv_pos[a] = pos;
 }
@@ -123,13 +151,10 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
   }
   int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
   int32_t* blk = reinterpret_cast<int32_t*>(ws + L.blk_counts);
-  int32_t* colp = reinterpret_cast<int32_t*>(ws + L.colprefix);
   hipLaunchKernelGGL(dispatch_rank_kernel, dim3(unsigned(L.nblk)), dim3(kDispatchBlock), 0,
                      st, idx, nk, s.n_experts, rank, blk);
-  hipLaunchKernelGGL(dispatch_scan_kernel, dim3(1), dim3(64 * kMaxExperts), 0, st, blk,
-                     L.nblk, s.n_experts, colp, counts, offsets);
-  hipLaunchKernelGGL(dispatch_scatter_kernel, dim3(unsigned(L.nblk)), dim3(kDispatchBlock), 0,
-                     st, idx, rank, colp, offsets, nk, s.n_experts, perm, inv_pos);
+  hipLaunchKernelGGL(dispatch_place_kernel, dim3(unsigned(L.nblk)), dim3(kDispatchBlock), 0,
+                     st, idx, rank, blk, L.nblk, nk, s.n_experts, perm, inv_pos, counts, offsets);
   return hipGetLastError();
 }
 

@@ -18,7 +18,6 @@ constexpr int kGemmRowPad = 256;     // rows of padding after h (one GEMM m-tile
 struct WorkspaceLayout {
   size_t xb;         // bf16 copy of x when x is f32        [N, d]
   size_t blk_counts; // per-dispatch-block expert counts    [nblk, E]
-  size_t colprefix;  // exclusive prefix over blocks        [nblk, E]
   size_t rank;       // stable rank inside the block        [N*k]
   size_t h;          // SwiGLU activations, bf16            [N*k, F]
   size_t y_perm;     // expert outputs, bf16                [N*k, d]
@@ -36,8 +35,6 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   w.xb = off;
   off += align256(s.x_dtype == G5MOE_DTYPE_F32 ? size_t(s.n_tokens) * s.d_model * 2 : 0);
   w.blk_counts = off;
-  off += align256(size_t(w.nblk) * s.n_experts * 4);
-  w.colprefix = off;
   off += align256(size_t(w.nblk) * s.n_experts * 4);
   w.rank = off;
   off += align256(size_t(nk) * 4);

@@ -145,7 +145,7 @@ def _h_offset(shape: _lib.Shape) -> int:
     N, d, F, E, k = shape.n_tokens, shape.d_model, shape.d_ff, shape.n_experts, shape.top_k
     nblk = (N * k + 255) // 256
     off = a(N * d * 2 if shape.x_dtype == _lib.DTYPE_F32 else 0)
-    off += a(nblk * E * 4) * 2
+    off += a(nblk * E * 4)
     off += a(N * k * 4)
     return off
 

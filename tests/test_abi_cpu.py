@@ -51,10 +51,10 @@ def test_workspace_size_layout(g5lib):
     a = lambda v: (v + 255) // 256 * 256
     nblk = (nk + 255) // 256
     # h carries one 256-row GEMM tile of padding after its last row
-    assert n == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4) + a((nk + 256) * 3072 * 2) + a(nk * 768 * 2)
+    assert n == a(0) + a(nblk * 16 * 4) + a(nk * 4) + a((nk + 256) * 3072 * 2) + a(nk * 768 * 2)
     n32 = _lib.workspace_size(shape(x_dtype=1))
     assert n32 == n + a(36400 * 768 * 2)
-    assert ops._h_offset(s) == a(0) + 2 * a(nblk * 16 * 4) + a(nk * 4)
+    assert ops._h_offset(s) == a(0) + a(nblk * 16 * 4) + a(nk * 4)
 
 
 @pytest.mark.parametrize("kw,code,msg", [
