@@ -110,13 +110,14 @@ struct RowLoader<float, L> {
   }
 };
 
-// Round an fp32 value to the activation dtype and back (exact widening).
+// Round two fp32 values to the activation dtype and back, one conversion.
 template <typename XT>
-__device__ __forceinline__ float round_to(float v) {
-  if constexpr (sizeof(XT) == 2)
-    return __uint_as_float(uint32_t(f32_to_bf16_bits(v)) << 16);
-  else
-    return v;
+__device__ __forceinline__ void round_pair(float& a, float& b) {
+  if constexpr (sizeof(XT) == 2) {
+    const uint32_t u = pack_bf16x2(a, b);
+    a = __uint_as_float(u << 16);
+    b = __uint_as_float(u & 0xffff0000u);
+  }
 }
 
 template <typename XT, int L>
@@ -198,7 +199,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ x,
       float xa[L];
       RowLoader<XT, L>::load(x_add + size_t(t) * D + lane * L, xa);
 #pragma unroll
-      for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>(xv[m][i] + xa[i]);
+      for (int i = 0; i < L; ++i) xv[m][i] = xv[m][i] + xa[i];
+#pragma unroll
+      for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
     }
     float acc = 0.f;
 #pragma unroll
@@ -217,7 +220,9 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ x,
       if (sum_out != nullptr) store_row<XT, L>(sum_out + size_t(row0 + m) * D + lane * L, xv[m]);
     }
 #pragma unroll
-    for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>((xv[m][i] * rstd) * nw[i]);
+    for (int i = 0; i < L; ++i) xv[m][i] = (xv[m][i] * rstd) * nw[i];
+#pragma unroll
+    for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
     store_row<XT, L>(normed_out + size_t(row0 + m) * D + lane * L, xv[m]);
   }
 }
@@ -287,7 +292,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           RowLoader<XT, L>::load(static_cast<const XT*>(na.x_add) + size_t(t) * D + lane * L,
                                  xa);
 #pragma unroll
-          for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>(xv[m][i] + xa[i]);
+          for (int i = 0; i < L; ++i) xv[m][i] = xv[m][i] + xa[i];
+#pragma unroll
+          for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
         }
         float acc = 0.f;
 #pragma unroll
@@ -308,7 +315,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
                              xv[m]);
         }
 #pragma unroll
-        for (int i = 0; i < L; ++i) xv[m][i] = round_to<XT>((xv[m][i] * rstd) * nw[i]);
+        for (int i = 0; i < L; ++i) xv[m][i] = (xv[m][i] * rstd) * nw[i];
+#pragma unroll
+        for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
         if (store)
           store_row<XT, L>(static_cast<XT*>(na.normed_out) + size_t(tb + m) * D + lane * L,
                            xv[m]);
