@@ -97,12 +97,21 @@ class ALiBiSelfAttention(nn.Module):
                                              scale=1.0 / math.sqrt(self.head_dim))
         return self.o(out.transpose(1, 2).reshape(B, L, D))
 
+    def qkv_weight(self) -> torch.Tensor:
+        """[3D, D] concatenation of the q, k and v weights, rebuilt when any changes."""
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in
+                    (self.q.weight, self.k.weight, self.v.weight))
+        if getattr(self, "_qkv_key", None) != key:
+            self._qkv = torch.cat([self.q.weight, self.k.weight, self.v.weight]).detach()
+            self._qkv_key = key
+        return self._qkv
+
     def _attend_hip(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor]) -> torch.Tensor:
         B, L, D = h.shape
         H, hd = self.num_heads, self.head_dim
-        q = self.q(h).view(B * L, H, hd)
-        k = self.k(h).view(B * L, H, hd)
-        v = self.v(h).view(B * L, H, hd)
+        # one projection for q, k and v; the kernel reads them as strided views
+        qkv = F.linear(h, self.qkv_weight()).view(B * L, 3, H, hd)
+        q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
         if cu_seqlens is None:
             key = (B, L, h.device)
             cu = self._cu_cache.get(key)
