@@ -258,9 +258,9 @@ def bench_config5(args) -> dict:
 
 def bench_train(args) -> dict:
     """Training step of the layer at config 2: forward (router with logits, dispatch,
-    experts, combine) + backward (gate/router gradients, gate|up recompute, dh GEMM,
-    SwiGLU backward, dX GEMM, input gradient, weight-gradient GEMMs), one HIP event
-    between consecutive stages on the stream they run on."""
+    experts with the gate|up products kept, combine) + backward (gate/router gradients,
+    dh GEMM, SwiGLU backward, dX GEMM, input gradient, weight-gradient GEMMs), one HIP
+    event between consecutive stages on the stream they run on."""
     import ctypes
     import torch
     from genet5_amd import _lib, ops, synth
@@ -278,13 +278,14 @@ def bench_train(args) -> dict:
     shape = _lib.make_shape(N, d, F, E, k, _lib.DTYPE_BF16)
     P, S = ops._ptr, ops._stream(dev)
     stream = torch.cuda.current_stream(dev)
-    names = ["fwd", "gate_router_grad", "gate_up_recompute", "dh_gemm", "swiglu_bwd",
-             "dx_gemm", "input_grad", "wgrad_operands", "wgrad_gemms"]
+    names = ["fwd", "gate_router_grad", "dh_gemm", "swiglu_bwd", "dx_gemm", "input_grad",
+             "wgrad_operands", "wgrad_gemms"]
 
     def step(ev=None):
         rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
         rec(0)
-        y, logits, idx, w, offsets, perm, inv_pos, y_perm = ops.moe_forward_train(x, wr, wgu, wd, k)
+        y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(
+            x, wr, wgu, wd, k)
         rec(1)
         dw = torch.empty((N, k), dtype=torch.float32, device=dev)
         dyp = torch.empty((N * k + ops.ROW_PAD, d), dtype=torch.bfloat16, device=dev)
@@ -293,13 +294,8 @@ def bench_train(args) -> dict:
         dl = torch.empty((N, E), dtype=torch.float32, device=dev)
         _lib.call("g5moe_router_grad", P(dw), P(w), P(idx), None, P(dl), ctypes.byref(shape), S)
         rec(2)
-        gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
-        ws = ops.workspace(shape, dev)
-        _lib.call("g5moe_expert_gate_up_raw", P(x), P(perm), P(offsets), P(wgu), P(gu), P(ws),
-                  ctypes.byref(shape), S)
-        rec(3)
         dh = ops.grouped_gemm(dyp, N * k, offsets, wd_t)
-        rec(4)
+        rec(3)
         offs = offsets.tolist()
         kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
         h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
@@ -307,23 +303,23 @@ def bench_train(args) -> dict:
         dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
         _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(offsets), None, P(h_pad),
                   P(dgu_buf), kmax, ctypes.byref(shape), S)
-        rec(5)
+        rec(4)
         dxp = ops.grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, wgu_t)
-        rec(6)
+        rec(5)
         dx = torch.empty((N, d), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),
                   ctypes.byref(shape), S)
-        rec(7)
+        rec(6)
         dyT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_pad_transpose", P(dyp), None, P(offsets), P(dyT), d, kmax,
                   ctypes.byref(shape), S)
         xT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_pad_transpose", P(x), P(perm), P(offsets), P(xT), d, kmax,
                   ctypes.byref(shape), S)
-        rec(8)
+        rec(7)
         torch.bmm(dyT, h_pad)
         ops.transpose_experts(torch.bmm(xT, dgu_pad))
-        rec(9)
+        rec(8)
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]
@@ -338,7 +334,7 @@ def bench_train(args) -> dict:
     st = {n: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
           for j, n in enumerate(names)}
     g = 2 * d * F * N * k  # one d x F product over the routed rows
-    flops = {"gate_up_recompute": 2 * g, "dh_gemm": g, "dx_gemm": 2 * g, "wgrad_gemms": 3 * g}
+    flops = {"dh_gemm": g, "dx_gemm": 2 * g, "wgrad_gemms": 3 * g}
     return {
         "metric": "MoE layer training step (forward + backward) tokens/s, 36.4k tok, 16e top-2",
         "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,

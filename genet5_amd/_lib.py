@@ -27,6 +27,7 @@ EXPORTED = (
     "g5moe_router_topk",
     "g5moe_dispatch",
     "g5moe_expert_gate_up",
+    "g5moe_expert_gate_up_train",
     "g5moe_expert_down",
     "g5moe_expert_swiglu",
     "g5moe_combine",
@@ -102,6 +103,7 @@ _SIGS = {
     "g5moe_router_topk": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_dispatch": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_expert_gate_up_train": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_down": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_swiglu": ([_P, _P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_combine": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),

@@ -154,8 +154,32 @@ g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int3
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up (cast)"));
   const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                                   reinterpret_cast<uint16_t*>(w + L.h), *shape, st),
+                                   reinterpret_cast<uint16_t*>(w + L.h), nullptr, *shape, st),
                     "g5moe_expert_gate_up");
+}
+
+g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
+                                        const int32_t* offsets, const void* w_gate_up,
+                                        void* gu, void* ws, const g5moe_shape* shape,
+                                        void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(x);
+  G5_NONNULL(perm);
+  G5_NONNULL(offsets);
+  G5_NONNULL(w_gate_up);
+  G5_NONNULL(gu);
+  G5_NONNULL(ws);
+  char* w = static_cast<char*>(ws);
+  const hipStream_t st = as_stream(stream);
+  hipError_t err;
+  const uint16_t* xb = gemm_input(x, w, *shape, st, &err);
+  G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train (cast)"));
+  const WorkspaceLayout L = workspace_layout(*shape);
+  return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
+                                   reinterpret_cast<uint16_t*>(w + L.h),
+                                   static_cast<uint16_t*>(gu), *shape, st),
+                    "g5moe_expert_gate_up_train");
 }
 
 g5moe_status g5moe_expert_down(const int32_t* offsets, const void* w_down, void* y_perm,

@@ -65,7 +65,7 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
                            int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                            hipStream_t st);
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                          const uint16_t* wgu, uint16_t* h, const g5moe_shape& s,
+                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
                           hipStream_t st);
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);

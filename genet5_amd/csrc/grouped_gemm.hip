@@ -62,6 +62,8 @@ struct GemmArgs {
   int K;
   int Nout;
   int ldc;
+  uint16_t* C2;           // MODE 3: raw gate|up outputs [N*k, Nout] (packed order)
+  int ldc2;
   int a_rows_per_expert;  // 0: A row of sorted position p is p; > 0: expert e's j-th
                           // row is A row e * a_rows_per_expert + j (per-expert padded
                           // layout; at most a_rows_per_expert rows of each expert are used)
@@ -180,7 +182,8 @@ constexpr int persist_smem_bytes() {
 // tiles, BNF / 2 for half tiles, decoded in the full-tile numbering).
 // MODE: 0 = A rows in place (down, and the backward GEMMs), 1 = gathered x
 // rows with the SwiGLU epilogue (gate|up), 2 = gathered x rows, raw outputs
-// (the gate|up recompute of the backward).
+// (the gate|up recompute of the backward), 3 = gathered x rows, raw outputs
+// into C2 and the SwiGLU outputs into C (the training forward's gate|up).
 template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF>
 __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, const Units un) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
@@ -206,7 +209,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   static_assert(HALF ? 2 * BN == BNF : BN == BNF, "tile width");
   static_assert(S >= 2 && S * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
   static_assert((S - 2) * PER < 64, "vmcnt range");
-  constexpr bool SWIGLU = MODE == 1;
+  constexpr bool SWIGLU = MODE == 1 || MODE == 3;
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
   // Fragment f of the next substeps is read after the f-th MFMA of a substep,
   // so a substep must hold at least as many MFMAs as fragments.
@@ -490,7 +493,64 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
     // OB blocks of 32 columns (SwiGLU: h columns, half the feature columns) of
     // bf16, RBY bytes per token row; a pass stages ROWS token rows, chunk c of
     // row r at c ^ ((r / (256 / RBY)) % CR), then writes them back as 16-byte
-    // stores, CR lanes per row.
+    // stores, CR lanes per row.  MODE 3 first writes the raw feature columns
+    // into C2 the same way, then the SwiGLU outputs into C.
+    if constexpr (MODE == 3)
+    {
+      constexpr int OB = NB;
+      constexpr int RBY = OB * 64;
+      constexpr int CR = RBY / 16;
+      constexpr int ROWS = kEpiBytesPerWave / RBY;
+      constexpr int JP = ROWS / 32;  // token blocks per pass
+      constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
+      static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+      const int col0 = cur.n0 + wn * WTN;
+#pragma unroll
+      for (int pass = 0; pass < MB / JP; ++pass) {
+#pragma unroll
+        for (int jl = 0; jl < JP; ++jl) {
+          const int j = pass * JP + jl;
+          const int row = jl * 32 + tok_l;
+          const int swz = (row / LPR) % CR;
+#pragma unroll
+          for (int ob = 0; ob < OB; ++ob) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              float h[4];
+#pragma unroll
+              for (int uu = 0; uu < 4; ++uu) {
+                h[uu] = acc[ob][j][4 * q + uu];
+              }
+              uint2 o;
+              o.x = pack_bf16x2(h[0], h[1]);
+              o.y = pack_bf16x2(h[2], h[3]);
+              const int c = ob * 4 + q;
+              *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+              // keep only one group's accumulators in VGPRs at a time
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < ROWS * RBY / 1024; ++it) {
+          const int row = it * (1024 / RBY) + lane / CR;
+          const int c = lane % CR;
+          const uint4 v = *reinterpret_cast<const uint4*>(
+              epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
+          const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
+          if (p < cur.p_end)
+            *reinterpret_cast<uint4*>(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8) = v;
+        }
+      }
+    }
+    if constexpr (MODE == 3) {
+      // the SwiGLU sweep re-reads the accumulators from their AGPRs instead of
+      // keeping the raw sweep's copies live in VGPRs
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+#pragma unroll
+        for (int j = 0; j < MB; ++j) asm volatile("" : "+a"(acc[i][j]));
+    }
     {
       constexpr int OB = SWIGLU ? NB / 2 : NB;
       constexpr int RBY = OB * 64;
@@ -697,7 +757,7 @@ void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
 }  // namespace
 
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                          const uint16_t* wgu, uint16_t* h, const g5moe_shape& s,
+                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
                           hipStream_t st) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
@@ -707,15 +767,20 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.offsets = offsets;
   a.B = wgu;
   a.C = h;
+  a.C2 = gu;
   a.topk = s.top_k;
   a.n_experts = s.n_experts;
   a.K = s.d_model;
   a.Nout = 2 * s.d_ff;
   a.ldc = s.d_ff;
+  a.ldc2 = 2 * s.d_ff;
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);
+  if (gu != nullptr)  // h and the raw gate|up outputs (training forward)
+    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false>(pgrid, a, st);
+  else
+    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);
   return hipGetLastError();
 }
 

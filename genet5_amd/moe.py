@@ -74,7 +74,8 @@ _pack_gate_up_op.register_autograd(_pack_backward)
 def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
                           w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                                     torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+                                     torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                     torch.Tensor]:
     return tuple(t.contiguous() for t in
                  ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias))
 
@@ -88,25 +89,29 @@ def _(x, w_router, bias, w_gate_up, w_down, top_k):
     return (torch.empty_like(x), torch.empty((N, E), **f32), torch.empty((N, top_k), **i32),
             torch.empty((N, top_k), **f32), torch.empty((E + 1,), **i32),
             torch.empty((N * top_k,), **i32), torch.empty((N * top_k,), **i32),
-            torch.empty((N * top_k, d), dtype=torch.bfloat16, device=x.device))
+            torch.empty((N * top_k, d), dtype=torch.bfloat16, device=x.device),
+            torch.empty((N * top_k, w_gate_up.shape[1]), dtype=torch.bfloat16, device=x.device))
 
 
 def _train_setup(ctx, inputs, output):
     x, w_router, bias, w_gate_up, w_down, top_k = inputs
-    _, _, idx, w, offsets, perm, inv_pos, y_perm = output
+    _, _, idx, w, offsets, perm, inv_pos, y_perm, gu = output
     ctx.top_k = top_k
-    ctx.save_for_backward(x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm)
-    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm)
+    # gu: the forward's raw gate|up products, kept so the backward does not
+    # recompute them (894 MB at 36,400 tokens: HBM for time)
+    ctx.save_for_backward(x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm,
+                          gu)
+    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu)
 
 
 def _train_backward(ctx, dy, dlogits, *unused):
-    x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm = ctx.saved_tensors
+    x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm, gu = ctx.saved_tensors
     if dy is None:
         dy = torch.zeros_like(x)
     dx, d_wr, d_wgu, d_wd = ops.moe_backward(
         dy.to(torch.bfloat16).contiguous(), x, w_router, w_gate_up, w_down, ctx.top_k, idx, w,
         offsets, perm, inv_pos, y_perm,
-        grad_logits=None if dlogits is None else dlogits.float().contiguous())
+        grad_logits=None if dlogits is None else dlogits.float().contiguous(), gu=gu)
     return dx, d_wr, None, d_wgu, d_wd, None
 
 
@@ -222,7 +227,7 @@ class MoEFeedForward(nn.Module):
                             "dtype); got " + str(x2.dtype))
         wgu = _pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16))
         wd = self.w_down.to(torch.bfloat16)
-        y, logits, idx, _, offsets, _, _, _ = _moe_forward_train_op(
+        y, logits, idx, _, offsets, _, _, _, _ = _moe_forward_train_op(
             x2, w_router, self.router_bias, wgu, wd.contiguous(), self.top_k)
         self.aux_loss = None
         if self.aux_loss_coef > 0:

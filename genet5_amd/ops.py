@@ -314,15 +314,29 @@ ROW_PAD = 256  # padding rows of buffers read as the A operand of the grouped GE
 def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
                       w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None):
     """The layer forward as stage calls, returning what the backward needs:
-    (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm)."""
+    (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm, gu) with
+    gu the raw gate|up products bf16 [N*k, 2F] (packed column order), which the
+    gate|up GEMM stores beside h (g5moe_expert_gate_up_train) so that the backward
+    does not recompute them."""
     dev = _check_device(x2d)
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
+    F = F2 // 2
     idx, w, logits = router_topk(x2d, w_router, top_k, bias=bias, return_logits=True)
     _, offsets, perm, inv_pos = dispatch(idx, E, d)
-    y_perm = expert_swiglu(x2d, perm, offsets, w_gate_up, w_down, top_k)
+    _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
+    shape = _lib.make_shape(N, d, F, E, top_k, _dtype_code(x2d.dtype))
+    ws = workspace(shape, dev)
+    gu = torch.empty((N * top_k, F2), dtype=torch.bfloat16, device=dev)
+    y_perm = torch.empty((N * top_k, d), dtype=torch.bfloat16, device=dev)
+    S = _stream(dev)
+    _lib.call("g5moe_expert_gate_up_train", _ptr(x2d), _ptr(perm), _ptr(offsets),
+              _ptr(w_gate_up), _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
+    _lib.call("g5moe_expert_down", _ptr(offsets), _ptr(w_down), _ptr(y_perm), _ptr(ws),
+              ctypes.byref(shape), S)
+    del ws
     y = combine(y_perm, inv_pos, w, x2d.dtype)
-    return y, logits, idx, w, offsets, perm, inv_pos, y_perm
+    return y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu
 
 
 def transpose_experts(w: torch.Tensor) -> torch.Tensor:
@@ -369,7 +383,7 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
                  topk_idx: torch.Tensor, topk_w: torch.Tensor, offsets: torch.Tensor,
                  perm: torch.Tensor, inv_pos: torch.Tensor, y_perm: torch.Tensor,
                  grad_logits: Optional[torch.Tensor] = None, w_down_t: Optional[torch.Tensor] = None,
-                 w_gate_up_t: Optional[torch.Tensor] = None):
+                 w_gate_up_t: Optional[torch.Tensor] = None, gu: Optional[torch.Tensor] = None):
     """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer.
 
     HIP stages: gate gradient and dY (g5moe_gate_grad), router-logit gradient
@@ -400,11 +414,15 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     dlogits = torch.empty((N, E), dtype=torch.float32, device=dev)
     _lib.call("g5moe_router_grad", _ptr(dw), _ptr(topk_w), _ptr(topk_idx), _ptr(grad_logits),
               _ptr(dlogits), ctypes.byref(shape), S)
-    gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
-    ws = workspace(shape, dev)
-    _lib.call("g5moe_expert_gate_up_raw", _ptr(x2d), _ptr(perm), _ptr(offsets), _ptr(w_gate_up),
-              _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
-    del ws
+    if gu is None:
+        # the forward's gate|up products were not kept: recompute them
+        gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
+        ws = workspace(shape, dev)
+        _lib.call("g5moe_expert_gate_up_raw", _ptr(x2d), _ptr(perm), _ptr(offsets),
+                  _ptr(w_gate_up), _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
+        del ws
+    else:
+        _require(gu, "gu", (N * k, 2 * F), torch.bfloat16, dev)
     if w_down_t is None:
         w_down_t = transpose_experts(w_down)            # [E, F, d]
     dh = grouped_gemm(dyp, N * k, offsets, w_down_t)    # [N*k, F]

@@ -123,6 +123,17 @@ g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int3
                                   const void* w_gate_up, void* ws,
                                   const g5moe_shape* shape, void* stream);
 
+/* g5moe_expert_gate_up for training: the same h into the workspace, and the raw
+ * products gu[p] = x[perm[p] / k] . Wgu_e^T (bf16 [N*k, 2F], packed gate|up column
+ * order, the layout of g5moe_expert_gate_up_raw and bit for bit its values) for
+ * the SwiGLU backward, so the backward need not recompute them.  Replaces
+ * keeping `self.wi_0(x)` / `self.wi_1(x)` for autograd
+ * (lib/blocks/_component.py:50). */
+g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
+                                        const int32_t* offsets, const void* w_gate_up,
+                                        void* gu, void* ws, const g5moe_shape* shape,
+                                        void* stream);
+
 /* Grouped down GEMM: y_perm[p] = h[p] . Wd_e^T (bf16 out, fp32 accumulate),
  * h read from the workspace written by g5moe_expert_gate_up.  Replaces
  * `self.wo(hidden)` (lib/blocks/_component.py:44, :52).

@@ -49,17 +49,28 @@ def test_backward_stages_vs_oracle(cuda_device, n, d, F, E, k):
     rng = np.random.default_rng(5)
     dy_np = synth.f32_to_bf16_bits(rng.standard_normal((n, d)).astype(np.float32))
     dy = dev_t(dy_np, cuda_device, True)
-    y, logits, idx, w, offsets, perm, inv_pos, y_perm = ops.moe_forward_train(x, wr, wgu, wd, k)
+    y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(x, wr, wgu,
+                                                                                 wd, k)
     torch.cuda.synchronize()
     ref_i, _ = oracle.topk_gates_c(oracle.router_logits(inp.x, inp.w_router), k)
     np.testing.assert_array_equal(idx.cpu().numpy(), ref_i)
+    # the training forward (gate|up GEMM storing h and the raw products) gives the
+    # inference forward's output bit for bit, and its kept products equal the
+    # backward's recompute (g5moe_expert_gate_up_raw) bit for bit
+    assert torch.equal(y, ops.moe_forward(x, wr, wgu, wd, k))
+    from genet5_amd import _lib
+    import ctypes
+    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
+    gu_re = torch.empty_like(gu)
+    _lib.call("g5moe_expert_gate_up_raw", ops._ptr(x), ops._ptr(perm), ops._ptr(offsets),
+              ops._ptr(wgu), ops._ptr(gu_re), ops._ptr(ops.workspace(shape, cuda_device)),
+              ctypes.byref(shape), ops._stream(cuda_device))
+    torch.cuda.synchronize()
+    assert torch.equal(gu, gu_re)
 
     # gate gradient: dy_perm exact, dw in the contract's order (exact products)
     dw = torch.empty((n, k), dtype=torch.float32, device=cuda_device)
     dyp = torch.empty((n * k + ops.ROW_PAD, d), dtype=torch.bfloat16, device=cuda_device)
-    from genet5_amd import _lib
-    import ctypes
-    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
     _lib.call("g5moe_gate_grad", ops._ptr(dy), ops._ptr(y_perm), ops._ptr(inv_pos),
               ops._ptr(w), ops._ptr(dw), ops._ptr(dyp), ctypes.byref(shape),
               ops._stream(cuda_device))
@@ -83,8 +94,11 @@ def test_backward_stages_vs_oracle(cuda_device, n, d, F, E, k):
     np.testing.assert_array_equal(dw.cpu().numpy().view(np.uint32), acc[..., 0].view(np.uint32))
 
     dx, d_wr, d_wgu, d_wd = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm,
-                                             inv_pos, y_perm)
+                                             inv_pos, y_perm, gu=gu)
+    recomputed = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm)
     torch.cuda.synchronize()
+    for a, b in zip((dx, d_wr, d_wgu, d_wd), recomputed):
+        assert torch.equal(a, b)
     ref = oracle.moe_backward(inp.x, inp.w_router, inp.w_gate, inp.w_up, inp.w_down, ref_i, dy_np)
     d_wg, d_wu = ops.unpack_gate_up(d_wgu)
     check("dx", host(dx), ref["dx"])
