@@ -413,13 +413,15 @@ g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int
                                  void* out, int32_t cols, int32_t kmax,
                                  const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));
-  if (cols <= 0 || cols % 64 != 0 || kmax < 0)
+  if (cols <= 0 || cols % 64 != 0 || kmax < 0 || kmax % 8 != 0)
     return fail(G5MOE_ERR_INVALID_ARG, "pad_transpose: cols %d must be a positive multiple of "
-                "64 and kmax %d >= 0", int(cols), int(kmax));
+                "64 and kmax %d a multiple of 8 >= 0", int(cols), int(kmax));
   if (kmax == 0) return G5MOE_OK;
   G5_NONNULL(src);
   G5_NONNULL(offsets);
   G5_NONNULL(out);
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "pad_transpose: src and out must be 16-byte aligned");
   return hip_status(launch_pad_transpose(static_cast<const uint16_t*>(src), perm, offsets,
                                          static_cast<uint16_t*>(out), shape->n_experts, cols,
                                          kmax, shape->top_k, as_stream(stream)),

@@ -161,30 +161,45 @@ __global__ __launch_bounds__(256) void pad_transpose_kernel(
     const uint16_t* __restrict__ src, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, uint16_t* __restrict__ out, int C, int kmax,
     int topk) {
-  __shared__ uint16_t tile[64][66];
+  // 64 positions x 64 columns per block.  Tile row r (position j0 + r) holds its
+  // eight 16-byte column chunks at chunk ^ ((r >> 3) & 7): the 16-byte writes of
+  // the load phase and the 2-byte column reads of the store phase are both free
+  // of bank conflicts.  Global loads and stores are 16 bytes per lane.
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][64];
   const int e = blockIdx.z;
   const int j0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
   const int m = offsets[e + 1] - offsets[e];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int t = threadIdx.x;
+  const int ch = t & 7;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int jj = ty + 4 * i;  // tile row = position j0 + jj
-    const int j = j0 + jj;
-    uint16_t v = 0;
+  for (int i = 0; i < 2; ++i) {
+    const int r = (t >> 3) + 32 * i;
+    const int j = j0 + r;
+    uint4 v = make_uint4(0, 0, 0, 0);
     if (j < m) {
       const int64_t p = offsets[e] + j;
       const int64_t row = perm != nullptr ? int64_t(perm[p] / topk) : p;
-      v = src[row * C + c0 + tx];
+      v = *reinterpret_cast<const uint4*>(src + row * C + c0 + ch * 8);
     }
-    tile[jj][tx] = v;
+    *reinterpret_cast<uint4*>(&tile[r][(ch ^ ((r >> 3) & 7)) * 8]) = v;
   }
   __syncthreads();
   uint16_t* dst = out + int64_t(e) * C * kmax;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int c = ty + 4 * i;
-    const int j = j0 + tx;
-    if (j < kmax) dst[int64_t(c0 + c) * kmax + j] = tile[tx][c];
+  for (int i = 0; i < 2; ++i) {
+    const int c = (t >> 3) + 32 * i;  // output row c0 + c
+    const int oc = ch;                // positions j0 + 8 oc .. + 8
+    uint32_t w[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int r0 = 8 * oc + 2 * q;
+      const uint32_t lo = tile[r0][((c >> 3) ^ oc) * 8 + (c & 7)];
+      const uint32_t hi = tile[r0 + 1][((c >> 3) ^ oc) * 8 + (c & 7)];
+      w[q] = lo | (hi << 16);
+    }
+    if (j0 + 8 * oc < kmax)  // kmax is a multiple of 8: a chunk is wholly in or out
+      *reinterpret_cast<uint4*>(dst + int64_t(c0 + c) * kmax + j0 + 8 * oc) =
+          make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -320,7 +335,7 @@ hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const 
                                 uint16_t* out, int n_experts, int C, int kmax, int topk,
                                 hipStream_t st) {
   if (n_experts == 0 || C == 0 || kmax == 0) return hipSuccess;
-  if (C % 64 != 0) return hipErrorInvalidValue;
+  if (C % 64 != 0 || kmax % 8 != 0) return hipErrorInvalidValue;
   hipLaunchKernelGGL(pad_transpose_kernel,
                      dim3(unsigned(C / 64), unsigned((kmax + 63) / 64), unsigned(n_experts)),
                      dim3(256), 0, st, src, perm, offsets, out, C, kmax, topk);

@@ -279,7 +279,8 @@ g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t
 /* Per-expert padded transpose: out[e][c][j] = column c of the row of expert
  * e's j-th sorted position, 0 for j >= M_e.  The row of sorted position p is
  * src row p (perm == NULL: dY) or src row perm[p] / k (the gathered x row).
- *   src : bf16 [rows, cols];  out : bf16 [E, cols, kmax];  cols multiple of 64. */
+ *   src : bf16 [rows, cols];  out : bf16 [E, cols, kmax];  cols multiple of 64,
+ *   kmax multiple of 8; src and out 16-byte aligned. */
 g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int32_t* offsets,
                                  void* out, int32_t cols, int32_t kmax,
                                  const g5moe_shape* shape, void* stream);
