@@ -28,7 +28,9 @@
 // issued one DMA instruction after every other MFMA over those substeps, which
 // keeps the texture path busy without stalling the matrix core (issuing a
 // stage's 16 instructions in one burst stalled the MFMA stream for about as
-// long as the DMA took).
+// long as the DMA took).  The in-place GEMMs (down and the backward's, whose A
+// rows come from HBM rather than the small gathered x) keep a third A stage in
+// the epilogue region and issue A three k-steps ahead (down 9 % faster).
 //
 // Scheduling: expert row counts live on the device (offsets[]); the grid is
 // one workgroup per CU, and each workgroup walks a list of tiles derived from
@@ -141,6 +143,10 @@ __device__ __forceinline__ void wait_vmcnt_upto(int n) {
 // row segments: 8 lanes per 128 bytes of one output row.
 constexpr int kEpiBytesPerWave = 8192;
 
+#ifndef G5_A3
+#define G5_A3 1
+#endif
+
 template <int BM, int BN, int GM>
 __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileCoord& tc) {
   const int ntn = args.Nout / BN;
@@ -222,6 +228,14 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   // The gate|up GEMMs gather token rows through perm; the others read the
   // expert-contiguous A rows in place.
   constexpr bool GATHER = MODE != 0;
+  // Three A stages (MODE 0 with three fragment slots): the epilogue region,
+  // which is exactly one A stage (wave w's DMA slice of it is wave w's own
+  // region), doubles as A buffer 2, so A is issued three k-steps ahead and B
+  // two.  A buffers rotate with the k-step mod 3 (tiles start at 0 mod 3, so
+  // every tile's last step reads its A from the epilogue region: the next
+  // tile's third A stage goes out after the epilogue), B buffers mod 2.
+  constexpr bool A3 = G5_A3 && MODE == 0 && NSLOT == 3 && S == 2 &&
+                      A_BYTES == 4 * kEpiBytesPerWave;
   auto decode_unit = [&](int i, TileCoord& tc) {
     const int h = un.first + i * un.stride;
     if constexpr (HALF) {
@@ -238,6 +252,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   const int wm = wave >> 1, wn = wave & 1;
   const int K = args.K;
   const int nk = K / BK;  // >= S (checked by the launcher)
+  // LDS byte address of a pointer into smem as 32-bit scalar arithmetic (a
+  // generic-to-LDS cast of each DMA target would add a 64-bit null check)
+  const uint32_t smem_lds = lds_addr(smem);
+  auto lds_of = [&](const char* p) __attribute__((always_inline)) -> uint32_t { return smem_lds + uint32_t(p - smem); };
 
   auto sw = [](int r) { return (r / G) % CPR; };
   const int lrow = lane / CPR;
@@ -281,7 +299,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   auto dma_rows = [&](const TileCoord& tc) {
     if constexpr (GATHER) {
       const int p = min(tc.p_begin + wave * 64 + lane, tc.p_end - 1);
-      lds_dma4_s(args.perm, uint32_t(p) * 4u, lds_addr(epi));
+      lds_dma4_s(args.perm, uint32_t(p) * 4u, lds_of(epi));
     }
   };
   auto finish_rows = [&](uint32_t* rows) {
@@ -314,20 +332,37 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
     char* Bs = As + A_BYTES;
     if (q < AI) {
       if constexpr (GATHER)
-        lds_dma16_s(a_base + 2 * k0, row_off, lds_addr(As + (wave * AI + q) * 1024));
+        lds_dma16_s(a_base + 2 * k0, row_off, lds_of(As + (wave * AI + q) * 1024));
       else
         lds_dma16_s(a_base + 2 * k0 + size_t(q) * slot_bytes, lane_off[q & 1],
-                    lds_addr(As + (wave * AI + q) * 1024));
+                    lds_of(As + (wave * AI + q) * 1024));
     } else {
       const int j = q - AI;
       lds_dma16_s(b_base + 2 * k0 + size_t(j) * slot_bytes, lane_off[j & 1],
-                  lds_addr(Bs + (wave * BI + j) * 1024));
+                  lds_of(Bs + (wave * BI + j) * 1024));
     }
   };
   auto row_of = [&](const uint32_t* rows, int q) -> uint32_t {
     if constexpr (GATHER) return q < AI ? rows[q < AI ? q : 0] : 0u;
     return 0u;
   };
+  // A3: A slot q (in-place rows) into A buffer As, B slot j into B buffer Bs.
+  // The slot's source offset rides in the lane offset (one VGPR per slot), so
+  // a stage needs one scalar base per operand.
+  char* const epi_base = smem + S * STAGE;
+  constexpr int NV3 = A3 ? (AI > BI ? AI : BI) : 1;
+  uint32_t voff3[NV3];
+#pragma unroll
+  for (int q = 0; q < NV3; ++q) voff3[q] = lane_off[q & 1] + uint32_t(q) * slot_bytes;
+  auto issue_a = [&](char* As, const char* a_base, int k0, int q) __attribute__((always_inline)) {
+    lds_dma16_s(a_base + 2 * k0, voff3[q], lds_of(As + (wave * AI + q) * 1024));
+  };
+  auto issue_b = [&](char* Bs, const char* b_base, int k0, int j) __attribute__((always_inline)) {
+    lds_dma16_s(b_base + 2 * k0, voff3[j], lds_of(Bs + (wave * BI + j) * 1024));
+  };
+  // A3 buffers: A of k-step phase p (k-step mod 3), B of k-step g.
+  auto abuf3 = [&](int p) __attribute__((always_inline)) -> char* { return p == 2 ? epi_base : smem + p * STAGE; };
+  auto bbuf3 = [&](int g) __attribute__((always_inline)) -> char* { return smem + (g % S) * STAGE + A_BYTES; };
 
   TileCoord cur, nxt;
   int ui = 0;
@@ -365,22 +400,37 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
           *reinterpret_cast<const bf16x8*>(Bs + b_row + (f - MB) * 32 * RB + pc);
   };
 
-  // Prologue: stages 0 .. S-1 of the first tile (nk >= S).
+  // Prologue: stages 0 .. S-1 of the first tile (nk >= S); A3: A0 B0 A1 B1 A2
+  // (nk >= 6).
+  if constexpr (A3) {
 #pragma unroll
-  for (int st = 0; st < S; ++st)
+    for (int st = 0; st < 2; ++st) {
 #pragma unroll
-    for (int q = 0; q < PER; ++q) issue_one(st, row_of(rows_fill, q), a_cur, b_cur, st * BK, q);
+      for (int q = 0; q < AI; ++q) issue_a(abuf3(st), a_cur, st * BK, q);
+#pragma unroll
+      for (int j = 0; j < BI; ++j) issue_b(bbuf3(st), b_cur, st * BK, j);
+    }
+#pragma unroll
+    for (int q = 0; q < AI; ++q) issue_a(abuf3(2), a_cur, 2 * BK, q);
+    wait_vmcnt<PER + AI>();  // A0 and B0 landed
+  } else {
+#pragma unroll
+    for (int st = 0; st < S; ++st)
+#pragma unroll
+      for (int q = 0; q < PER; ++q)
+        issue_one(st, row_of(rows_fill, q), a_cur, b_cur, st * BK, q);
+    wait_vmcnt<(S - 1) * PER>();  // stage 0 landed
+  }
   int issued = S;  // stages issued so far (global step numbering)
-  wait_vmcnt<(S - 1) * PER>();  // stage 0 landed
   __syncthreads();
   // fragments of the tile's first LA substeps (slots 0 .. LA - 1)
-  auto load_first_frags = [&](const char* As) {
+  auto load_first_frags = [&](const char* As, const char* Bs) {
 #pragma unroll
     for (int ks = 0; ks < LA; ++ks)
 #pragma unroll
-      for (int f = 0; f < MB + NB; ++f) load_frag(As, As + A_BYTES, ks, ks, f);
+      for (int f = 0; f < MB + NB; ++f) load_frag(As, Bs, ks, ks, f);
   };
-  load_first_frags(smem);
+  load_first_frags(smem, smem + A_BYTES);
 
   const int tok_l = lane & 31;
   const int half = lane >> 5;
@@ -392,17 +442,19 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   // last substep the wave waits for step g + 1's stage, syncs (every wave is
   // done reading buffer g % S), and then refills that buffer with stage g + S,
   // one DMA instruction after every other MFMA of the substep.
-  auto kstep = [&](auto first_c, auto last_c, auto phase_c, int kt) {
+  auto kstep = [&](auto first_c, auto last_c, auto phase_c, int kt) __attribute__((always_inline)) {
     constexpr bool FIRST = decltype(first_c)::value;
     constexpr bool LAST = decltype(last_c)::value;
     constexpr int PHASE = decltype(phase_c)::value;  // gstep % 3 when NSLOT == 3
     auto slot = [](int ks) { return NSLOT == 2 ? (ks & 1) : (PHASE * KS + ks) % 3; };
     const int cb = gstep % S;
     const int nb = (gstep + 1) % S;
-    const char* As = smem + cb * STAGE;
-    const char* Bs = As + A_BYTES;
-    const char* As_n = smem + nb * STAGE;
-    const char* Bs_n = As_n + A_BYTES;
+    char* const Aw = A3 ? abuf3(PHASE) : smem + cb * STAGE;
+    char* const Bw = A3 ? bbuf3(gstep) : smem + cb * STAGE + A_BYTES;
+    const char* As = Aw;
+    const char* Bs = Bw;
+    const char* As_n = A3 ? abuf3((PHASE + 1) % 3) : smem + nb * STAGE;
+    const char* Bs_n = A3 ? bbuf3(gstep + 1) : smem + nb * STAGE + A_BYTES;
     // the stage that refills buffer cb: tile-relative k-step kt + S of this
     // tile or of the next.  Past the end of the tile list the refill still
     // goes out (stage 0 of the current tile again, into a buffer no later
@@ -412,15 +464,31 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
     const bool fill = fill_cur || has_nxt;
     const bool use_nxt = !fill_cur && has_nxt;
     const int k0_fill = fill_cur ? ks_fill * BK : (has_nxt ? (ks_fill - nk) * BK : 0);
-    const char* a_fill = use_nxt ? a_nxt : a_cur;
-    const char* b_fill = use_nxt ? b_nxt : b_cur;
+    // select values, not the captured lvalues (a select of two captures'
+    // addresses can keep the closures in scratch memory)
+    const char* const a_cur_v = a_cur;
+    const char* const a_nxt_v = a_nxt;
+    const char* const b_cur_v = b_cur;
+    const char* const b_nxt_v = b_nxt;
+    const char* a_fill = use_nxt ? a_nxt_v : a_cur_v;
+    const char* b_fill = use_nxt ? b_nxt_v : b_cur_v;
+    // A3: B refills as above (stage kt + 2); A refills with stage kt + 3,
+    // except on the tile's last step, whose A buffer the epilogue uses.
+    const int ka_fill = kt + 3;
+    const bool afill_cur = ka_fill < nk;
+    const int k0_afill = afill_cur ? ka_fill * BK : (has_nxt ? (ka_fill - nk) * BK : 0);
+    const char* a3_fill = (!afill_cur && has_nxt) ? a_nxt_v : a_cur_v;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks == BS) {
         __builtin_amdgcn_sched_barrier(0);
         // stage g + 1 landed; stages g + 2 .. issued - 1 may still be in flight
-        // (epilogue stores issued after them only make this wait longer)
-        wait_vmcnt_upto<S - 2, PER>(min(S - 2, max(0, issued - (gstep + 2))));
+        // (epilogue stores issued after them only make this wait longer).  A3:
+        // the last AI instructions (A of step g + 2) may still be in flight.
+        if constexpr (A3)
+          wait_vmcnt<AI>();
+        else
+          wait_vmcnt_upto<S - 2, PER>(min(S - 2, max(0, issued - (gstep + 2))));
         __syncthreads();
         if (fill && !fill_cur && ks_fill == nk) {
           // the next tile's perm block went out at this tile's start, before
@@ -453,8 +521,17 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
           constexpr int W = (KS - BS) * NT;
           const int w = (ks - BS) * NT + t;
 #pragma unroll
-          for (int q = (w * PER) / W; q < ((w + 1) * PER) / W; ++q)
-            issue_one(cb, row_of(rows_fill, q), a_fill, b_fill, k0_fill, q);
+          for (int q = (w * PER) / W; q < ((w + 1) * PER) / W; ++q) {
+            if constexpr (A3) {
+              // B first: the stage barrier's wait leaves only A in flight
+              if (q < BI)
+                issue_b(Bw, b_fill, k0_fill, q);
+              else if (!LAST)
+                issue_a(Aw, a3_fill, k0_afill, q - BI);
+            } else {
+              issue_one(cb, row_of(rows_fill, q), a_fill, b_fill, k0_fill, q);
+            }
+          }
         }
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -619,9 +696,20 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
       a_nxt = a_base_of(nxt);
       b_nxt = b_base_of(nxt);
     }
+    if constexpr (A3) {
+      // the new tile's third A stage, into the epilogue region: this wave's
+      // slice is its own region, whose epilogue LDS reads completed before
+      // their global stores, and every wave's last reads of it as the old
+      // tile's A buffer preceded the last step's stage barrier
+#pragma unroll
+      for (int q = 0; q < AI; ++q) issue_a(epi_base, a_cur, 2 * BK, q);
+    }
     // first substeps' fragments of the new tile (its stage 0 landed at the
     // last stage barrier)
-    load_first_frags(smem + (gstep % S) * STAGE);
+    if constexpr (A3)
+      load_first_frags(abuf3(0), bbuf3(gstep));
+    else
+      load_first_frags(smem + (gstep % S) * STAGE, smem + (gstep % S) * STAGE + A_BYTES);
   }
 }
 
