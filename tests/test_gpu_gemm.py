@@ -1,0 +1,58 @@
+"""The persistent grouped GEMM (g5moe_grouped_gemm, the kernel of the down product
+and the backward's dh / dX products) across its pipeline variants: two fragment
+slots (k-steps not a multiple of 3), three slots with the third A stage in the
+epilogue region (k-steps a multiple of 3, at least 6), 128- and 256-column tiles,
+the n-half tail, experts with no rows, partial last tiles and workgroups that run
+many tiles in a row.
+
+Two checks per case.  (1) Each expert launched alone gives the same bits as the
+full launch: an output element's MFMA chain runs over k in one fixed order whatever
+workgroup, tile slot or stage buffer computes it, so a stage that lands in the wrong
+buffer, a stale refill or a skipped tile breaks equality.  (2) Every expert's rows
+match a float32 torch product of the same bf16 operands (rtol = atol = 2e-2 on
+unit-scale outputs)."""
+import numpy as np
+import pytest
+import torch
+
+from genet5_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _offsets(counts, device):
+    off = np.zeros(len(counts) + 1, np.int32)
+    off[1:] = np.cumsum(counts)
+    return off, torch.tensor(off, dtype=torch.int32, device=device)
+
+
+@pytest.mark.parametrize("K,n_out,counts", [
+    (384, 256, [40000, 0, 257, 9000]),         # nk = 6: shortest three-stage tile
+    (576, 768, [0, 1, 255, 256, 4097, 30000]),  # nk = 9, three n-tiles, half tail
+    (448, 256, [12000, 3, 700]),               # nk = 7: two fragment slots
+    (128, 128, [5000, 0, 999]),                # nk = 2, 128-column tiles
+    (3072, 768, [9000, 4551, 0, 311]),         # the down product's K
+    (6144, 768, [2500, 1300]),                 # the dX product's K
+])
+def test_grouped_gemm_pipeline_variants(cuda_device, K, n_out, counts):
+    print(f"case K={K} n_out={n_out} counts={counts}", flush=True)
+    g = torch.Generator(device=cuda_device).manual_seed(K + n_out)
+    E = len(counts)
+    rows = int(sum(counts))
+    off, t_off = _offsets(counts, cuda_device)
+    a = torch.randn(rows + ops.ROW_PAD, K, device=cuda_device, generator=g).to(torch.bfloat16)
+    b = (torch.randn(E, n_out, K, device=cuda_device, generator=g) / K ** 0.5).to(torch.bfloat16)
+    c = ops.grouped_gemm(a, rows, t_off, b)
+    for e in range(E):
+        o0, o1 = int(off[e]), int(off[e + 1])
+        if o1 == o0:
+            continue
+        m = o1 - o0
+        a_e = torch.zeros(m + ops.ROW_PAD, K, dtype=torch.bfloat16, device=cuda_device)
+        a_e[:m] = a[o0:o1]
+        one = torch.tensor([0, m], dtype=torch.int32, device=cuda_device)
+        alone = ops.grouped_gemm(a_e, m, one, b[e:e + 1].contiguous())
+        assert torch.equal(alone, c[o0:o1]), f"expert {e} differs from its solo launch"
+        ref = a[o0:o1].float() @ b[e].float().T
+        torch.testing.assert_close(c[o0:o1].float(), ref, rtol=2e-2, atol=2e-2)
+    torch.cuda.synchronize()
