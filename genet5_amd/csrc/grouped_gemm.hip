@@ -30,7 +30,9 @@
 // stage's 16 instructions in one burst stalled the MFMA stream for about as
 // long as the DMA took).  The in-place GEMMs (down and the backward's, whose A
 // rows come from HBM rather than the small gathered x) keep a third A stage in
-// the epilogue region and issue A three k-steps ahead (down 9 % faster).
+// the epilogue region and issue A three k-steps ahead (down 9 % faster); the
+// SwiGLU GEMMs do the same for B, the weight tiles, which stream from beyond
+// the L2 (the training forward's gate|up 5 % faster, the inference one even).
 //
 // Scheduling: expert row counts live on the device (offsets[]); the grid is
 // one workgroup per CU, and each workgroup walks a list of tiles derived from
@@ -82,10 +84,25 @@ struct TileCoord {
   int a_row;  // A row of position p_begin (non-gathered A)
 };
 
+// The expert offsets as the tile decoding reads them: one VGPR whose lane e
+// holds offsets[e] (e <= n_experts <= 16), read with v_readlane.  A vector
+// load of offsets[e] between tiles made the compiler wait for every
+// outstanding memory operation of the wave (vmcnt 0), the stage DMAs in
+// flight and the epilogue's stores included (gate|up 2 % slower).
+struct Offsets {
+  int v;
+  __device__ __forceinline__ int operator()(int e) const { return __builtin_amdgcn_readlane(v, e); }
+};
+static_assert(kMaxExperts + 1 <= 64, "offsets[] fits one lane per entry");
+__device__ __forceinline__ Offsets load_offsets(const GemmArgs& args) {
+  const int lane = threadIdx.x & 63;
+  return Offsets{lane <= args.n_experts ? args.offsets[lane] : 0};
+}
+
 // Rows of expert e the GEMM computes: its sorted positions, capped at the padded
 // layout's per-expert row count.
-__device__ __forceinline__ int expert_rows(const GemmArgs& args, int e) {
-  const int cnt = args.offsets[e + 1] - args.offsets[e];
+__device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& off, int e) {
+  const int cnt = off(e + 1) - off(e);
   return args.a_rows_per_expert > 0 ? min(cnt, args.a_rows_per_expert) : cnt;
 }
 
@@ -146,13 +163,17 @@ constexpr int kEpiBytesPerWave = 8192;
 #ifndef G5_A3
 #define G5_A3 1
 #endif
+#ifndef G5_B3
+#define G5_B3 1
+#endif
 
 template <int BM, int BN, int GM>
-__device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileCoord& tc) {
+__device__ __forceinline__ void decode_tile_u(const GemmArgs& args, const Offsets& off, int u,
+                                              TileCoord& tc) {
   const int ntn = args.Nout / BN;
   int e = 0, mt_e = 0;
   for (; e < args.n_experts; ++e) {
-    const int cnt = expert_rows(args, e);
+    const int cnt = expert_rows(args, off, e);
     mt_e = (cnt + BM - 1) / BM;
     const int t = mt_e * ntn;
     if (u < t) break;
@@ -165,8 +186,8 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, int u, TileC
   const int mt = first_m + rr % gs;
   const int nt = rr / gs;
   tc.e = e;
-  tc.p_begin = args.offsets[e] + mt * BM;
-  tc.p_end = args.offsets[e] + expert_rows(args, e);
+  tc.p_begin = off(e) + mt * BM;
+  tc.p_end = off(e) + expert_rows(args, off, e);
   tc.a_row = args.a_rows_per_expert > 0 ? e * args.a_rows_per_expert + mt * BM : tc.p_begin;
   tc.n0 = nt * BN;
 }
@@ -191,7 +212,8 @@ constexpr int persist_smem_bytes() {
 // (the gate|up recompute of the backward), 3 = gathered x rows, raw outputs
 // into C2 and the SwiGLU outputs into C (the training forward's gate|up).
 template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF>
-__device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, const Units un) {
+__device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& off, char* smem,
+                                          const Units un) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
   constexpr int MB = WTM / 32, NB = WTN / 32;
   constexpr int RB = BK * 2;          // bytes per tile row in LDS
@@ -236,13 +258,20 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   // tile's third A stage goes out after the epilogue), B buffers mod 2.
   constexpr bool A3 = G5_A3 && MODE == 0 && NSLOT == 3 && S == 2 &&
                       A_BYTES == 4 * kEpiBytesPerWave;
+  // Three B stages (the SwiGLU modes, whose weight tiles are the operand that
+  // streams from beyond the L2): the same scheme with the roles swapped, B
+  // buffer 2 being the epilogue region, B issued three k-steps ahead and A
+  // two.  The next tile's gathered rows then travel through a VGPR instead of
+  // that region.
+  constexpr bool B3 = G5_B3 && SWIGLU && NSLOT == 3 && S == 2 &&
+                      B_BYTES == 4 * kEpiBytesPerWave;
   auto decode_unit = [&](int i, TileCoord& tc) {
     const int h = un.first + i * un.stride;
     if constexpr (HALF) {
-      decode_tile_u<BM, BNF, GM>(args, un.base + (h >> 1), tc);
+      decode_tile_u<BM, BNF, GM>(args, off, un.base + (h >> 1), tc);
       tc.n0 += (h & 1) * BN;
     } else {
-      decode_tile_u<BM, BNF, GM>(args, h, tc);
+      decode_tile_u<BM, BNF, GM>(args, off, h, tc);
     }
   };
 
@@ -269,12 +298,13 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
     lane_off[par] = uint32_t(lrow * K * 2 + (lpc ^ sw(par * RPB + lrow)) * 16);
 
   // Gathered rows.  The rows of the first tile are loaded directly; those of
-  // every later tile travel by LDS DMA (one dword per lane, the wave's 64
-  // rows) into the wave's epilogue region a tile ahead, where the stage waits
-  // cover them, and become byte offsets of token rows of x when the tile's
-  // first stage is issued.  Positions past the expert's end repeat its last
-  // row.  Wave w reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile: slot j's
-  // rows (w * AI + j) * RPB + lrow.
+  // every later tile travel a tile ahead (one dword per lane, the wave's 64
+  // rows) by LDS DMA into the wave's epilogue region, or, with three B stages
+  // (which use that region), into a VGPR; the stage waits cover them, and
+  // they become byte offsets of token rows of x when the tile's first stage
+  // is issued.  Positions past the expert's end repeat its last row.  Wave w
+  // reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile: slot j's rows
+  // (w * AI + j) * RPB + lrow.
   static_assert(AI * RPB == 64, "one 64-row perm block per wave");
   char* epi = smem + S * STAGE + wave * kEpiBytesPerWave;
   // rows_fill: byte offsets of the gathered rows of the tile whose stages
@@ -296,17 +326,33 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
       for (int j = 0; j < AI; ++j) rows[j] = to_offset(v[j], j);
     }
   };
+  // B3: the lane's perm entry of the next tile (one of the wave's 64 rows),
+  // loaded into a VGPR at the tile's start and read at the stage barrier
+  // that waits for every load of the wave (finish_rows).
+  uint32_t perm_v = 0;
   auto dma_rows = [&](const TileCoord& tc) {
     if constexpr (GATHER) {
       const int p = min(tc.p_begin + wave * 64 + lane, tc.p_end - 1);
-      lds_dma4_s(args.perm, uint32_t(p) * 4u, lds_of(epi));
+      if constexpr (B3)
+        perm_v = uint32_t(__builtin_nontemporal_load(args.perm + p));
+      else
+        lds_dma4_s(args.perm, uint32_t(p) * 4u, lds_of(epi));
     }
   };
   auto finish_rows = [&](uint32_t* rows) {
     if constexpr (GATHER) {
-      const uint32_t* pr = reinterpret_cast<const uint32_t*>(epi);
+      if constexpr (B3) {
+        // after the caller's vmcnt(0): the empty asm keeps every use of
+        // perm_v (and the compiler's own wait for it) behind that wait
+        asm volatile("" : "+v"(perm_v));
 #pragma unroll
-      for (int j = 0; j < AI; ++j) rows[j] = to_offset(pr[j * RPB + lrow], j);
+        for (int j = 0; j < AI; ++j)
+          rows[j] = to_offset(uint32_t(__shfl(int(perm_v), j * RPB + lrow)), j);
+      } else {
+        const uint32_t* pr = reinterpret_cast<const uint32_t*>(epi);
+#pragma unroll
+        for (int j = 0; j < AI; ++j) rows[j] = to_offset(pr[j * RPB + lrow], j);
+      }
     }
   };
   // Scalar source bases of a tile's DMA slot 0 (A and B), in bytes: slot q of
@@ -350,7 +396,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   // The slot's source offset rides in the lane offset (one VGPR per slot), so
   // a stage needs one scalar base per operand.
   char* const epi_base = smem + S * STAGE;
-  constexpr int NV3 = A3 ? (AI > BI ? AI : BI) : 1;
+  constexpr int NV3 = (A3 || B3) ? (AI > BI ? AI : BI) : 1;
   uint32_t voff3[NV3];
 #pragma unroll
   for (int q = 0; q < NV3; ++q) voff3[q] = lane_off[q & 1] + uint32_t(q) * slot_bytes;
@@ -363,6 +409,15 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
   // A3 buffers: A of k-step phase p (k-step mod 3), B of k-step g.
   auto abuf3 = [&](int p) __attribute__((always_inline)) -> char* { return p == 2 ? epi_base : smem + p * STAGE; };
   auto bbuf3 = [&](int g) __attribute__((always_inline)) -> char* { return smem + (g % S) * STAGE + A_BYTES; };
+  // B3 buffers: B of k-step phase p; A stays in stage g % 2.  A slot q of the
+  // gathered rows (row_off: the row's byte offset in x).
+  auto bbuf3b = [&](int p) __attribute__((always_inline)) -> char* {
+    return p == 2 ? epi_base : smem + p * STAGE + A_BYTES;
+  };
+  auto issue_ag = [&](char* As, uint32_t row_off, const char* a_base, int k0, int q)
+      __attribute__((always_inline)) {
+    lds_dma16_s(a_base + 2 * k0, row_off, lds_of(As + (wave * AI + q) * 1024));
+  };
 
   TileCoord cur, nxt;
   int ui = 0;
@@ -413,6 +468,17 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
 #pragma unroll
     for (int q = 0; q < AI; ++q) issue_a(abuf3(2), a_cur, 2 * BK, q);
     wait_vmcnt<PER + AI>();  // A0 and B0 landed
+  } else if constexpr (B3) {  // A0 B0 A1 B1 B2
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int q = 0; q < AI; ++q) issue_ag(smem + st * STAGE, rows_fill[q], a_cur, st * BK, q);
+#pragma unroll
+      for (int j = 0; j < BI; ++j) issue_b(bbuf3b(st), b_cur, st * BK, j);
+    }
+#pragma unroll
+    for (int j = 0; j < BI; ++j) issue_b(bbuf3b(2), b_cur, 2 * BK, j);
+    wait_vmcnt<PER + BI>();  // A0 and B0 landed
   } else {
 #pragma unroll
     for (int st = 0; st < S; ++st)
@@ -430,7 +496,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
 #pragma unroll
       for (int f = 0; f < MB + NB; ++f) load_frag(As, Bs, ks, ks, f);
   };
-  load_first_frags(smem, smem + A_BYTES);
+  load_first_frags(smem, B3 ? bbuf3b(0) : smem + A_BYTES);
 
   const int tok_l = lane & 31;
   const int half = lane >> 5;
@@ -450,11 +516,12 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
     const int cb = gstep % S;
     const int nb = (gstep + 1) % S;
     char* const Aw = A3 ? abuf3(PHASE) : smem + cb * STAGE;
-    char* const Bw = A3 ? bbuf3(gstep) : smem + cb * STAGE + A_BYTES;
+    char* const Bw = A3 ? bbuf3(gstep) : (B3 ? bbuf3b(PHASE) : smem + cb * STAGE + A_BYTES);
     const char* As = Aw;
     const char* Bs = Bw;
     const char* As_n = A3 ? abuf3((PHASE + 1) % 3) : smem + nb * STAGE;
-    const char* Bs_n = A3 ? bbuf3(gstep + 1) : smem + nb * STAGE + A_BYTES;
+    const char* Bs_n =
+        A3 ? bbuf3(gstep + 1) : (B3 ? bbuf3b((PHASE + 1) % 3) : smem + nb * STAGE + A_BYTES);
     // the stage that refills buffer cb: tile-relative k-step kt + S of this
     // tile or of the next.  Past the end of the tile list the refill still
     // goes out (stage 0 of the current tile again, into a buffer no later
@@ -473,11 +540,13 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
     const char* a_fill = use_nxt ? a_nxt_v : a_cur_v;
     const char* b_fill = use_nxt ? b_nxt_v : b_cur_v;
     // A3: B refills as above (stage kt + 2); A refills with stage kt + 3,
-    // except on the tile's last step, whose A buffer the epilogue uses.
+    // except on the tile's last step, whose A buffer the epilogue uses.  B3:
+    // the same with A and B swapped.
     const int ka_fill = kt + 3;
     const bool afill_cur = ka_fill < nk;
     const int k0_afill = afill_cur ? ka_fill * BK : (has_nxt ? (ka_fill - nk) * BK : 0);
     const char* a3_fill = (!afill_cur && has_nxt) ? a_nxt_v : a_cur_v;
+    const char* b3_fill = (!afill_cur && has_nxt) ? b_nxt_v : b_cur_v;
 #pragma unroll
     for (int ks = 0; ks < KS; ++ks) {
       if (ks == BS) {
@@ -487,13 +556,17 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
         // the last AI instructions (A of step g + 2) may still be in flight.
         if constexpr (A3)
           wait_vmcnt<AI>();
+        else if constexpr (B3)
+          wait_vmcnt<BI>();
         else
           wait_vmcnt_upto<S - 2, PER>(min(S - 2, max(0, issued - (gstep + 2))));
         __syncthreads();
         if (fill && !fill_cur && ks_fill == nk) {
           // the next tile's perm block went out at this tile's start, before
-          // stage kt + 1 when nk >= 2S - 1; otherwise wait for it explicitly
-          if (nk < 2 * S - 1) wait_vmcnt<0>();
+          // stage kt + 1 when nk >= 2S - 1; otherwise wait for it explicitly.
+          // B3: its VGPR is read after all of this wave's loads landed (this
+          // step's B(g + 2) included), once per tile
+          if (B3 || nk < 2 * S - 1) wait_vmcnt<0>();
           finish_rows(rows_fill);
         }
         __builtin_amdgcn_sched_barrier(0);
@@ -528,6 +601,12 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
                 issue_b(Bw, b_fill, k0_fill, q);
               else if (!LAST)
                 issue_a(Aw, a3_fill, k0_afill, q - BI);
+            } else if constexpr (B3) {
+              // A first: the stage barrier's wait leaves only B in flight
+              if (q < AI)
+                issue_ag(Aw, rows_fill[q < AI ? q : 0], a_fill, k0_fill, q);
+              else if (!LAST)
+                issue_b(Bw, b3_fill, k0_afill, q - AI);
             } else {
               issue_one(cb, row_of(rows_fill, q), a_fill, b_fill, k0_fill, q);
             }
@@ -704,10 +783,17 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, char* smem, cons
 #pragma unroll
       for (int q = 0; q < AI; ++q) issue_a(epi_base, a_cur, 2 * BK, q);
     }
+    if constexpr (B3) {
+      // the same for the new tile's third B stage
+#pragma unroll
+      for (int j = 0; j < BI; ++j) issue_b(epi_base, b_cur, 2 * BK, j);
+    }
     // first substeps' fragments of the new tile (its stage 0 landed at the
     // last stage barrier)
     if constexpr (A3)
       load_first_frags(abuf3(0), bbuf3(gstep));
+    else if constexpr (B3)
+      load_first_frags(smem + (gstep % S) * STAGE, bbuf3b(0));
     else
       load_first_frags(smem + (gstep % S) * STAGE, smem + (gstep % S) * STAGE + A_BYTES);
   }
@@ -726,9 +812,10 @@ template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
   const int ntn = args.Nout / BN;
+  const Offsets off = load_offsets(args);
   int total = 0;
   for (int e = 0; e < args.n_experts; ++e) {
-    const int cnt = expert_rows(args, e);
+    const int cnt = expert_rows(args, off, e);
     total += ((cnt + BM - 1) / BM) * ntn;
   }
   const int ng = gridDim.x;
@@ -741,20 +828,21 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   const int q = (hi - lo) / nslot, r = (hi - lo) % nslot;
   if constexpr (HALF_TAIL) {
     if (q > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, smem,
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, off, smem,
                                                            Units{lo + slot, nslot, q, 0});
     if (slot < 2 * r) {
       // every wave's DMAs of the full pass have landed (each waited for its
       // own) before the half pass refills the stage buffers
       if (q > 0) __syncthreads();
       tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, MODE, true>(
-          args, smem, Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
+          args, off, smem,
+          Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
     }
   } else {
     // one pass: the remainder tile of slots s < r is lo + s + q * nslot
     const int cnt = q + (slot < r ? 1 : 0);
     if (cnt > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, smem,
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, off, smem,
                                                            Units{lo + slot, nslot, cnt, 0});
   }
 }
