@@ -110,9 +110,9 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   const int64_t gpo = prow * 2 * F + 64 * q + r;
   if (jr >= offsets[e + 1] - offsets[e]) {
     const uint4 z = make_uint4(0, 0, 0, 0);
-    *reinterpret_cast<uint4*>(dgu_pad + gpo) = z;
-    *reinterpret_cast<uint4*>(dgu_pad + gpo + 32) = z;
-    *reinterpret_cast<uint4*>(h_pad + prow * F + f0) = z;
+    store16_nt(dgu_pad + gpo, z);
+    store16_nt(dgu_pad + gpo + 32, z);
+    store16_nt(h_pad + prow * F + f0, z);
     return;
   }
   const int64_t p = offsets[e] + jr;
@@ -144,13 +144,15 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   }
   const uint4 vog = make_uint4(og[0], og[1], og[2], og[3]);
   const uint4 vou = make_uint4(ou[0], ou[1], ou[2], ou[3]);
+  // non-temporal stores: later kernels read these (the dX product's
+  // operand reads run faster for it)
   if (dgu != nullptr) {
-    *reinterpret_cast<uint4*>(dgu + go) = vog;
-    *reinterpret_cast<uint4*>(dgu + go + 32) = vou;
+    store16_nt(dgu + go, vog);
+    store16_nt(dgu + go + 32, vou);
   }
-  *reinterpret_cast<uint4*>(dgu_pad + gpo) = vog;
-  *reinterpret_cast<uint4*>(dgu_pad + gpo + 32) = vou;
-  *reinterpret_cast<uint4*>(h_pad + prow * F + f0) = make_uint4(oh[0], oh[1], oh[2], oh[3]);
+  store16_nt(dgu_pad + gpo, vog);
+  store16_nt(dgu_pad + gpo + 32, vou);
+  store16_nt(h_pad + prow * F + f0, make_uint4(oh[0], oh[1], oh[2], oh[3]));
 }
 
 // out[e][c][j] = src row (expert e's j-th sorted position) column c, zero for

@@ -124,4 +124,13 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, g5_bf16x2));
 }
 
+// 16-byte global store marked non-temporal, for outputs that a later kernel
+// reads and this one does not: they stay out of the L2's retained set, which
+// is left to the kernel's own operands.
+typedef unsigned g5_u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store16_nt(void* p, const uint4& v) {
+  const g5_u32x4 w = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(w, static_cast<g5_u32x4*>(p));
+}
+
 }  // namespace g5moe
