@@ -458,10 +458,11 @@ def main():
         and np.array_equal(r.perm.cpu().numpy(), rp)
         and np.array_equal(r.inv_pos.cpu().numpy(), ri))
 
+    # calibrated HBM bytes per gate|up launch, measured at config 2 (null elsewhere)
     traffic = None
     tf_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                            "gate_up_traffic.json")
-    if os.path.exists(tf_path):
+    if cfg == 2 and args.shard is None and os.path.exists(tf_path):
         with open(tf_path) as f:
             traffic = json.load(f).get("bytes_per_launch")
 
