@@ -297,7 +297,7 @@ def bench_train(args) -> dict:
         dh = ops.grouped_gemm(dyp, N * k, offsets, wd_t)
         rec(3)
         offs = offsets.tolist()
-        kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
+        kmax = ops.wgrad_kmax(max(b - a for a, b in zip(offs[:-1], offs[1:])))
         h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
         dgu_buf = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
         dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
@@ -310,15 +310,10 @@ def bench_train(args) -> dict:
         _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),
                   ctypes.byref(shape), S)
         rec(6)
-        dyT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
-        _lib.call("g5moe_pad_transpose", P(dyp), None, P(offsets), P(dyT), d, kmax,
-                  ctypes.byref(shape), S)
-        xT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
-        _lib.call("g5moe_pad_transpose", P(x), P(perm), P(offsets), P(xT), d, kmax,
-                  ctypes.byref(shape), S)
+        dy_pad = ops.pad_rows(dyp, None, offsets, E, kmax, k)
+        x_pad = ops.pad_rows(x, perm, offsets, E, kmax, k)
         rec(7)
-        torch.bmm(dyT, h_pad)
-        ops.transpose_experts(torch.bmm(xT, dgu_pad))
+        ops.weight_grad(dy_pad, h_pad, dgu_pad, x_pad, offsets, kmax, top_k=k)
         rec(8)
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
@@ -345,10 +340,10 @@ def bench_train(args) -> dict:
         "stage_ms": st,
         "stage_tflops": {n: flops[n] / (st[n] * 1e-3) / 1e12 for n in flops},
         "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
-        "note": "weight-gradient GEMMs are two torch.bmm (hipBLASLt) over per-expert operands "
-                "padded to kmax rows (the padding's zero products count in the time, not in the "
-                "FLOP); the host reads the expert offsets once per step; every other stage is "
-                "this library's HIP kernels",
+        "note": "weight-gradient products: one g5moe_weight_grad launch over per-expert "
+                "token-major operands padded to 192-row groups (the padding's zero products "
+                "count in the time, not in the FLOP); the host reads the expert offsets once "
+                "per step; every stage is this library's HIP kernels",
     }
 
 

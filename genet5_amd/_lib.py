@@ -43,6 +43,8 @@ EXPORTED = (
     "g5moe_swiglu_backward",
     "g5moe_input_grad",
     "g5moe_pad_transpose",
+    "g5moe_pad_rows",
+    "g5moe_weight_grad",
     "g5moe_forward",
     "g5moe_attn_workspace_size",
     "g5moe_attn_varlen_fwd",
@@ -127,6 +129,10 @@ _SIGS = {
                               ctypes.c_int),
     "g5moe_pad_transpose": ([_P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _SHAPE_P, _P],
                             ctypes.c_int),
+    "g5moe_pad_rows": ([_P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _SHAPE_P, _P],
+                       ctypes.c_int),
+    "g5moe_weight_grad": ([_P, _P, _P, _P, _P, _P, _P, ctypes.c_int32, _SHAPE_P, _P],
+                          ctypes.c_int),
     "g5moe_input_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
     "g5moe_attn_workspace_size": ([ctypes.POINTER(AttnShape), ctypes.POINTER(ctypes.c_size_t)],

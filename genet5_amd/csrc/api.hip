@@ -428,6 +428,68 @@ g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int
                     "g5moe_pad_transpose");
 }
 
+g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t* offsets,
+                            void* out, int32_t cols, int32_t kmax, const g5moe_shape* shape,
+                            void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (cols <= 0 || cols % 8 != 0 || kmax < 0)
+    return fail(G5MOE_ERR_INVALID_ARG,
+                "pad_rows: cols %d must be a positive multiple of 8 and kmax %d >= 0", int(cols),
+                int(kmax));
+  if (kmax == 0) return G5MOE_OK;
+  G5_NONNULL(src);
+  G5_NONNULL(offsets);
+  G5_NONNULL(out);
+  if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "pad_rows: src and out must be 16-byte aligned");
+  if (int64_t(shape->n_experts) * kmax * (cols / 8) >= (int64_t(1) << 40))
+    return fail(G5MOE_ERR_UNSUPPORTED, "pad_rows: output too large");
+  return hip_status(launch_pad_rows(static_cast<const uint16_t*>(src), perm, offsets,
+                                    static_cast<uint16_t*>(out), shape->n_experts, cols, kmax,
+                                    shape->top_k, as_stream(stream)),
+                    "g5moe_pad_rows");
+}
+
+g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_down,
+                               const void* dgu_pad, const void* x_pad, void* d_w_gate_up,
+                               const int32_t* offsets, int32_t kmax, const g5moe_shape* shape,
+                               void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->d_model % 256 != 0 || shape->d_ff % 256 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "weight_grad: d_model %d and d_ff %d must be multiples "
+                "of 256", int(shape->d_model), int(shape->d_ff));
+  if (kmax < 384 || kmax % 192 != 0)
+    return fail(G5MOE_ERR_INVALID_ARG,
+                "weight_grad: kmax %d must be a multiple of 192 and >= 384", int(kmax));
+  if (d_w_down == nullptr && d_w_gate_up == nullptr) return G5MOE_OK;
+  G5_NONNULL(offsets);
+  uintptr_t align = 0;
+  if (d_w_down != nullptr) {
+    G5_NONNULL(dy_pad);
+    G5_NONNULL(h_pad);
+    align |= reinterpret_cast<uintptr_t>(dy_pad) | reinterpret_cast<uintptr_t>(h_pad) |
+             reinterpret_cast<uintptr_t>(d_w_down);
+  }
+  if (d_w_gate_up != nullptr) {
+    G5_NONNULL(dgu_pad);
+    G5_NONNULL(x_pad);
+    align |= reinterpret_cast<uintptr_t>(dgu_pad) | reinterpret_cast<uintptr_t>(x_pad) |
+             reinterpret_cast<uintptr_t>(d_w_gate_up);
+  }
+  if (align % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "weight_grad: buffers must be 16-byte aligned");
+  const int d = shape->d_model, F = shape->d_ff;
+  const bool down = d_w_down != nullptr;
+  const bool gu = d_w_gate_up != nullptr;
+  return hip_status(
+      launch_wgrad(down ? static_cast<const uint16_t*>(dy_pad) : nullptr,
+                   static_cast<const uint16_t*>(h_pad), static_cast<uint16_t*>(d_w_down), d, F,
+                   gu ? static_cast<const uint16_t*>(dgu_pad) : nullptr,
+                   static_cast<const uint16_t*>(x_pad), static_cast<uint16_t*>(d_w_gate_up),
+                   2 * F, d, offsets, shape->n_experts, kmax, as_stream(stream)),
+      "g5moe_weight_grad");
+}
+
 g5moe_status g5moe_input_grad(const void* dx_perm, const int32_t* inv_pos, const float* dlogits,
                               const void* w_router, void* dx, const g5moe_shape* shape,
                               void* stream) {

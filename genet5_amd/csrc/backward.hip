@@ -205,6 +205,29 @@ __global__ __launch_bounds__(256) void pad_transpose_kernel(
   }
 }
 
+// out[e][j][:] = the row of expert e's j-th sorted position, zero for j >= M_e:
+// the token-major per-expert padded operands of the weight-gradient products
+// (dY, and the gathered x rows).  The source row of sorted position p is p
+// itself (perm == nullptr) or the token perm[p] / topk.  One thread per 16 bytes.
+__global__ __launch_bounds__(256) void pad_rows_kernel(
+    const uint16_t* __restrict__ src, const int32_t* __restrict__ perm,
+    const int32_t* __restrict__ offsets, uint16_t* __restrict__ out, int C, int kmax,
+    int topk, int64_t total_chunks) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= total_chunks) return;
+  const int cpr = C / 8;
+  const int64_t prow = i / cpr;
+  const int ch = int(i - prow * cpr);
+  const int e = int(prow / kmax), j = int(prow - int64_t(e) * kmax);
+  uint4 v = make_uint4(0, 0, 0, 0);
+  if (j < offsets[e + 1] - offsets[e]) {
+    const int64_t pos = offsets[e] + j;
+    const int64_t row = perm != nullptr ? int64_t(perm[pos] / topk) : pos;
+    v = *reinterpret_cast<const uint4*>(src + row * C + ch * 8);
+  }
+  *reinterpret_cast<uint4*>(out + prow * C + ch * 8) = v;
+}
+
 // One thread per 8 consecutive outputs: dx = sum over slots of dX_perm rows
 // (slot order) + sum over experts of dl * Wr (expert order), fp32, one rounding.
 template <bool OUT_F32>
@@ -330,6 +353,17 @@ hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32
   if (work == 0) return hipSuccess;
   hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, st,
                      dh, gu, offsets, dgu, h_pad, dgu_pad, s.n_experts, kmax, s.d_ff);
+  return hipGetLastError();
+}
+
+hipError_t launch_pad_rows(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
+                           uint16_t* out, int n_experts, int C, int kmax, int topk,
+                           hipStream_t st) {
+  if (n_experts == 0 || C == 0 || kmax == 0) return hipSuccess;
+  if (C % 8 != 0) return hipErrorInvalidValue;
+  const int64_t chunks = int64_t(n_experts) * kmax * (C / 8);
+  hipLaunchKernelGGL(pad_rows_kernel, dim3(unsigned((chunks + 255) / 256)), dim3(256), 0, st,
+                     src, perm, offsets, out, C, kmax, topk, chunks);
   return hipGetLastError();
 }
 

@@ -87,6 +87,12 @@ hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32
 hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
                                 uint16_t* out, int n_experts, int C, int kmax, int topk,
                                 hipStream_t st);
+hipError_t launch_pad_rows(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
+                           uint16_t* out, int n_experts, int C, int kmax, int topk,
+                           hipStream_t st);
+hipError_t launch_wgrad(const uint16_t* a0, const uint16_t* b0, uint16_t* c0, int m0, int n0,
+                        const uint16_t* a1, const uint16_t* b1, uint16_t* c1, int m1, int n1,
+                        const int32_t* offsets, int n_experts, int kmax, hipStream_t st);
 hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const float* dlogits,
                              const void* w_router, void* dx, const g5moe_shape& s,
                              hipStream_t st);
@@ -101,6 +107,9 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
                            float* lse, float* kmax_ws, const g5moe_attn_shape& s,
                            hipStream_t st);
+
+// CUs of the current device (the persistent kernels' grid size).
+int device_cu_count();
 
 // ---- device helpers -------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {

@@ -47,13 +47,12 @@
 #include <algorithm>
 #include <type_traits>
 
-#include "g5moe_internal.h"
+#include "gemm_common.h"
 
 namespace g5moe {
 namespace {
 
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+using namespace gemm;
 
 struct GemmArgs {
   const uint16_t* A;      // gate|up: x (bf16) [N, K]; down: h [N*k, K]
@@ -84,63 +83,11 @@ struct TileCoord {
   int a_row;  // A row of position p_begin (non-gathered A)
 };
 
-// The expert offsets as the tile decoding reads them: one VGPR whose lane e
-// holds offsets[e] (e <= n_experts <= 16), read with v_readlane.  A vector
-// load of offsets[e] between tiles made the compiler wait for every
-// outstanding memory operation of the wave (vmcnt 0), the stage DMAs in
-// flight and the epilogue's stores included (gate|up 2 % slower).
-struct Offsets {
-  int v;
-  __device__ __forceinline__ int operator()(int e) const { return __builtin_amdgcn_readlane(v, e); }
-};
-static_assert(kMaxExperts + 1 <= 64, "offsets[] fits one lane per entry");
-__device__ __forceinline__ Offsets load_offsets(const GemmArgs& args) {
-  const int lane = threadIdx.x & 63;
-  return Offsets{lane <= args.n_experts ? args.offsets[lane] : 0};
-}
-
 // Rows of expert e the GEMM computes: its sorted positions, capped at the padded
 // layout's per-expert row count.
 __device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& off, int e) {
   const int cnt = off(e + 1) - off(e);
   return args.a_rows_per_expert > 0 ? min(cnt, args.a_rows_per_expert) : cnt;
-}
-
-// The same DMA with an explicit scalar base and a 32-bit per-lane byte offset
-// (global_load_lds_dwordx4 voff, sbase), M0 = LDS byte address of the 1 KB
-// block.  The compiler never holds M0 in the kernels that use these helpers:
-// every LDS DMA there goes through them and sets M0 itself.
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
-}
-__device__ __forceinline__ void lds_dma16_s(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
-}
-__device__ __forceinline__ void lds_dma4_s(const void* sbase, uint32_t voff, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
-}
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// Wait until at most n * PER vector-memory instructions of this thread are
-// outstanding, for a wave-uniform n in [0, MAXN] (the immediate must be a
-// constant, so dispatch over the possible values).
-template <int MAXN, int PER>
-__device__ __forceinline__ void wait_vmcnt_upto(int n) {
-  if constexpr (MAXN <= 0) {
-    wait_vmcnt<0>();
-  } else {
-    if (n >= MAXN)
-      wait_vmcnt<MAXN * PER>();
-    else
-      wait_vmcnt_upto<MAXN - 1, PER>(n);
-  }
 }
 
 // ---------------------------------------------------------------------------
@@ -158,8 +105,6 @@ __device__ __forceinline__ void wait_vmcnt_upto(int n) {
 // The epilogue goes through a wave-private 8 KB LDS region (after the two
 // stage buffers) so that every global store instruction writes whole 128-byte
 // row segments: 8 lanes per 128 bytes of one output row.
-constexpr int kEpiBytesPerWave = 8192;
-
 #ifndef G5_A3
 #define G5_A3 1
 #endif
@@ -814,7 +759,7 @@ template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
   const int ntn = args.Nout / BN;
-  const Offsets off = load_offsets(args);
+  const Offsets off = load_offsets(args.offsets, args.n_experts);
   int total = 0;
   for (int e = 0; e < args.n_experts; ++e) {
     const int cnt = expert_rows(args, off, e);
@@ -849,6 +794,9 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   }
 }
 
+}  // namespace
+
+// CUs of the current device (cached per device; 256 if the query fails).
 int device_cu_count() {
   static int cached[64] = {0};
   int dev = 0;
@@ -862,6 +810,8 @@ int device_cu_count() {
   }
   return cached[dev];
 }
+
+namespace {
 
 // Upper bound on the number of tiles: sum_e ceil(cnt_e / BM) <= ceil(Nk / BM) + E.
 template <int BM, int BN>

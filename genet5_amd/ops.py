@@ -426,10 +426,12 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     if w_down_t is None:
         w_down_t = transpose_experts(w_down)            # [E, F, d]
     dh = grouped_gemm(dyp, N * k, offsets, w_down_t)    # [N*k, F]
-    # every expert's rows padded to kmax (a multiple of 64 >= max M_e) for the
-    # weight-gradient batched products; the host reads the offsets once here
+    # every expert's rows padded to kmax (>= max M_e) for the weight-gradient
+    # products; the host reads the offsets once here
     offs = offsets.tolist()
-    kmax = max(64, -(-max(b - a for a, b in zip(offs[:-1], offs[1:])) // 64) * 64)
+    m_max = max(b - a for a, b in zip(offs[:-1], offs[1:]))
+    hip_wgrad = d % 256 == 0 and F % 256 == 0
+    kmax = wgrad_kmax(m_max) if hip_wgrad else max(64, -(-m_max // 64) * 64)
     h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
     # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
     dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
@@ -445,8 +447,17 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     _lib.call("g5moe_input_grad", _ptr(dxp), _ptr(inv_pos), _ptr(dlogits), _ptr(w_router),
               _ptr(dx), ctypes.byref(shape), S)
     del dxp
-    # weight gradients: batched products over the per-expert padded operands
-    # (zero rows past each expert's own): dWd_e = dY_e^T h_e, dWgu_e^T = X_e^T dGU_e
+    if hip_wgrad:
+        # weight gradients on the HIP kernel over token-major padded operands
+        dy_pad = pad_rows(dyp, None, offsets, E, kmax, k)
+        del dyp
+        x_pad = pad_rows(x2d, perm, offsets, E, kmax, k)
+        d_wd, d_wgu = weight_grad(dy_pad, h_pad, dgu_pad, x_pad, offsets, kmax, top_k=k)
+        del dy_pad, x_pad, h_pad, dgu_buf
+        d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
+        return dx, d_wr, d_wgu, d_wd
+    # other shapes: batched products over the per-expert padded operands (zero
+    # rows past each expert's own): dWd_e = dY_e^T h_e, dWgu_e^T = X_e^T dGU_e
     dyT = torch.empty((E, d, kmax), dtype=torch.bfloat16, device=dev)
     _lib.call("g5moe_pad_transpose", _ptr(dyp), None, _ptr(offsets), _ptr(dyT), d, kmax,
               ctypes.byref(shape), S)
@@ -459,6 +470,51 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     d_wgu = transpose_experts(torch.bmm(xT, dgu_pad))  # [E, d, 2F] -> [E, 2F, d]
     d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
     return dx, d_wr, d_wgu, d_wd
+
+
+def wgrad_kmax(m_max: int) -> int:
+    """Row count of the weight-gradient kernel's per-expert padded operands for a
+    largest expert of m_max rows: a multiple of 192, at least 384."""
+    return max(384, -(-m_max // 192) * 192)
+
+
+def pad_rows(src: torch.Tensor, perm: Optional[torch.Tensor], offsets: torch.Tensor,
+             n_experts: int, kmax: int, top_k: int = 1) -> torch.Tensor:
+    """out[e, j] = src row of expert e's j-th sorted position (src row p, or
+    src row perm[p] // top_k with perm), zero for j >= M_e: [E, kmax, cols]."""
+    dev = _check_device(src)
+    cols = src.shape[1]
+    if src.dtype != torch.bfloat16 or not src.is_contiguous():
+        raise TypeError("pad_rows takes a contiguous bf16 source")
+    _require(offsets, "offsets", (n_experts + 1,), torch.int32, dev)
+    out = torch.empty((n_experts, kmax, cols), dtype=torch.bfloat16, device=dev)
+    shape = _lib.make_shape(max(1, src.shape[0] // top_k), 256, 256, n_experts, top_k,
+                            _lib.DTYPE_BF16)
+    _lib.call("g5moe_pad_rows", _ptr(src), _ptr(perm), _ptr(offsets), _ptr(out), cols, kmax,
+              ctypes.byref(shape), _stream(dev))
+    return out
+
+
+def weight_grad(dy_pad: torch.Tensor, h_pad: torch.Tensor, dgu_pad: torch.Tensor,
+                x_pad: torch.Tensor, offsets: torch.Tensor, kmax: int, top_k: int = 2):
+    """(d_w_down [E, d, F], d_w_gate_up [E, 2F, d] packed) = per-expert
+    dy_pad[e]^T h_pad[e] and dgu_pad[e]^T x_pad[e] over token-major padded
+    operands ([E, kmax, .], zero rows past each expert's count; kmax from
+    wgrad_kmax)."""
+    dev = _check_device(dy_pad)
+    E, _, d = dy_pad.shape
+    F = h_pad.shape[2]
+    _require(dy_pad, "dy_pad", (E, kmax, d), torch.bfloat16, dev)
+    _require(h_pad, "h_pad", (E, kmax, F), torch.bfloat16, dev)
+    _require(dgu_pad, "dgu_pad", (E, kmax, 2 * F), torch.bfloat16, dev)
+    _require(x_pad, "x_pad", (E, kmax, d), torch.bfloat16, dev)
+    _require(offsets, "offsets", (E + 1,), torch.int32, dev)
+    d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
+    d_wgu = torch.empty((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
+    shape = _lib.make_shape(1, d, F, E, top_k, _lib.DTYPE_BF16)
+    _lib.call("g5moe_weight_grad", _ptr(dy_pad), _ptr(h_pad), _ptr(d_wd), _ptr(dgu_pad),
+              _ptr(x_pad), _ptr(d_wgu), _ptr(offsets), kmax, ctypes.byref(shape), _stream(dev))
+    return d_wd, d_wgu
 
 
 def unpack_gate_up(w_gate_up: torch.Tensor):

@@ -285,6 +285,33 @@ g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int
                                  void* out, int32_t cols, int32_t kmax,
                                  const g5moe_shape* shape, void* stream);
 
+/* Per-expert padded rows (no transpose): out[e][j][c] = column c of the row of
+ * expert e's j-th sorted position, 0 for j >= M_e; the row of sorted position
+ * p is src row p (perm == NULL: dY) or src row perm[p] / k (the gathered x
+ * row).  These are g5moe_weight_grad's token-major operands.
+ *   src : bf16 [rows, cols];  out : bf16 [E, kmax, cols];  cols multiple of 8,
+ *   kmax >= 0; src and out 16-byte aligned. */
+g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t* offsets,
+                            void* out, int32_t cols, int32_t kmax, const g5moe_shape* shape,
+                            void* stream);
+
+/* Expert weight gradients, the products autograd forms for FeedForward's wo
+ * and wi_0 / wi_1 (lib/blocks/_component.py:42-52) summed over each expert's
+ * rows, from per-expert padded token-major operands (zero rows past each
+ * expert's count; g5moe_pad_rows and g5moe_swiglu_backward write them):
+ *   d_w_down[e]    = dy_pad[e]^T  h_pad[e]  : bf16 [E, d, F]
+ *   d_w_gate_up[e] = dgu_pad[e]^T x_pad[e]  : bf16 [E, 2F, d] (packed gate|up)
+ *   dy_pad, x_pad : bf16 [E, kmax, d];  h_pad : bf16 [E, kmax, F];
+ *   dgu_pad : bf16 [E, kmax, 2F] (g5moe_swiglu_backward's dgu_pad rows).
+ * kmax a multiple of 192, >= 384 and >= every expert's row count; d and F
+ * multiples of 256; all buffers 16-byte aligned.  A product whose output is
+ * NULL is skipped.  fp32 accumulation over the expert's rows in a fixed order,
+ * one bf16 rounding. */
+g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_down,
+                               const void* dgu_pad, const void* x_pad, void* d_w_gate_up,
+                               const int32_t* offsets, int32_t kmax, const g5moe_shape* shape,
+                               void* stream);
+
 /* Input gradient: dx[t] = sum over s of dx_perm[inv_pos[t, s]] (slot order)
  * + sum over e of dlogits[t, e] * w_router[e] (expert order), fp32, one
  * rounding.  dx_perm : bf16 [N*k, d];  w_router, dx : [E, d], [N, d] in x_dtype. */

@@ -163,3 +163,54 @@ def test_rmsnorm_argument_checks(g5lib, args, code, msg):
     st = g5lib.g5moe_rmsnorm(None, None, None, ctypes.c_float(a["eps"]), so, None, a["n"],
                              a["d"], a["dtype"], None)
     assert st == code and msg in g5lib.g5moe_last_error().decode()
+
+
+def _wg_shape(d=768, F=3072):
+    return _lib.make_shape(100, d, F, 16, 2, _lib.DTYPE_BF16)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(kmax=200), 1, "multiple of 192"),
+    (dict(kmax=192), 1, ">= 384"),
+    (dict(F=384), 2, "multiples of 256"),
+    (dict(d=128), 2, "multiples of 256"),
+    (dict(), 1, "NULL"),
+    (dict(misaligned=True), 2, "aligned"),
+])
+def test_weight_grad_argument_checks(g5lib, kw, code, msg):
+    a = dict(kmax=384, d=768, F=3072, misaligned=False)
+    a.update(kw)
+    s = _wg_shape(a["d"], a["F"])
+    p = ctypes.c_void_p(0x1000)
+    bad = ctypes.c_void_p(0x1008)
+    if a["misaligned"]:
+        args = (p, bad, p, None, None, None, p)
+    else:
+        args = (None, None, p, None, None, None, None)   # an output without its operands
+    st = g5lib.g5moe_weight_grad(*args, a["kmax"], ctypes.byref(s), None)
+    assert st == code and msg in g5lib.g5moe_last_error().decode(), (st, g5lib.g5moe_last_error())
+
+
+def test_weight_grad_and_pad_rows_nothing_to_do(g5lib):
+    s = _wg_shape()
+    # both outputs NULL: no work, no pointer touched
+    assert g5lib.g5moe_weight_grad(None, None, None, None, None, None, None, 384,
+                                   ctypes.byref(s), None) == 0
+    assert g5lib.g5moe_pad_rows(None, None, None, None, 768, 0, ctypes.byref(s), None) == 0
+
+
+@pytest.mark.parametrize("cols,kmax,code,msg", [
+    (12, 64, 1, "multiple of 8"),
+    (768, -1, 1, "kmax"),
+    (768, 64, 1, "NULL"),
+])
+def test_pad_rows_argument_checks(g5lib, cols, kmax, code, msg):
+    s = _wg_shape()
+    st = g5lib.g5moe_pad_rows(None, None, None, None, cols, kmax, ctypes.byref(s), None)
+    assert st == code and msg in g5lib.g5moe_last_error().decode()
+
+
+def test_wgrad_kmax_rule():
+    assert ops.wgrad_kmax(1) == 384 and ops.wgrad_kmax(384) == 384
+    assert ops.wgrad_kmax(385) == 576 and ops.wgrad_kmax(5071) == 5184
+    assert all(ops.wgrad_kmax(m) % 192 == 0 and ops.wgrad_kmax(m) >= m for m in range(0, 9000, 37))

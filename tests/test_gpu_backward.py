@@ -264,3 +264,62 @@ def test_padded_dx_product_equals_sorted(cuda_device):
         if o1 > o0:
             exp = dg[o0:o1] @ wt[e].float().T
             torch.testing.assert_close(got[o0:o1].float(), exp, rtol=2e-2, atol=2e-2)
+
+
+def test_weight_grad_kernel_vs_fp32(cuda_device):
+    """g5moe_weight_grad (both products in one launch) against float32 torch
+    products per expert, over token-major padded operands from g5moe_pad_rows,
+    with an empty expert, a one-row expert, counts on and just past the 192-row
+    k-step groups, and large experts.  Also: g5moe_pad_rows copies rows exactly
+    (zero past each count), an empty expert's gradients are exactly zero, and
+    each product alone gives the same bits as the two in one launch (an output
+    element's reduction order does not depend on the launch's other tiles)."""
+    import ctypes
+    from genet5_amd import _lib
+    dev = cuda_device
+    g = torch.Generator(device=dev).manual_seed(5)
+    E, d, F, k = 7, 256, 512, 2
+    counts = [0, 1, 192, 384, 385, 2000, 4100]
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    T = int(offsets[-1])
+    n_tok = (T + k - 1) // k
+    t_off = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    dy = torch.randn(T + ops.ROW_PAD, d, device=dev, generator=g).to(torch.bfloat16)
+    x = torch.randn(n_tok, d, device=dev, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(n_tok * k, device=dev, generator=g)[:T].to(torch.int32)
+    kmax = ops.wgrad_kmax(max(counts))
+    print(f"  E={E} d={d} F={F} counts={counts} kmax={kmax}", flush=True)
+    dy_pad = ops.pad_rows(dy, None, t_off, E, kmax, k)
+    x_pad = ops.pad_rows(x, perm, t_off, E, kmax, k)
+    h_pad = torch.zeros(E, kmax, F, dtype=torch.bfloat16, device=dev)
+    dgu_pad = torch.zeros(E, kmax, 2 * F, dtype=torch.bfloat16, device=dev)
+    for e, c in enumerate(counts):
+        h_pad[e, :c] = torch.randn(c, F, device=dev, generator=g).to(torch.bfloat16)
+        dgu_pad[e, :c] = torch.randn(c, 2 * F, device=dev, generator=g).to(torch.bfloat16)
+    d_wd, d_wgu = ops.weight_grad(dy_pad, h_pad, dgu_pad, x_pad, t_off, kmax, top_k=k)
+    # each product alone
+    shape = _lib.make_shape(n_tok, d, F, E, k, _lib.DTYPE_BF16)
+    wd1 = torch.empty_like(d_wd)
+    wgu1 = torch.empty_like(d_wgu)
+    S = ops._stream(dev)
+    _lib.call("g5moe_weight_grad", ops._ptr(dy_pad), ops._ptr(h_pad), ops._ptr(wd1), None, None,
+              None, ops._ptr(t_off), kmax, ctypes.byref(shape), S)
+    _lib.call("g5moe_weight_grad", None, None, None, ops._ptr(dgu_pad), ops._ptr(x_pad),
+              ops._ptr(wgu1), ops._ptr(t_off), kmax, ctypes.byref(shape), S)
+    torch.cuda.synchronize()
+    assert torch.equal(wd1, d_wd) and torch.equal(wgu1, d_wgu)
+    for e, c in enumerate(counts):
+        o0, o1 = int(offsets[e]), int(offsets[e + 1])
+        assert torch.equal(dy_pad[e, :c], dy[o0:o1])
+        assert torch.equal(x_pad[e, :c], x[(perm[o0:o1] // k).long()])
+        assert not dy_pad[e, c:].any() and not x_pad[e, c:].any()
+        if c == 0:
+            assert not d_wd[e].any() and not d_wgu[e].any()
+            continue
+        ref_wd = dy[o0:o1].float().t() @ h_pad[e, :c].float()
+        ref_wgu = dgu_pad[e, :c].float().t() @ x_pad[e, :c].float()
+        for got, ref, name in ((d_wd[e], ref_wd, "dWd"), (d_wgu[e], ref_wgu, "dWgu")):
+            err = (got.float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
+            print(f"  expert {e} ({c} rows) {name}: max_rel={err:.2e}", flush=True)
+            assert err <= 8e-3, (e, name, err)
