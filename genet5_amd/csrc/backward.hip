@@ -22,6 +22,8 @@
 // dWgu_e^T = X_e^T dGU_e are batched products over operands padded per expert
 // to kmax rows (zeros past the expert's own): pad_transpose writes dY^T and
 // X^T as [E, C, kmax], swiglu_bwd writes h and dGU as [E, kmax, .].
+#include <type_traits>
+
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -230,11 +232,15 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(
 
 // One thread per 8 consecutive outputs: dx = sum over slots of dX_perm rows
 // (slot order) + sum over experts of dl * Wr (expert order), fp32, one rounding.
-template <bool OUT_F32>
+// TOPK (1, 2; 0 = runtime) and NE (16; 0 = runtime) fix the loop counts so that
+// a thread's row loads and router-weight loads are all in flight together.
+template <bool OUT_F32, int TOPK, int NE>
 __global__ __launch_bounds__(256) void input_grad_kernel(
     const uint16_t* __restrict__ dxp, const int32_t* __restrict__ inv_pos,
     const float* __restrict__ dlogits, const void* __restrict__ w_router, void* __restrict__ dx,
-    int64_t n_tokens, int d, int topk, int n_experts) {
+    int64_t n_tokens, int d, int topk_rt, int n_experts_rt) {
+  const int topk = TOPK > 0 ? TOPK : topk_rt;
+  const int n_experts = NE > 0 ? NE : n_experts_rt;
   const int cpr = d / 8;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n_tokens * cpr) return;
@@ -243,20 +249,34 @@ __global__ __launch_bounds__(256) void input_grad_kernel(
   float acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-  for (int s = 0; s < topk; ++s) {
-    const int32_t p = inv_pos[t * topk + s];
-    if (p < 0) continue;
-    const uint4 v = *reinterpret_cast<const uint4*>(dxp + int64_t(p) * d + c0);
+  auto add_row = [&](const uint4& v) {
     const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       acc[2 * j] += bf_lo(vv[j]);
       acc[2 * j + 1] += bf_hi(vv[j]);
     }
+  };
+  if constexpr (TOPK > 0) {
+    int32_t p[TOPK];
+    uint4 v[TOPK];
+#pragma unroll
+    for (int s = 0; s < TOPK; ++s) p[s] = inv_pos[t * TOPK + s];
+#pragma unroll
+    for (int s = 0; s < TOPK; ++s)
+      v[s] = p[s] >= 0 ? *reinterpret_cast<const uint4*>(dxp + int64_t(p[s]) * d + c0)
+                       : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int s = 0; s < TOPK; ++s)
+      if (p[s] >= 0) add_row(v[s]);
+  } else {
+    for (int s = 0; s < topk; ++s) {
+      const int32_t p = inv_pos[t * topk + s];
+      if (p < 0) continue;
+      add_row(*reinterpret_cast<const uint4*>(dxp + int64_t(p) * d + c0));
+    }
   }
-  for (int e = 0; e < n_experts; ++e) {
-    const float g = dlogits[t * n_experts + e];
-    float wv[8];
+  auto load_w = [&](int e, float* wv) {
     if constexpr (OUT_F32) {
       const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(w_router) +
                                                         int64_t(e) * d + c0);
@@ -273,8 +293,29 @@ __global__ __launch_bounds__(256) void input_grad_kernel(
         wv[2 * j + 1] = bf_hi(vv[j]);
       }
     }
+  };
+  if constexpr (NE > 0) {
+    float g[NE];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(g, wv[j], acc[j]);
+    for (int e = 0; e < NE; e += 4) {
+      const float4 q = *reinterpret_cast<const float4*>(dlogits + t * NE + e);
+      g[e] = q.x, g[e + 1] = q.y, g[e + 2] = q.z, g[e + 3] = q.w;
+    }
+    float wv[NE][8];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) load_w(e, wv[e]);
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(g[e], wv[e][j], acc[j]);
+  } else {
+    for (int e = 0; e < n_experts; ++e) {
+      const float g = dlogits[t * n_experts + e];
+      float wv[8];
+      load_w(e, wv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(g, wv[j], acc[j]);
+    }
   }
   if constexpr (OUT_F32) {
     float4* o = reinterpret_cast<float4*>(static_cast<float*>(dx) + t * d + c0);
@@ -384,12 +425,34 @@ hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const 
   const int64_t work = s.n_tokens * (s.d_model / 8);
   if (work == 0) return hipSuccess;
   const unsigned grid = unsigned((work + 255) / 256);
+  auto go = [&](auto f32_c, auto topk_c, auto ne_c) {
+    hipLaunchKernelGGL((input_grad_kernel<decltype(f32_c)::value, decltype(topk_c)::value,
+                                          decltype(ne_c)::value>),
+                       dim3(grid), dim3(256), 0, st, dxp, inv_pos, dlogits, w_router, dx,
+                       s.n_tokens, s.d_model, s.top_k, s.n_experts);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I16 = std::integral_constant<int, 16>;
+  auto by_ne = [&](auto f32_c, auto topk_c) {
+    if (s.n_experts == 16)
+      go(f32_c, topk_c, I16{});
+    else
+      go(f32_c, topk_c, I0{});
+  };
+  auto by_topk = [&](auto f32_c) {
+    if (s.top_k == 2)
+      by_ne(f32_c, I2{});
+    else if (s.top_k == 1)
+      by_ne(f32_c, I1{});
+    else
+      by_ne(f32_c, I0{});
+  };
   if (s.x_dtype == G5MOE_DTYPE_F32)
-    hipLaunchKernelGGL(input_grad_kernel<true>, dim3(grid), dim3(256), 0, st, dxp, inv_pos,
-                       dlogits, w_router, dx, s.n_tokens, s.d_model, s.top_k, s.n_experts);
+    by_topk(std::true_type{});
   else
-    hipLaunchKernelGGL(input_grad_kernel<false>, dim3(grid), dim3(256), 0, st, dxp, inv_pos,
-                       dlogits, w_router, dx, s.n_tokens, s.d_model, s.top_k, s.n_experts);
+    by_topk(std::false_type{});
   return hipGetLastError();
 }
 
