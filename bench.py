@@ -281,23 +281,29 @@ def bench_train(args) -> dict:
     names = ["fwd", "gate_router_grad", "dh_gemm", "swiglu_bwd", "dx_gemm", "input_grad",
              "wgrad_operands", "wgrad_gemms"]
 
+    # the expert offsets reach the host by a non-blocking copy issued right after
+    # the forward's dispatch, so reading them does not drain the queue
+    offs_host = torch.empty(E + 1, dtype=torch.int32, pin_memory=True)
+    offs_ready = torch.cuda.Event()
+
     def step(ev=None):
         rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
         rec(0)
         y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(
-            x, wr, wgu, wd, k)
+            x, wr, wgu, wd, k, offsets_host=offs_host, offsets_ready=offs_ready)
         rec(1)
+        offs_ready.synchronize()
+        offs = offs_host.tolist()
+        kmax = ops.wgrad_kmax(max(b - a for a, b in zip(offs[:-1], offs[1:])))
         dw = torch.empty((N, k), dtype=torch.float32, device=dev)
-        dyp = torch.empty((N * k + ops.ROW_PAD, d), dtype=torch.bfloat16, device=dev)
-        _lib.call("g5moe_gate_grad", P(dy), P(y_perm), P(inv_pos), P(w), P(dw), P(dyp),
-                  ctypes.byref(shape), S)
+        dy_buf = torch.empty((E * kmax + ops.ROW_PAD, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_gate_grad_padded", P(dy), P(y_perm), P(inv_pos), P(w), P(offsets),
+                  P(dw), P(dy_buf), kmax, ctypes.byref(shape), S)
         dl = torch.empty((N, E), dtype=torch.float32, device=dev)
         _lib.call("g5moe_router_grad", P(dw), P(w), P(idx), None, P(dl), ctypes.byref(shape), S)
         rec(2)
-        dh = ops.grouped_gemm(dyp, N * k, offsets, wd_t)
+        dh = ops.grouped_gemm_padded(dy_buf, kmax, N * k, offsets, wd_t)
         rec(3)
-        offs = offsets.tolist()
-        kmax = ops.wgrad_kmax(max(b - a for a, b in zip(offs[:-1], offs[1:])))
         h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
         dgu_buf = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
         dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
@@ -310,7 +316,7 @@ def bench_train(args) -> dict:
         _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),
                   ctypes.byref(shape), S)
         rec(6)
-        dy_pad = ops.pad_rows(dyp, None, offsets, E, kmax, k)
+        dy_pad = dy_buf[:E * kmax].view(E, kmax, d)
         x_pad = ops.pad_rows(x, perm, offsets, E, kmax, k)
         rec(7)
         ops.weight_grad(dy_pad, h_pad, dgu_pad, x_pad, offsets, kmax, top_k=k)
@@ -342,8 +348,11 @@ def bench_train(args) -> dict:
         "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
         "note": "weight-gradient products: one g5moe_weight_grad launch over per-expert "
                 "token-major operands padded to 192-row groups (the padding's zero products "
-                "count in the time, not in the FLOP); the host reads the expert offsets once "
-                "per step; every stage is this library's HIP kernels",
+                "count in the time, not in the FLOP); the gate gradient writes dY in that "
+                "padded layout, which the dh product also reads (wgrad_operands is the "
+                "gathered-X padding alone); the expert offsets reach the host by a "
+                "non-blocking copy issued after the dispatch; every stage is this "
+                "library's HIP kernels",
     }
 
 

@@ -38,6 +38,7 @@ EXPORTED = (
     "g5moe_grouped_gemm",
     "g5moe_grouped_gemm_padded",
     "g5moe_gate_grad",
+    "g5moe_gate_grad_padded",
     "g5moe_router_grad",
     "g5moe_expert_gate_up_raw",
     "g5moe_swiglu_backward",
@@ -123,6 +124,8 @@ _SIGS = {
                                    ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _P],
                                   ctypes.c_int),
     "g5moe_gate_grad": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_gate_grad_padded": ([_P, _P, _P, _P, _P, _P, _P, ctypes.c_int32, _SHAPE_P, _P],
+                               ctypes.c_int),
     "g5moe_router_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up_raw": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_swiglu_backward": ([_P, _P, _P, _P, _P, _P, ctypes.c_int32, _SHAPE_P, _P],

@@ -352,8 +352,34 @@ g5moe_status g5moe_gate_grad(const void* dy, const void* y_perm, const int32_t* 
   G5_NONNULL(dy_perm);
   return hip_status(launch_gate_grad(static_cast<const uint16_t*>(dy),
                                      static_cast<const uint16_t*>(y_perm), inv_pos, topk_w, dw,
-                                     static_cast<uint16_t*>(dy_perm), *shape, as_stream(stream)),
+                                     static_cast<uint16_t*>(dy_perm), nullptr, 0, *shape,
+                                     as_stream(stream)),
                     "g5moe_gate_grad");
+}
+
+g5moe_status g5moe_gate_grad_padded(const void* dy, const void* y_perm, const int32_t* inv_pos,
+                                    const float* topk_w, const int32_t* offsets, float* dw,
+                                    void* dy_pad, int32_t kmax, const g5moe_shape* shape,
+                                    void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->x_dtype != G5MOE_DTYPE_BF16)
+    return fail(G5MOE_ERR_UNSUPPORTED, "the backward takes bf16 activations");
+  if (kmax < 0) return fail(G5MOE_ERR_INVALID_ARG, "kmax %d < 0", int(kmax));
+  if (shape->n_tokens == 0 && kmax == 0) return G5MOE_OK;
+  G5_NONNULL(offsets);
+  G5_NONNULL(dy_pad);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(dy);
+    G5_NONNULL(y_perm);
+    G5_NONNULL(inv_pos);
+    G5_NONNULL(topk_w);
+    G5_NONNULL(dw);
+  }
+  return hip_status(launch_gate_grad(static_cast<const uint16_t*>(dy),
+                                     static_cast<const uint16_t*>(y_perm), inv_pos, topk_w, dw,
+                                     static_cast<uint16_t*>(dy_pad), offsets, kmax, *shape,
+                                     as_stream(stream)),
+                    "g5moe_gate_grad_padded");
 }
 
 g5moe_status g5moe_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,

@@ -22,6 +22,7 @@
 // dWgu_e^T = X_e^T dGU_e are batched products over operands padded per expert
 // to kmax rows (zeros past the expert's own): pad_transpose writes dY^T and
 // X^T as [E, C, kmax], swiglu_bwd writes h and dGU as [E, kmax, .].
+#include <algorithm>
 #include <type_traits>
 
 #include "g5moe_internal.h"
@@ -34,37 +35,81 @@ __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 
 
 // One wavefront per assignment a = t * k + s.  Lane c holds columns
 // [c * L, c * L + L); the dot product is an fma chain per lane added over lane
-// bits 5 .. 0, so dw is deterministic.
-template <int L>
+// bits 5 .. 0, so dw is deterministic.  PAD: the scaled dY row of sorted
+// position p = offsets[e] + j goes to row e * kmax + j of the per-expert padded
+// layout [E, kmax, D] instead of row p, and wave a also zeroes padded row a
+// when a lies past its expert's count (the grid covers max(N k, E kmax) waves).
+template <int L, bool PAD>
 __global__ __launch_bounds__(256) void gate_grad_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ y_perm,
     const int32_t* __restrict__ inv_pos, const float* __restrict__ topk_w,
-    float* __restrict__ dw, uint16_t* __restrict__ dyp, int64_t nk, int topk) {
+    float* __restrict__ dw, uint16_t* __restrict__ dyp, int64_t nk, int topk,
+    const int32_t* __restrict__ offsets, int n_experts, int kmax) {
   constexpr int D = 64 * L;
   const int lane = threadIdx.x & 63;
-  const int64_t a = int64_t(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (a >= nk) return;
-  const int64_t t = a / topk;
-  const int32_t p = inv_pos[a];
-  if (p < 0) {
-    if (lane == 0) dw[a] = 0.f;
-    return;
+  const int64_t a = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // PAD: lane l <= E holds offsets[l]; issued beside the inv_pos load
+  const int ol = PAD ? offsets[lane <= n_experts ? lane : n_experts] : 0;
+  const int32_t p = a < nk ? inv_pos[a] : -1;
+  // PAD: padded row a = e * kmax + j is zeroed when j >= M_e, with e the
+  // number of l in [1, E] with l * kmax <= a.  Decided here, before any store:
+  // CDNA's vmcnt also counts stores, so a use of ol after them would wait for
+  // their completion.
+  bool zero_row = false;
+  if constexpr (PAD) {
+    if (a < int64_t(n_experts) * kmax) {
+      const int e = __popcll(__ballot(lane >= 1 && lane <= n_experts && int64_t(lane) * kmax <= a));
+      const int64_t j = a - int64_t(e) * kmax;
+      zero_row = j >= __shfl(ol, e + 1, 64) - __shfl(ol, e, 64);
+    }
   }
-  const float w = topk_w[a];
-  const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
-  const uint32_t* yr = reinterpret_cast<const uint32_t*>(y_perm + int64_t(p) * D + lane * L);
-  uint32_t* outr = reinterpret_cast<uint32_t*>(dyp + int64_t(p) * D + lane * L);
-  float acc = 0.f;
+  if (a < nk && p < 0 && lane == 0) dw[a] = 0.f;
+  if (p >= 0) {
+    const int64_t t = a / topk;
+    int64_t row = p;
+    bool store = true;
+    if constexpr (PAD) {
+      // offsets are non-decreasing and offsets[E] > p: the number of experts
+      // l in [1, E] with offsets[l] <= p is p's expert
+      const int e = __popcll(__ballot(lane >= 1 && lane <= n_experts && ol <= p));
+      const int j = p - __shfl(ol, e, 64);
+      row = int64_t(e) * kmax + j;
+      store = j < kmax;  // a kmax below the expert's count: keep the writes in bounds
+    }
+    const float w = topk_w[a];
+    const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
+    const uint32_t* yr = reinterpret_cast<const uint32_t*>(y_perm + int64_t(p) * D + lane * L);
+    uint32_t* outr = reinterpret_cast<uint32_t*>(dyp + row * D + lane * L);
+    // every load of the row in flight before the first use
+    uint32_t gv[L / 2], yv[L / 2], ov[L / 2];
 #pragma unroll
-  for (int i = 0; i < L / 2; ++i) {
-    const uint32_t g = dyr[i], y = yr[i];
-    acc = __builtin_fmaf(bf_lo(g), bf_lo(y), acc);
-    acc = __builtin_fmaf(bf_hi(g), bf_hi(y), acc);
-    outr[i] = pack_bf16x2(w * bf_lo(g), w * bf_hi(g));
+    for (int i = 0; i < L / 2; ++i) {
+      gv[i] = dyr[i];
+      yv[i] = yr[i];
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < L / 2; ++i) {
+      const uint32_t g = gv[i], y = yv[i];
+      acc = __builtin_fmaf(bf_lo(g), bf_lo(y), acc);
+      acc = __builtin_fmaf(bf_hi(g), bf_hi(y), acc);
+      ov[i] = pack_bf16x2(w * bf_lo(g), w * bf_hi(g));
+    }
+    // the reduction (which needs every load) ahead of the stores, so that no
+    // wait for a load also waits for them
+#pragma unroll
+    for (int bit = 32; bit >= 1; bit >>= 1) acc = acc + __shfl_xor(acc, bit, 64);
+    if (store) {
+#pragma unroll
+      for (int i = 0; i < L / 2; ++i) outr[i] = ov[i];
+    }
+    if (lane == 0) dw[a] = acc;
   }
+  if (zero_row) {
+    uint32_t* zr = reinterpret_cast<uint32_t*>(dyp + a * D + lane * L);
 #pragma unroll
-  for (int bit = 32; bit >= 1; bit >>= 1) acc = acc + __shfl_xor(acc, bit, 64);
-  if (lane == 0) dw[a] = acc;
+    for (int i = 0; i < L / 2; ++i) zr[i] = 0u;
+  }
 }
 
 // One thread per token.
@@ -356,15 +401,24 @@ __global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restri
 
 hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const int32_t* inv_pos,
                             const float* topk_w, float* dw, uint16_t* dyp,
-                            const g5moe_shape& s, hipStream_t st) {
+                            const int32_t* offsets, int kmax, const g5moe_shape& s,
+                            hipStream_t st) {
   const int64_t nk = s.n_tokens * s.top_k;
-  if (nk == 0) return hipSuccess;
-  const unsigned grid = unsigned((nk + 3) / 4);
+  const bool pad = offsets != nullptr;
+  const int64_t waves = pad ? std::max<int64_t>(nk, int64_t(s.n_experts) * kmax) : nk;
+  if (waves == 0) return hipSuccess;
+  const unsigned grid = unsigned((waves + 3) / 4);
   switch (s.d_model / 64) {
 #define G5_GG(LL)                                                                          \
   case LL:                                                                                 \
-    hipLaunchKernelGGL(gate_grad_kernel<LL>, dim3(grid), dim3(256), 0, st, dy, y_perm,    \
-                       inv_pos, topk_w, dw, dyp, nk, s.top_k);                             \
+    if (pad)                                                                               \
+      hipLaunchKernelGGL((gate_grad_kernel<LL, true>), dim3(grid), dim3(256), 0, st, dy,   \
+                         y_perm, inv_pos, topk_w, dw, dyp, nk, s.top_k, offsets,           \
+                         s.n_experts, kmax);                                               \
+    else                                                                                   \
+      hipLaunchKernelGGL((gate_grad_kernel<LL, false>), dim3(grid), dim3(256), 0, st, dy,  \
+                         y_perm, inv_pos, topk_w, dw, dyp, nk, s.top_k, offsets,           \
+                         s.n_experts, kmax);                                               \
     break;
     G5_GG(2)
     G5_GG(4)

@@ -75,9 +75,11 @@ hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int
 hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
                              uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
                              int a_rows_per_expert, hipStream_t st);
+// offsets == nullptr: dyp in sorted order; otherwise per expert padded to kmax rows
 hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const int32_t* inv_pos,
                             const float* topk_w, float* dw, uint16_t* dyp,
-                            const g5moe_shape& s, hipStream_t st);
+                            const int32_t* offsets, int kmax, const g5moe_shape& s,
+                            hipStream_t st);
 hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
                               const float* grad_logits, float* dlogits, const g5moe_shape& s,
                               hipStream_t st);

@@ -312,18 +312,33 @@ ROW_PAD = 256  # padding rows of buffers read as the A operand of the grouped GE
 
 
 def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
-                      w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None):
+                      w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None,
+                      offsets_host: Optional[torch.Tensor] = None,
+                      offsets_ready: Optional["torch.cuda.Event"] = None):
     """The layer forward as stage calls, returning what the backward needs:
     (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm, gu) with
     gu the raw gate|up products bf16 [N*k, 2F] (packed column order), which the
     gate|up GEMM stores beside h (g5moe_expert_gate_up_train) so that the backward
-    does not recompute them."""
+    does not recompute them.
+
+    offsets_host (pinned int32 [E + 1] on the host): the expert offsets are copied
+    there without blocking as soon as the dispatch has written them, and
+    offsets_ready (if given) is recorded after the copy.  Once the event has
+    completed, moe_backward(..., offsets_host=...) reads them without waiting for
+    the rest of the forward."""
     dev = _check_device(x2d)
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
     F = F2 // 2
     idx, w, logits = router_topk(x2d, w_router, top_k, bias=bias, return_logits=True)
     _, offsets, perm, inv_pos = dispatch(idx, E, d)
+    if offsets_host is not None:
+        if offsets_host.device.type != "cpu" or offsets_host.shape != (E + 1,) or \
+                offsets_host.dtype != torch.int32 or not offsets_host.is_pinned():
+            raise ValueError("offsets_host must be a pinned host int32 tensor of shape [E + 1]")
+        offsets_host.copy_(offsets, non_blocking=True)
+        if offsets_ready is not None:
+            offsets_ready.record(torch.cuda.current_stream(dev))
     _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
     shape = _lib.make_shape(N, d, F, E, top_k, _dtype_code(x2d.dtype))
     ws = workspace(shape, dev)
@@ -383,17 +398,26 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
                  topk_idx: torch.Tensor, topk_w: torch.Tensor, offsets: torch.Tensor,
                  perm: torch.Tensor, inv_pos: torch.Tensor, y_perm: torch.Tensor,
                  grad_logits: Optional[torch.Tensor] = None, w_down_t: Optional[torch.Tensor] = None,
-                 w_gate_up_t: Optional[torch.Tensor] = None, gu: Optional[torch.Tensor] = None):
+                 w_gate_up_t: Optional[torch.Tensor] = None, gu: Optional[torch.Tensor] = None,
+                 offsets_host: Optional[torch.Tensor] = None):
     """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer.
 
-    HIP stages: gate gradient and dY (g5moe_gate_grad), router-logit gradient
-    (g5moe_router_grad, plus grad_logits), the gate|up recompute
-    (g5moe_expert_gate_up_raw), dh = dY Wd_e (g5moe_grouped_gemm on Wd^T),
-    SwiGLU backward (g5moe_swiglu_backward, dGU written once, per expert padded),
-    dX_perm = dGU Wgu_e (g5moe_grouped_gemm_padded on the packed gate|up's
-    transpose) and dx (g5moe_input_grad).  The weight
-    gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e and dWr = dlogits^T x are
-    plain GEMMs (torch / hipBLASLt), which read the expert row ranges on the host."""
+    offsets_host: a completed host copy of offsets (moe_forward_train's, after its
+    offsets_ready event); without it the offsets are read from the device here,
+    which waits for every kernel queued before the call.
+
+    HIP stages: gate gradient and dY (g5moe_gate_grad_padded: dY per expert
+    padded to kmax rows), router-logit gradient (g5moe_router_grad, plus
+    grad_logits), the gate|up recompute (g5moe_expert_gate_up_raw, unless gu
+    is given), dh = dY Wd_e (g5moe_grouped_gemm_padded on Wd^T), SwiGLU
+    backward (g5moe_swiglu_backward: h and dGU per expert padded), dX_perm =
+    dGU Wgu_e (g5moe_grouped_gemm_padded on the packed gate|up's transpose),
+    dx (g5moe_input_grad), the gathered X rows padded (g5moe_pad_rows) and the
+    weight gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e in one launch
+    (g5moe_weight_grad).  kmax is read from the offsets once on the host.
+    dWr = dlogits^T x is a plain GEMM.  For d or F not a multiple of 256 the
+    weight gradients are batched torch products over transposed padded
+    operands instead."""
     dev = _check_device(x2d)
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
@@ -405,10 +429,26 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     _require(y_perm, "y_perm", (N * k, d), torch.bfloat16, dev)
     shape = _lib.make_shape(N, d, F, E, k, _lib.DTYPE_BF16)
     S = _stream(dev)
+    # every expert's rows padded to kmax (>= max M_e) for the weight-gradient
+    # products; the host reads the offsets once here
+    offs = (offsets_host if offsets_host is not None else offsets).tolist()
+    if len(offs) != E + 1:
+        raise ValueError(f"offsets_host has {len(offs)} entries, expected {E + 1}")
+    m_max = max(b - a for a, b in zip(offs[:-1], offs[1:]))
+    hip_wgrad = d % 256 == 0 and F % 256 == 0
+    kmax = wgrad_kmax(m_max) if hip_wgrad else max(64, -(-m_max // 64) * 64)
     dw = torch.empty((N, k), dtype=torch.float32, device=dev)
-    dyp = torch.empty((N * k + ROW_PAD, d), dtype=torch.bfloat16, device=dev)
-    _lib.call("g5moe_gate_grad", _ptr(dy), _ptr(y_perm), _ptr(inv_pos), _ptr(topk_w), _ptr(dw),
-              _ptr(dyp), ctypes.byref(shape), S)
+    if hip_wgrad:
+        # dY scaled by the gates, straight into the padded layout the dh product
+        # and the weight-gradient kernel both read
+        dy_buf = torch.empty((E * kmax + ROW_PAD, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_gate_grad_padded", _ptr(dy), _ptr(y_perm), _ptr(inv_pos),
+                  _ptr(topk_w), _ptr(offsets), _ptr(dw), _ptr(dy_buf), kmax,
+                  ctypes.byref(shape), S)
+    else:
+        dyp = torch.empty((N * k + ROW_PAD, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_gate_grad", _ptr(dy), _ptr(y_perm), _ptr(inv_pos), _ptr(topk_w),
+                  _ptr(dw), _ptr(dyp), ctypes.byref(shape), S)
     if grad_logits is not None:
         _require(grad_logits, "grad_logits", (N, E), torch.float32, dev)
     dlogits = torch.empty((N, E), dtype=torch.float32, device=dev)
@@ -425,13 +465,10 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
         _require(gu, "gu", (N * k, 2 * F), torch.bfloat16, dev)
     if w_down_t is None:
         w_down_t = transpose_experts(w_down)            # [E, F, d]
-    dh = grouped_gemm(dyp, N * k, offsets, w_down_t)    # [N*k, F]
-    # every expert's rows padded to kmax (>= max M_e) for the weight-gradient
-    # products; the host reads the offsets once here
-    offs = offsets.tolist()
-    m_max = max(b - a for a, b in zip(offs[:-1], offs[1:]))
-    hip_wgrad = d % 256 == 0 and F % 256 == 0
-    kmax = wgrad_kmax(m_max) if hip_wgrad else max(64, -(-m_max // 64) * 64)
+    if hip_wgrad:
+        dh = grouped_gemm_padded(dy_buf, kmax, N * k, offsets, w_down_t)   # [N*k, F]
+    else:
+        dh = grouped_gemm(dyp, N * k, offsets, w_down_t)
     h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
     # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
     dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
@@ -449,11 +486,10 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     del dxp
     if hip_wgrad:
         # weight gradients on the HIP kernel over token-major padded operands
-        dy_pad = pad_rows(dyp, None, offsets, E, kmax, k)
-        del dyp
+        dy_pad = dy_buf[:E * kmax].view(E, kmax, d)
         x_pad = pad_rows(x2d, perm, offsets, E, kmax, k)
         d_wd, d_wgu = weight_grad(dy_pad, h_pad, dgu_pad, x_pad, offsets, kmax, top_k=k)
-        del dy_pad, x_pad, h_pad, dgu_buf
+        del dy_pad, dy_buf, x_pad, h_pad, dgu_buf
         d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
         return dx, d_wr, d_wgu, d_wd
     # other shapes: batched products over the per-expert padded operands (zero

@@ -247,6 +247,19 @@ g5moe_status g5moe_gate_grad(const void* dy, const void* y_perm, const int32_t* 
                              const float* topk_w, float* dw, void* dy_perm,
                              const g5moe_shape* shape, void* stream);
 
+/* g5moe_gate_grad with dy_perm written in the per-expert padded row layout:
+ * sorted position offsets[e] + j goes to row e*kmax + j, and rows
+ * e*kmax + j for j in [M_e, kmax) are zeroed.  dy_pad : bf16 [E*kmax + 256, d]
+ * out (the last 256 rows are not written).  kmax >= every M_e (rows of an
+ * expert past kmax are not written).  dh = dY Wd^T then runs as
+ * g5moe_grouped_gemm_padded over dy_pad, and dy_pad's first E*kmax rows are
+ * g5moe_weight_grad's dy_pad operand, so no g5moe_pad_rows pass over dY is
+ * needed.  One launch of max(N*k, E*kmax) wavefronts. */
+g5moe_status g5moe_gate_grad_padded(const void* dy, const void* y_perm, const int32_t* inv_pos,
+                                    const float* topk_w, const int32_t* offsets, float* dw,
+                                    void* dy_pad, int32_t kmax, const g5moe_shape* shape,
+                                    void* stream);
+
 /* Router-logit gradient through the renormalised top-k softmax:
  *   dlogits[t, i_r] = w_r * (dw_r - sum_s w_s dw_s) for the chosen experts,
  *   0 for the others, plus grad_logits[t, e] (an extra gradient on the logits,

@@ -210,6 +210,24 @@ def test_pad_rows_argument_checks(g5lib, cols, kmax, code, msg):
     assert st == code and msg in g5lib.g5moe_last_error().decode()
 
 
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(kmax=-1), 1, "kmax"),
+    (dict(offsets=None), 1, "NULL"),
+    (dict(dtype=_lib.DTYPE_F32), 2, "bf16"),
+])
+def test_gate_grad_padded_argument_checks(g5lib, kw, code, msg):
+    a = dict(kmax=384, offsets=ctypes.c_void_p(0x1000), dtype=_lib.DTYPE_BF16)
+    a.update(kw)
+    s = _lib.make_shape(100, 768, 3072, 16, 2, a["dtype"])
+    p = ctypes.c_void_p(0x1000)
+    st = g5lib.g5moe_gate_grad_padded(p, p, p, p, a["offsets"], p, p, a["kmax"],
+                                      ctypes.byref(s), None)
+    assert st == code and msg in g5lib.g5moe_last_error().decode(), (st, g5lib.g5moe_last_error())
+    s0 = _lib.make_shape(0, 768, 3072, 16, 2, _lib.DTYPE_BF16)
+    assert g5lib.g5moe_gate_grad_padded(None, None, None, None, None, None, None, 0,
+                                        ctypes.byref(s0), None) == 0
+
+
 def test_wgrad_kmax_rule():
     assert ops.wgrad_kmax(1) == 384 and ops.wgrad_kmax(384) == 384
     assert ops.wgrad_kmax(385) == 576 and ops.wgrad_kmax(5071) == 5184

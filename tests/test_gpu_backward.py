@@ -96,9 +96,17 @@ def test_backward_stages_vs_oracle(cuda_device, n, d, F, E, k):
     dx, d_wr, d_wgu, d_wd = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm,
                                              inv_pos, y_perm, gu=gu)
     recomputed = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm)
+    # the forward's non-blocking host copy of the offsets, handed to the backward
+    offs_host = torch.full((E + 1,), -1, dtype=torch.int32, pin_memory=True)
+    ready = torch.cuda.Event()
+    fw2 = ops.moe_forward_train(x, wr, wgu, wd, k, offsets_host=offs_host, offsets_ready=ready)
+    ready.synchronize()
+    assert offs_host.tolist() == offsets.tolist()
+    via_host = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm,
+                                gu=fw2[8], offsets_host=offs_host)
     torch.cuda.synchronize()
-    for a, b in zip((dx, d_wr, d_wgu, d_wd), recomputed):
-        assert torch.equal(a, b)
+    for a, b, c in zip((dx, d_wr, d_wgu, d_wd), recomputed, via_host):
+        assert torch.equal(a, b) and torch.equal(a, c)
     ref = oracle.moe_backward(inp.x, inp.w_router, inp.w_gate, inp.w_up, inp.w_down, ref_i, dy_np)
     d_wg, d_wu = ops.unpack_gate_up(d_wgu)
     check("dx", host(dx), ref["dx"])
@@ -217,6 +225,69 @@ def test_padded_weight_gradient_operands(cuda_device):
         assert not hp[e, o1 - o0:].any()
         got = mo.bf16_to_f32(hp[e, : o1 - o0]).astype(np.float64)
         np.testing.assert_allclose(got, h_ref[o0:o1], rtol=8e-3, atol=1e-6)
+
+
+@pytest.mark.parametrize("d,garbage", [(768, 7.0), (256, float("nan"))])
+def test_gate_grad_padded_equals_sorted(cuda_device, d, garbage):
+    """g5moe_gate_grad_padded writes the same dw as g5moe_gate_grad bit for bit,
+    and dY scaled by the gates at row e*kmax + j for sorted position
+    offsets[e] + j (equal to g5moe_pad_rows over the sorted copy), zero rows past
+    each expert's count (the buffer starts as garbage), with empty experts, an
+    assignment outside [0, E) (inv_pos -1, dw 0) and ragged counts; the dh
+    product over it equals the sorted product bit for bit."""
+    import ctypes
+    from genet5_amd import _lib
+    print(f"gate_grad_padded d={d}", flush=True)
+    rng = np.random.default_rng(31)
+    E, k, F = 6, 2, 256
+    counts = np.array([300, 0, 41, 0, 513, 3], np.int32)
+    nk_valid = int(counts.sum())
+    nk = nk_valid + 1                    # one assignment is not placed
+    assert nk % k == 0
+    n = nk // k
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    dropped = 7
+    inv = np.full(nk, -1, np.int32)
+    inv[np.arange(nk) != dropped] = rng.permutation(nk_valid).astype(np.int32)
+    kmax = ops.wgrad_kmax(int(counts.max()))
+    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
+    S = ops._stream(cuda_device)
+    t_off = dev_t(offsets, cuda_device)
+    t_inv = dev_t(inv, cuda_device)
+    w = torch.tensor(rng.random((n, k)).astype(np.float32), device=cuda_device)
+    dy = dev_t(synth.f32_to_bf16_bits(rng.standard_normal((n, d)).astype(np.float32)),
+               cuda_device, True)
+    y_perm = dev_t(synth.f32_to_bf16_bits(rng.standard_normal((nk_valid, d))
+                                          .astype(np.float32)), cuda_device, True)
+    dw1 = torch.full((n, k), 5.0, dtype=torch.float32, device=cuda_device)
+    dw2 = torch.full_like(dw1, 5.0)
+    dyp = torch.zeros((nk_valid + ops.ROW_PAD, d), dtype=torch.bfloat16, device=cuda_device)
+    buf = torch.full((E * kmax + ops.ROW_PAD, d), garbage, dtype=torch.bfloat16,
+                     device=cuda_device)
+    _lib.call("g5moe_gate_grad", ops._ptr(dy), ops._ptr(y_perm), ops._ptr(t_inv), ops._ptr(w),
+              ops._ptr(dw1), ops._ptr(dyp), ctypes.byref(shape), S)
+    _lib.call("g5moe_gate_grad_padded", ops._ptr(dy), ops._ptr(y_perm), ops._ptr(t_inv),
+              ops._ptr(w), ops._ptr(t_off), ops._ptr(dw2), ops._ptr(buf), kmax,
+              ctypes.byref(shape), S)
+    ref_pad = ops.pad_rows(dyp, None, t_off, E, kmax, k)
+    torch.cuda.synchronize()
+    assert torch.equal(dw1.view(torch.int32), dw2.view(torch.int32))
+    assert float(dw2.view(-1)[dropped]) == 0.0
+    got = buf[:E * kmax].view(E, kmax, d)
+    assert torch.equal(got.view(torch.int16), ref_pad.view(torch.int16))
+    for e in range(E):
+        m = int(counts[e])
+        assert torch.equal(got[e, :m], dyp[offsets[e]:offsets[e + 1]])
+        assert not torch.any(got[e, m:].view(torch.int16))      # +0.0 bits
+    # the dh product over the padded dY equals the sorted one: the trailing
+    # buffer rows (never written, NaN here in one case) reach only discarded
+    # output rows
+    wt = (torch.randn(E, F, d, device=cuda_device) * 0.05).to(torch.bfloat16)
+    dh_ref = ops.grouped_gemm(dyp, nk_valid, t_off, wt)
+    dh = ops.grouped_gemm_padded(buf, kmax, nk_valid, t_off, wt)
+    torch.cuda.synchronize()
+    assert torch.equal(dh, dh_ref)
 
 
 def test_padded_dx_product_equals_sorted(cuda_device):
