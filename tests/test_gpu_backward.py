@@ -227,8 +227,9 @@ def test_padded_weight_gradient_operands(cuda_device):
         np.testing.assert_allclose(got, h_ref[o0:o1], rtol=8e-3, atol=1e-6)
 
 
-@pytest.mark.parametrize("d,garbage", [(768, 7.0), (256, float("nan"))])
-def test_gate_grad_padded_equals_sorted(cuda_device, d, garbage):
+@pytest.mark.parametrize("d,k,garbage", [(768, 2, 7.0), (256, 2, float("nan")),
+                                         (512, 1, float("nan")), (128, 4, 7.0)])
+def test_gate_grad_padded_equals_sorted(cuda_device, d, k, garbage):
     """g5moe_gate_grad_padded writes the same dw as g5moe_gate_grad bit for bit,
     and dY scaled by the gates at row e*kmax + j for sorted position
     offsets[e] + j (equal to g5moe_pad_rows over the sorted copy), zero rows past
@@ -237,10 +238,11 @@ def test_gate_grad_padded_equals_sorted(cuda_device, d, garbage):
     product over it equals the sorted product bit for bit."""
     import ctypes
     from genet5_amd import _lib
-    print(f"gate_grad_padded d={d}", flush=True)
+    print(f"gate_grad_padded d={d} k={k}", flush=True)
     rng = np.random.default_rng(31)
-    E, k, F = 6, 2, 256
+    E, F = 6, 256
     counts = np.array([300, 0, 41, 0, 513, 3], np.int32)
+    counts[-1] += (-(int(counts.sum()) + 1)) % k   # N k assignments in all
     nk_valid = int(counts.sum())
     nk = nk_valid + 1                    # one assignment is not placed
     assert nk % k == 0
