@@ -35,20 +35,28 @@ __device__ __forceinline__ Offsets load_offsets(const int32_t* offsets, int n_ex
 
 // global_load_lds_dwordx4 with an explicit scalar base and a 32-bit per-lane
 // byte offset (voff, sbase), M0 = LDS byte address of the 1 KB block: one
-// instruction moves 64 x 16 bytes, lane l's to byte 16 l.  The compiler never
-// holds M0 in the kernels that use these helpers: every LDS DMA there goes
-// through them and sets M0 itself.
+// instruction moves 64 x 16 bytes, lane l's to byte 16 l.  Every LDS DMA of the
+// kernels that use these helpers goes through them and sets M0 itself.  M0 is
+// declared clobbered so that the compiler treats each statement as a write of
+// M0 and never keeps a value of its own there across one (clang warns that M0
+// is a reserved register, which it will not save and restore: that is not
+// needed, no caller expects M0 to survive).
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const char*)p));
 }
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16_s(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
 }
 __device__ __forceinline__ void lds_dma4_s(const void* sbase, uint32_t voff, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1"
-               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds)) : "memory");
+               :: "v"(voff), "s"(sbase), "s"(__builtin_amdgcn_readfirstlane(lds))
+               : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

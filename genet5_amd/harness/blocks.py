@@ -27,7 +27,9 @@ class RMSNorm(nn.Module):
 
     hip = True: the HIP kernel g5moe_rmsnorm (the fused norm+router kernel's
     arithmetic: fixed reduction order, correctly rounded sqrt and division);
-    otherwise the torch composition."""
+    otherwise the torch composition.  The kernel builds no autograd graph, so
+    when a gradient is needed (grad enabled and x or the weight requiring grad)
+    the torch composition runs even with hip = True."""
 
     def __init__(self, dim: int, eps: float = 1e-6):
         super().__init__()
@@ -36,7 +38,8 @@ class RMSNorm(nn.Module):
         self.hip = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.hip:
+        needs_grad = torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad)
+        if self.hip and not needs_grad:
             from .. import ops
             d = x.shape[-1]
             w = self.weight.detach().to(torch.float32).contiguous()

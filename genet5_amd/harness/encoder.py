@@ -19,7 +19,8 @@ Reference shapes followed:
     row, unlike the reference SDPA fallback's global-offset mask).
   * diffusion_generate (lib/inference/diffusion_engine.py:18-95): linear unmask
     schedule, mask/pad logits suppressed, argmax (temperature 0) or sampling,
-    confidence = log-prob of the prediction, per-sample top-n unmasking of the
+    confidence = log-prob of the prediction (strategy "confidence") or the gap
+    between the two largest logits ("margin"), per-sample top-n unmasking of the
     most confident masked positions, final fill pass.  The per-sample Python
     loop with host syncs (diffusion_engine.py:69-82) is replaced by one
     sort-based selection on the device; among equal confidences the lower
@@ -209,12 +210,53 @@ def linear_unmask_schedule(num_steps: int, eps: float = 1e-3) -> List[float]:
     return [(t[i] - t[i + 1]).item() for i in range(num_steps)]
 
 
+def unmask_confidence(logits: torch.Tensor, preds: torch.Tensor, strategy: str) -> torch.Tensor:
+    """Per-position confidence [B, L] of logits [B, L, V] (mask and pad already -inf):
+    "confidence" = log-softmax of the prediction (lib/inference/diffusion_engine.py:58-60),
+    "margin" = largest minus second-largest logit (:54-56)."""
+    if strategy == "margin":
+        top2 = logits.topk(2, dim=-1).values
+        return top2[..., 0] - top2[..., 1]
+    if strategy == "confidence":
+        return F.log_softmax(logits, dim=-1).gather(-1, preds.unsqueeze(-1)).squeeze(-1)
+    raise ValueError(f"strategy {strategy!r} is neither 'confidence' nor 'margin'")
+
+
+def select_unmask(conf: torch.Tensor, is_masked: torch.Tensor,
+                  n_unmask: torch.Tensor) -> torch.Tensor:
+    """Boolean [B, L]: in each row i, the n_unmask[i] still-masked positions of largest
+    confidence (n_unmask[i] <= masked count of the row).
+
+    The reference takes a per-row topk over the masked positions
+    (diffusion_engine.py:70-82, a Python loop over rows); here every row at once:
+    unmasked positions carry -inf, a stable descending sort ranks the row, and
+    the first n_unmask[i] ranks are taken.  On distinct confidences both give the
+    same set (the topk's order among equal values is unspecified, the stable sort
+    takes the lower position)."""
+    B, L = conf.shape
+    conf = conf.masked_fill(~is_masked, float("-inf"))
+    order = torch.sort(conf, dim=1, descending=True, stable=True).indices
+    rank = torch.empty_like(order)
+    rank.scatter_(1, order, torch.arange(L, device=conf.device).expand(B, -1))
+    return (rank < n_unmask[:, None]) & is_masked
+
+
 @torch.no_grad()
 def diffusion_generate(model, prefix_ids: torch.Tensor, target_len: int, mask_token_id: int,
                        pad_token_id: int, num_steps: int = 16, temperature: float = 0.0,
                        generator: Optional[torch.Generator] = None,
-                       stats: Optional[dict] = None) -> torch.Tensor:
-    """Iterative unmasking of a fully masked target appended to prefix_ids [B, P]."""
+                       stats: Optional[dict] = None,
+                       strategy: str = "confidence") -> torch.Tensor:
+    """Iterative unmasking of a fully masked target appended to prefix_ids [B, P]
+    (lib/inference/diffusion_engine.py:18-95): per step the model runs once, the
+    mask and pad tokens are suppressed, each position's prediction (argmax, or a
+    sample at temperature > 0) gets a confidence (`strategy` "confidence" or
+    "margin"), and the scheduled count of most confident masked positions takes
+    its predictions; a last pass fills what is still masked.  The logits are taken
+    in fp32 (the reference uses the logits' own dtype), so confidences of a bf16
+    model do not collapse into ties."""
+    if strategy not in ("confidence", "margin"):
+        raise ValueError(f"strategy {strategy!r} is neither 'confidence' nor 'margin'")
     device = prefix_ids.device
     B, P = prefix_ids.shape
     target = torch.full((B, target_len), mask_token_id, dtype=torch.long, device=device)
@@ -232,15 +274,11 @@ def diffusion_generate(model, prefix_ids: torch.Tensor, target_len: int, mask_to
                                       generator=generator).view(B, target_len)
         else:
             preds = logits.argmax(dim=-1)
-        conf = F.log_softmax(logits, dim=-1).gather(-1, preds.unsqueeze(-1)).squeeze(-1)
-        conf = conf.masked_fill(~is_masked, float("-inf"))
+        conf = unmask_confidence(logits, preds, strategy)
         # same float32 product and truncation as diffusion_engine.py:63-64
         n_unmask = torch.minimum(
             (frac * target_len * torch.ones(B, device=device)).long(), is_masked.sum(dim=1))
-        order = torch.sort(conf, dim=1, descending=True, stable=True).indices
-        rank = torch.empty_like(order)
-        rank.scatter_(1, order, torch.arange(target_len, device=device).expand(B, -1))
-        unmask = (rank < n_unmask[:, None]) & is_masked
+        unmask = select_unmask(conf, is_masked, n_unmask)
         input_ids[:, P:] = torch.where(unmask, preds, input_ids[:, P:])
         is_masked &= ~unmask
     if bool(is_masked.any()):

@@ -119,7 +119,11 @@ _moe_forward_train_op.register_autograd(_train_backward, setup_context=_train_se
 
 
 class MoEFeedForward(nn.Module):
-    """Top-k routed mixture of SwiGLU experts (forward only)."""
+    """Top-k routed mixture of SwiGLU experts.
+
+    Inference (no gradient needed): the custom op g5moe::moe_forward.  Training
+    (grad enabled and x or a parameter requiring grad): g5moe::moe_forward_train,
+    whose registered backward runs the HIP backward kernels."""
 
     def __init__(self, embed_dim: int, ff_dim: int, dropout: float = 0.0,
                  activation: str = "silu", num_experts: int = 16, top_k: int = 2,
@@ -190,6 +194,14 @@ class MoEFeedForward(nn.Module):
             self._packed_key = key
         return self._packed
 
+    def _block_needs_grad(self, residual: torch.Tensor, norm_weight: torch.Tensor,
+                          x_add: Optional[torch.Tensor]) -> bool:
+        return torch.is_grad_enabled() and (
+            residual.requires_grad or norm_weight.requires_grad
+            or (x_add is not None and x_add.requires_grad)
+            or any(p.requires_grad for p in
+                   (self.router.weight, self.w_gate, self.w_up, self.w_down)))
+
     def _needs_grad(self, x: torch.Tensor) -> bool:
         return torch.is_grad_enabled() and (
             x.requires_grad or any(p.requires_grad for p in
@@ -251,14 +263,27 @@ class MoEFeedForward(nn.Module):
         g5moe_dispatch -> g5moe_expert_swiglu -> g5moe_combine_residual: the
         normalised rows feed the router in the same pass, and the layer output is
         added into the residual inside the combine.  The RMSNorm follows the C
-        ABI's reduction order (fp32, correctly rounded sqrt and division)."""
-        if self.training and self.dropout > 0.0:
-            raise NotImplementedError(
-                "MoEFeedForward is forward-only: dropout on the expert hidden state in "
-                "training mode is not implemented")
+        ABI's reduction order (fp32, correctly rounded sqrt and division).
+
+        The fused kernels build no autograd graph.  When a gradient is needed (grad
+        enabled and residual, x_add, norm_weight or a parameter of this module
+        requiring grad) the block runs as the differentiable composition instead:
+        torch's add and fp32 RMSNorm, this module's training forward (its own
+        backward kernels) and torch's residual add, all on the GPU."""
         d = self.embed_dim
         if residual.shape[-1] != d:
             raise ValueError(f"last dim {residual.shape[-1]} != embed_dim {d}")
+        if self._block_needs_grad(residual, norm_weight, x_add):
+            h = residual if x_add is None else residual + x_add.to(residual.dtype)
+            hf = h.float()
+            normed = hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps)
+            normed = (normed * norm_weight.float()).to(h.dtype)
+            return h + self(normed) * alpha
+        if self.training and self.dropout > 0.0:
+            raise NotImplementedError(
+                "residual_block's fused kernels apply no dropout; in training mode with "
+                "dropout > 0 call it with gradients enabled (the differentiable path "
+                "applies the module's dropout)")
         lead = residual.shape[:-1]
         r2 = residual.reshape(-1, d).contiguous()
         xa2 = None if x_add is None else x_add.reshape(-1, d).to(r2.dtype).contiguous()

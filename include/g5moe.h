@@ -205,9 +205,12 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
  * The MoE layer's backward, stage by stage.  The reference trains its dense
  * FeedForward through autograd (lib/blocks/_component.py:48-52; loss.backward()
  * at train/diffusion_finet:761); the MoE and its backward are new.  The
- * weight-gradient products (dWd_e = dY_e^T h_e, dWgu_e^T = X_e^T dGU_e) are plain
- * batched GEMMs over per-expert padded operands, left to the caller (hipBLASLt);
- * everything else, including those operands, is here.
+ * weight-gradient products (dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e) run in one
+ * launch of g5moe_weight_grad over per-expert padded token-major operands when d
+ * and F are multiples of 256 (every GeneT5 shape); for other shapes they are
+ * batched GEMMs the caller issues (the Python host uses hipBLASLt through
+ * torch.bmm) over the transposed operands g5moe_pad_transpose writes.
+ * Everything else is here.
  * Activations are bf16 (x_dtype must be BF16), gradients of the routing fp32.
  * A row count "+ 256" means the buffer carries 256 rows of padding after its
  * last row: g5moe_grouped_gemm reads whole 256-row tiles of its A operand. */

@@ -132,6 +132,46 @@ def test_grad_mode_selects_the_differentiable_op(cuda_device):
         out.float().sum().backward()
 
 
+def test_fused_block_under_grad_is_the_differentiable_composition(cuda_device):
+    """With gradients needed, the fused block (residual_block) and the HIP RMSNorm
+    switch to the differentiable composition: the output carries a graph, and the
+    output and every gradient (input, norm weight, router, experts) equal those of
+    the unfused torch composition bit for bit.  Without gradients the fused kernels
+    run and no graph is built."""
+    torch.manual_seed(0)
+    blk = blocks.MoEBlock(256, 512, num_experts=4, top_k=2, residual_scale=0.5)
+    blk = blk.to(cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        blk.norm.weight.copy_(torch.linspace(0.5, 1.5, 256))
+    h0 = torch.randn(300, 256, device=cuda_device).to(torch.bfloat16)
+
+    def run(fused):
+        blk.fused = fused
+        blk.zero_grad(set_to_none=True)
+        h = h0.clone().requires_grad_(True)
+        out = blk(h)
+        assert out.grad_fn is not None
+        out.float().square().sum().backward()
+        return out.detach(), h.grad, [p.grad for p in blk.parameters()]
+
+    o_f, g_f, p_f = run(True)
+    o_u, g_u, p_u = run(False)
+    assert torch.equal(o_f, o_u) and torch.equal(g_f, g_u)
+    for a, b in zip(p_f, p_u):
+        assert a is not None and torch.equal(a, b)
+    assert blk.norm.weight.grad.abs().sum() > 0 and blk.ff.router.weight.grad.abs().sum() > 0
+    blk.fused = True
+    with torch.no_grad():
+        assert blk(h0).grad_fn is None
+    n = blocks.RMSNorm(256).to(cuda_device)
+    n.hip = True
+    x = h0.clone().requires_grad_(True)
+    y = n(x)
+    assert y.grad_fn is not None
+    y.float().sum().backward()
+    assert n.weight.grad is not None and x.grad is not None
+
+
 def check_fused_layer(ff, h2, nw, x_add2=None, alpha=1.0, out2=None, label="",
                       tol_check=False):
     """One fused MoE block on its actual inputs: normed/sum rows bit-exact, routing
