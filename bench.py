@@ -307,8 +307,8 @@ def bench_train(args) -> dict:
         h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
         dgu_buf = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
         dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
-        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(offsets), None, P(h_pad),
-                  P(dgu_buf), kmax, ctypes.byref(shape), S)
+        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(perm), P(offsets), None, P(h_pad),
+                  P(dgu_buf), kmax, None, ctypes.byref(shape), S)
         rec(4)
         dxp = ops.grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, wgu_t)
         rec(5)

@@ -66,6 +66,23 @@ class Shape(ctypes.Structure):
     ]
 
 
+class Dropout(ctypes.Structure):
+    """Mirror of `g5moe_dropout`."""
+
+    _fields_ = [
+        ("p", ctypes.c_float),
+        ("seed_lo", ctypes.c_uint32),
+        ("seed_hi", ctypes.c_uint32),
+        ("reserved", ctypes.c_int32),
+    ]
+
+
+def make_dropout(p: float, seed: int) -> Dropout:
+    """g5moe_dropout for drop probability p and a 64-bit seed."""
+    seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    return Dropout(float(p), seed & 0xFFFFFFFF, seed >> 32, 0)
+
+
 class AttnShape(ctypes.Structure):
     """Mirror of `g5moe_attn_shape`."""
 
@@ -98,6 +115,7 @@ class G5MoEError(RuntimeError):
 
 _P = ctypes.c_void_p
 _SHAPE_P = ctypes.POINTER(Shape)
+_DROP_P = ctypes.POINTER(Dropout)
 _SIGS = {
     "g5moe_last_error": ([], ctypes.c_char_p),
     "g5moe_version": ([], ctypes.c_int32),
@@ -106,7 +124,8 @@ _SIGS = {
     "g5moe_router_topk": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_dispatch": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
-    "g5moe_expert_gate_up_train": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_expert_gate_up_train": ([_P, _P, _P, _P, _P, _P, _DROP_P, _SHAPE_P, _P],
+                                   ctypes.c_int),
     "g5moe_expert_down": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_swiglu": ([_P, _P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_combine": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
@@ -128,8 +147,8 @@ _SIGS = {
                                ctypes.c_int),
     "g5moe_router_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up_raw": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
-    "g5moe_swiglu_backward": ([_P, _P, _P, _P, _P, _P, ctypes.c_int32, _SHAPE_P, _P],
-                              ctypes.c_int),
+    "g5moe_swiglu_backward": ([_P, _P, _P, _P, _P, _P, _P, ctypes.c_int32, _DROP_P,
+                               _SHAPE_P, _P], ctypes.c_int),
     "g5moe_pad_transpose": ([_P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _SHAPE_P, _P],
                             ctypes.c_int),
     "g5moe_pad_rows": ([_P, _P, _P, _P, ctypes.c_int32, ctypes.c_int32, _SHAPE_P, _P],

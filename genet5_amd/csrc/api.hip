@@ -78,13 +78,33 @@ const uint16_t* gemm_input(const void* x, char* ws, const g5moe_shape& s, hipStr
   return xb;
 }
 
+// g5moe_dropout -> the kernels' parameters (NULL or p == 0: off).
+g5moe_status dropout_params(const g5moe_dropout* d, DropoutParams* out) {
+  *out = DropoutParams{};
+  if (d == nullptr) return G5MOE_OK;
+  if (d->reserved != 0) return fail(G5MOE_ERR_INVALID_ARG, "dropout.reserved must be 0");
+  if (!(d->p >= 0.0f && d->p <= 1.0f))
+    return fail(G5MOE_ERR_INVALID_ARG, "dropout.p = %g is not in [0, 1]", double(d->p));
+  if (d->p == 0.0f) return G5MOE_OK;
+  out->on = true;
+  out->seed_lo = d->seed_lo;
+  out->seed_hi = d->seed_hi;
+  // round(p * 65536), halves away from zero; p * 65536 is exact in double
+  const double t = double(d->p) * 65536.0;
+  uint32_t thr = uint32_t(t + 0.5);
+  if (thr > 65536u) thr = 65536u;
+  out->thr = thr;
+  out->scale = thr >= 65536u ? 0.0f : float(65536.0 / double(65536u - thr));
+  return G5MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
 
 const char* g5moe_last_error(void) { return g_err; }
 
-int32_t g5moe_version(void) { return (1 << 16) | 1; }
+int32_t g5moe_version(void) { return (1 << 16) | 2; }
 
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes) {
   G5_CHECK(check_shape(shape));
@@ -160,9 +180,11 @@ g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int3
 
 g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
                                         const int32_t* offsets, const void* w_gate_up,
-                                        void* gu, void* ws, const g5moe_shape* shape,
-                                        void* stream) {
+                                        void* gu, void* ws, const g5moe_dropout* dropout,
+                                        const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));
+  DropoutParams drop;
+  G5_CHECK(dropout_params(dropout, &drop));
   if (shape->n_tokens == 0) return G5MOE_OK;
   G5_NONNULL(x);
   G5_NONNULL(perm);
@@ -178,7 +200,7 @@ g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
   const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
                                    reinterpret_cast<uint16_t*>(w + L.h),
-                                   static_cast<uint16_t*>(gu), *shape, st),
+                                   static_cast<uint16_t*>(gu), *shape, st, &drop),
                     "g5moe_expert_gate_up_train");
 }
 
@@ -416,21 +438,25 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
                     "g5moe_expert_gate_up_raw");
 }
 
-g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* offsets,
-                                   void* dgu, void* h_pad, void* dgu_pad, int32_t kmax,
+g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* perm,
+                                   const int32_t* offsets, void* dgu, void* h_pad,
+                                   void* dgu_pad, int32_t kmax, const g5moe_dropout* dropout,
                                    const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));
   if (kmax < 0) return fail(G5MOE_ERR_INVALID_ARG, "kmax %d < 0", int(kmax));
+  DropoutParams drop;
+  G5_CHECK(dropout_params(dropout, &drop));
   if (shape->n_tokens == 0 || kmax == 0) return G5MOE_OK;
   G5_NONNULL(dh);
   G5_NONNULL(gu);
   G5_NONNULL(offsets);
   G5_NONNULL(h_pad);
   G5_NONNULL(dgu_pad);
+  if (drop.on) G5_NONNULL(perm);
   return hip_status(launch_swiglu_bwd(static_cast<const uint16_t*>(dh),
-                                      static_cast<const uint16_t*>(gu), offsets,
+                                      static_cast<const uint16_t*>(gu), perm, offsets,
                                       static_cast<uint16_t*>(dgu), static_cast<uint16_t*>(h_pad),
-                                      static_cast<uint16_t*>(dgu_pad), kmax, *shape,
+                                      static_cast<uint16_t*>(dgu_pad), kmax, drop, *shape,
                                       as_stream(stream)),
                     "g5moe_swiglu_backward");
 }

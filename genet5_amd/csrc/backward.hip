@@ -142,11 +142,15 @@ __global__ __launch_bounds__(256) void router_grad_kernel(
 // [32q, 32q + 32), the next 32 the matching u.  Outputs: h and dgu in the
 // padded row layout [E, kmax, .] the weight-gradient batched products and the
 // padded dX product read, and optionally (dgu != nullptr) dgu in sorted order.
+// DROP: the forward applied dropout to h (g5moe_dropout): dh is the gradient of
+// h' = h * keep * scale, so the SwiGLU derivative takes dh * keep * scale and
+// h_pad holds h'; the mask is regenerated from the row's assignment perm[p].
+template <bool DROP>
 __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     const uint16_t* __restrict__ dh, const uint16_t* __restrict__ gu,
-    const int32_t* __restrict__ offsets, uint16_t* __restrict__ dgu,
-    uint16_t* __restrict__ h_pad, uint16_t* __restrict__ dgu_pad, int n_experts, int kmax,
-    int F) {
+    const int32_t* __restrict__ perm, const int32_t* __restrict__ offsets,
+    uint16_t* __restrict__ dgu, uint16_t* __restrict__ h_pad, uint16_t* __restrict__ dgu_pad,
+    int n_experts, int kmax, int F, DropoutParams drop) {
   const int cpr = F / 8;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t prow = i / cpr;
@@ -164,6 +168,13 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   }
   const int64_t p = offsets[e] + jr;
   const int64_t go = p * 2 * F + 64 * q + r;
+  // DROP: 16 mask bits per column, columns f0 .. f0 + 7 = pairs f0 / 2 .. + 3
+  [[maybe_unused]] uint32_t mbits[DROP ? 4 : 1];
+  if constexpr (DROP) {
+    const uint32_t key = dropout_row_key(uint32_t(perm[p]), drop.seed_lo, drop.seed_hi);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) mbits[c] = dropout_pair_bits(key, uint32_t(f0 >> 1) + c);
+  }
   const uint4 vd = *reinterpret_cast<const uint4*>(dh + p * F + f0);
   const uint4 vg = *reinterpret_cast<const uint4*>(gu + go);
   const uint4 vu = *reinterpret_cast<const uint4*>(gu + go + 32);
@@ -176,14 +187,22 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     float rg[2], ru[2], rh[2];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
-      const float d = hh ? bf_hi(ad[j]) : bf_lo(ad[j]);
+      float d = hh ? bf_hi(ad[j]) : bf_lo(ad[j]);
       const float g = hh ? bf_hi(ag[j]) : bf_lo(ag[j]);
       const float u = hh ? bf_hi(au[j]) : bf_lo(au[j]);
       const float sg = 1.0f / (1.0f + expf(-g));
       const float silu = g * sg;
+      float hv = silu * u;
+      if constexpr (DROP) {
+        // column f0 + 2 j + hh: pair j, low (hh = 0) or high 16 bits
+        const uint32_t rb = hh ? (mbits[j] >> 16) : (mbits[j] & 0xffffu);
+        const float m = rb >= drop.thr ? drop.scale : 0.0f;
+        d = d * m;
+        hv = hv * m;
+      }
       rg[hh] = d * u * (sg * (1.0f + g * (1.0f - sg)));
       ru[hh] = d * silu;
-      rh[hh] = silu * u;
+      rh[hh] = hv;
     }
     og[j] = pack_bf16x2(rg[0], rg[1]);
     ou[j] = pack_bf16x2(ru[0], ru[1]);
@@ -441,13 +460,20 @@ hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_
   return hipGetLastError();
 }
 
-hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32_t* offsets,
-                             uint16_t* dgu, uint16_t* h_pad, uint16_t* dgu_pad, int kmax,
+hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32_t* perm,
+                             const int32_t* offsets, uint16_t* dgu, uint16_t* h_pad,
+                             uint16_t* dgu_pad, int kmax, const DropoutParams& drop,
                              const g5moe_shape& s, hipStream_t st) {
   const int64_t work = int64_t(s.n_experts) * kmax * (s.d_ff / 8);
   if (work == 0) return hipSuccess;
-  hipLaunchKernelGGL(swiglu_bwd_kernel, dim3(unsigned((work + 255) / 256)), dim3(256), 0, st,
-                     dh, gu, offsets, dgu, h_pad, dgu_pad, s.n_experts, kmax, s.d_ff);
+  if (drop.on && perm == nullptr) return hipErrorInvalidValue;
+  const dim3 grid(unsigned((work + 255) / 256));
+  if (drop.on)
+    hipLaunchKernelGGL(swiglu_bwd_kernel<true>, grid, dim3(256), 0, st, dh, gu, perm, offsets,
+                       dgu, h_pad, dgu_pad, s.n_experts, kmax, s.d_ff, drop);
+  else
+    hipLaunchKernelGGL(swiglu_bwd_kernel<false>, grid, dim3(256), 0, st, dh, gu, perm, offsets,
+                       dgu, h_pad, dgu_pad, s.n_experts, kmax, s.d_ff, drop);
   return hipGetLastError();
 }
 

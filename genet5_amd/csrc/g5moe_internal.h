@@ -48,6 +48,35 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   return w;
 }
 
+// Dropout on the expert hidden state as the kernels apply it (the mask of
+// g5moe_dropout in g5moe.h).  on = false: no dropout, nothing is evaluated.
+struct DropoutParams {
+  bool on;
+  uint32_t seed_lo, seed_hi;
+  uint32_t thr;   // keep iff the column's 16 hash bits are >= thr (0 .. 65536)
+  float scale;    // 65536 / (65536 - thr), 0 when thr = 65536
+};
+
+// MurmurHash3's 32-bit finalizer (a bijection of uint32 with full avalanche).
+__host__ __device__ __forceinline__ uint32_t fmix32(uint32_t x) {
+  x ^= x >> 16;
+  x *= 0x85ebca6bu;
+  x ^= x >> 13;
+  x *= 0xc2b2ae35u;
+  x ^= x >> 16;
+  return x;
+}
+// Per-assignment key of the dropout mask.
+__host__ __device__ __forceinline__ uint32_t dropout_row_key(uint32_t a, uint32_t seed_lo,
+                                                             uint32_t seed_hi) {
+  return fmix32(fmix32(a ^ seed_lo) + seed_hi);
+}
+// 32 hash bits of the column pair (2c, 2c + 1): the low 16 decide column 2c,
+// the high 16 column 2c + 1.
+__host__ __device__ __forceinline__ uint32_t dropout_pair_bits(uint32_t key, uint32_t c) {
+  return fmix32(key + c * 0x9e3779b9u);
+}
+
 // ---- kernel launchers (each returns hipSuccess or the launch error) -------
 hipError_t launch_router(const void* x, const void* wr, const float* bias, int32_t* idx,
                          float* w, float* logits, const g5moe_shape& s, hipStream_t st);
@@ -66,7 +95,7 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
                            hipStream_t st);
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
                           const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
-                          hipStream_t st);
+                          hipStream_t st, const DropoutParams* drop = nullptr);
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
@@ -83,8 +112,9 @@ hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const in
 hipError_t launch_router_grad(const float* dw, const float* topk_w, const int32_t* topk_idx,
                               const float* grad_logits, float* dlogits, const g5moe_shape& s,
                               hipStream_t st);
-hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32_t* offsets,
-                             uint16_t* dgu, uint16_t* h_pad, uint16_t* dgu_pad, int kmax,
+hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32_t* perm,
+                             const int32_t* offsets, uint16_t* dgu, uint16_t* h_pad,
+                             uint16_t* dgu_pad, int kmax, const DropoutParams& drop,
                              const g5moe_shape& s, hipStream_t st);
 hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
                                 uint16_t* out, int n_experts, int C, int kmax, int topk,

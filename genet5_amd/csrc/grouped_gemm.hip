@@ -70,6 +70,9 @@ struct GemmArgs {
   int a_rows_per_expert;  // 0: A row of sorted position p is p; > 0: expert e's j-th
                           // row is A row e * a_rows_per_expert + j (per-expert padded
                           // layout; at most a_rows_per_expert rows of each expert are used)
+  // MODE 3 with dropout (the kernel's DROP flag): the mask of g5moe_dropout
+  uint32_t drop_seed_lo, drop_seed_hi, drop_thr;
+  float drop_scale;
 };
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
@@ -156,7 +159,10 @@ constexpr int persist_smem_bytes() {
 // rows with the SwiGLU epilogue (gate|up), 2 = gathered x rows, raw outputs
 // (the gate|up recompute of the backward), 3 = gathered x rows, raw outputs
 // into C2 and the SwiGLU outputs into C (the training forward's gate|up).
-template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF>
+// DROP (MODE 3 only): dropout on the SwiGLU outputs (the raw products stay
+// unmasked), keyed on each row's assignment perm[p].
+template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF,
+          bool DROP = false>
 __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& off, char* smem,
                                           const Units un) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
@@ -184,6 +190,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   static_assert((S - 2) * PER < 64, "vmcnt range");
   constexpr bool SWIGLU = MODE == 1 || MODE == 3;
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
+  static_assert(!DROP || MODE == 3, "dropout belongs to the training gate|up GEMM");
   // Fragment f of the next substeps is read after the f-th MFMA of a substep,
   // so a substep must hold at least as many MFMAs as fragments.
   static_assert(MB * NB >= MB + NB, "fragment prefetch needs MB * NB >= MB + NB");
@@ -590,119 +597,255 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
       kstep(F_{}, T_{}, P2{}, nk - 1);
     }
 
-    // Epilogue of `cur` through the wave's LDS region.  The wave's output is
-    // OB blocks of 32 columns (SwiGLU: h columns, half the feature columns) of
-    // bf16, RBY bytes per token row; a pass stages ROWS token rows, chunk c of
-    // row r at c ^ ((r / (256 / RBY)) % CR), then writes them back as 16-byte
-    // stores, CR lanes per row.  MODE 3 first writes the raw feature columns
-    // into C2 the same way, then the SwiGLU outputs into C.
-    if constexpr (MODE == 3)
-    {
-      constexpr int OB = NB;
-      constexpr int RBY = OB * 64;
-      constexpr int CR = RBY / 16;
-      constexpr int ROWS = kEpiBytesPerWave / RBY;
-      constexpr int JP = ROWS / 32;  // token blocks per pass
-      constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
-      static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
-      const int col0 = cur.n0 + wn * WTN;
+    // DROP (the training forward with dropout): the same epilogue with the
+    // SwiGLU outputs masked and scaled.  The kernels without dropout keep the
+    // epilogue's statements exactly as they are (else branch): any extra
+    // declaration in their epilogue, even a dead one, changed their register
+    // allocation (456 -> 512 VGPRs with spills).
+    if constexpr (DROP) {
+      // the dropout key of each of the lane's MB token rows (its assignment
+      // perm[p]; rows past the expert's end are never stored), loaded before
+      // the raw sweep, whose stores then cover the loads' latency
+      uint32_t dkey[MB];
+      {
+        uint32_t av[MB];
 #pragma unroll
-      for (int pass = 0; pass < MB / JP; ++pass) {
+        for (int j = 0; j < MB; ++j)
+          av[j] = uint32_t(
+              args.perm[min(cur.p_begin + wm * WTM + 32 * j + tok_l, cur.p_end - 1)]);
 #pragma unroll
-        for (int jl = 0; jl < JP; ++jl) {
-          const int j = pass * JP + jl;
-          const int row = jl * 32 + tok_l;
-          const int swz = (row / LPR) % CR;
-#pragma unroll
-          for (int ob = 0; ob < OB; ++ob) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float h[4];
-#pragma unroll
-              for (int uu = 0; uu < 4; ++uu) {
-                h[uu] = acc[ob][j][4 * q + uu];
-              }
-              uint2 o;
-              o.x = pack_bf16x2(h[0], h[1]);
-              o.y = pack_bf16x2(h[2], h[3]);
-              const int c = ob * 4 + q;
-              *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
-              // keep only one group's accumulators in VGPRs at a time
-              __builtin_amdgcn_sched_barrier(0);
-            }
-          }
-        }
-#pragma unroll
-        for (int it = 0; it < ROWS * RBY / 1024; ++it) {
-          const int row = it * (1024 / RBY) + lane / CR;
-          const int c = lane % CR;
-          const uint4 v = *reinterpret_cast<const uint4*>(
-              epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
-          const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
-          if (p < cur.p_end)
-            store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
-        }
+        for (int j = 0; j < MB; ++j)
+          dkey[j] = dropout_row_key(av[j], args.drop_seed_lo, args.drop_seed_hi);
       }
-    }
-    if constexpr (MODE == 3) {
-      // the SwiGLU sweep re-reads the accumulators from their AGPRs instead of
-      // keeping the raw sweep's copies live in VGPRs
+      if constexpr (MODE == 3)
+      {
+        constexpr int OB = NB;
+        constexpr int RBY = OB * 64;
+        constexpr int CR = RBY / 16;
+        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
+        static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+        const int col0 = cur.n0 + wn * WTN;
 #pragma unroll
-      for (int i = 0; i < NB; ++i)
+        for (int pass = 0; pass < MB / JP; ++pass) {
 #pragma unroll
-        for (int j = 0; j < MB; ++j) asm volatile("" : "+a"(acc[i][j]));
-    }
-    {
-      constexpr int OB = SWIGLU ? NB / 2 : NB;
-      constexpr int RBY = OB * 64;
-      constexpr int CR = RBY / 16;
-      constexpr int ROWS = kEpiBytesPerWave / RBY;
-      constexpr int JP = ROWS / 32;  // token blocks per pass
-      constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
-      static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
-      const int col0 = SWIGLU ? (cur.n0 + wn * WTN) / 2 : cur.n0 + wn * WTN;
+          for (int jl = 0; jl < JP; ++jl) {
+            const int j = pass * JP + jl;
+            const int row = jl * 32 + tok_l;
+            const int swz = (row / LPR) % CR;
 #pragma unroll
-      for (int pass = 0; pass < MB / JP; ++pass) {
+            for (int ob = 0; ob < OB; ++ob) {
 #pragma unroll
-        for (int jl = 0; jl < JP; ++jl) {
-          const int j = pass * JP + jl;
-          const int row = jl * 32 + tok_l;
-          const int swz = (row / LPR) % CR;
+              for (int q = 0; q < 4; ++q) {
+                float h[4];
 #pragma unroll
-          for (int ob = 0; ob < OB; ++ob) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) {
-              float h[4];
-#pragma unroll
-              for (int uu = 0; uu < 4; ++uu) {
-                if constexpr (SWIGLU)
-                  h[uu] = silu_mul(acc[2 * ob][j][4 * q + uu], acc[2 * ob + 1][j][4 * q + uu]);
-                else
+                for (int uu = 0; uu < 4; ++uu) {
                   h[uu] = acc[ob][j][4 * q + uu];
+                }
+                uint2 o;
+                o.x = pack_bf16x2(h[0], h[1]);
+                o.y = pack_bf16x2(h[2], h[3]);
+                const int c = ob * 4 + q;
+                *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+                // keep only one group's accumulators in VGPRs at a time
+                __builtin_amdgcn_sched_barrier(0);
               }
-              uint2 o;
-              o.x = pack_bf16x2(h[0], h[1]);
-              o.y = pack_bf16x2(h[2], h[3]);
-              const int c = ob * 4 + q;
-              *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
-              // keep only one group's accumulators in VGPRs at a time
-              __builtin_amdgcn_sched_barrier(0);
             }
           }
-        }
 #pragma unroll
-        for (int it = 0; it < ROWS * RBY / 1024; ++it) {
-          const int row = it * (1024 / RBY) + lane / CR;
-          const int c = lane % CR;
-          const uint4 v = *reinterpret_cast<const uint4*>(
-              epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
-          const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
-          if (p < cur.p_end)
-            // non-temporal: the outputs are the next kernel's, and the L2 is
-            // left to the operand tiles (training forward 3 % faster)
-            store16_nt(args.C + int64_t(p) * args.ldc + col0 + c * 8, v);
+          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
+            const int row = it * (1024 / RBY) + lane / CR;
+            const int c = lane % CR;
+            const uint4 v = *reinterpret_cast<const uint4*>(
+                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
+            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
+            if (p < cur.p_end)
+              store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
+          }
         }
       }
+      if constexpr (MODE == 3) {
+        // the SwiGLU sweep re-reads the accumulators from their AGPRs instead of
+        // keeping the raw sweep's copies live in VGPRs
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) asm volatile("" : "+a"(acc[i][j]));
+      }
+      {
+        constexpr int OB = SWIGLU ? NB / 2 : NB;
+        constexpr int RBY = OB * 64;
+        constexpr int CR = RBY / 16;
+        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
+        static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+        const int col0 = SWIGLU ? (cur.n0 + wn * WTN) / 2 : cur.n0 + wn * WTN;
+#pragma unroll
+        for (int pass = 0; pass < MB / JP; ++pass) {
+#pragma unroll
+          for (int jl = 0; jl < JP; ++jl) {
+            const int j = pass * JP + jl;
+            const int row = jl * 32 + tok_l;
+            const int swz = (row / LPR) % CR;
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                float h[4];
+#pragma unroll
+                for (int uu = 0; uu < 4; ++uu)
+                  h[uu] = silu_mul(acc[2 * ob][j][4 * q + uu], acc[2 * ob + 1][j][4 * q + uu]);
+                // h columns col0 + 8 (4 ob + q) + 4 half + uu: column pairs cp, cp + 1
+                const uint32_t cp = uint32_t(col0 + 8 * (ob * 4 + q) + 4 * half) >> 1;
+                const uint32_t b0 = dropout_pair_bits(dkey[j], cp);
+                const uint32_t b1 = dropout_pair_bits(dkey[j], cp + 1);
+                const uint32_t r[4] = {b0 & 0xffffu, b0 >> 16, b1 & 0xffffu, b1 >> 16};
+#pragma unroll
+                for (int uu = 0; uu < 4; ++uu)
+                  h[uu] = r[uu] >= args.drop_thr ? h[uu] * args.drop_scale : 0.0f;
+                uint2 o;
+                o.x = pack_bf16x2(h[0], h[1]);
+                o.y = pack_bf16x2(h[2], h[3]);
+                const int c = ob * 4 + q;
+                *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+                // keep only one group's accumulators in VGPRs at a time
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            }
+          }
+#pragma unroll
+          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
+            const int row = it * (1024 / RBY) + lane / CR;
+            const int c = lane % CR;
+            const uint4 v = *reinterpret_cast<const uint4*>(
+                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
+            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
+            if (p < cur.p_end)
+              // non-temporal: the outputs are the next kernel's, and the L2 is
+              // left to the operand tiles (training forward 3 % faster)
+              store16_nt(args.C + int64_t(p) * args.ldc + col0 + c * 8, v);
+          }
+        }
+      }
+
+    } else {
+      // Epilogue of `cur` through the wave's LDS region.  The wave's output is
+      // OB blocks of 32 columns (SwiGLU: h columns, half the feature columns) of
+      // bf16, RBY bytes per token row; a pass stages ROWS token rows, chunk c of
+      // row r at c ^ ((r / (256 / RBY)) % CR), then writes them back as 16-byte
+      // stores, CR lanes per row.  MODE 3 first writes the raw feature columns
+      // into C2 the same way, then the SwiGLU outputs into C.
+      if constexpr (MODE == 3)
+      {
+        constexpr int OB = NB;
+        constexpr int RBY = OB * 64;
+        constexpr int CR = RBY / 16;
+        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
+        static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+        const int col0 = cur.n0 + wn * WTN;
+#pragma unroll
+        for (int pass = 0; pass < MB / JP; ++pass) {
+#pragma unroll
+          for (int jl = 0; jl < JP; ++jl) {
+            const int j = pass * JP + jl;
+            const int row = jl * 32 + tok_l;
+            const int swz = (row / LPR) % CR;
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                float h[4];
+#pragma unroll
+                for (int uu = 0; uu < 4; ++uu) {
+                  h[uu] = acc[ob][j][4 * q + uu];
+                }
+                uint2 o;
+                o.x = pack_bf16x2(h[0], h[1]);
+                o.y = pack_bf16x2(h[2], h[3]);
+                const int c = ob * 4 + q;
+                *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+                // keep only one group's accumulators in VGPRs at a time
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            }
+          }
+#pragma unroll
+          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
+            const int row = it * (1024 / RBY) + lane / CR;
+            const int c = lane % CR;
+            const uint4 v = *reinterpret_cast<const uint4*>(
+                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
+            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
+            if (p < cur.p_end)
+              store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
+          }
+        }
+      }
+      if constexpr (MODE == 3) {
+        // the SwiGLU sweep re-reads the accumulators from their AGPRs instead of
+        // keeping the raw sweep's copies live in VGPRs
+#pragma unroll
+        for (int i = 0; i < NB; ++i)
+#pragma unroll
+          for (int j = 0; j < MB; ++j) asm volatile("" : "+a"(acc[i][j]));
+      }
+      {
+        constexpr int OB = SWIGLU ? NB / 2 : NB;
+        constexpr int RBY = OB * 64;
+        constexpr int CR = RBY / 16;
+        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
+        static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+        const int col0 = SWIGLU ? (cur.n0 + wn * WTN) / 2 : cur.n0 + wn * WTN;
+#pragma unroll
+        for (int pass = 0; pass < MB / JP; ++pass) {
+#pragma unroll
+          for (int jl = 0; jl < JP; ++jl) {
+            const int j = pass * JP + jl;
+            const int row = jl * 32 + tok_l;
+            const int swz = (row / LPR) % CR;
+#pragma unroll
+            for (int ob = 0; ob < OB; ++ob) {
+#pragma unroll
+              for (int q = 0; q < 4; ++q) {
+                float h[4];
+#pragma unroll
+                for (int uu = 0; uu < 4; ++uu) {
+                  if constexpr (SWIGLU)
+                    h[uu] = silu_mul(acc[2 * ob][j][4 * q + uu], acc[2 * ob + 1][j][4 * q + uu]);
+                  else
+                    h[uu] = acc[ob][j][4 * q + uu];
+                }
+                uint2 o;
+                o.x = pack_bf16x2(h[0], h[1]);
+                o.y = pack_bf16x2(h[2], h[3]);
+                const int c = ob * 4 + q;
+                *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+                // keep only one group's accumulators in VGPRs at a time
+                __builtin_amdgcn_sched_barrier(0);
+              }
+            }
+          }
+#pragma unroll
+          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
+            const int row = it * (1024 / RBY) + lane / CR;
+            const int c = lane % CR;
+            const uint4 v = *reinterpret_cast<const uint4*>(
+                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
+            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
+            if (p < cur.p_end)
+              // non-temporal: the outputs are the next kernel's, and the L2 is
+              // left to the operand tiles (training forward 3 % faster)
+              store16_nt(args.C + int64_t(p) * args.ldc + col0 + c * 8, v);
+          }
+        }
+      }
+
     }
 
     if (!has_nxt) {
@@ -755,7 +898,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
 // dominated by its A rows and its MFMAs scale with its width, so a half takes
 // about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
 // the gate|up GEMM (K = 768), which therefore keeps whole tiles.
-template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL>
+template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
+          bool DROP = false>
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
   const int ntn = args.Nout / BN;
@@ -789,8 +933,8 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
     // one pass: the remainder tile of slots s < r is lo + s + q * nslot
     const int cnt = q + (slot < r ? 1 : 0);
     if (cnt > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, off, smem,
-                                                           Units{lo + slot, nslot, cnt, 0});
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP>(
+          args, off, smem, Units{lo + slot, nslot, cnt, 0});
   }
 }
 
@@ -871,22 +1015,24 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #endif
 
 // Persistent launch: three fragment slots when the k-step count allows it.
-template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL>
+template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL, bool DROP = false>
 void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
   const int nk = a.K / BK;
   if (nk % 3 == 0 && nk >= 6)
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, MODE, HALF_TAIL>),
-                       dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(
+        (grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, MODE, HALF_TAIL, DROP>), dim3(grid),
+        dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, MODE, HALF_TAIL>),
-                       dim3(grid), dim3(256), 0, st, a);
+    hipLaunchKernelGGL(
+        (grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, MODE, HALF_TAIL, DROP>), dim3(grid),
+        dim3(256), 0, st, a);
 }
 
 }  // namespace
 
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
                           const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
-                          hipStream_t st) {
+                          hipStream_t st, const DropoutParams* drop) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
   GemmArgs a{};
@@ -905,7 +1051,17 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  if (gu != nullptr)  // h and the raw gate|up outputs (training forward)
+  const bool dropout = drop != nullptr && drop->on;
+  if (dropout) {
+    if (gu == nullptr) return hipErrorInvalidValue;  // dropout is a training-forward mode
+    a.drop_seed_lo = drop->seed_lo;
+    a.drop_seed_hi = drop->seed_hi;
+    a.drop_thr = drop->thr;
+    a.drop_scale = drop->scale;
+  }
+  if (gu != nullptr && dropout)  // h' (dropout) and the raw gate|up outputs
+    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false, true>(pgrid, a, st);
+  else if (gu != nullptr)  // h and the raw gate|up outputs (training forward)
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false>(pgrid, a, st);
   else
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);

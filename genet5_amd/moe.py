@@ -24,6 +24,7 @@ weight changes.
 from __future__ import annotations
 
 import math
+from collections import OrderedDict
 from typing import Optional, Tuple
 
 import torch
@@ -70,18 +71,54 @@ def _pack_backward(ctx, grad):
 _pack_gate_up_op.register_autograd(_pack_backward)
 
 
+@torch.library.custom_op("g5moe::transpose_experts", mutates_args=())
+def _transpose_experts_op(w: torch.Tensor) -> torch.Tensor:
+    return ops.transpose_experts(w)
+
+
+@_transpose_experts_op.register_fake
+def _(w):
+    E, R, C = w.shape
+    return w.new_empty((E, C, R))
+
+
+# Host copies of the expert offsets made by the training forward, waiting for
+# their autograd node: offsets' storage address -> (pinned int32 [E + 1], event
+# recorded after the non-blocking copy).  The backward needs the largest expert
+# count on the host (it sizes the padded operands); with the copy issued right
+# after the dispatch, reading it waits for that point of the forward only, not
+# for the device to drain.  Entries of forwards whose node never comes (no
+# gradient) are dropped oldest first.
+_HOST_OFFSETS: "OrderedDict[int, Tuple[torch.Tensor, torch.cuda.Event]]" = OrderedDict()
+_HOST_OFFSETS_MAX = 256
+
+
 @torch.library.custom_op("g5moe::moe_forward_train", mutates_args=())
 def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
-                          w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int
+                          w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+                          w_gate_up: torch.Tensor, w_gate_up_t: torch.Tensor,
+                          w_down_t: torch.Tensor, top_k: int, dropout_p: float, seed: int
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                      torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                      torch.Tensor]:
-    return tuple(t.contiguous() for t in
-                 ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias))
+    """Training forward.  w_gate / w_up / w_down are the differentiable parameters
+    (bf16); the kernels read w_gate_up (their packed copy) and w_down, and the
+    backward the transposed copies w_gate_up_t [E, d, 2F] and w_down_t [E, F, d]."""
+    E = w_router.shape[0]
+    host = torch.empty((E + 1,), dtype=torch.int32, pin_memory=True)
+    ready = torch.cuda.Event()
+    outs = ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias,
+                                 offsets_host=host, offsets_ready=ready,
+                                 dropout=(dropout_p, seed) if dropout_p > 0 else None)
+    _HOST_OFFSETS[outs[4].data_ptr()] = (host, ready)
+    while len(_HOST_OFFSETS) > _HOST_OFFSETS_MAX:
+        _HOST_OFFSETS.popitem(last=False)
+    return tuple(t.contiguous() for t in outs)
 
 
 @_moe_forward_train_op.register_fake
-def _(x, w_router, bias, w_gate_up, w_down, top_k):
+def _(x, w_router, bias, w_gate, w_up, w_down, w_gate_up, w_gate_up_t, w_down_t, top_k,
+      dropout_p, seed):
     N, d = x.shape
     E = w_router.shape[0]
     i32 = dict(dtype=torch.int32, device=x.device)
@@ -94,25 +131,39 @@ def _(x, w_router, bias, w_gate_up, w_down, top_k):
 
 
 def _train_setup(ctx, inputs, output):
-    x, w_router, bias, w_gate_up, w_down, top_k = inputs
+    (x, w_router, bias, w_gate, w_up, w_down, w_gate_up, w_gate_up_t, w_down_t, top_k,
+     dropout_p, seed) = inputs
     _, _, idx, w, offsets, perm, inv_pos, y_perm, gu = output
     ctx.top_k = top_k
+    ctx.dropout = (dropout_p, seed) if dropout_p > 0 else None
+    try:
+        ctx.host_offsets = _HOST_OFFSETS.pop(offsets.data_ptr(), None)
+    except Exception:  # traced (fake) tensors have no storage: read on the device later
+        ctx.host_offsets = None
     # gu: the forward's raw gate|up products, kept so the backward does not
     # recompute them (894 MB at 36,400 tokens: HBM for time)
-    ctx.save_for_backward(x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm,
-                          gu)
+    ctx.save_for_backward(x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w,
+                          offsets, perm, inv_pos, y_perm, gu)
     ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu)
 
 
 def _train_backward(ctx, dy, dlogits, *unused):
-    x, w_router, w_gate_up, w_down, idx, w, offsets, perm, inv_pos, y_perm, gu = ctx.saved_tensors
+    (x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w, offsets, perm, inv_pos,
+     y_perm, gu) = ctx.saved_tensors
     if dy is None:
         dy = torch.zeros_like(x)
+    offsets_host = None
+    if ctx.host_offsets is not None:
+        offsets_host, ready = ctx.host_offsets
+        ready.synchronize()  # the copy issued right after the forward's dispatch
     dx, d_wr, d_wgu, d_wd = ops.moe_backward(
         dy.to(torch.bfloat16).contiguous(), x, w_router, w_gate_up, w_down, ctx.top_k, idx, w,
         offsets, perm, inv_pos, y_perm,
-        grad_logits=None if dlogits is None else dlogits.float().contiguous(), gu=gu)
-    return dx, d_wr, None, d_wgu, d_wd, None
+        grad_logits=None if dlogits is None else dlogits.float().contiguous(),
+        w_down_t=w_down_t, w_gate_up_t=w_gate_up_t, gu=gu, offsets_host=offsets_host,
+        dropout=ctx.dropout)
+    d_wg, d_wu = ops.unpack_gate_up(d_wgu)
+    return dx, d_wr, None, d_wg, d_wu, d_wd, None, None, None, None, None, None
 
 
 _moe_forward_train_op.register_autograd(_train_backward, setup_context=_train_setup)
@@ -156,6 +207,7 @@ class MoEFeedForward(nn.Module):
         self.reset_parameters()
         self._packed_key = None
         self._packed = None
+        self._transposed = None
         # Switch-style load-balancing loss weight (0 = off); the loss of the last
         # differentiable forward is left in self.aux_loss.
         self.aux_loss_coef = 0.0
@@ -175,13 +227,19 @@ class MoEFeedForward(nn.Module):
         self.w_up.copy_(wi_1.unsqueeze(0).expand_as(self.w_up))
         self.w_down.copy_(wo.unsqueeze(0).expand_as(self.w_down))
 
-    def _expert_weights(self):
-        """bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F], cached by version.
-        Under torch.compile the cache (Python-side state) is bypassed and the packing
-        runs as its own custom op on every call."""
+    def _expert_weights(self, transposed: bool = False):
+        """bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F] (with transposed:
+        also their per-expert transposes [E, d, 2F] and [E, F, d], the backward's
+        operands), cached by the parameters' versions: rebuilt only when a weight
+        changes, so forwards and backwards between two optimizer steps (gradient
+        accumulation) share one copy.  Under torch.compile the cache (Python-side
+        state) is bypassed and the copies are made by custom ops on every call."""
         if torch.compiler.is_compiling():
-            return (_pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16)),
-                    self.w_down.to(torch.bfloat16))
+            wgu = _pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16))
+            wd = self.w_down.to(torch.bfloat16)
+            if not transposed:
+                return wgu, wd
+            return wgu, wd, _transpose_experts_op(wgu), _transpose_experts_op(wd)
         key = (self.w_gate.data_ptr(), self.w_gate._version, self.w_up.data_ptr(),
                self.w_up._version, self.w_down.data_ptr(), self.w_down._version,
                self.w_gate.device, self.w_gate.dtype)
@@ -192,7 +250,13 @@ class MoEFeedForward(nn.Module):
                 wd = self.w_down.detach().to(torch.bfloat16).contiguous()
                 self._packed = (ops.pack_gate_up(wg, wu), wd)
             self._packed_key = key
-        return self._packed
+            self._transposed = None
+        if not transposed:
+            return self._packed
+        if self._transposed is None:
+            with torch.no_grad():
+                self._transposed = tuple(ops.transpose_experts(w) for w in self._packed)
+        return self._packed + self._transposed
 
     def _block_needs_grad(self, residual: torch.Tensor, norm_weight: torch.Tensor,
                           x_add: Optional[torch.Tensor]) -> bool:
@@ -208,10 +272,6 @@ class MoEFeedForward(nn.Module):
                                    (self.router.weight, self.w_gate, self.w_up, self.w_down)))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.training and self.dropout > 0.0:
-            raise NotImplementedError(
-                "MoEFeedForward has no dropout on the expert hidden state; construct it "
-                "with dropout=0.0 for training")
         if x.shape[-1] != self.embed_dim:
             raise ValueError(f"last dim {x.shape[-1]} != embed_dim {self.embed_dim}")
         lead = x.shape[:-1]
@@ -221,26 +281,33 @@ class MoEFeedForward(nn.Module):
         w_router = self.router.weight
         if w_router.dtype != x2.dtype:
             w_router = w_router.to(x2.dtype)
-        if self._needs_grad(x2):
+        if self._needs_grad(x2) or (self.training and self.dropout > 0.0):
             return self._forward_train(x2, w_router.contiguous()).view(*lead, self.embed_dim)
         wgu, wd = self._expert_weights()
         y = _moe_forward_op(x2, w_router.contiguous(), self.router_bias, wgu, wd, self.top_k)
         return y.view(*lead, self.embed_dim)
 
     def _forward_train(self, x2: torch.Tensor, w_router: torch.Tensor) -> torch.Tensor:
-        """Differentiable forward (bf16 activations).  The expert weights are packed
-        through the differentiable packing op so their gradients reach w_gate and
-        w_up.  With aux_loss_coef > 0 the Switch-style load-balancing loss
+        """Training forward (bf16 activations), differentiable in x, the router and
+        the expert weights.  In training mode with dropout > 0 the expert hidden
+        state gets dropout (FeedForward.forward's `self.dropout(hidden)`,
+        lib/blocks/_component.py:51) with the counter-based mask of g5moe_dropout,
+        seeded by a 64-bit draw from torch's default CPU generator (so
+        torch.manual_seed makes it reproducible); the backward regenerates the
+        mask.  With aux_loss_coef > 0 the Switch-style load-balancing loss
         coef * E * sum_e f_e * P_e (f_e: share of assignments routed to e, P_e:
         mean softmax probability of e) is left in self.aux_loss for the caller
         to add to its loss (the module's output stays one tensor)."""
         if x2.dtype != torch.bfloat16:
             raise TypeError("MoEFeedForward trains on bf16 activations (the model's autocast "
                             "dtype); got " + str(x2.dtype))
-        wgu = _pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16))
-        wd = self.w_down.to(torch.bfloat16)
+        p = self.dropout if self.training else 0.0
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if p > 0.0 else 0
+        wgu, wd, wgu_t, wd_t = self._expert_weights(transposed=True)
         y, logits, idx, _, offsets, _, _, _, _ = _moe_forward_train_op(
-            x2, w_router, self.router_bias, wgu, wd.contiguous(), self.top_k)
+            x2, w_router, self.router_bias, self.w_gate.to(torch.bfloat16),
+            self.w_up.to(torch.bfloat16), self.w_down.to(torch.bfloat16), wgu, wgu_t, wd_t,
+            self.top_k, p, seed)
         self.aux_loss = None
         if self.aux_loss_coef > 0:
             counts = (offsets[1:] - offsets[:-1]).float()
@@ -265,25 +332,22 @@ class MoEFeedForward(nn.Module):
         added into the residual inside the combine.  The RMSNorm follows the C
         ABI's reduction order (fp32, correctly rounded sqrt and division).
 
-        The fused kernels build no autograd graph.  When a gradient is needed (grad
-        enabled and residual, x_add, norm_weight or a parameter of this module
-        requiring grad) the block runs as the differentiable composition instead:
+        The fused kernels build no autograd graph and apply no dropout.  When a
+        gradient is needed (grad enabled and residual, x_add, norm_weight or a
+        parameter of this module requiring grad), or in training mode with
+        dropout > 0, the block runs as the differentiable composition instead:
         torch's add and fp32 RMSNorm, this module's training forward (its own
-        backward kernels) and torch's residual add, all on the GPU."""
+        backward kernels and dropout) and torch's residual add, all on the GPU."""
         d = self.embed_dim
         if residual.shape[-1] != d:
             raise ValueError(f"last dim {residual.shape[-1]} != embed_dim {d}")
-        if self._block_needs_grad(residual, norm_weight, x_add):
+        if self._block_needs_grad(residual, norm_weight, x_add) or (
+                self.training and self.dropout > 0.0):
             h = residual if x_add is None else residual + x_add.to(residual.dtype)
             hf = h.float()
             normed = hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps)
             normed = (normed * norm_weight.float()).to(h.dtype)
             return h + self(normed) * alpha
-        if self.training and self.dropout > 0.0:
-            raise NotImplementedError(
-                "residual_block's fused kernels apply no dropout; in training mode with "
-                "dropout > 0 call it with gradients enabled (the differentiable path "
-                "applies the module's dropout)")
         lead = residual.shape[:-1]
         r2 = residual.reshape(-1, d).contiguous()
         xa2 = None if x_add is None else x_add.reshape(-1, d).to(r2.dtype).contiguous()

@@ -10,7 +10,7 @@ from __future__ import annotations
 
 import ctypes
 from dataclasses import dataclass
-from typing import Optional
+from typing import Optional, Tuple
 
 import torch
 
@@ -311,10 +311,21 @@ def moe_forward(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tens
 ROW_PAD = 256  # padding rows of buffers read as the A operand of the grouped GEMM
 
 
+def _dropout_arg(dropout: Optional[Tuple[float, int]]):
+    """(p, seed) -> a g5moe_dropout reference for the C ABI (None: no dropout)."""
+    if dropout is None or float(dropout[0]) == 0.0:
+        return None
+    p, seed = dropout
+    if not (0.0 <= float(p) <= 1.0):
+        raise ValueError(f"dropout p = {p} is not in [0, 1]")
+    return ctypes.byref(_lib.make_dropout(p, seed))
+
+
 def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tensor,
                       w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None,
                       offsets_host: Optional[torch.Tensor] = None,
-                      offsets_ready: Optional["torch.cuda.Event"] = None):
+                      offsets_ready: Optional["torch.cuda.Event"] = None,
+                      dropout: Optional[Tuple[float, int]] = None):
     """The layer forward as stage calls, returning what the backward needs:
     (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm, gu) with
     gu the raw gate|up products bf16 [N*k, 2F] (packed column order), which the
@@ -325,7 +336,11 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
     there without blocking as soon as the dispatch has written them, and
     offsets_ready (if given) is recorded after the copy.  Once the event has
     completed, moe_backward(..., offsets_host=...) reads them without waiting for
-    the rest of the forward."""
+    the rest of the forward.
+
+    dropout = (p, seed): dropout with drop probability p on the expert hidden
+    state, the mask of g5moe_dropout keyed on the 64-bit seed (pass the same pair
+    to moe_backward)."""
     dev = _check_device(x2d)
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
@@ -346,7 +361,7 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
     y_perm = torch.empty((N * top_k, d), dtype=torch.bfloat16, device=dev)
     S = _stream(dev)
     _lib.call("g5moe_expert_gate_up_train", _ptr(x2d), _ptr(perm), _ptr(offsets),
-              _ptr(w_gate_up), _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
+              _ptr(w_gate_up), _ptr(gu), _ptr(ws), _dropout_arg(dropout), ctypes.byref(shape), S)
     _lib.call("g5moe_expert_down", _ptr(offsets), _ptr(w_down), _ptr(y_perm), _ptr(ws),
               ctypes.byref(shape), S)
     del ws
@@ -399,12 +414,14 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
                  perm: torch.Tensor, inv_pos: torch.Tensor, y_perm: torch.Tensor,
                  grad_logits: Optional[torch.Tensor] = None, w_down_t: Optional[torch.Tensor] = None,
                  w_gate_up_t: Optional[torch.Tensor] = None, gu: Optional[torch.Tensor] = None,
-                 offsets_host: Optional[torch.Tensor] = None):
+                 offsets_host: Optional[torch.Tensor] = None,
+                 dropout: Optional[Tuple[float, int]] = None):
     """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer.
 
     offsets_host: a completed host copy of offsets (moe_forward_train's, after its
     offsets_ready event); without it the offsets are read from the device here,
     which waits for every kernel queued before the call.
+    dropout: the forward's (p, seed); the SwiGLU backward regenerates its mask.
 
     HIP stages: gate gradient and dY (g5moe_gate_grad_padded: dY per expert
     padded to kmax rows), router-logit gradient (g5moe_router_grad, plus
@@ -473,8 +490,8 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
     dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
     dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
-    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(offsets), None,
-              _ptr(h_pad), _ptr(dgu_buf), kmax, ctypes.byref(shape), S)
+    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(perm), _ptr(offsets), None,
+              _ptr(h_pad), _ptr(dgu_buf), kmax, _dropout_arg(dropout), ctypes.byref(shape), S)
     del dh, gu
     if w_gate_up_t is None:
         w_gate_up_t = transpose_experts(w_gate_up)      # [E, d, 2F]

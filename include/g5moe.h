@@ -123,16 +123,42 @@ g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int3
                                   const void* w_gate_up, void* ws,
                                   const g5moe_shape* shape, void* stream);
 
+/* Dropout on the expert hidden state, the training-mode `self.dropout(hidden)`
+ * of FeedForward.forward (lib/blocks/_component.py:45, :51; GeneT5 builds it
+ * with the model's dropout, 0.1, lib/blocks/encoder.py:69, lib/model/genet5.py:17).
+ * The mask is a counter-based hash of (seed, assignment, column), so the
+ * backward regenerates it instead of storing it.  For assignment a = t*k + s
+ * (token t, slot s) and h column f, with fmix32 the 32-bit finalizer of
+ * MurmurHash3 (x ^= x >> 16; x *= 0x85ebca6b; x ^= x >> 13; x *= 0xc2b2ae35;
+ * x ^= x >> 16; arithmetic mod 2^32):
+ *   key  = fmix32(fmix32(a ^ seed_lo) + seed_hi)
+ *   bits = fmix32(key + (f >> 1) * 0x9e3779b9)
+ *   r    = (f & 1) ? bits >> 16 : bits & 0xffff          (16 bits per column)
+ *   thr  = round(p * 65536) (half away from zero), in [0, 65536]
+ *   keep = r >= thr;  scale = 65536 / (65536 - thr) (0 when thr = 65536)
+ *   h'[i, f] = keep ? h[i, f] * scale : 0   (fp32, one rounding to bf16)
+ * where i is the sorted position of assignment a.  The kept fraction is
+ * (65536 - thr) / 65536 and E[h'] = h.  p = 0 (or a NULL descriptor) is no
+ * dropout, bit for bit the plain entry point's result.  No reference
+ * counterpart: torch's Philox stream is not reproduced. */
+typedef struct g5moe_dropout {
+  float p;          /* drop probability, 0 <= p <= 1 */
+  uint32_t seed_lo; /* 64-bit seed, low and high words */
+  uint32_t seed_hi;
+  int32_t reserved; /* must be 0 */
+} g5moe_dropout;
+
 /* g5moe_expert_gate_up for training: the same h into the workspace, and the raw
  * products gu[p] = x[perm[p] / k] . Wgu_e^T (bf16 [N*k, 2F], packed gate|up column
  * order, the layout of g5moe_expert_gate_up_raw and bit for bit its values) for
  * the SwiGLU backward, so the backward need not recompute them.  Replaces
  * keeping `self.wi_0(x)` / `self.wi_1(x)` for autograd
- * (lib/blocks/_component.py:50). */
+ * (lib/blocks/_component.py:50).  dropout (NULL = none): h in the workspace is
+ * h' of g5moe_dropout (the down GEMM's input); gu stays the raw products. */
 g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
                                         const int32_t* offsets, const void* w_gate_up,
-                                        void* gu, void* ws, const g5moe_shape* shape,
-                                        void* stream);
+                                        void* gu, void* ws, const g5moe_dropout* dropout,
+                                        const g5moe_shape* shape, void* stream);
 
 /* Grouped down GEMM: y_perm[p] = h[p] . Wd_e^T (bf16 out, fp32 accumulate),
  * h read from the workspace written by g5moe_expert_gate_up.  Replaces
@@ -287,9 +313,14 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
  * offsets[e] + j, zero rows for j >= M_e (kmax >= every M_e): the weight
  * gradients' batched operands and g5moe_grouped_gemm_padded's A operand (give
  * dgu_pad 256 rows of padding after row E*kmax for that);  dgu : bf16
- * [N*k + 256, 2F] packed out in sorted order, or NULL (not written). */
-g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* offsets,
-                                   void* dgu, void* h_pad, void* dgu_pad, int32_t kmax,
+ * [N*k + 256, 2F] packed out in sorted order, or NULL (not written).
+ * dropout (NULL = none; the forward's descriptor): dh is the gradient of h',
+ * so dg and du use dh * keep * scale, and h_pad holds h' (the down product's
+ * input) — the mask of g5moe_dropout regenerated from perm (sorted position ->
+ * assignment a), which must then be non-NULL. */
+g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t* perm,
+                                   const int32_t* offsets, void* dgu, void* h_pad,
+                                   void* dgu_pad, int32_t kmax, const g5moe_dropout* dropout,
                                    const g5moe_shape* shape, void* stream);
 
 /* Per-expert padded transpose: out[e][c][j] = column c of the row of expert

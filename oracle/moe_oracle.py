@@ -53,6 +53,23 @@ moe_backward
     gradients as outer products.  Pins: central finite differences of a
     scalar loss in random directions (float64), and torch.autograd in float64
     on a torch restatement of the same forward.
+dropout_keep / dropout_keep_py / dropout_scale
+    The dropout mask on the expert hidden state as the C ABI defines it
+    (g5moe_dropout in include/g5moe.h; the reference applies nn.Dropout to the
+    SwiGLU output in training, lib/blocks/_component.py:45, :51, whose Philox
+    stream is torch's own and not reproduced): for assignment a and h column f,
+    key = fmix32(fmix32(a ^ seed_lo) + seed_hi), bits = fmix32(key + (f >> 1) *
+    0x9e3779b9), keep = 16 bits of it (low for even f, high for odd) >= thr with
+    thr = round(p * 65536), scale = 65536 / (65536 - thr).  fmix32 is
+    MurmurHash3's 32-bit finalizer.  dropout_keep is vectorised numpy,
+    dropout_keep_py a pure-Python integer restatement.  Pins
+    (tests/test_oracle_dropout.py): numpy == pure Python bit for bit; fmix32 is a
+    bijection on sampled inputs with its published avalanche (each input bit
+    flips about half the output bits); the kept fraction is within a binomial
+    bound of (65536 - thr) / 65536; neighbouring columns, rows and seeds are
+    uncorrelated; p = 0 keeps everything and p = 1 nothing.
+    expert_forward / moe_forward / moe_backward take `keep` [N*k, F] (by
+    assignment) and `scale`: h' = h * keep * scale feeds the down product.
 add_rmsnorm / add_rmsnorm_np
     s = T(x + r); ss = sum s^2 in the router's lane/tree order; rstd =
     1 / sqrt(ss / d + eps); normed = T((s * rstd) * w) — fused_add_rmsnorm /
@@ -238,19 +255,86 @@ def dispatch_c(topk_idx: np.ndarray, n_experts: int):
 
 # ---- experts and combine ---------------------------------------------------------
 
+# ---- dropout mask (g5moe_dropout) -------------------------------------------------
+
+_M32 = np.uint32(0xFFFFFFFF)
+
+
+def _fmix32_np(x: np.ndarray) -> np.ndarray:
+    x = np.asarray(x, dtype=np.uint32).copy()
+    with np.errstate(over="ignore"):
+        x ^= x >> np.uint32(16)
+        x = (x.astype(np.uint64) * np.uint64(0x85EBCA6B) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+        x ^= x >> np.uint32(13)
+        x = (x.astype(np.uint64) * np.uint64(0xC2B2AE35) & np.uint64(0xFFFFFFFF)).astype(np.uint32)
+        x ^= x >> np.uint32(16)
+    return x
+
+
+def dropout_threshold(p: float) -> int:
+    """round(p * 65536), halves away from zero, of the fp32 value of p."""
+    t = float(np.float32(p)) * 65536.0
+    return min(65536, int(t + 0.5))
+
+
+def dropout_scale(p: float) -> np.float32:
+    """fp32 65536 / (65536 - thr); 0 when everything is dropped."""
+    thr = dropout_threshold(p)
+    return np.float32(0.0) if thr >= 65536 else np.float32(65536.0 / (65536 - thr))
+
+
+def dropout_keep(assignments: np.ndarray, n_cols: int, p: float, seed: int) -> np.ndarray:
+    """bool [len(assignments), n_cols]: the mask of each assignment's h row."""
+    seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    lo, hi = np.uint32(seed & 0xFFFFFFFF), np.uint32(seed >> 32)
+    a = np.asarray(assignments, dtype=np.int64).astype(np.uint32)
+    key = _fmix32_np(((_fmix32_np(a ^ lo).astype(np.uint64) + np.uint64(hi))
+                      & np.uint64(0xFFFFFFFF)).astype(np.uint32))
+    pairs = np.arange((n_cols + 1) // 2, dtype=np.uint64)
+    x = (key[:, None].astype(np.uint64) + pairs[None, :] * np.uint64(0x9E3779B9)) \
+        & np.uint64(0xFFFFFFFF)
+    bits = _fmix32_np(x.astype(np.uint32))
+    r = np.empty((a.size, 2 * pairs.size), dtype=np.uint32)
+    r[:, 0::2] = bits & np.uint32(0xFFFF)
+    r[:, 1::2] = bits >> np.uint32(16)
+    return r[:, :n_cols] >= np.uint32(dropout_threshold(p))
+
+
+def _fmix32_py(x: int) -> int:
+    x ^= x >> 16
+    x = (x * 0x85EBCA6B) & 0xFFFFFFFF
+    x ^= x >> 13
+    x = (x * 0xC2B2AE35) & 0xFFFFFFFF
+    x ^= x >> 16
+    return x
+
+
+def dropout_keep_py(a: int, f: int, p: float, seed: int) -> bool:
+    """One mask element in plain Python integers (the pin of dropout_keep)."""
+    seed = int(seed) & 0xFFFFFFFFFFFFFFFF
+    key = _fmix32_py((_fmix32_py((a & 0xFFFFFFFF) ^ (seed & 0xFFFFFFFF)) + (seed >> 32))
+                     & 0xFFFFFFFF)
+    bits = _fmix32_py((key + (f >> 1) * 0x9E3779B9) & 0xFFFFFFFF)
+    r = (bits >> 16) if f & 1 else (bits & 0xFFFF)
+    return r >= dropout_threshold(p)
+
+
 def _silu(g: np.ndarray) -> np.ndarray:
     return g / (1.0 + np.exp(-g))
 
 
 def expert_forward(x_f: np.ndarray, perm: np.ndarray, offsets: np.ndarray, top_k: int,
                    w_gate: np.ndarray, w_up: np.ndarray, w_down: np.ndarray,
-                   dtype=np.float32, return_h: bool = False, storage: str = "fp32"):
+                   dtype=np.float32, return_h: bool = False, storage: str = "fp32",
+                   keep: Optional[np.ndarray] = None, scale: float = 1.0):
     """Per-expert SwiGLU over the routed rows, in `dtype` (float32 or float64).
     Weights may be uint16 bf16 bits or float arrays.  -> y_perm [N*k, d] (and h).
 
     storage="bf16" rounds h (the down product's input) and y_perm to bf16, the
     two points where the layer's bf16 dataflow stores bf16 — as the reference's
-    bf16 FeedForward does with the SiLU-mul output and the `wo` output."""
+    bf16 FeedForward does with the SiLU-mul output and the `wo` output.
+    keep (bool [N*k, F], indexed by assignment) and scale: dropout, h' = h * keep
+    * scale before the rounding and the down product (h is then h')."""
     if storage not in ("fp32", "bf16"):
         raise ValueError(storage)
     E = w_gate.shape[0]
@@ -268,6 +352,8 @@ def expert_forward(x_f: np.ndarray, perm: np.ndarray, offsets: np.ndarray, top_k
         wu = widen(w_up[e]).astype(dtype, copy=False)
         wd = widen(w_down[e]).astype(dtype, copy=False)
         h = _silu(rows @ wg.T) * (rows @ wu.T)
+        if keep is not None:
+            h = h * (keep[perm[o0:o1]].astype(dtype) * dtype(scale))
         if storage == "bf16":
             h = round_bf16(h).astype(dtype)
         y = h @ wd.T
@@ -292,9 +378,11 @@ def combine(y_perm: np.ndarray, inv_pos: np.ndarray, topk_w: np.ndarray) -> np.n
 
 def moe_forward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray,
                 w_down: np.ndarray, top_k: int, bias: Optional[np.ndarray] = None,
-                dtype=np.float32, return_h: bool = False, storage: str = "fp32") -> dict:
+                dtype=np.float32, return_h: bool = False, storage: str = "fp32",
+                dropout: Optional[tuple] = None) -> dict:
     """Whole layer.  x / w_router: fp32 or uint16 bf16 bits (same kind).  Expert
-    weights: bf16 bits or float arrays.  Returns every intermediate."""
+    weights: bf16 bits or float arrays.  dropout = (p, seed): the mask of
+    dropout_keep on h.  Returns every intermediate."""
     E = w_router.shape[0]
     logits = router_logits(x, w_router, bias)
     idx, w = topk_gates_c(logits, top_k)
@@ -302,8 +390,12 @@ def moe_forward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: n
     xf = widen(x)
     if storage == "bf16" and x.dtype != np.uint16:
         xf = round_bf16(xf)  # an fp32 x enters the bf16 expert GEMMs rounded to bf16
+    keep, scale = None, 1.0
+    if dropout is not None and dropout[0] > 0:
+        keep = dropout_keep(np.arange(perm.size), w_gate.shape[1], dropout[0], dropout[1])
+        scale = float(dropout_scale(dropout[0]))
     res = expert_forward(xf, perm, offsets, top_k, w_gate, w_up, w_down, dtype=dtype,
-                         return_h=return_h, storage=storage)
+                         return_h=return_h, storage=storage, keep=keep, scale=scale)
     y_perm, h = res if return_h else (res, None)
     y = combine(y_perm, inv_pos, w)
     out = dict(logits=logits, topk_idx=idx, topk_w=w, counts=counts, offsets=offsets,
@@ -396,7 +488,8 @@ def combine_c(y_perm_bits: np.ndarray, inv_pos: np.ndarray, topk_w: np.ndarray,
 def moe_backward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: np.ndarray,
                  w_down: np.ndarray, topk_idx: np.ndarray, dy: np.ndarray,
                  grad_logits: Optional[np.ndarray] = None,
-                 bias: Optional[np.ndarray] = None) -> dict:
+                 bias: Optional[np.ndarray] = None,
+                 keep: Optional[np.ndarray] = None, scale: float = 1.0) -> dict:
     """Textbook float64 backward of the layer for the routing indices topk_idx
     (the top-k choice is piecewise constant in the logits, so it carries no
     gradient).  Forward: logits = x Wr^T (+ b); w = softmax over the chosen
@@ -404,8 +497,11 @@ def moe_backward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: 
     h = silu(x Wg_e^T) * (x Wu_e^T), Y = h Wd_e^T; y[t] = sum_s w[t, s] Y[t, s]
     (FeedForward.forward, lib/blocks/_component.py:48-52, per expert).  The loss
     is L(y, logits) with dL/dy = dy and an optional dL/dlogits = grad_logits.
-    Inputs: float arrays or uint16 bf16 bits (widened).  Returns dict with dx,
-    d_w_router, d_w_gate, d_w_up, d_w_down, dlogits, dw, y."""
+    Inputs: float arrays or uint16 bf16 bits (widened).  keep (bool [N*k, F], by
+    assignment t*k + s) and scale: dropout on h, h' = h * keep * scale feeds the
+    down product, so dWd uses h' and the SwiGLU derivative takes dh' * keep *
+    scale.  Returns dict with dx, d_w_router, d_w_gate, d_w_up, d_w_down,
+    dlogits, dw, y."""
     f = lambda a: widen(a).astype(np.float64)
     X, Wr, Wg, Wu, Wd, DY = f(x), f(w_router), f(w_gate), f(w_up), f(w_down), f(dy)
     N, d = X.shape
@@ -431,13 +527,17 @@ def moe_backward(x: np.ndarray, w_router: np.ndarray, w_gate: np.ndarray, w_up: 
             g, u = xe @ Wg[e].T, xe @ Wu[e].T
             sg = 1.0 / (1.0 + np.exp(-g))
             h = g * sg * u
+            m = 1.0
+            if keep is not None:
+                m = keep[rows * k + s].astype(np.float64) * float(scale)
+                h = h * m
             Y = h @ Wd[e].T
             we = w[rows, s:s + 1]
             y[rows] += we * Y
             dw[rows, s] = (DY[rows] * Y).sum(axis=1)
             dY = we * DY[rows]
             dwd[e] += dY.T @ h
-            dh = dY @ Wd[e]
+            dh = (dY @ Wd[e]) * m
             dg = dh * u * sg * (1.0 + g * (1.0 - sg))
             du = dh * g * sg
             dwg[e] += dg.T @ xe

@@ -122,10 +122,14 @@ def test_module_constructor_contract():
         MoEFeedForward(768, 3000)
     with pytest.raises(ValueError):
         MoEFeedForward(768, 3072, num_experts=4, top_k=5)
+    # dropout in training mode runs the training path (bf16 activations, GPU only;
+    # no CPU fallback)
     m.train()
     m.dropout = 0.1
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(TypeError, match="bf16"):
         m(torch.zeros(1, 768))
+    with pytest.raises(RuntimeError, match="GPU only"):
+        m.to(torch.bfloat16)(torch.zeros(1, 768, dtype=torch.bfloat16))
 
 
 def test_module_load_dense_upcycles():

@@ -198,8 +198,8 @@ def test_padded_weight_gradient_operands(cuda_device):
     dgu_pad = torch.full((E, kmax, 2 * F), 7, dtype=torch.int16,
                          device=cuda_device).view(torch.bfloat16)
     _lib.call("g5moe_swiglu_backward", ops._ptr(dev_t(dh, cuda_device, True)),
-              ops._ptr(dev_t(gu, cuda_device, True)), ops._ptr(t_off), ops._ptr(dgu),
-              ops._ptr(h_pad), ops._ptr(dgu_pad), kmax, ctypes.byref(shape), S)
+              ops._ptr(dev_t(gu, cuda_device, True)), None, ops._ptr(t_off), ops._ptr(dgu),
+              ops._ptr(h_pad), ops._ptr(dgu_pad), kmax, None, ctypes.byref(shape), S)
     torch.cuda.synchronize()
     bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
     exp = np.zeros((E, d, kmax), np.uint16)
@@ -320,10 +320,10 @@ def test_padded_dx_product_equals_sorted(cuda_device):
     p1 = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=cuda_device)
     h2 = torch.empty_like(h1)
     p2 = torch.empty_like(p1)
-    _lib.call("g5moe_swiglu_backward", ops._ptr(dh), ops._ptr(gu), ops._ptr(t_off),
-              ops._ptr(dgu), ops._ptr(h1), ops._ptr(p1), kmax, ctypes.byref(shape), S)
-    _lib.call("g5moe_swiglu_backward", ops._ptr(dh), ops._ptr(gu), ops._ptr(t_off), None,
-              ops._ptr(h2), ops._ptr(p2), kmax, ctypes.byref(shape), S)
+    _lib.call("g5moe_swiglu_backward", ops._ptr(dh), ops._ptr(gu), None, ops._ptr(t_off),
+              ops._ptr(dgu), ops._ptr(h1), ops._ptr(p1), kmax, None, ctypes.byref(shape), S)
+    _lib.call("g5moe_swiglu_backward", ops._ptr(dh), ops._ptr(gu), None, ops._ptr(t_off), None,
+              ops._ptr(h2), ops._ptr(p2), kmax, None, ctypes.byref(shape), S)
     wt = (torch.randn(E, d, 2 * F, device=cuda_device) * 0.05).to(torch.bfloat16)
     ref = ops.grouped_gemm(dgu, nk, t_off, wt)
     got = ops.grouped_gemm_padded(p1, kmax, nk, t_off, wt)

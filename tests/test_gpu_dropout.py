@@ -1,0 +1,189 @@
+"""Dropout on the expert hidden state (g5moe_dropout), through the C ABI and the
+module's autograd, and the training backward's freedom from host synchronisation.
+
+* The GPU mask equals the host restatement (oracle.moe_oracle.dropout_keep, pinned
+  in tests/test_oracle_dropout.py) bit for bit: the dropped h entries are exactly
+  the zeros of the dropout forward's h, whose kept entries are the plain h times the
+  scale (within one bf16 rounding); the raw gate|up products are untouched; the
+  kept fraction is within a binomial bound of 1 - p.
+* p = 0 is the plain path bit for bit.
+* Forward and backward against the float64 oracle given the same mask, at the
+  bars of the mask-free tests (2e-2 / 2e-3 forward, 1.5e-2 / 6e-3 gradients).
+* MoEFeedForward(768, 3072, 0.1).train(): forward and backward through autograd,
+  reproducible under torch.manual_seed, different masks for different seeds.
+* loss.backward() through the module raises nothing under
+  torch.cuda.set_sync_debug_mode("error"), with the same gradients as the
+  backward that reads the offsets from the device.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from oracle import moe_oracle as mo
+from genet5_amd import _lib, ops, synth
+from genet5_amd.moe import MoEFeedForward
+from test_gpu_backward import check
+from test_gpu_parity import dev_t, host, layer_tensors, normwise
+
+pytestmark = pytest.mark.gpu
+
+SEED = 0x5EED_1234_ABCD_0077
+
+
+def gate_up_train(x, perm, offsets, wgu, shape, dev, dropout):
+    """g5moe_expert_gate_up_train through the C ABI -> (h [N*k, F], gu [N*k, 2F])."""
+    N, k, F = shape.n_tokens, shape.top_k, shape.d_ff
+    ws = ops.workspace(shape, dev)
+    gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
+    drop = None if dropout is None else ctypes.byref(_lib.make_dropout(*dropout))
+    _lib.call("g5moe_expert_gate_up_train", ops._ptr(x), ops._ptr(perm), ops._ptr(offsets),
+              ops._ptr(wgu), ops._ptr(gu), ops._ptr(ws), drop, ctypes.byref(shape),
+              ops._stream(dev))
+    off = ops._h_offset(shape)
+    h = ws[off: off + N * k * F * 2].view(torch.bfloat16).view(N * k, F)
+    return h, gu
+
+
+@pytest.mark.parametrize("p", [0.1, 0.5])
+def test_gpu_mask_equals_host_restatement(cuda_device, p):
+    n, d, F, E, k = 4096, 768, 3072, 16, 2
+    print(f"dropout mask p={p} n={n}", flush=True)
+    inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=31, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    idx, w = ops.router_topk(x, wr, k)
+    _, offsets, perm, inv_pos = ops.dispatch(idx, E, d)
+    shape = _lib.make_shape(n, d, F, E, k, _lib.DTYPE_BF16)
+    h0, gu0 = gate_up_train(x, perm, offsets, wgu, shape, cuda_device, None)
+    h1, gu1 = gate_up_train(x, perm, offsets, wgu, shape, cuda_device, (p, SEED))
+    hz, guz = gate_up_train(x, perm, offsets, wgu, shape, cuda_device, (0.0, SEED))
+    torch.cuda.synchronize()
+    assert torch.equal(gu0, gu1) and torch.equal(hz, h0) and torch.equal(guz, gu0)
+    a0, a1 = host(h0), host(h1)
+    assert np.all(a0 != 0), "the check below needs an h without exact zeros"
+    keep = mo.dropout_keep(perm.cpu().numpy(), F, p, SEED)
+    np.testing.assert_array_equal(a1 != 0, keep)
+    sc = np.float32(mo.dropout_scale(p))
+    err = np.abs(a1[keep].astype(np.float64) - a0[keep].astype(np.float64) * sc)
+    assert np.all(err <= 2.0 ** -7 * np.abs(a1[keep])), err.max()
+    q = (65536 - mo.dropout_threshold(p)) / 65536
+    frac = keep.mean()
+    assert abs(frac - q) <= 6 * np.sqrt(q * (1 - q) / keep.size), (frac, q)
+    print(f"  kept {frac:.5f} (expected {q:.5f})", flush=True)
+
+
+@pytest.mark.parametrize("n,d,F,E,k,p", [(700, 256, 512, 8, 2, 0.2), (2048, 768, 3072, 16, 2, 0.1)])
+def test_forward_backward_vs_oracle_with_mask(cuda_device, n, d, F, E, k, p):
+    print(f"dropout fwd/bwd n={n} d={d} F={F} E={E} k={k} p={p}", flush=True)
+    inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=41, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    rng = np.random.default_rng(9)
+    dy_np = synth.f32_to_bf16_bits(rng.standard_normal((n, d)).astype(np.float32))
+    dy = dev_t(dy_np, cuda_device, True)
+    y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(
+        x, wr, wgu, wd, k, dropout=(p, SEED))
+    grads = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm,
+                             gu=gu, dropout=(p, SEED))
+    y0 = ops.moe_forward_train(x, wr, wgu, wd, k)[0]
+    torch.cuda.synchronize()
+    ref_i, _ = oracle.topk_gates_c(oracle.router_logits(inp.x, inp.w_router), k)
+    np.testing.assert_array_equal(idx.cpu().numpy(), ref_i)
+    ref_f = oracle.moe_forward(inp.x, inp.w_router, inp.w_gate, inp.w_up, inp.w_down, k,
+                               storage="bf16", dropout=(p, SEED))
+    mx, mean = normwise(host(y), ref_f["y"])
+    print(f"  y: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+    assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
+    assert not torch.equal(y, y0)
+    keep = mo.dropout_keep(np.arange(n * k), F, p, SEED)
+    ref = oracle.moe_backward(inp.x, inp.w_router, inp.w_gate, inp.w_up, inp.w_down, ref_i,
+                              dy_np, keep=keep, scale=float(mo.dropout_scale(p)))
+    dx, d_wr, d_wgu, d_wd = grads
+    d_wg, d_wu = ops.unpack_gate_up(d_wgu)
+    check("dx", host(dx), ref["dx"])
+    check("d_w_router", host(d_wr), ref["d_w_router"])
+    check("d_w_gate", host(d_wg), ref["d_w_gate"])
+    check("d_w_up", host(d_wu), ref["d_w_up"])
+    check("d_w_down", host(d_wd), ref["d_w_down"])
+
+
+def make_module(dev, dropout, d=768, F=3072, E=16):
+    torch.manual_seed(3)
+    m = MoEFeedForward(d, F, dropout, num_experts=E).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        for prm in (m.w_gate, m.w_up, m.w_down, m.router.weight):
+            prm.normal_(0, 0.02)
+    return m
+
+
+def run(m, x, seed):
+    torch.manual_seed(seed)
+    xr = x.clone().requires_grad_(True)
+    m.zero_grad(set_to_none=True)
+    y = m(xr)
+    y.float().square().sum().backward()
+    return y.detach(), [xr.grad] + [p.grad for p in
+                                    (m.router.weight, m.w_gate, m.w_up, m.w_down)]
+
+
+def test_module_dropout_through_autograd(cuda_device):
+    m = make_module(cuda_device, 0.1).train()
+    x = torch.randn(3000, 768, device=cuda_device).to(torch.bfloat16)
+    y1, g1 = run(m, x, 11)
+    y2, g2 = run(m, x, 11)
+    y3, g3 = run(m, x, 12)
+    assert torch.equal(y1, y2) and all(torch.equal(a, b) for a, b in zip(g1, g2))
+    assert not torch.equal(y1, y3)
+    assert all(g is not None and torch.isfinite(g.float()).all() for g in g1)
+    # eval mode and p = 0 in training mode: no dropout, the inference op's output
+    m.eval()
+    with torch.no_grad():
+        ye = m(x)
+    m.train()
+    m.dropout = 0.0
+    y0, _ = run(m, x, 11)
+    assert torch.equal(y0, ye) and not torch.equal(y1, ye)
+    # train mode with dropout but no gradient still applies the dropout
+    m.dropout = 0.1
+    torch.manual_seed(11)
+    with torch.no_grad():
+        yn = m(x)
+    assert torch.equal(yn, y1)
+
+
+def test_backward_has_no_host_sync(cuda_device):
+    """The offsets reach the backward through the forward's pinned copy and event,
+    the transposed weights come from the module's cache: no synchronising call."""
+    m = make_module(cuda_device, 0.1).train()
+    m.aux_loss_coef = 0.01
+    x = torch.randn(3000, 768, device=cuda_device).to(torch.bfloat16)
+    run(m, x, 5)  # warm the caches (pinned memory, transposed weights)
+    torch.cuda.synchronize()
+    torch.cuda.set_sync_debug_mode("error")
+    try:
+        torch.manual_seed(5)
+        xr = x.clone().requires_grad_(True)
+        m.zero_grad(set_to_none=True)
+        y = m(xr)
+        loss = y.float().square().sum() + m.aux_loss
+        loss.backward()
+    finally:
+        torch.cuda.set_sync_debug_mode("default")
+    g_nosync = [xr.grad] + [p.grad for p in (m.router.weight, m.w_gate, m.w_up, m.w_down)]
+    # the same step with the offsets read from the device in the backward
+    from genet5_amd import moe as moe_mod
+    saved = moe_mod._HOST_OFFSETS_MAX
+    moe_mod._HOST_OFFSETS_MAX = 0  # no host copies are kept: the backward reads the device
+    try:
+        torch.manual_seed(5)
+        xr2 = x.clone().requires_grad_(True)
+        m.zero_grad(set_to_none=True)
+        y2 = m(xr2)
+        (y2.float().square().sum() + m.aux_loss).backward()
+    finally:
+        moe_mod._HOST_OFFSETS_MAX = saved
+    g_dev = [xr2.grad] + [p.grad for p in (m.router.weight, m.w_gate, m.w_up, m.w_down)]
+    assert torch.equal(y, y2)
+    for a, b in zip(g_nosync, g_dev):
+        assert torch.equal(a, b)
