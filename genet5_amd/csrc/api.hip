@@ -157,6 +157,28 @@ g5moe_status g5moe_dispatch(const int32_t* topk_idx, int32_t* counts, int32_t* o
                     "g5moe_dispatch");
 }
 
+g5moe_status g5moe_dispatch_noalloc(const int32_t* topk_idx, int32_t* counts, int32_t* offsets,
+                                    int32_t* perm, int32_t* inv_pos, const g5moe_shape* shape,
+                                    void* stream) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(counts);
+  G5_NONNULL(offsets);
+  const int64_t nk = shape->n_tokens * shape->top_k;
+  if (nk > kNoAllocMaxAssignments)
+    return fail(G5MOE_ERR_UNSUPPORTED,
+                "g5moe_dispatch_noalloc: n_tokens * top_k = %lld exceeds its scratch of %lld "
+                "assignments (%zu bytes per GPU); use g5moe_dispatch with a workspace",
+                (long long)nk, (long long)kNoAllocMaxAssignments, kNoAllocScratchBytes);
+  if (nk > 0) {
+    G5_NONNULL(topk_idx);
+    G5_NONNULL(perm);
+    G5_NONNULL(inv_pos);
+  }
+  return hip_status(launch_dispatch_noalloc(topk_idx, counts, offsets, perm, inv_pos, *shape,
+                                            as_stream(stream)),
+                    "g5moe_dispatch_noalloc");
+}
+
 g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int32_t* offsets,
                                   const void* w_gate_up, void* ws,
                                   const g5moe_shape* shape, void* stream) {

@@ -17,9 +17,19 @@
 //             offsets over experts, and writes position = offsets[e] + prefix +
 //             rank into perm and inv_pos; block 0 also writes counts[] and
 //             offsets[].  Integer sums are exact in any order.
+#include <mutex>
+
 #include "g5moe_internal.h"
 
 namespace g5moe {
+
+// Scratch of the allocation-free dispatch (g5moe_dispatch_noalloc): the rank
+// pass's in-block ranks [N*k] and block counts [nblk, E], for at most
+// kNoAllocMaxAssignments assignments.  Each GPU the library runs on holds its
+// own copy for the life of the process.  Host code never uses this name as a
+// device address: the per-device address comes from hipGetSymbolAddress.
+__device__ __align__(256) char scratch[kNoAllocScratchBytes];
+
 namespace {
 
 constexpr int kWaves = kDispatchBlock / 64;
@@ -137,25 +147,77 @@ __global__ void zero_counts_kernel(int32_t* counts, int32_t* offsets, int n_expe
   if (i <= n_experts) offsets[i] = 0;
 }
 
+
+// The two dispatch launches over caller-given rank [N*k] and block-count
+// [nblk, E] buffers.  The rank pass writes every entry the place pass reads, so
+// neither buffer needs clearing.
+hipError_t dispatch_launches(const int32_t* idx, int32_t* counts, int32_t* offsets,
+                             int32_t* perm, int32_t* inv_pos, int32_t* rank, int32_t* blk,
+                             int64_t nk, int n_experts, hipStream_t st) {
+  if (nk == 0) {
+    hipLaunchKernelGGL(zero_counts_kernel, dim3(1), dim3(64), 0, st, counts, offsets,
+                       n_experts);
+    return hipGetLastError();
+  }
+  const int64_t nblk = (nk + kDispatchBlock - 1) / kDispatchBlock;
+  hipLaunchKernelGGL(dispatch_rank_kernel, dim3(unsigned(nblk)), dim3(kDispatchBlock), 0, st,
+                     idx, nk, n_experts, rank, blk);
+  hipLaunchKernelGGL(dispatch_place_kernel, dim3(unsigned(nblk)), dim3(kDispatchBlock), 0, st,
+                     idx, rank, blk, nblk, nk, n_experts, perm, inv_pos, counts, offsets);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets,
                            int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                            hipStream_t st) {
   const WorkspaceLayout L = workspace_layout(s);
-  const int64_t nk = s.n_tokens * s.top_k;
-  if (nk == 0) {
-    hipLaunchKernelGGL(zero_counts_kernel, dim3(1), dim3(64), 0, st, counts, offsets,
-                       s.n_experts);
-    return hipGetLastError();
+  return dispatch_launches(idx, counts, offsets, perm, inv_pos,
+                           reinterpret_cast<int32_t*>(ws + L.rank),
+                           reinterpret_cast<int32_t*>(ws + L.blk_counts),
+                           s.n_tokens * s.top_k, s.n_experts, st);
+}
+
+namespace {
+
+// Device address of `scratch` on the current device, looked up once per device
+// (hipGetSymbolAddress with that device current) and kept; nullptr with the HIP
+// error in *err if the lookup fails.
+char* noalloc_scratch(hipError_t* err) {
+  static std::mutex mu;
+  static char* addr[kMaxDevices] = {};
+  int dev = -1;
+  *err = hipGetDevice(&dev);
+  if (*err != hipSuccess) return nullptr;
+  if (dev < 0 || dev >= kMaxDevices) {
+    *err = hipErrorInvalidDevice;
+    return nullptr;
   }
-  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
-  int32_t* blk = reinterpret_cast<int32_t*>(ws + L.blk_counts);
-  hipLaunchKernelGGL(dispatch_rank_kernel, dim3(unsigned(L.nblk)), dim3(kDispatchBlock), 0,
-                     st, idx, nk, s.n_experts, rank, blk);
-  hipLaunchKernelGGL(dispatch_place_kernel, dim3(unsigned(L.nblk)), dim3(kDispatchBlock), 0,
-                     st, idx, rank, blk, L.nblk, nk, s.n_experts, perm, inv_pos, counts, offsets);
-  return hipGetLastError();
+  std::lock_guard<std::mutex> lock(mu);
+  if (addr[dev] == nullptr) {
+    void* p = nullptr;
+    *err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (*err != hipSuccess) return nullptr;
+    addr[dev] = static_cast<char*>(p);
+  }
+  return addr[dev];
+}
+
+}  // namespace
+
+hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t* offsets,
+                                   int32_t* perm, int32_t* inv_pos, const g5moe_shape& s,
+                                   hipStream_t st) {
+  const int64_t nk = s.n_tokens * s.top_k;
+  if (nk > kNoAllocMaxAssignments) return hipErrorInvalidValue;  // checked by the caller too
+  hipError_t err = hipSuccess;
+  char* base = noalloc_scratch(&err);
+  if (base == nullptr) return err;
+  // ranks first (kNoAllocMaxAssignments entries), then the block counts
+  int32_t* rank = reinterpret_cast<int32_t*>(base);
+  int32_t* blk = reinterpret_cast<int32_t*>(base + kNoAllocRankBytes);
+  return dispatch_launches(idx, counts, offsets, perm, inv_pos, rank, blk, nk, s.n_experts, st);
 }
 
 }  // namespace g5moe

@@ -13,6 +13,16 @@ constexpr int kMaxExperts = 16;
 constexpr int kMaxTopK = 4;
 constexpr int kDispatchBlock = 256;  // assignments per dispatch block
 constexpr int kGemmRowPad = 256;     // rows of padding after h (one GEMM m-tile)
+constexpr int kMaxDevices = 64;      // devices the per-device host caches cover
+
+// Allocation-free dispatch (g5moe_dispatch_noalloc): its rank pass's buffers live
+// in a fixed device array of kNoAllocScratchBytes per GPU — in-block ranks for up
+// to kNoAllocMaxAssignments assignments, then the block counts [nblk, 16].
+constexpr int64_t kNoAllocMaxAssignments = int64_t(1) << 20;
+constexpr size_t kNoAllocRankBytes = size_t(kNoAllocMaxAssignments) * 4;
+constexpr size_t kNoAllocScratchBytes =
+    kNoAllocRankBytes + size_t(kNoAllocMaxAssignments / kDispatchBlock) * kMaxExperts * 4;
+static_assert(kNoAllocRankBytes % 256 == 0, "block counts 256-byte aligned");
 
 // Byte offsets of the workspace regions (each 256-byte aligned).
 struct WorkspaceLayout {
@@ -93,6 +103,11 @@ hipError_t launch_combine_residual(const uint16_t* y_perm, const int32_t* inv_po
 hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets,
                            int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                            hipStream_t st);
+// g5moe_dispatch with its buffers in the library's per-device scratch array
+// (n_tokens * top_k <= kNoAllocMaxAssignments).
+hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t* offsets,
+                                   int32_t* perm, int32_t* inv_pos, const g5moe_shape& s,
+                                   hipStream_t st);
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
                           const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
                           hipStream_t st, const DropoutParams* drop = nullptr);

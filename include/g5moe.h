@@ -113,6 +113,21 @@ g5moe_status g5moe_dispatch(const int32_t* topk_idx, int32_t* counts, int32_t* o
                             int32_t* perm, int32_t* inv_pos, void* ws,
                             const g5moe_shape* shape, void* stream);
 
+/* g5moe_dispatch without a workspace, for callers that cannot allocate (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference.  Same outputs as g5moe_dispatch,
+ * bit for bit; the two passes' in-block ranks and block counts live in a
+ * static device array of the library (4,456,448 bytes, held by every GPU the
+ * library runs on until the process ends) instead of `ws`.  The call allocates
+ * and frees nothing.  Limit: n_tokens * top_k <= 1,048,576 (2^20) assignments;
+ * larger shapes fail with G5MOE_ERR_UNSUPPORTED.  Every call on one GPU shares
+ * that array: calls that overlap on one GPU (e.g. on two streams) race and must
+ * be serialised by the caller.  No part of the array needs to start at zero
+ * (each call writes every entry it reads). */
+g5moe_status g5moe_dispatch_noalloc(const int32_t* topk_idx, int32_t* counts, int32_t* offsets,
+                                    int32_t* perm, int32_t* inv_pos, const g5moe_shape* shape,
+                                    void* stream);
+
 /* Grouped gate|up GEMM with SwiGLU: for sorted position p of expert e and
  * token t = perm[p] / k, h[p] = silu(x[t] . Wg_e^T) * (x[t] . Wu_e^T), stored
  * bf16 into the workspace.  Replaces `self.wi_0(x)`, `self.wi_1(x)` and the
