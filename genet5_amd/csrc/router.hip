@@ -18,14 +18,25 @@
 // keeps 16 of its 32 values and adds the partner's copy of those 16, then
 // 16 -> 8 at xor-16, ..., 2 -> 1 at xor-2, and a plain xor-1 butterfly.  Each
 // sum is therefore the pairwise tree of the contract; lanes 2m and 2m+1 end up
-// holding the logit of (token m >> 3, expert m & 7).  Each level's shuffles are
-// independent of each other, so the exchange latency overlaps; per token a wave
-// spends 8 exchanges instead of 17.  Logits go through LDS; one thread per token
-// does the top-k scan and the gates.
+// holding the logit of (token m >> 3, expert m & 7).  The exchanges use no LDS:
+// the xor-32 and xor-16 levels are gfx950's v_permlane32_swap and
+// v_permlane16_swap, the others DPP row rotates and a quad permute folded into
+// the adds.
+//
+// Schedule.  Persistent: at most two resident workgroups per CU; each wave pair
+// owns a contiguous range of tokens per round, walks it in 4-token batches with
+// the next batch's rows in flight while the current one computes (row
+// addresses are scalar: the wave index is made uniform), and stages the logits
+// in LDS; one thread per token then does the top-k scan and the gates.  The
+// weights are loaded into registers once per wave.
 //
 // Cost.  The E*d fused multiply-adds per token are the floor: N*E*d = 447M
-// FMAs at N = 36,400, about 11-14 us of VALU time on 256 CUs at 2.0-2.4 GHz;
-// reading x (55.9 MB) takes about 7 us at 8 TB/s, so the kernel is VALU-bound.
+// FMAs at N = 36,400, about 11-14 us of VALU time on 256 CUs at 2.0-2.4 GHz
+// (the contract's order rules out the matrix cores, and packed fp32 FMAs are
+// not used); reading x (55.9 MB) takes about 7 us at 8 TB/s, so the kernel is
+// VALU-bound.  NaN payloads are outside the contract: a level adds own +
+// partner in one lane and partner + own in the other, equal for every
+// non-NaN value.
 //
 // Fused pre-norm variant (MODE 1: RMSNorm, MODE 2: residual add + RMSNorm),
 // the step before the MoE in GeneT5's encoder block: fused_add_rmsnorm
@@ -43,6 +54,8 @@
 // ones g5moe_router_topk gives on the written normed rows.  Both waves of a
 // pair compute the row (the second one's loads hit the L2); the even wave
 // stores s and n.
+#include <algorithm>
+
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -51,9 +64,6 @@ namespace {
 constexpr int kRouterThreads = 256;
 constexpr int kHalfExperts = 8;           // experts per wave
 constexpr int kTokBatch = 4;              // tokens reduced together
-constexpr int kPairBatches = 4;           // batches per wave pair
-constexpr int kTokensPerPair = kTokBatch * kPairBatches;
-constexpr int kTokensPerBlock = 2 * kTokensPerPair;
 
 template <typename XT, int L>
 struct RowLoader;
@@ -158,18 +168,6 @@ struct NormArgs {
   void* normed_out;    // normed rows (the MoE input)
 };
 
-// One reduce-scatter level over V values: lanes with `bit` set keep the upper
-// half.  p[i] and the partner's p[i] (same index) hold the same (token, expert).
-template <int HALF>
-__device__ __forceinline__ void rs_level(float* p, int lane, int bit) {
-  const bool hi = (lane & bit) != 0;
-  float recv[HALF];
-#pragma unroll
-  for (int i = 0; i < HALF; ++i) recv[i] = __shfl_xor(hi ? p[i] : p[HALF + i], bit, 64);
-#pragma unroll
-  for (int i = 0; i < HALF; ++i) p[i] = (hi ? p[HALF + i] : p[i]) + recv[i];
-}
-
 // Plain (residual add +) RMSNorm with the fused variant's arithmetic, so its
 // normed rows equal the ones g5moe_add_rmsnorm_router writes bit for bit: one
 // wave per row, lane c holding columns [c*L, c*L + L), kRowsPerWave rows per
@@ -227,22 +225,133 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ x,
   }
 }
 
+// A lane's L elements of one row as loaded (raw bits), so the next batch's rows
+// can be in flight while the current one computes.
+template <typename XT, int L>
+struct RawRow {
+  static constexpr int kWords = L * int(sizeof(XT)) / 4;
+  uint32_t u[kWords];
+};
+
+template <typename XT, int L>
+__device__ __forceinline__ void load_raw(const XT* p, RawRow<XT, L>& r) {
+  constexpr int W = RawRow<XT, L>::kWords;
+  if constexpr (W % 4 == 0 && (sizeof(XT) == 4 || L % 8 == 0)) {
+    const uint4* q = reinterpret_cast<const uint4*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 4; ++i) {
+      const uint4 v = q[i];
+      r.u[4 * i] = v.x, r.u[4 * i + 1] = v.y, r.u[4 * i + 2] = v.z, r.u[4 * i + 3] = v.w;
+    }
+  } else if constexpr (W % 2 == 0) {
+    const uint2* q = reinterpret_cast<const uint2*>(p);
+#pragma unroll
+    for (int i = 0; i < W / 2; ++i) {
+      const uint2 v = q[i];
+      r.u[2 * i] = v.x, r.u[2 * i + 1] = v.y;
+    }
+  } else {
+    const uint32_t* q = reinterpret_cast<const uint32_t*>(p);
+#pragma unroll
+    for (int i = 0; i < W; ++i) r.u[i] = q[i];
+  }
+}
+
+// Raw bits -> fp32 values in column order (a bf16 pair's low half is the lower
+// column), as RowLoader converts them.
+template <typename XT, int L>
+__device__ __forceinline__ void to_floats(const RawRow<XT, L>& r, float (&v)[L]) {
+  if constexpr (sizeof(XT) == 2) {
+#pragma unroll
+    for (int i = 0; i < L / 2; ++i) {
+      v[2 * i] = __uint_as_float(r.u[i] << 16);
+      v[2 * i + 1] = __uint_as_float(r.u[i] & 0xffff0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < L; ++i) v[i] = __uint_as_float(r.u[i]);
+  }
+}
+
+// Reduce-scatter levels over lane bits 5 and 4 with gfx950's lane-swap
+// instructions: v_permlane32_swap exchanges the upper 32 lanes of its first
+// operand with the lower 32 lanes of its second, v_permlane16_swap the odd
+// 16-lane rows of the first with the even rows of the second.  With p[i] (the
+// half a low lane keeps) as the first operand and p[HALF + i] (the half a high
+// lane keeps) as the second, every lane ends up with its own kept value and its
+// partner's copy of it in the two results, whose sum is the pairwise sum of the
+// contract (own + partner in low lanes, partner + own in high lanes: the same
+// value for every non-NaN input, fp addition being commutative).
+__device__ __forceinline__ void rs_swap32(float* p) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[i]),
+                                                    __float_as_uint(p[16 + i]), false, false);
+    p[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+__device__ __forceinline__ void rs_swap16(float* p) {
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(p[i]),
+                                                    __float_as_uint(p[8 + i]), false, false);
+    p[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  }
+}
+
+// One reduce-scatter level over lane bit BIT in {8, 4, 2, 1} (inside a 16-lane
+// row) with DPP rotates, no LDS.  DPP row_ror:R gives lane l the value of lane
+// (l - R) mod 16 of its row, so a low lane (bit clear) reads the copy of p[i]
+// held by lane + BIT with row_ror:16-BIT, a high lane the copy of p[HALF + i]
+// held by lane - BIT with row_ror:BIT; a low lane keeps p[0 .. HALF), a high
+// lane p[HALF .. 2 HALF) (into slots 0 .. HALF).
+template <int BIT>
+__device__ __forceinline__ float from_lane_plus(float v) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x120 + 16 - BIT,
+                                                     0xf, 0xf, false));
+}
+template <int BIT>
+__device__ __forceinline__ float from_lane_minus(float v) {
+  return __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x120 + BIT, 0xf,
+                                                     0xf, false));
+}
+template <int HALF, int BIT>
+__device__ __forceinline__ void rs_dpp(float* p, int lane) {
+  const bool hi = (lane & BIT) != 0;
+#pragma unroll
+  for (int i = 0; i < HALF; ++i) {
+    const float lo = p[i] + from_lane_plus<BIT>(p[i]);
+    const float up = p[HALF + i] + from_lane_minus<BIT>(p[HALF + i]);
+    p[i] = hi ? up : lo;
+  }
+}
+
+// Tokens a wave pair handles per round (the logit staging in LDS).
+constexpr int kMaxPairTokens = 64;
+
 // MODE 0: router on x.  MODE 1 / 2: x is the residual stream, normalised
 // (after adding na.x_add in MODE 2) on the way in; see the header comment.
+//
+// Persistent schedule: the grid is at most the resident block count; in each
+// round wave pair q of the grid owns the contiguous token range [base + q *
+// tpp, base + (q + 1) * tpp), walks it in batches of 4 tokens with the next
+// batch's rows loaded while the current one computes, and stages the logits in
+// LDS; after a block barrier one thread per token does the top-k scan.  The
+// weights are loaded into registers once per wave.
 template <typename XT, int L, int MODE>
 __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     const XT* __restrict__ x, const XT* __restrict__ wr, const float* __restrict__ bias,
     int64_t n_tokens, int n_experts, int top_k, int32_t* __restrict__ topk_idx,
-    float* __restrict__ topk_w, float* __restrict__ logits_out, NormArgs na) {
+    float* __restrict__ topk_w, float* __restrict__ logits_out, NormArgs na, int tpp) {
   constexpr int D = 64 * L;
-  __shared__ float lg[kTokensPerBlock][kMaxExperts + 1];
+  __shared__ float lg[2 * kMaxPairTokens][kMaxExperts + 1];
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // wave-uniform (scalar), so every row address is scalar arithmetic
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = wave & 1;      // experts [8*half, 8*half + 8)
-  const int pair = wave >> 1;     // token group of the block
+  const int pair = wave >> 1;     // wave pair of the block
   const int e0 = half * kHalfExperts;
-  const int64_t tok0 = int64_t(blockIdx.x) * kTokensPerBlock + pair * kTokensPerPair;
 
   // This lane's weight slice for its wave's 8 experts (0 for experts >= E).
   float w[kHalfExperts][L];
@@ -255,7 +364,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
       for (int i = 0; i < L; ++i) w[e][i] = 0.f;
     }
   }
-
   // This lane's columns of the RMSNorm weight.
   float nw[MODE == 0 ? 1 : L];
   if constexpr (MODE != 0) {
@@ -263,139 +371,183 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     for (int i = 0; i < L; ++i) nw[i] = na.weight[lane * L + i];
   }
 
-  for (int b = 0; b < kPairBatches; ++b) {
-    const int64_t tb = tok0 + b * kTokBatch;
-    if (tb >= n_tokens) break;
-    float p[kTokBatch * kHalfExperts];
-    if constexpr (MODE == 0) {
-#pragma unroll
-      for (int m = 0; m < kTokBatch; ++m) {
-        float xv[L];
-        const int64_t t = min(tb + m, n_tokens - 1);  // rows past the end are computed, not stored
-        RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv);
-#pragma unroll
-        for (int e = 0; e < kHalfExperts; ++e) {
-          float acc = 0.f;
-#pragma unroll
-          for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[i], w[e][i], acc);
-          p[m * kHalfExperts + e] = acc;
-        }
-      }
-    } else {
-      float xv[kTokBatch][L], ss[kTokBatch];
-#pragma unroll
-      for (int m = 0; m < kTokBatch; ++m) {
-        const int64_t t = min(tb + m, n_tokens - 1);
-        RowLoader<XT, L>::load(x + size_t(t) * D + lane * L, xv[m]);
-        if constexpr (MODE == 2) {
-          float xa[L];
-          RowLoader<XT, L>::load(static_cast<const XT*>(na.x_add) + size_t(t) * D + lane * L,
-                                 xa);
-#pragma unroll
-          for (int i = 0; i < L; ++i) xv[m][i] = xv[m][i] + xa[i];
-#pragma unroll
-          for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
-        }
-        float acc = 0.f;
-#pragma unroll
-        for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], xv[m][i], acc);
-        ss[m] = acc;
-      }
-#pragma unroll
-      for (int bit = 32; bit >= 1; bit >>= 1)
-#pragma unroll
-        for (int m = 0; m < kTokBatch; ++m) ss[m] = ss[m] + __shfl_xor(ss[m], bit, 64);
-#pragma unroll
-      for (int m = 0; m < kTokBatch; ++m) {
-        const float rstd = 1.0f / __builtin_sqrtf(ss[m] / float(D) + na.eps);
-        const bool store = half == 0 && tb + m < n_tokens;
-        if constexpr (MODE == 2) {
-          if (store && na.sum_out != nullptr)
-            store_row<XT, L>(static_cast<XT*>(na.sum_out) + size_t(tb + m) * D + lane * L,
-                             xv[m]);
-        }
-#pragma unroll
-        for (int i = 0; i < L; ++i) xv[m][i] = (xv[m][i] * rstd) * nw[i];
-#pragma unroll
-        for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
-        if (store)
-          store_row<XT, L>(static_cast<XT*>(na.normed_out) + size_t(tb + m) * D + lane * L,
-                           xv[m]);
-#pragma unroll
-        for (int e = 0; e < kHalfExperts; ++e) {
-          float acc = 0.f;
-#pragma unroll
-          for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], w[e][i], acc);
-          p[m * kHalfExperts + e] = acc;
-        }
-      }
-    }
-    rs_level<16>(p, lane, 32);
-    rs_level<8>(p, lane, 16);
-    rs_level<4>(p, lane, 8);
-    rs_level<2>(p, lane, 4);
-    rs_level<1>(p, lane, 2);
-    p[0] = p[0] + __shfl_xor(p[0], 1, 64);
-    // lane holds value index v = 16*b5 + 8*b4 + 4*b3 + 2*b2 + b1 of its bits,
-    // i.e. token m = v >> 3, expert e0 + (v & 7).
-    const int v = lane >> 1;
-    const int m = v >> 3, e = e0 + (v & 7);
-    if ((lane & 1) == 0 && e < n_experts && tb + m < n_tokens) {
-      float val = p[0];
-      if (bias != nullptr) val = val + bias[e];
-      lg[pair * kTokensPerPair + b * kTokBatch + m][e] = val;
-    }
-  }
-  __syncthreads();
+  // the bias of the expert this lane's logits belong to (loaded once: a load in
+  // the batch loop would make its waits cover the prefetched rows)
+  const int e_lane = e0 + ((lane >> 1) & 7);
+  const float bias_e = (bias != nullptr && e_lane < n_experts) ? bias[e_lane] : 0.f;
 
-  // Top-k scan and gates: one thread per token.
-  const int tl = threadIdx.x;
-  const int64_t t = int64_t(blockIdx.x) * kTokensPerBlock + tl;
-  if (tl < kTokensPerBlock && t < n_tokens) {
-    float l[kMaxExperts];
+  const int64_t round_tokens = int64_t(gridDim.x) * 2 * tpp;
+  const int64_t pid = int64_t(blockIdx.x) * 2 + pair;
+  constexpr int NX = MODE == 2 ? 2 : 1;  // rows loaded per token (x, and x_add)
+  RawRow<XT, L> ra[NX][kTokBatch], rb[NX][kTokBatch];
+
+  for (int64_t base = 0; base < n_tokens; base += round_tokens) {
+    const int64_t t0 = base + pid * tpp;
+    const int64_t t1 = min(t0 + int64_t(tpp), n_tokens);
+    const int nb = t1 > t0 ? int((t1 - t0 + kTokBatch - 1) / kTokBatch) : 0;
+    float* lgp = &lg[pair * kMaxPairTokens][0];
+
+    // rows of batch b (rows past the end are computed, not stored)
+    auto load_batch = [&](RawRow<XT, L> (&r)[NX][kTokBatch], int b) {
 #pragma unroll
-    for (int e = 0; e < kMaxExperts; ++e) l[e] = (e < n_experts) ? lg[tl][e] : 0.f;
-    if (logits_out != nullptr) {
-      for (int e = 0; e < n_experts; ++e) logits_out[size_t(t) * n_experts + e] = l[e];
-    }
-    uint32_t chosen = 0;
-    int sel[kMaxTopK];
-    float sl[kMaxTopK];
+      for (int m = 0; m < kTokBatch; ++m) {
+        const int64_t t = min(t0 + b * kTokBatch + m, n_tokens - 1);
+        load_raw<XT, L>(x + size_t(t) * D + lane * L, r[0][m]);
+        if constexpr (MODE == 2)
+          load_raw<XT, L>(static_cast<const XT*>(na.x_add) + size_t(t) * D + lane * L,
+                          r[NX - 1][m]);
+      }
+    };
+    auto compute_batch = [&](const RawRow<XT, L> (&r)[NX][kTokBatch], int b) {
+      const int64_t tb = t0 + b * kTokBatch;
+      float p[kTokBatch * kHalfExperts];
+      if constexpr (MODE == 0) {
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) {
-      if (s < top_k) {
-        int best = -1;
-        float bv = 0.f;
+        for (int m = 0; m < kTokBatch; ++m) {
+          float xv[L];
+          to_floats<XT, L>(r[0][m], xv);
 #pragma unroll
-        for (int e = 0; e < kMaxExperts; ++e) {
-          if (e < n_experts && !((chosen >> e) & 1u)) {
-            if (best < 0 || l[e] > bv) {
-              best = e;
-              bv = l[e];
-            }
+          for (int e = 0; e < kHalfExperts; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[i], w[e][i], acc);
+            p[m * kHalfExperts + e] = acc;
           }
         }
-        chosen |= 1u << best;
-        sel[s] = best;
-        sl[s] = bv;
-      }
-    }
-    float ex[kMaxTopK];
-    float sum = 0.f;
+      } else {
+        float xv[kTokBatch][L], ss[kTokBatch];
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) {
-      if (s < top_k) {
-        ex[s] = expf(sl[s] - sl[0]);
-        sum = sum + ex[s];
-      }
-    }
+        for (int m = 0; m < kTokBatch; ++m) {
+          to_floats<XT, L>(r[0][m], xv[m]);
+          if constexpr (MODE == 2) {
+            float xa[L];
+            to_floats<XT, L>(r[NX - 1][m], xa);
 #pragma unroll
-    for (int s = 0; s < kMaxTopK; ++s) {
-      if (s < top_k) {
-        topk_idx[size_t(t) * top_k + s] = sel[s];
-        topk_w[size_t(t) * top_k + s] = ex[s] / sum;
+            for (int i = 0; i < L; ++i) xv[m][i] = xv[m][i] + xa[i];
+#pragma unroll
+            for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
+          }
+          float acc = 0.f;
+#pragma unroll
+          for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], xv[m][i], acc);
+          ss[m] = acc;
+        }
+#pragma unroll
+        for (int bit = 32; bit >= 1; bit >>= 1)
+#pragma unroll
+          for (int m = 0; m < kTokBatch; ++m) ss[m] = ss[m] + __shfl_xor(ss[m], bit, 64);
+#pragma unroll
+        for (int m = 0; m < kTokBatch; ++m) {
+          const float rstd = 1.0f / __builtin_sqrtf(ss[m] / float(D) + na.eps);
+          const bool store = half == 0 && tb + m < n_tokens;
+          if constexpr (MODE == 2) {
+            if (store && na.sum_out != nullptr)
+              store_row<XT, L>(static_cast<XT*>(na.sum_out) + size_t(tb + m) * D + lane * L,
+                               xv[m]);
+          }
+#pragma unroll
+          for (int i = 0; i < L; ++i) xv[m][i] = (xv[m][i] * rstd) * nw[i];
+#pragma unroll
+          for (int i = 0; i < L; i += 2) round_pair<XT>(xv[m][i], xv[m][i + 1]);
+          if (store)
+            store_row<XT, L>(static_cast<XT*>(na.normed_out) + size_t(tb + m) * D + lane * L,
+                             xv[m]);
+#pragma unroll
+          for (int e = 0; e < kHalfExperts; ++e) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < L; ++i) acc = __builtin_fmaf(xv[m][i], w[e][i], acc);
+            p[m * kHalfExperts + e] = acc;
+          }
+        }
+      }
+      rs_swap32(p);
+      rs_swap16(p);
+      rs_dpp<4, 8>(p, lane);
+      rs_dpp<2, 4>(p, lane);
+      rs_dpp<1, 2>(p, lane);
+      // the last level is a plain butterfly: lanes 2m and 2m + 1 both get the sum
+      // (quad_perm [1,0,3,2] hands every lane its xor-1 partner; a per-lane choice
+      // between two rotates would become a branch, and a DPP read from a lane
+      // the branch has masked off returns 0)
+      p[0] = p[0] + __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(p[0]), 0xB1,
+                                                                0xf, 0xf, false));
+      // lane holds value index v = 16*b5 + 8*b4 + 4*b3 + 2*b2 + b1 of its bits,
+      // i.e. token m = v >> 3, expert e0 + (v & 7).
+      const int v = lane >> 1;
+      const int m = v >> 3, e = e0 + (v & 7);
+      if ((lane & 1) == 0 && e < n_experts && tb + m < n_tokens) {
+        float val = p[0];
+        if (bias != nullptr) val = val + bias_e;
+        lgp[(b * kTokBatch + m) * (kMaxExperts + 1) + e] = val;
+      }
+    };
+    // The next batch's loads go out unconditionally (rows clamped to the last
+    // token, so a batch past the range is a harmless reload): a load under a
+    // branch makes the compiler's wait counts assume it may be missing, and the
+    // current batch's waits then also wait for the prefetch.
+    load_batch(ra, 0);
+    for (int b = 0; b < nb; b += 2) {
+      load_batch(rb, b + 1);
+      compute_batch(ra, b);
+      load_batch(ra, b + 2);
+      if (b + 1 < nb) compute_batch(rb, b + 1);
+    }
+    __syncthreads();
+
+    // Top-k scan and gates: one thread per token of the block's two ranges.
+    {
+      const int q = threadIdx.x >> 7, tl = threadIdx.x & 127;
+      const int64_t t = base + (int64_t(blockIdx.x) * 2 + q) * tpp + tl;
+      if (tl < tpp && t < n_tokens) {
+        const float* row = &lg[q * kMaxPairTokens + tl][0];
+        float l[kMaxExperts];
+#pragma unroll
+        for (int e = 0; e < kMaxExperts; ++e) l[e] = (e < n_experts) ? row[e] : 0.f;
+        if (logits_out != nullptr) {
+          for (int e = 0; e < n_experts; ++e) logits_out[size_t(t) * n_experts + e] = l[e];
+        }
+        uint32_t chosen = 0;
+        int sel[kMaxTopK];
+        float sl[kMaxTopK];
+#pragma unroll
+        for (int s = 0; s < kMaxTopK; ++s) {
+          if (s < top_k) {
+            int best = -1;
+            float bv = 0.f;
+#pragma unroll
+            for (int e = 0; e < kMaxExperts; ++e) {
+              if (e < n_experts && !((chosen >> e) & 1u)) {
+                if (best < 0 || l[e] > bv) {
+                  best = e;
+                  bv = l[e];
+                }
+              }
+            }
+            chosen |= 1u << best;
+            sel[s] = best;
+            sl[s] = bv;
+          }
+        }
+        float ex[kMaxTopK];
+        float sum = 0.f;
+#pragma unroll
+        for (int s = 0; s < kMaxTopK; ++s) {
+          if (s < top_k) {
+            ex[s] = expf(sl[s] - sl[0]);
+            sum = sum + ex[s];
+          }
+        }
+#pragma unroll
+        for (int s = 0; s < kMaxTopK; ++s) {
+          if (s < top_k) {
+            topk_idx[size_t(t) * top_k + s] = sel[s];
+            topk_w[size_t(t) * top_k + s] = ex[s] / sum;
+          }
+        }
       }
     }
+    __syncthreads();
   }
 }
 
@@ -404,12 +556,19 @@ hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* i
                         float* logits, const NormArgs& na, const g5moe_shape& s,
                         hipStream_t st) {
   const int64_t n = s.n_tokens;
-  const unsigned grid = unsigned((n + kTokensPerBlock - 1) / kTokensPerBlock);
+  // at most two resident blocks per CU (each wave holds its 8 experts' weights
+  // and two batches of rows in registers), at least one 4-token batch per pair
+  const int64_t max_grid = 2 * int64_t(device_cu_count());
+  const int64_t grid = std::max<int64_t>(
+      1, std::min<int64_t>(max_grid, (n + 2 * kTokBatch - 1) / (2 * kTokBatch)));
+  int64_t tpp = (n + 2 * grid - 1) / (2 * grid);
+  tpp = std::min<int64_t>(kMaxPairTokens, (tpp + kTokBatch - 1) / kTokBatch * kTokBatch);
   const int L = s.d_model / 64;
 #define G5_ROUTER_CASE(LL)                                                                  \
   case LL:                                                                                  \
-    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE>), dim3(grid), dim3(kRouterThreads), \
-                       0, st, x, wr, bias, n, s.n_experts, s.top_k, idx, w, logits, na);    \
+    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE>), dim3(unsigned(grid)),             \
+                       dim3(kRouterThreads), 0, st, x, wr, bias, n, s.n_experts, s.top_k,    \
+                       idx, w, logits, na, int(tpp));                                        \
     break;
   switch (L) {
     G5_ROUTER_CASE(2)
