@@ -35,8 +35,10 @@ def parse():
     ap.add_argument("--config", type=int, default=2, choices=(2, 3, 4, 5))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--train", action="store_true",
-                    help="time the training step instead: the forward that keeps the backward's "
-                         "inputs, then every backward stage (HIP events between stages)")
+                    help="time the training step instead: MoEFeedForward's forward and its "
+                         "autograd backward, with a per-stage breakdown")
+    ap.add_argument("--dropout", type=float, default=0.1,
+                    help="--train: dropout on the expert hidden state (GeneT5 trains with 0.1)")
     ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
     ap.add_argument("--shard", choices=("dp8", "ep8"), default=None,
                     help="one GPU's share of config 2 sharded over 8 GPUs: dp8 = 4,550 tokens "
@@ -256,11 +258,13 @@ def bench_config5(args) -> dict:
     }
 
 
-def bench_train(args) -> dict:
-    """Training step of the layer at config 2: forward (router with logits, dispatch,
-    experts with the gate|up products kept, combine) + backward (gate/router gradients,
-    dh GEMM, SwiGLU backward, dX GEMM, input gradient, weight-gradient GEMMs), one HIP
-    event between consecutive stages on the stream they run on."""
+def train_stage_breakdown(args) -> dict:
+    """The module's training step as its stages, for the per-stage times: the forward
+    (router with logits, dispatch, experts keeping the gate|up products, combine) and
+    every backward stage (gate/router gradients, dh GEMM, SwiGLU backward, dX GEMM,
+    input gradient, weight-gradient operands and GEMMs) through the C ABI — the
+    kernels ops.moe_backward enqueues — with one HIP event between consecutive
+    stages on the stream they run on (no dropout)."""
     import ctypes
     import torch
     from genet5_amd import _lib, ops, synth
@@ -336,23 +340,87 @@ def bench_train(args) -> dict:
           for j, n in enumerate(names)}
     g = 2 * d * F * N * k  # one d x F product over the routed rows
     flops = {"dh_gemm": g, "dx_gemm": 2 * g, "wgrad_gemms": 3 * g}
+    return {"stage_ms": st, "stage_ms_per_step": ms,
+            "stage_tflops": {n: flops[n] / (st[n] * 1e-3) / 1e12 for n in flops}}
+
+
+def bench_train(args) -> dict:
+    """Training step of the layer at config 2 as GeneT5 runs it: y = module(x) then
+    y.backward(dy) through autograd, with MoEFeedForward(768, 3072, dropout) in train
+    mode (bf16 parameters, as GeneT5 holds the model) and x requiring grad.  Before
+    every step the module's cache of packed and transposed expert weights is
+    dropped, as an optimizer step changing the weights would, so they are rebuilt
+    each step (the optimizer's own kernels are not timed);
+    `accumulation_ms_per_step` is the same step with them cached (micro-steps of
+    gradient accumulation).  Dropout defaults to GeneT5's 0.1
+    (`dropout_zero_ms_per_step` without it).  The per-stage breakdown comes from the
+    same kernels enqueued stage by stage (train_stage_breakdown)."""
+    import torch
+    from genet5_amd import synth
+    from genet5_amd.moe import MoEFeedForward
+    dev = torch.device("cuda:0")
+    inp = synth.make_config(args.config, seed=0)
+    N, d = inp.x.shape
+    E, F = inp.w_gate.shape[0], inp.w_gate.shape[1]
+    k = inp.top_k
+    tt = synth.to_torch(inp, dev)
+    x = tt["x"]
+    m = MoEFeedForward(d, F, args.dropout, num_experts=E, top_k=k).to(dev).to(torch.bfloat16)
+    with torch.no_grad():
+        m.router.weight.copy_(tt["w_router"])
+        m.w_gate.copy_(tt["w_gate"])
+        m.w_up.copy_(tt["w_up"])
+        m.w_down.copy_(tt["w_down"])
+    m.train()
+    dy = (torch.randn(N, d, device=dev) * 0.01).to(torch.bfloat16)
+    xr = x.clone().requires_grad_(True)
+
+    def step(update=True):
+        if update:
+            # what an optimizer step does to the layer's caches (its own kernels are
+            # not the layer's): the packed and transposed weights are rebuilt
+            m._packed_key = None
+        m.zero_grad(set_to_none=True)
+        xr.grad = None
+        y = m(xr)
+        y.backward(dy)
+
+    def run(steps, warmup, update):
+        for _ in range(warmup):
+            step(update)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            step(update)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / steps
+
+    ms = run(args.steps, args.warmup, True)
+    ms_acc = run(args.steps, 2, False)
+    p_saved = m.dropout
+    m.dropout = 0.0
+    ms_p0 = run(args.steps, 2, True)
+    m.dropout = p_saved
+    bd = train_stage_breakdown(args)
+    g = 2 * d * F * N * k
     return {
         "metric": "MoE layer training step (forward + backward) tokens/s, 36.4k tok, 16e top-2",
         "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
-        "config": {"workload": synth.CONFIGS[args.config]["name"] + ", training step",
-                   "n_tokens": N, "d_model": d, "d_ff": F, "n_experts": E, "top_k": k},
-        "stage_ms": st,
-        "stage_tflops": {n: flops[n] / (st[n] * 1e-3) / 1e12 for n in flops},
+        "config": {"workload": synth.CONFIGS[args.config]["name"] + ", training step "
+                               "(MoEFeedForward forward + autograd backward)",
+                   "n_tokens": N, "d_model": d, "d_ff": F, "n_experts": E, "top_k": k,
+                   "dropout": args.dropout},
+        "accumulation_ms_per_step": ms_acc,
+        "dropout_zero_ms_per_step": ms_p0,
         "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
-        "note": "weight-gradient products: one g5moe_weight_grad launch over per-expert "
-                "token-major operands padded to 192-row groups (the padding's zero products "
-                "count in the time, not in the FLOP); the gate gradient writes dY in that "
-                "padded layout, which the dh product also reads (wgrad_operands is the "
-                "gathered-X padding alone); the expert offsets reach the host by a "
-                "non-blocking copy issued after the dispatch; every stage is this "
-                "library's HIP kernels",
+        "breakdown": bd,
+        "note": "every stage is this library's HIP kernels; the backward reads the expert "
+                "offsets from the forward's pinned host copy (no host synchronisation); "
+                "weight-gradient products in one g5moe_weight_grad launch over per-expert "
+                "operands padded to 192-row groups (their zero rows' products count in the "
+                "time, not in the FLOP)",
     }
 
 
@@ -501,7 +569,7 @@ def main():
             "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
         },
         "roofline": {
-            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,1,false> (gate|up + SwiGLU)",
+            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,1,false,false> (gate|up + SwiGLU)",
             "bound": "mfma",
             "achieved": gu_tflops,
             "peak": PEAK_BF16_TFLOPS,
