@@ -262,9 +262,10 @@ def train_stage_breakdown(args) -> dict:
     """The module's training step as its stages, for the per-stage times: the forward
     (router with logits, dispatch, experts keeping the gate|up products, combine) and
     every backward stage (gate/router gradients, dh GEMM, SwiGLU backward, dX GEMM,
-    input gradient, weight-gradient operands and GEMMs) through the C ABI — the
-    kernels ops.moe_backward enqueues — with one HIP event between consecutive
-    stages on the stream they run on (no dropout)."""
+    input gradient, weight-gradient operands, the expert weight gradients from the
+    forward's h, the router weight gradient) through the C ABI — the kernels
+    ops.moe_backward enqueues for the module — with one HIP event between
+    consecutive stages on the stream they run on (no dropout)."""
     import ctypes
     import torch
     from genet5_amd import _lib, ops, synth
@@ -283,7 +284,7 @@ def train_stage_breakdown(args) -> dict:
     P, S = ops._ptr, ops._stream(dev)
     stream = torch.cuda.current_stream(dev)
     names = ["fwd", "gate_router_grad", "dh_gemm", "swiglu_bwd", "dx_gemm", "input_grad",
-             "wgrad_operands", "wgrad_gemms"]
+             "wgrad_operands", "wgrad_gemms", "router_wgrad"]
 
     # the expert offsets reach the host by a non-blocking copy issued right after
     # the forward's dispatch, so reading them does not drain the queue
@@ -293,8 +294,8 @@ def train_stage_breakdown(args) -> dict:
     def step(ev=None):
         rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
         rec(0)
-        y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(
-            x, wr, wgu, wd, k, offsets_host=offs_host, offsets_ready=offs_ready)
+        y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu, h = ops.moe_forward_train(
+            x, wr, wgu, wd, k, offsets_host=offs_host, offsets_ready=offs_ready, return_h=True)
         rec(1)
         offs_ready.synchronize()
         offs = offs_host.tolist()
@@ -308,10 +309,9 @@ def train_stage_breakdown(args) -> dict:
         rec(2)
         dh = ops.grouped_gemm_padded(dy_buf, kmax, N * k, offsets, wd_t)
         rec(3)
-        h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
         dgu_buf = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
         dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
-        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(perm), P(offsets), None, P(h_pad),
+        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(perm), P(offsets), None, None,
                   P(dgu_buf), kmax, None, ctypes.byref(shape), S)
         rec(4)
         dxp = ops.grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, wgu_t)
@@ -323,8 +323,14 @@ def train_stage_breakdown(args) -> dict:
         dy_pad = dy_buf[:E * kmax].view(E, kmax, d)
         x_pad = ops.pad_rows(x, perm, offsets, E, kmax, k)
         rec(7)
-        ops.weight_grad(dy_pad, h_pad, dgu_pad, x_pad, offsets, kmax, top_k=k)
+        d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
+        d_wg = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
+        d_wu = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_weight_grad_sorted_h", P(dy_pad), P(h), P(d_wd), P(dgu_pad), P(x_pad),
+                  P(d_wg), P(d_wu), P(offsets), kmax, ctypes.byref(shape), S)
         rec(8)
+        ops.router_weight_grad(dl, x, shape)
+        rec(9)
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]

@@ -47,6 +47,9 @@ EXPORTED = (
     "g5moe_pad_transpose",
     "g5moe_pad_rows",
     "g5moe_weight_grad",
+    "g5moe_weight_grad_sorted_h",
+    "g5moe_router_weight_grad_scratch",
+    "g5moe_router_weight_grad",
     "g5moe_forward",
     "g5moe_attn_workspace_size",
     "g5moe_attn_varlen_fwd",
@@ -157,6 +160,10 @@ _SIGS = {
                        ctypes.c_int),
     "g5moe_weight_grad": ([_P, _P, _P, _P, _P, _P, _P, ctypes.c_int32, _SHAPE_P, _P],
                           ctypes.c_int),
+    "g5moe_weight_grad_sorted_h": ([_P] * 8 + [ctypes.c_int32, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_router_weight_grad_scratch": ([_SHAPE_P, ctypes.POINTER(ctypes.c_size_t)],
+                                         ctypes.c_int),
+    "g5moe_router_weight_grad": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_input_grad": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_forward": ([_P] * 13 + [_SHAPE_P, _P], ctypes.c_int),
     "g5moe_attn_workspace_size": ([ctypes.POINTER(AttnShape), ctypes.POINTER(ctypes.c_size_t)],

@@ -207,19 +207,25 @@ g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
   G5_CHECK(check_shape(shape));
   DropoutParams drop;
   G5_CHECK(dropout_params(dropout, &drop));
+  G5_NONNULL(ws);
+  char* w = static_cast<char*>(ws);
+  const hipStream_t st = as_stream(stream);
+  const WorkspaceLayout L = workspace_layout(*shape);
+  // the kWgradSlackRows rows after h's last row, which the weight gradient reads
+  // in sorted order (g5moe_weight_grad_sorted_h), are zeroed
+  const int64_t nk = shape->n_tokens * shape->top_k;
+  G5_CHECK(hip_status(launch_zero16(w + L.h + size_t(nk) * shape->d_ff * 2,
+                                    int64_t(kWgradSlackRows) * shape->d_ff * 2 / 16, st),
+                      "g5moe_expert_gate_up_train (h slack rows)"));
   if (shape->n_tokens == 0) return G5MOE_OK;
   G5_NONNULL(x);
   G5_NONNULL(perm);
   G5_NONNULL(offsets);
   G5_NONNULL(w_gate_up);
   G5_NONNULL(gu);
-  G5_NONNULL(ws);
-  char* w = static_cast<char*>(ws);
-  const hipStream_t st = as_stream(stream);
   hipError_t err;
   const uint16_t* xb = gemm_input(x, w, *shape, st, &err);
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train (cast)"));
-  const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
                                    reinterpret_cast<uint16_t*>(w + L.h),
                                    static_cast<uint16_t*>(gu), *shape, st, &drop),
@@ -472,7 +478,6 @@ g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t
   G5_NONNULL(dh);
   G5_NONNULL(gu);
   G5_NONNULL(offsets);
-  G5_NONNULL(h_pad);
   G5_NONNULL(dgu_pad);
   if (drop.on) G5_NONNULL(perm);
   return hip_status(launch_swiglu_bwd(static_cast<const uint16_t*>(dh),
@@ -524,11 +529,19 @@ g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t*
                     "g5moe_pad_rows");
 }
 
-g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_down,
-                               const void* dgu_pad, const void* x_pad, void* d_w_gate_up,
-                               const int32_t* offsets, int32_t kmax, const g5moe_shape* shape,
-                               void* stream) {
+namespace {
+// g5moe_weight_grad (h_sorted false, packed d_w_gate_up) and
+// g5moe_weight_grad_sorted_h (h in sorted order, d_w_gate / d_w_up split).
+g5moe_status weight_grad(const char* fn, const void* dy_pad, const void* h, bool h_sorted,
+                         void* d_w_down, const void* dgu_pad, const void* x_pad, void* d_wg,
+                         void* d_wu, const int32_t* offsets, int32_t kmax,
+                         const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));
+  void* d_w_gate_up = d_wg;
+  if (d_wu != nullptr && d_wg == nullptr)
+    return fail(G5MOE_ERR_INVALID_ARG, "%s: d_w_gate is NULL but d_w_up is not", fn);
+  if (d_wg != nullptr && h_sorted && d_wu == nullptr)
+    return fail(G5MOE_ERR_INVALID_ARG, "%s: d_w_up is NULL but d_w_gate is not", fn);
   if (shape->d_model % 256 != 0 || shape->d_ff % 256 != 0)
     return fail(G5MOE_ERR_UNSUPPORTED, "weight_grad: d_model %d and d_ff %d must be multiples "
                 "of 256", int(shape->d_model), int(shape->d_ff));
@@ -540,8 +553,8 @@ g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_
   uintptr_t align = 0;
   if (d_w_down != nullptr) {
     G5_NONNULL(dy_pad);
-    G5_NONNULL(h_pad);
-    align |= reinterpret_cast<uintptr_t>(dy_pad) | reinterpret_cast<uintptr_t>(h_pad) |
+    G5_NONNULL(h);
+    align |= reinterpret_cast<uintptr_t>(dy_pad) | reinterpret_cast<uintptr_t>(h) |
              reinterpret_cast<uintptr_t>(d_w_down);
   }
   if (d_w_gate_up != nullptr) {
@@ -552,16 +565,63 @@ g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_
   }
   if (align % 16 != 0)
     return fail(G5MOE_ERR_UNSUPPORTED, "weight_grad: buffers must be 16-byte aligned");
+  if (d_wu != nullptr && reinterpret_cast<uintptr_t>(d_wu) % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "%s: buffers must be 16-byte aligned", fn);
   const int d = shape->d_model, F = shape->d_ff;
   const bool down = d_w_down != nullptr;
   const bool gu = d_w_gate_up != nullptr;
   return hip_status(
       launch_wgrad(down ? static_cast<const uint16_t*>(dy_pad) : nullptr,
-                   static_cast<const uint16_t*>(h_pad), static_cast<uint16_t*>(d_w_down), d, F,
-                   gu ? static_cast<const uint16_t*>(dgu_pad) : nullptr,
+                   static_cast<const uint16_t*>(h), static_cast<uint16_t*>(d_w_down), d, F,
+                   h_sorted, gu ? static_cast<const uint16_t*>(dgu_pad) : nullptr,
                    static_cast<const uint16_t*>(x_pad), static_cast<uint16_t*>(d_w_gate_up),
-                   2 * F, d, offsets, shape->n_experts, kmax, as_stream(stream)),
-      "g5moe_weight_grad");
+                   static_cast<uint16_t*>(d_wu), 2 * F, d, offsets, shape->n_experts, kmax,
+                   as_stream(stream)),
+      fn);
+}
+}  // namespace
+
+g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_down,
+                               const void* dgu_pad, const void* x_pad, void* d_w_gate_up,
+                               const int32_t* offsets, int32_t kmax, const g5moe_shape* shape,
+                               void* stream) {
+  return weight_grad("g5moe_weight_grad", dy_pad, h_pad, false, d_w_down, dgu_pad, x_pad,
+                     d_w_gate_up, nullptr, offsets, kmax, shape, stream);
+}
+
+g5moe_status g5moe_weight_grad_sorted_h(const void* dy_pad, const void* h, void* d_w_down,
+                                        const void* dgu_pad, const void* x_pad, void* d_w_gate,
+                                        void* d_w_up, const int32_t* offsets, int32_t kmax,
+                                        const g5moe_shape* shape, void* stream) {
+  return weight_grad("g5moe_weight_grad_sorted_h", dy_pad, h, true, d_w_down, dgu_pad, x_pad,
+                     d_w_gate, d_w_up, offsets, kmax, shape, stream);
+}
+
+g5moe_status g5moe_router_weight_grad_scratch(const g5moe_shape* shape, size_t* bytes) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(bytes);
+  *bytes = size_t(router_wgrad_chunks(shape->n_tokens)) * shape->n_experts * shape->d_model * 4;
+  return G5MOE_OK;
+}
+
+g5moe_status g5moe_router_weight_grad(const float* dlogits, const void* x, float* scratch,
+                                      void* d_w_router, const g5moe_shape* shape,
+                                      void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->x_dtype != G5MOE_DTYPE_BF16)
+    return fail(G5MOE_ERR_UNSUPPORTED, "router_weight_grad: x must be bf16");
+  G5_NONNULL(d_w_router);
+  G5_NONNULL(scratch);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(dlogits);
+    G5_NONNULL(x);
+  }
+  if ((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(scratch) |
+       reinterpret_cast<uintptr_t>(d_w_router)) % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "router_weight_grad: buffers must be 16-byte aligned");
+  return hip_status(launch_router_wgrad(dlogits, x, scratch, d_w_router, *shape,
+                                        as_stream(stream)),
+                    "g5moe_router_weight_grad");
 }
 
 g5moe_status g5moe_input_grad(const void* dx_perm, const int32_t* inv_pos, const float* dlogits,

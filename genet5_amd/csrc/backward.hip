@@ -112,6 +112,130 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
   }
 }
 
+// Router weight gradient d_w_router = dlogits^T x (the nn.Linear weight
+// gradient of lib/blocks/_component.py's router projection, fp32).  Pass 1:
+// block g sums its chunk of tokens [g * chunk, (g + 1) * chunk) in token order,
+// thread i owning columns 4 i .. 4 i + 3 for every expert; partials[g][e][c].
+// The chunk's dlogits rows go through LDS in windows of kRwWin tokens (every
+// lane reads the same row: broadcast reads), and the x values of the next
+// kRwSub tokens are in flight while the current ones are used.  Pass 2 adds the
+// chunks in a fixed order (32 groups of consecutive chunks, then the groups), so
+// the result does not depend on scheduling.
+constexpr int kRouterWgradMinChunk = 64;   // tokens per chunk at least ...
+constexpr int kRouterWgradMaxChunks = 512; // ... and at most this many chunks
+constexpr int kRwWin = 64;                 // tokens per LDS window of dlogits rows
+constexpr int kRwSub = 16;                 // tokens per register batch of x
+__global__ __launch_bounds__(256) void router_wgrad_partial_kernel(
+    const float* __restrict__ dlogits, const uint16_t* __restrict__ x,
+    float* __restrict__ partials, int64_t n_tokens, int n_experts, int d, int64_t chunk) {
+  __shared__ __attribute__((aligned(16))) float dls[kRwWin * kMaxExperts];
+  const int tid = threadIdx.x, nthr = blockDim.x;
+  const int c0 = tid * 4;
+  const int64_t t0 = int64_t(blockIdx.x) * chunk;
+  const int64_t t1 = t0 + chunk < n_tokens ? t0 + chunk : n_tokens;
+  float acc[kMaxExperts][4];
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; ++e)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[e][j] = 0.f;
+  // x values of tokens base + i (clamped to the chunk's last token: unconditional
+  // loads, never used past the end)
+  auto load_x = [&](uint2 (&xv)[kRwSub], int64_t base) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < kRwSub; ++i) {
+      const int64_t t = base + i < t1 ? base + i : t1 - 1;
+      xv[i] = *reinterpret_cast<const uint2*>(x + t * d + c0);
+    }
+  };
+  for (int64_t w0 = t0; w0 < t1; w0 += kRwWin) {
+    const int nw = int(t1 - w0 < kRwWin ? t1 - w0 : kRwWin);
+    __syncthreads();  // the previous window's rows are read
+    for (int i = tid; i < nw * kMaxExperts; i += nthr) {
+      const int r = i / kMaxExperts, e = i % kMaxExperts;
+      dls[i] = e < n_experts ? dlogits[(w0 + r) * n_experts + e] : 0.f;
+    }
+    __syncthreads();
+    uint2 xa[kRwSub], xb[kRwSub];
+    load_x(xa, w0);
+    for (int sb = 0; sb < nw; sb += kRwSub) {
+      load_x(xb, w0 + sb + kRwSub);
+#pragma unroll
+      for (int i = 0; i < kRwSub; ++i) {
+        if (sb + i < nw) {
+          const float xf[4] = {bf_lo(xa[i].x), bf_hi(xa[i].x), bf_lo(xa[i].y), bf_hi(xa[i].y)};
+          const float4* dr = reinterpret_cast<const float4*>(dls + (sb + i) * kMaxExperts);
+#pragma unroll
+          for (int q = 0; q < kMaxExperts / 4; ++q) {
+            const float4 w4 = dr[q];
+            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
+            // experts past n_experts have zero weights and are never stored
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+              for (int j = 0; j < 4; ++j)
+                acc[4 * q + u][j] = __builtin_fmaf(wv[u], xf[j], acc[4 * q + u][j]);
+          }
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < kRwSub; ++i) xa[i] = xb[i];
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < kMaxExperts; ++e)
+    if (e < n_experts)
+      *reinterpret_cast<float4*>(partials + (int64_t(blockIdx.x) * n_experts + e) * d + c0) =
+          make_float4(acc[e][0], acc[e][1], acc[e][2], acc[e][3]);
+}
+
+// Block: 8 float4 outputs x 32 chunk groups; group p sums chunks
+// p * gper .. p * gper + gper - 1 (gper <= 16) in order, then lane group 0 adds
+// the 32 group sums in order and rounds to bf16 once.
+__global__ __launch_bounds__(256) void router_wgrad_reduce_kernel(
+    const float* __restrict__ partials, uint16_t* __restrict__ dwr, int n_chunks, int64_t q4) {
+  __shared__ float4 red[32][8];
+  const int o = threadIdx.x & 7, pg = threadIdx.x >> 3;
+  const int64_t q = int64_t(blockIdx.x) * 8 + o;
+  const int gper = (n_chunks + 31) / 32;
+  float4 v[16];
+  const float4* p4 = reinterpret_cast<const float4*>(partials);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int g = pg * gper + i;
+    v[i] = (i < gper && g < n_chunks && q < q4) ? p4[int64_t(g) * q4 + q]
+                                                 : make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  float4 sum = v[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    sum.x += v[i].x;
+    sum.y += v[i].y;
+    sum.z += v[i].z;
+    sum.w += v[i].w;
+  }
+  red[pg][o] = sum;
+  __syncthreads();
+  if (pg == 0 && q < q4) {
+    float4 t = red[0][o];
+#pragma unroll
+    for (int p = 1; p < 32; ++p) {
+      const float4 w = red[p][o];
+      t.x += w.x;
+      t.y += w.y;
+      t.z += w.z;
+      t.w += w.w;
+    }
+    *reinterpret_cast<uint2*>(dwr + q * 4) =
+        make_uint2(pack_bf16x2(t.x, t.y), pack_bf16x2(t.z, t.w));
+  }
+}
+
+__global__ __launch_bounds__(256) void zero16_kernel(uint4* __restrict__ p, int64_t n16) {
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < n16;
+       i += int64_t(gridDim.x) * 256)
+    p[i] = make_uint4(0, 0, 0, 0);
+}
+
 // One thread per token.
 __global__ __launch_bounds__(256) void router_grad_kernel(
     const float* __restrict__ dw, const float* __restrict__ topk_w,
@@ -163,7 +287,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
     const uint4 z = make_uint4(0, 0, 0, 0);
     store16_nt(dgu_pad + gpo, z);
     store16_nt(dgu_pad + gpo + 32, z);
-    store16_nt(h_pad + prow * F + f0, z);
+    if (h_pad != nullptr) store16_nt(h_pad + prow * F + f0, z);
     return;
   }
   const int64_t p = offsets[e] + jr;
@@ -218,7 +342,7 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   }
   store16_nt(dgu_pad + gpo, vog);
   store16_nt(dgu_pad + gpo + 32, vou);
-  store16_nt(h_pad + prow * F + f0, make_uint4(oh[0], oh[1], oh[2], oh[3]));
+  if (h_pad != nullptr) store16_nt(h_pad + prow * F + f0, make_uint4(oh[0], oh[1], oh[2], oh[3]));
 }
 
 // out[e][c][j] = src row (expert e's j-th sorted position) column c, zero for
@@ -533,6 +657,34 @@ hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const 
     by_topk(std::true_type{});
   else
     by_topk(std::false_type{});
+  return hipGetLastError();
+}
+
+int router_wgrad_chunks(int64_t n_tokens) {
+  const int64_t c = (n_tokens + kRouterWgradMinChunk - 1) / kRouterWgradMinChunk;
+  return int(c < 1 ? 1 : (c > kRouterWgradMaxChunks ? kRouterWgradMaxChunks : c));
+}
+
+hipError_t launch_router_wgrad(const float* dlogits, const void* x, float* partials,
+                               void* d_w_router, const g5moe_shape& s, hipStream_t st) {
+  const int E = s.n_experts, d = s.d_model;
+  if (d % 4 != 0 || d / 4 > 256 || E < 1 || E > kMaxExperts) return hipErrorInvalidValue;
+  const int G = router_wgrad_chunks(s.n_tokens);
+  const int64_t chunk = (s.n_tokens + G - 1) / G;
+  hipLaunchKernelGGL(router_wgrad_partial_kernel, dim3(unsigned(G)), dim3(unsigned(d / 4)), 0,
+                     st, dlogits, static_cast<const uint16_t*>(x), partials, s.n_tokens, E, d,
+                     chunk);
+  const int64_t q = int64_t(E) * d / 4;
+  hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3(unsigned((q + 7) / 8)), dim3(256), 0, st,
+                     partials, static_cast<uint16_t*>(d_w_router), G, q);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero16(void* p, int64_t n16, hipStream_t st) {
+  if (n16 <= 0) return hipSuccess;
+  const int64_t blocks = (n16 + 255) / 256;
+  hipLaunchKernelGGL(zero16_kernel, dim3(unsigned(blocks < 4096 ? blocks : 4096)), dim3(256), 0,
+                     st, static_cast<uint4*>(p), n16);
   return hipGetLastError();
 }
 

@@ -13,6 +13,10 @@ constexpr int kMaxExperts = 16;
 constexpr int kMaxTopK = 4;
 constexpr int kDispatchBlock = 256;  // assignments per dispatch block
 constexpr int kGemmRowPad = 256;     // rows of padding after h (one GEMM m-tile)
+// Rows the weight-gradient kernel may read past an expert's count: its per-expert
+// row count wgrad_rows(M) = max(384, 192 * ceil(M / 192)) exceeds M by at most 384.
+constexpr int kWgradSlackRows = 384;
+constexpr int kHPadRows = kWgradSlackRows > kGemmRowPad ? kWgradSlackRows : kGemmRowPad;
 constexpr int kMaxDevices = 64;      // devices the per-device host caches cover
 
 // Allocation-free dispatch (g5moe_dispatch_noalloc): its rank pass's buffers live
@@ -49,9 +53,11 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   w.rank = off;
   off += align256(size_t(nk) * 4);
   w.h = off;
-  // kGemmRowPad rows of padding: the down GEMM reads whole 256-row tiles of h
-  // without clamping (rows past the end are computed and never stored).
-  off += align256(size_t(nk + kGemmRowPad) * s.d_ff * 2);
+  // kHPadRows rows of padding: the down GEMM reads whole 256-row tiles of h
+  // without clamping (rows past the end are computed and never stored), and the
+  // weight gradient reads h in sorted order up to kWgradSlackRows rows past the
+  // last expert (the training gate|up zeroes those rows).
+  off += align256(size_t(nk + kHPadRows) * s.d_ff * 2);
   w.y_perm = off;
   off += align256(size_t(nk) * s.d_model * 2);
   w.total = off;
@@ -137,9 +143,22 @@ hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const 
 hipError_t launch_pad_rows(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
                            uint16_t* out, int n_experts, int C, int kmax, int topk,
                            hipStream_t st);
+// Problem 0: c0 = a0^T b0 per expert ([E * m0, n0]); b0_sorted: b0's rows of expert
+// e start at offsets[e] (sorted order, >= kWgradSlackRows finite rows after the last)
+// instead of e * kmax.  Problem 1: c1 = a1^T b1 ([E * m1, n1]), or, with c1_up, its
+// rows split as the packed gate|up order interleaves them (32-row groups: gate
+// rows into c1 [E, m1 / 2, n1], up rows into c1_up).
 hipError_t launch_wgrad(const uint16_t* a0, const uint16_t* b0, uint16_t* c0, int m0, int n0,
-                        const uint16_t* a1, const uint16_t* b1, uint16_t* c1, int m1, int n1,
-                        const int32_t* offsets, int n_experts, int kmax, hipStream_t st);
+                        bool b0_sorted, const uint16_t* a1, const uint16_t* b1, uint16_t* c1,
+                        uint16_t* c1_up, int m1, int n1, const int32_t* offsets, int n_experts,
+                        int kmax, hipStream_t st);
+// d_w_router [E, d] (x's dtype) = dlogits^T x in fp32: per-chunk partial sums
+// (partials: fp32 [router_wgrad_chunks(N), E, d]) reduced in chunk order.
+int router_wgrad_chunks(int64_t n_tokens);
+hipError_t launch_router_wgrad(const float* dlogits, const void* x, float* partials,
+                               void* d_w_router, const g5moe_shape& s, hipStream_t st);
+// Zero n16 16-byte chunks at p (a fill kernel: no memset node if a caller captures).
+hipError_t launch_zero16(void* p, int64_t n16, hipStream_t st);
 hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const float* dlogits,
                              const void* w_router, void* dx, const g5moe_shape& s,
                              hipStream_t st);
@@ -154,6 +173,13 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
                            float* lse, float* kmax_ws, const g5moe_attn_shape& s,
                            hipStream_t st);
+
+// Rows of expert e the weight-gradient kernel reduces over: a multiple of 192
+// (three 64-row k-steps), at least 384, at most kmax.
+__host__ __device__ __forceinline__ int wgrad_rows(int count, int kmax) {
+  const int r = 192 * ((count + 191) / 192);
+  return r < 384 ? (384 < kmax ? 384 : kmax) : (r < kmax ? r : kmax);
+}
 
 // CUs of the current device (the persistent kernels' grid size).
 int device_cu_count();

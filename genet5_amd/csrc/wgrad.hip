@@ -9,6 +9,10 @@
 // A_p[e][t][i] * B_p[e][t][j], with A_p [E, kmax, M_p] and B_p [E, kmax, N_p]
 // token-major in the per-expert padded layout (rows t >= M_e are zero) and
 // K_e = 64 * max(6, 3 * ceil(M_e / 192)) <= kmax: the zero rows add nothing.
+// B may instead be in sorted order (expert e's token t at row offsets[e] + t,
+// the forward's h): its rows t >= M_e are then other experts' finite rows, and
+// A's zero rows still cancel them (0 * finite = 0, so the sums are the padded
+// layout's bit for bit).
 //
 // The structure is the grouped GEMMs' (grouped_gemm.hip): a persistent grid of
 // one workgroup per CU, 256 x 256 tiles, 4 waves in a 2 x 2 grid with 128 x 128
@@ -40,9 +44,11 @@ using namespace gemm;
 
 struct WgradProblem {
   const uint16_t* A;  // [E, kmax, M] token-major, per-expert padded
-  const uint16_t* B;  // [E, kmax, N]
-  uint16_t* C;        // [E * M, N]
+  const uint16_t* B;  // [E, kmax, N], or (b_sorted) [rows + kWgradSlackRows, N] in sorted order
+  uint16_t* C;        // [E * M, N]; with C_up, the gate rows [E * M / 2, N]
+  uint16_t* C_up;     // nullptr, or the up rows [E * M / 2, N] of a packed gate|up C
   int M, N;           // multiples of 256
+  int b_sorted;       // B row of expert e's token t: offsets[e] + t instead of e * kmax + t
 };
 
 struct WgradArgs {
@@ -69,8 +75,7 @@ static_assert(kAI * 2 == 16, "a wave's DMA slots cover its 16 token rows of a st
 // k-steps of expert e: a multiple of 3 (the fragment slots rotate with the
 // k-step mod 3 and every tile starts at 0 mod 3), at least 6, at most kmax / 64.
 __device__ __forceinline__ int wgrad_ksteps(const Offsets& off, int e, int kmax) {
-  const int cnt = off(e + 1) - off(e);
-  return min(kmax / kBK, max(6, 3 * ((cnt + 3 * kBK - 1) / (3 * kBK))));
+  return wgrad_rows(off(e + 1) - off(e), kmax) / kBK;
 }
 
 struct WTile {
@@ -107,8 +112,11 @@ __device__ __forceinline__ void wgrad_decode(const WgradArgs& args, const Offset
   t.lda2 = pr.M * 2;
   t.ldb2 = pr.N * 2;
   const int64_t row = int64_t(e) * args.kmax + 16 * wave;
+  // a sorted B: the rows past the expert's count are the next experts' (or the
+  // buffer's zero slack rows), multiplied by A's zero padding rows
+  const int64_t brow = pr.b_sorted ? int64_t(off(e)) + 16 * wave : row;
   t.a = reinterpret_cast<const char*>(pr.A + row * pr.M + t.m0);
-  t.b = reinterpret_cast<const char*>(pr.B + row * pr.N + t.n0);
+  t.b = reinterpret_cast<const char*>(pr.B + brow * pr.N + t.n0);
 }
 
 __global__ __launch_bounds__(256) void wgrad_persist_kernel(WgradArgs args) {
@@ -342,11 +350,14 @@ __global__ __launch_bounds__(256) void wgrad_persist_kernel(WgradArgs args) {
 
     // Epilogue through the wave's LDS region: pass j stages C rows
     // 32 j .. 32 j + 31 of the wave (128 bf16 columns, 256 bytes per row, chunk
-    // c of row r at c ^ (r % 16)), then writes them with 16-byte stores.
+    // c of row r at c ^ (r % 16)), then writes them with 16-byte stores.  With
+    // C_up a pass's 32 rows are one packed gate or up group: they go to row
+    // 32 (r / 64) of C or C_up (r = the pass's first row of the expert).
     {
       const WgradProblem& pr = args.prob[cur.p];
       const int col0 = cur.n0 + wn * 128;
       const int64_t row0 = int64_t(cur.e) * pr.M + cur.m0 + wm * 128;
+      const bool split = pr.C_up != nullptr;
 #pragma unroll
       for (int j = 0; j < kMB; ++j) {
         const int swz = tok_l % 16;
@@ -362,12 +373,17 @@ __global__ __launch_bounds__(256) void wgrad_persist_kernel(WgradArgs args) {
             __builtin_amdgcn_sched_barrier(0);
           }
         }
+        const int r0 = cur.m0 + wm * 128 + j * 32;  // multiple of 32
+        uint16_t* const dst =
+            split ? (((r0 >> 5) & 1) ? pr.C_up : pr.C) +
+                        (int64_t(cur.e) * (pr.M / 2) + (r0 >> 6) * 32) * pr.N
+                  : pr.C + (row0 + j * 32) * pr.N;
 #pragma unroll
         for (int it = 0; it < 8; ++it) {
           const int row = it * 4 + lane / 16;
           const int c = lane % 16;
           const uint4 v = *reinterpret_cast<const uint4*>(epi + row * 256 + ((c ^ (row % 16)) * 16));
-          store16_nt(pr.C + (row0 + j * 32 + row) * pr.N + col0 + c * 8, v);
+          store16_nt(dst + int64_t(row) * pr.N + col0 + c * 8, v);
         }
       }
     }
@@ -390,8 +406,9 @@ __global__ __launch_bounds__(256) void wgrad_persist_kernel(WgradArgs args) {
 }  // namespace
 
 hipError_t launch_wgrad(const uint16_t* a0, const uint16_t* b0, uint16_t* c0, int m0, int n0,
-                        const uint16_t* a1, const uint16_t* b1, uint16_t* c1, int m1, int n1,
-                        const int32_t* offsets, int n_experts, int kmax, hipStream_t st) {
+                        bool b0_sorted, const uint16_t* a1, const uint16_t* b1, uint16_t* c1,
+                        uint16_t* c1_up, int m1, int n1, const int32_t* offsets, int n_experts,
+                        int kmax, hipStream_t st) {
   if (n_experts < 1 || n_experts > kMaxExperts || kmax < 6 * kBK || kmax % (3 * kBK) != 0)
     return hipErrorInvalidValue;
   WgradArgs a{};
@@ -401,13 +418,15 @@ hipError_t launch_wgrad(const uint16_t* a0, const uint16_t* b0, uint16_t* c0, in
   const uint16_t* A[2] = {a0, a1};
   const uint16_t* B[2] = {b0, b1};
   uint16_t* C[2] = {c0, c1};
+  uint16_t* Cu[2] = {nullptr, c1_up};
   const int M[2] = {m0, m1}, N[2] = {n0, n1};
+  const int sorted[2] = {b0_sorted ? 1 : 0, 0};
   int64_t tiles = 0;
   for (int p = 0; p < 2; ++p) {
     if (A[p] == nullptr) continue;
     if (M[p] <= 0 || N[p] <= 0 || M[p] % kTile != 0 || N[p] % kTile != 0)
       return hipErrorInvalidValue;
-    a.prob[a.n_problems] = WgradProblem{A[p], B[p], C[p], M[p], N[p]};
+    a.prob[a.n_problems] = WgradProblem{A[p], B[p], C[p], Cu[p], M[p], N[p], sorted[p]};
     ++a.n_problems;
     tiles += int64_t(n_experts) * (M[p] / kTile) * (N[p] / kTile);
   }

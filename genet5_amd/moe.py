@@ -100,16 +100,19 @@ def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optiona
                           w_down_t: torch.Tensor, top_k: int, dropout_p: float, seed: int
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                      torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                                     torch.Tensor]:
+                                     torch.Tensor, torch.Tensor]:
     """Training forward.  w_gate / w_up / w_down are the differentiable parameters
     (bf16); the kernels read w_gate_up (their packed copy) and w_down, and the
-    backward the transposed copies w_gate_up_t [E, d, 2F] and w_down_t [E, F, d]."""
+    backward the transposed copies w_gate_up_t [E, d, 2F] and w_down_t [E, F, d].
+    The last output is the forward's h [N*k + 384, F] (zero rows past N*k), which
+    the backward's down-weight gradient reads."""
     E = w_router.shape[0]
     host = torch.empty((E + 1,), dtype=torch.int32, pin_memory=True)
     ready = torch.cuda.Event()
     outs = ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias,
                                  offsets_host=host, offsets_ready=ready,
-                                 dropout=(dropout_p, seed) if dropout_p > 0 else None)
+                                 dropout=(dropout_p, seed) if dropout_p > 0 else None,
+                                 return_h=True)
     _HOST_OFFSETS[outs[4].data_ptr()] = (host, ready)
     while len(_HOST_OFFSETS) > _HOST_OFFSETS_MAX:
         _HOST_OFFSETS.popitem(last=False)
@@ -127,13 +130,15 @@ def _(x, w_router, bias, w_gate, w_up, w_down, w_gate_up, w_gate_up_t, w_down_t,
             torch.empty((N, top_k), **f32), torch.empty((E + 1,), **i32),
             torch.empty((N * top_k,), **i32), torch.empty((N * top_k,), **i32),
             torch.empty((N * top_k, d), dtype=torch.bfloat16, device=x.device),
-            torch.empty((N * top_k, w_gate_up.shape[1]), dtype=torch.bfloat16, device=x.device))
+            torch.empty((N * top_k, w_gate_up.shape[1]), dtype=torch.bfloat16, device=x.device),
+            torch.empty((N * top_k + ops.H_SLACK, w_gate_up.shape[1] // 2), dtype=torch.bfloat16,
+                        device=x.device))
 
 
 def _train_setup(ctx, inputs, output):
     (x, w_router, bias, w_gate, w_up, w_down, w_gate_up, w_gate_up_t, w_down_t, top_k,
      dropout_p, seed) = inputs
-    _, _, idx, w, offsets, perm, inv_pos, y_perm, gu = output
+    _, _, idx, w, offsets, perm, inv_pos, y_perm, gu, h = output
     ctx.top_k = top_k
     ctx.dropout = (dropout_p, seed) if dropout_p > 0 else None
     # gradients of the outputs nobody differentiates (gu alone is 894 MB at 36,400
@@ -144,28 +149,28 @@ def _train_setup(ctx, inputs, output):
     except Exception:  # traced (fake) tensors have no storage: read on the device later
         ctx.host_offsets = None
     # gu: the forward's raw gate|up products, kept so the backward does not
-    # recompute them (894 MB at 36,400 tokens: HBM for time)
+    # recompute them (894 MB at 36,400 tokens: HBM for time); h: the forward's
+    # SwiGLU outputs, the down-weight gradient's operand (447 MB)
     ctx.save_for_backward(x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w,
-                          offsets, perm, inv_pos, y_perm, gu)
-    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu)
+                          offsets, perm, inv_pos, y_perm, gu, h)
+    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu, h)
 
 
 def _train_backward(ctx, dy, dlogits, *unused):
     (x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w, offsets, perm, inv_pos,
-     y_perm, gu) = ctx.saved_tensors
+     y_perm, gu, h) = ctx.saved_tensors
     if dy is None:
         dy = torch.zeros_like(x)
     offsets_host = None
     if ctx.host_offsets is not None:
         offsets_host, ready = ctx.host_offsets
         ready.synchronize()  # the copy issued right after the forward's dispatch
-    dx, d_wr, d_wgu, d_wd = ops.moe_backward(
+    dx, d_wr, d_wg, d_wu, d_wd = ops.moe_backward(
         dy.to(torch.bfloat16).contiguous(), x, w_router, w_gate_up, w_down, ctx.top_k, idx, w,
         offsets, perm, inv_pos, y_perm,
         grad_logits=None if dlogits is None else dlogits.float().contiguous(),
         w_down_t=w_down_t, w_gate_up_t=w_gate_up_t, gu=gu, offsets_host=offsets_host,
-        dropout=ctx.dropout)
-    d_wg, d_wu = ops.unpack_gate_up(d_wgu)
+        dropout=ctx.dropout, h=h, split_gate_up=True)
     return dx, d_wr, None, d_wg, d_wu, d_wd, None, None, None, None, None, None
 
 
@@ -307,7 +312,7 @@ class MoEFeedForward(nn.Module):
         p = self.dropout if self.training else 0.0
         seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if p > 0.0 else 0
         wgu, wd, wgu_t, wd_t = self._expert_weights(transposed=True)
-        y, logits, idx, _, offsets, _, _, _, _ = _moe_forward_train_op(
+        y, logits, idx, _, offsets, _, _, _, _, _ = _moe_forward_train_op(
             x2, w_router, self.router_bias, self.w_gate.to(torch.bfloat16),
             self.w_up.to(torch.bfloat16), self.w_down.to(torch.bfloat16), wgu, wgu_t, wd_t,
             self.top_k, p, seed)

@@ -309,6 +309,7 @@ def moe_forward(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tens
 # ---- training: forward that keeps what the backward needs, and the backward -----------
 
 ROW_PAD = 256  # padding rows of buffers read as the A operand of the grouped GEMM
+H_SLACK = 384  # rows after the workspace's h that the training gate|up zeroes
 
 
 def _dropout_arg(dropout: Optional[Tuple[float, int]]):
@@ -325,12 +326,13 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
                       w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None,
                       offsets_host: Optional[torch.Tensor] = None,
                       offsets_ready: Optional["torch.cuda.Event"] = None,
-                      dropout: Optional[Tuple[float, int]] = None):
+                      dropout: Optional[Tuple[float, int]] = None, return_h: bool = False):
     """The layer forward as stage calls, returning what the backward needs:
     (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm, gu) with
     gu the raw gate|up products bf16 [N*k, 2F] (packed column order), which the
     gate|up GEMM stores beside h (g5moe_expert_gate_up_train) so that the backward
-    does not recompute them.
+    does not recompute them.  return_h: h (bf16 [N*k + H_SLACK, F], a view of the
+    workspace, the rows past N*k zero) is appended, for moe_backward(h=...).
 
     offsets_host (pinned int32 [E + 1] on the host): the expert offsets are copied
     there without blocking as soon as the dispatch has written them, and
@@ -364,9 +366,12 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
               _ptr(w_gate_up), _ptr(gu), _ptr(ws), _dropout_arg(dropout), ctypes.byref(shape), S)
     _lib.call("g5moe_expert_down", _ptr(offsets), _ptr(w_down), _ptr(y_perm), _ptr(ws),
               ctypes.byref(shape), S)
-    del ws
     y = combine(y_perm, inv_pos, w, x2d.dtype)
-    return y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu
+    if not return_h:
+        return y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu
+    off = _h_offset(shape)
+    h = ws[off: off + (N * top_k + H_SLACK) * F * 2].view(torch.bfloat16).view(-1, F)
+    return y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu, h
 
 
 def transpose_experts(w: torch.Tensor) -> torch.Tensor:
@@ -415,8 +420,15 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
                  grad_logits: Optional[torch.Tensor] = None, w_down_t: Optional[torch.Tensor] = None,
                  w_gate_up_t: Optional[torch.Tensor] = None, gu: Optional[torch.Tensor] = None,
                  offsets_host: Optional[torch.Tensor] = None,
-                 dropout: Optional[Tuple[float, int]] = None):
-    """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer.
+                 dropout: Optional[Tuple[float, int]] = None, h: Optional[torch.Tensor] = None,
+                 split_gate_up: bool = False):
+    """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer,
+    or with split_gate_up (dx, d_w_router, d_w_gate, d_w_up, d_w_down).
+
+    h: the forward's h (moe_forward_train(..., return_h=True)); the down weight
+    gradient then reads it in sorted order (g5moe_weight_grad_sorted_h) instead of
+    the SwiGLU backward writing a padded copy, and the gate and up gradients come
+    out of the weight-gradient kernel unpacked.
 
     offsets_host: a completed host copy of offsets (moe_forward_train's, after its
     offsets_ready event); without it the offsets are read from the device here,
@@ -432,9 +444,9 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     dx (g5moe_input_grad), the gathered X rows padded (g5moe_pad_rows) and the
     weight gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e in one launch
     (g5moe_weight_grad).  kmax is read from the offsets once on the host.
-    dWr = dlogits^T x is a plain GEMM.  For d or F not a multiple of 256 the
-    weight gradients are batched torch products over transposed padded
-    operands instead."""
+    and dWr = dlogits^T x (g5moe_router_weight_grad).  For d or F not a multiple
+    of 256 the expert weight gradients are batched torch products over transposed
+    padded operands instead."""
     dev = _check_device(x2d)
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
@@ -486,7 +498,12 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
         dh = grouped_gemm_padded(dy_buf, kmax, N * k, offsets, w_down_t)   # [N*k, F]
     else:
         dh = grouped_gemm(dyp, N * k, offsets, w_down_t)
-    h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
+    sorted_h = h is not None and hip_wgrad
+    if sorted_h:
+        _require(h, "h", (N * k + H_SLACK, F), torch.bfloat16, dev)
+        h_pad = None
+    else:
+        h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
     # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
     dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
     dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
@@ -501,13 +518,25 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     _lib.call("g5moe_input_grad", _ptr(dxp), _ptr(inv_pos), _ptr(dlogits), _ptr(w_router),
               _ptr(dx), ctypes.byref(shape), S)
     del dxp
+    d_wr = router_weight_grad(dlogits, x2d, shape)
     if hip_wgrad:
         # weight gradients on the HIP kernel over token-major padded operands
         dy_pad = dy_buf[:E * kmax].view(E, kmax, d)
         x_pad = pad_rows(x2d, perm, offsets, E, kmax, k)
+        if sorted_h:
+            d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
+            d_wg = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
+            d_wu = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
+            _lib.call("g5moe_weight_grad_sorted_h", _ptr(dy_pad), _ptr(h), _ptr(d_wd),
+                      _ptr(dgu_pad), _ptr(x_pad), _ptr(d_wg), _ptr(d_wu), _ptr(offsets), kmax,
+                      ctypes.byref(shape), S)
+            if split_gate_up:
+                return dx, d_wr, d_wg, d_wu, d_wd
+            return dx, d_wr, pack_gate_up(d_wg, d_wu), d_wd
         d_wd, d_wgu = weight_grad(dy_pad, h_pad, dgu_pad, x_pad, offsets, kmax, top_k=k)
         del dy_pad, dy_buf, x_pad, h_pad, dgu_buf
-        d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
+        if split_gate_up:
+            return (dx, d_wr) + unpack_gate_up(d_wgu) + (d_wd,)
         return dx, d_wr, d_wgu, d_wd
     # other shapes: batched products over the per-expert padded operands (zero
     # rows past each expert's own): dWd_e = dY_e^T h_e, dWgu_e^T = X_e^T dGU_e
@@ -521,8 +550,25 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     d_wd = torch.bmm(dyT, h_pad)                       # [E, d, F]
     del dyT, h_pad
     d_wgu = transpose_experts(torch.bmm(xT, dgu_pad))  # [E, d, 2F] -> [E, 2F, d]
-    d_wr = (dlogits.t() @ x2d.float()).to(w_router.dtype)
+    if split_gate_up:
+        return (dx, d_wr) + unpack_gate_up(d_wgu) + (d_wd,)
     return dx, d_wr, d_wgu, d_wd
+
+
+def router_weight_grad(dlogits: torch.Tensor, x2d: torch.Tensor,
+                       shape: "_lib.Shape") -> torch.Tensor:
+    """d_w_router = dlogits^T x (fp32 accumulation, bf16 [E, d]) on the HIP kernel."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E = shape.n_experts
+    _require(dlogits, "dlogits", (N, E), torch.float32, dev)
+    n = ctypes.c_size_t(0)
+    _lib.call("g5moe_router_weight_grad_scratch", ctypes.byref(shape), ctypes.byref(n))
+    scratch = torch.empty((n.value // 4,), dtype=torch.float32, device=dev)
+    out = torch.empty((E, d), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_router_weight_grad", _ptr(dlogits), _ptr(x2d), _ptr(scratch), _ptr(out),
+              ctypes.byref(shape), _stream(dev))
+    return out
 
 
 def wgrad_kmax(m_max: int) -> int:

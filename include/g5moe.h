@@ -71,7 +71,11 @@ const char* g5moe_last_error(void);
 /* ABI version: (major << 16) | minor. */
 int32_t g5moe_version(void);
 
-/* Bytes of workspace the stage entry points and g5moe_forward need for `shape`. */
+/* Bytes of workspace the stage entry points and g5moe_forward need for `shape`.
+ * Layout (regions in this order, each starting 256-byte aligned): the bf16 copy
+ * of x when x_dtype is F32 [N, d] (else empty); dispatch block counts
+ * int32 [ceil(N*k / 256), E]; in-block ranks int32 [N*k]; h bf16 [N*k + 384, F]
+ * (rows past N*k are padding); y_perm bf16 [N*k, d]. */
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes);
 
 /* Repack the two expert input projections into the interleaved gate|up layout
@@ -169,7 +173,9 @@ typedef struct g5moe_dropout {
  * the SwiGLU backward, so the backward need not recompute them.  Replaces
  * keeping `self.wi_0(x)` / `self.wi_1(x)` for autograd
  * (lib/blocks/_component.py:50).  dropout (NULL = none): h in the workspace is
- * h' of g5moe_dropout (the down GEMM's input); gu stays the raw products. */
+ * h' of g5moe_dropout (the down GEMM's input); gu stays the raw products.  The
+ * 384 rows after h's last row are zeroed, so that h can be the sorted-order
+ * operand of g5moe_weight_grad_sorted_h. */
 g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
                                         const int32_t* offsets, const void* w_gate_up,
                                         void* gu, void* ws, const g5moe_dropout* dropout,
@@ -247,8 +253,9 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
  * FeedForward through autograd (lib/blocks/_component.py:48-52; loss.backward()
  * at train/diffusion_finet:761); the MoE and its backward are new.  The
  * weight-gradient products (dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e) run in one
- * launch of g5moe_weight_grad over per-expert padded token-major operands when d
- * and F are multiples of 256 (every GeneT5 shape); for other shapes they are
+ * launch of g5moe_weight_grad (or g5moe_weight_grad_sorted_h, which reads the
+ * forward's h) over per-expert padded token-major operands when d and F are
+ * multiples of 256 (every GeneT5 shape); for other shapes they are
  * batched GEMMs the caller issues (the Python host uses hipBLASLt through
  * torch.bmm) over the transposed operands g5moe_pad_transpose writes.
  * Everything else is here.
@@ -327,7 +334,8 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
  * [E, kmax, 2F] out — rows placed per expert, row e*kmax + j = sorted position
  * offsets[e] + j, zero rows for j >= M_e (kmax >= every M_e): the weight
  * gradients' batched operands and g5moe_grouped_gemm_padded's A operand (give
- * dgu_pad 256 rows of padding after row E*kmax for that);  dgu : bf16
+ * dgu_pad 256 rows of padding after row E*kmax for that); h_pad may be NULL
+ * (not written: g5moe_weight_grad_sorted_h reads the forward's h);  dgu : bf16
  * [N*k + 256, 2F] packed out in sorted order, or NULL (not written).
  * dropout (NULL = none; the forward's descriptor): dh is the gradient of h',
  * so dg and du use dh * keep * scale, and h_pad holds h' (the down product's
@@ -373,6 +381,34 @@ g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_
                                const void* dgu_pad, const void* x_pad, void* d_w_gate_up,
                                const int32_t* offsets, int32_t kmax, const g5moe_shape* shape,
                                void* stream);
+
+/* g5moe_weight_grad with h in sorted order and the gate|up gradient unpacked:
+ *   d_w_down[e] = dy_pad[e]^T h[offsets[e] .. ]      : bf16 [E, d, F]
+ *   d_w_gate[e], d_w_up[e] = the gate and up rows of dgu_pad[e]^T x_pad[e]
+ *                                                     : bf16 [E, F, d] each
+ * h : bf16 [N*k + 384, F], the forward's h (g5moe_expert_gate_up_train's, in the
+ * workspace), with its 384 rows past N*k zero: expert e reduces over
+ * max(384, 192 * ceil(M_e / 192)) rows from offsets[e], and rows past M_e (the
+ * next experts' h, or the zero rows) meet dy_pad's zero rows, so the result is
+ * g5moe_weight_grad's on the padded h bit for bit while every h value is finite
+ * (a non-finite h in the first rows of expert e + 1 also makes expert e's
+ * d_w_down non-finite).  The outputs are the parameters' own layouts (no unpack
+ * pass).  Other arguments and rules as g5moe_weight_grad; d_w_gate and d_w_up
+ * are both given or both NULL. */
+g5moe_status g5moe_weight_grad_sorted_h(const void* dy_pad, const void* h, void* d_w_down,
+                                        const void* dgu_pad, const void* x_pad, void* d_w_gate,
+                                        void* d_w_up, const int32_t* offsets, int32_t kmax,
+                                        const g5moe_shape* shape, void* stream);
+
+/* Router weight gradient, the product autograd forms for the router
+ * nn.Linear's weight: d_w_router[e, c] = sum over tokens t of dlogits[t, e] *
+ * x[t, c], fp32, one rounding to bf16 [E, d].  x : bf16 [N, d];  scratch : fp32
+ * scratch of g5moe_router_weight_grad_scratch() bytes (per-chunk partial sums,
+ * added in a fixed chunk order: deterministic). */
+g5moe_status g5moe_router_weight_grad_scratch(const g5moe_shape* shape, size_t* bytes);
+g5moe_status g5moe_router_weight_grad(const float* dlogits, const void* x, float* scratch,
+                                      void* d_w_router, const g5moe_shape* shape,
+                                      void* stream);
 
 /* Input gradient: dx[t] = sum over s of dx_perm[inv_pos[t, s]] (slot order)
  * + sum over e of dlogits[t, e] * w_router[e] (expert order), fp32, one

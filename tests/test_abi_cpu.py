@@ -50,8 +50,10 @@ def test_workspace_size_layout(g5lib):
     nk = 36400 * 2
     a = lambda v: (v + 255) // 256 * 256
     nblk = (nk + 255) // 256
-    # h carries one 256-row GEMM tile of padding after its last row
-    assert n == a(0) + a(nblk * 16 * 4) + a(nk * 4) + a((nk + 256) * 3072 * 2) + a(nk * 768 * 2)
+    # h carries 384 rows after its last row: one 256-row GEMM tile of padding, and
+    # the weight gradient's sorted-order slack (ops.H_SLACK)
+    assert ops.H_SLACK == 384
+    assert n == a(0) + a(nblk * 16 * 4) + a(nk * 4) + a((nk + 384) * 3072 * 2) + a(nk * 768 * 2)
     n32 = _lib.workspace_size(shape(x_dtype=1))
     assert n32 == n + a(36400 * 768 * 2)
     assert ops._h_offset(s) == a(0) + a(nblk * 16 * 4) + a(nk * 4)
@@ -236,3 +238,45 @@ def test_wgrad_kmax_rule():
     assert ops.wgrad_kmax(1) == 384 and ops.wgrad_kmax(384) == 384
     assert ops.wgrad_kmax(385) == 576 and ops.wgrad_kmax(5071) == 5184
     assert all(ops.wgrad_kmax(m) % 192 == 0 and ops.wgrad_kmax(m) >= m for m in range(0, 9000, 37))
+
+
+def test_weight_grad_sorted_h_argument_checks(g5lib):
+    s = _wg_shape()
+    p = ctypes.c_void_p(0x1000)
+    fn = g5lib.g5moe_weight_grad_sorted_h
+    # gate without up (and the reverse)
+    assert fn(None, None, None, p, p, p, None, p, 384, ctypes.byref(s), None) == 1
+    assert "d_w_up is NULL" in g5lib.g5moe_last_error().decode()
+    assert fn(None, None, None, p, p, None, p, p, 384, ctypes.byref(s), None) == 1
+    assert "d_w_gate is NULL" in g5lib.g5moe_last_error().decode()
+    # the down product without h
+    assert fn(p, None, p, None, None, None, None, p, 384, ctypes.byref(s), None) == 1
+    assert "h is NULL" in g5lib.g5moe_last_error().decode()
+    assert fn(p, p, p, None, None, None, None, p, 200, ctypes.byref(s), None) == 1
+    assert fn(p, p, p, None, None, None, ctypes.c_void_p(0x1008), p, 384, ctypes.byref(s),
+              None) == 1
+    # nothing requested: nothing done
+    assert fn(None, None, None, None, None, None, None, None, 384, ctypes.byref(s), None) == 0
+
+
+@pytest.mark.parametrize("n,chunks", [(0, 1), (1, 1), (64, 1), (65, 2), (36400, 512),
+                                      (10 ** 6, 512)])
+def test_router_weight_grad_scratch_size(g5lib, n, chunks):
+    s = _lib.make_shape(n, 768, 3072, 16, 2, _lib.DTYPE_BF16)
+    b = ctypes.c_size_t(0)
+    assert g5lib.g5moe_router_weight_grad_scratch(ctypes.byref(s), ctypes.byref(b)) == 0
+    assert b.value == chunks * 16 * 768 * 4
+
+
+def test_router_weight_grad_argument_checks(g5lib):
+    p = ctypes.c_void_p(0x1000)
+    s = _lib.make_shape(10, 768, 3072, 16, 2, _lib.DTYPE_F32)
+    assert g5lib.g5moe_router_weight_grad(p, p, p, p, ctypes.byref(s), None) == 2
+    assert "bf16" in g5lib.g5moe_last_error().decode()
+    s = _lib.make_shape(10, 768, 3072, 16, 2, _lib.DTYPE_BF16)
+    assert g5lib.g5moe_router_weight_grad(None, p, p, p, ctypes.byref(s), None) == 1
+    assert "dlogits is NULL" in g5lib.g5moe_last_error().decode()
+    assert g5lib.g5moe_router_weight_grad(p, p, None, p, ctypes.byref(s), None) == 1
+    assert g5lib.g5moe_router_weight_grad(p, ctypes.c_void_p(0x1004), p, p, ctypes.byref(s),
+                                          None) == 2
+    assert "aligned" in g5lib.g5moe_last_error().decode()

@@ -396,3 +396,73 @@ def test_weight_grad_kernel_vs_fp32(cuda_device):
             err = (got.float() - ref).abs().max().item() / max(ref.abs().max().item(), 1e-30)
             print(f"  expert {e} ({c} rows) {name}: max_rel={err:.2e}", flush=True)
             assert err <= 8e-3, (e, name, err)
+
+
+@pytest.mark.parametrize("counts", [[0, 1, 192, 384, 385, 2000, 4100], [700, 3, 0, 0]])
+def test_weight_grad_sorted_h_equals_padded(cuda_device, counts):
+    """g5moe_weight_grad_sorted_h (h in sorted order with H_SLACK zero rows after
+    the last expert's, gate and up gradients written unpacked) against
+    g5moe_weight_grad on the padded copy of the same h: bit for bit, since the
+    rows past an expert's count meet dY's zero rows.  Empty experts first and last
+    (the last ones read only the zero slack rows)."""
+    import ctypes
+    from genet5_amd import _lib
+    dev = cuda_device
+    g = torch.Generator(device=dev).manual_seed(11)
+    E, d, F, k = len(counts), 256, 512, 2
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    T = int(offsets[-1])
+    n_tok = (T + k - 1) // k
+    t_off = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    dy = torch.randn(T + ops.ROW_PAD, d, device=dev, generator=g).to(torch.bfloat16)
+    x = torch.randn(n_tok, d, device=dev, generator=g).to(torch.bfloat16)
+    perm = torch.randperm(n_tok * k, device=dev, generator=g)[:T].to(torch.int32)
+    h = torch.zeros(T + ops.H_SLACK, F, dtype=torch.bfloat16, device=dev)
+    h[:T] = torch.randn(T, F, device=dev, generator=g).to(torch.bfloat16)
+    dgu = torch.randn(T + ops.ROW_PAD, 2 * F, device=dev, generator=g).to(torch.bfloat16)
+    kmax = ops.wgrad_kmax(max(counts))
+    print(f"  E={E} counts={counts} kmax={kmax}", flush=True)
+    dy_pad = ops.pad_rows(dy, None, t_off, E, kmax, k)
+    x_pad = ops.pad_rows(x, perm, t_off, E, kmax, k)
+    h_pad = ops.pad_rows(h, None, t_off, E, kmax, k)
+    dgu_pad = ops.pad_rows(dgu, None, t_off, E, kmax, k)
+    d_wd, d_wgu = ops.weight_grad(dy_pad, h_pad, dgu_pad, x_pad, t_off, kmax, top_k=k)
+    wd2 = torch.empty_like(d_wd)
+    wg2 = torch.empty(E, F, d, dtype=torch.bfloat16, device=dev)
+    wu2 = torch.empty_like(wg2)
+    shape = _lib.make_shape(n_tok, d, F, E, k, _lib.DTYPE_BF16)
+    _lib.call("g5moe_weight_grad_sorted_h", ops._ptr(dy_pad), ops._ptr(h), ops._ptr(wd2),
+              ops._ptr(dgu_pad), ops._ptr(x_pad), ops._ptr(wg2), ops._ptr(wu2), ops._ptr(t_off),
+              kmax, ctypes.byref(shape), ops._stream(dev))
+    torch.cuda.synchronize()
+    wg, wu = ops.unpack_gate_up(d_wgu)
+    assert torch.equal(wd2, d_wd)
+    assert torch.equal(wg2, wg) and torch.equal(wu2, wu)
+    assert d_wd.abs().sum() > 0 and wg.abs().sum() > 0
+
+
+@pytest.mark.parametrize("n,E,d", [(0, 16, 768), (1, 16, 768), (129, 9, 256), (4096, 4, 512),
+                                   (36400, 16, 768)])
+def test_router_weight_grad_vs_float64(cuda_device, n, E, d):
+    """g5moe_router_weight_grad against the float64 product dlogits^T x: within one
+    bf16 ulp of the result plus the fp32 accumulation bound 2e-5 * (|dlogits|^T |x|),
+    and the same bits on a second call (fixed reduction order)."""
+    from genet5_amd import _lib
+    dev = cuda_device
+    g = torch.Generator(device=dev).manual_seed(n + E)
+    x = torch.randn(n, d, device=dev, generator=g).to(torch.bfloat16)
+    dl = torch.randn(n, E, device=dev, generator=g) * 1e-2
+    shape = _lib.make_shape(n, d, 512, E, 2, _lib.DTYPE_BF16)
+    got = ops.router_weight_grad(dl, x, shape)
+    again = ops.router_weight_grad(dl, x, shape)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    xf = x.float().cpu().numpy().astype(np.float64)
+    df = dl.cpu().numpy().astype(np.float64)
+    ref = df.T @ xf
+    bound = 2.0 ** -8 * np.abs(ref) + 2e-5 * (np.abs(df).T @ np.abs(xf))
+    err = np.abs(host(got).astype(np.float64) - ref)
+    print(f"  n={n} E={E} d={d}: max err/bound {float((err / np.maximum(bound, 1e-30)).max()):.3f}",
+          flush=True)
+    assert np.all(err <= bound)
