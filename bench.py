@@ -261,9 +261,10 @@ def bench_config5(args) -> dict:
 def train_stage_breakdown(args) -> dict:
     """The module's training step as its stages, for the per-stage times: the forward
     (router with logits, dispatch, experts keeping the gate|up products, combine) and
-    every backward stage (gate/router gradients, dh GEMM, SwiGLU backward, dX GEMM,
-    input gradient, weight-gradient operands, the expert weight gradients from the
-    forward's h, the router weight gradient) through the C ABI — the kernels
+    every backward stage (gate/router gradients, the dh GEMM with the SwiGLU
+    backward in its epilogue, dX GEMM, input gradient, weight-gradient operands, the
+    expert weight gradients from the forward's h, the router weight gradient) through
+    the C ABI — the kernels
     ops.moe_backward enqueues for the module — with one HIP event between
     consecutive stages on the stream they run on (no dropout)."""
     import ctypes
@@ -283,7 +284,7 @@ def train_stage_breakdown(args) -> dict:
     shape = _lib.make_shape(N, d, F, E, k, _lib.DTYPE_BF16)
     P, S = ops._ptr, ops._stream(dev)
     stream = torch.cuda.current_stream(dev)
-    names = ["fwd", "gate_router_grad", "dh_gemm", "swiglu_bwd", "dx_gemm", "input_grad",
+    names = ["fwd", "gate_router_grad", "dh_swiglu", "dx_gemm", "input_grad",
              "wgrad_operands", "wgrad_gemms", "router_wgrad"]
 
     # the expert offsets reach the host by a non-blocking copy issued right after
@@ -294,8 +295,9 @@ def train_stage_breakdown(args) -> dict:
     def step(ev=None):
         rec = (lambda i: ev[i].record(stream)) if ev is not None else (lambda i: None)
         rec(0)
-        y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu, h = ops.moe_forward_train(
-            x, wr, wgu, wd, k, offsets_host=offs_host, offsets_ready=offs_ready, return_h=True)
+        y, logits, idx, w, offsets, perm, inv_pos, y_perm, fac, h = ops.moe_forward_train(
+            x, wr, wgu, wd, k, offsets_host=offs_host, offsets_ready=offs_ready, return_h=True,
+            factors=True)
         rec(1)
         offs_ready.synchronize()
         offs = offs_host.tolist()
@@ -307,30 +309,28 @@ def train_stage_breakdown(args) -> dict:
         dl = torch.empty((N, E), dtype=torch.float32, device=dev)
         _lib.call("g5moe_router_grad", P(dw), P(w), P(idx), None, P(dl), ctypes.byref(shape), S)
         rec(2)
-        dh = ops.grouped_gemm_padded(dy_buf, kmax, N * k, offsets, wd_t)
-        rec(3)
         dgu_buf = torch.empty((E * kmax + ops.ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
         dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
-        _lib.call("g5moe_swiglu_backward", P(dh), P(gu), P(perm), P(offsets), None, None,
-                  P(dgu_buf), kmax, None, ctypes.byref(shape), S)
-        rec(4)
+        _lib.call("g5moe_dh_swiglu_backward", P(dy_buf), kmax, P(offsets), P(wd_t), P(fac),
+                  P(dgu_buf), ctypes.byref(shape), S)
+        rec(3)
         dxp = ops.grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, wgu_t)
-        rec(5)
+        rec(4)
         dx = torch.empty((N, d), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_input_grad", P(dxp), P(inv_pos), P(dl), P(wr), P(dx),
                   ctypes.byref(shape), S)
-        rec(6)
+        rec(5)
         dy_pad = dy_buf[:E * kmax].view(E, kmax, d)
         x_pad = ops.pad_rows(x, perm, offsets, E, kmax, k)
-        rec(7)
+        rec(6)
         d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
         d_wg = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
         d_wu = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_weight_grad_sorted_h", P(dy_pad), P(h), P(d_wd), P(dgu_pad), P(x_pad),
                   P(d_wg), P(d_wu), P(offsets), kmax, ctypes.byref(shape), S)
-        rec(8)
+        rec(7)
         ops.router_weight_grad(dl, x, shape)
-        rec(9)
+        rec(8)
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]
@@ -345,7 +345,7 @@ def train_stage_breakdown(args) -> dict:
     st = {n: sum(ev[j].elapsed_time(ev[j + 1]) for ev in events) / args.steps
           for j, n in enumerate(names)}
     g = 2 * d * F * N * k  # one d x F product over the routed rows
-    flops = {"dh_gemm": g, "dx_gemm": 2 * g, "wgrad_gemms": 3 * g}
+    flops = {"dh_swiglu": g, "dx_gemm": 2 * g, "wgrad_gemms": 3 * g}
     return {"stage_ms": st, "stage_ms_per_step": ms,
             "stage_tflops": {n: flops[n] / (st[n] * 1e-3) / 1e12 for n in flops}}
 

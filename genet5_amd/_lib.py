@@ -29,6 +29,8 @@ EXPORTED = (
     "g5moe_dispatch_noalloc",
     "g5moe_expert_gate_up",
     "g5moe_expert_gate_up_train",
+    "g5moe_expert_gate_up_train_factors",
+    "g5moe_dh_swiglu_backward",
     "g5moe_expert_down",
     "g5moe_expert_swiglu",
     "g5moe_combine",
@@ -131,6 +133,10 @@ _SIGS = {
     "g5moe_expert_gate_up": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up_train": ([_P, _P, _P, _P, _P, _P, _DROP_P, _SHAPE_P, _P],
                                    ctypes.c_int),
+    "g5moe_expert_gate_up_train_factors": ([_P, _P, _P, _P, _P, _P, _DROP_P, _SHAPE_P, _P],
+                                           ctypes.c_int),
+    "g5moe_dh_swiglu_backward": ([_P, ctypes.c_int32, _P, _P, _P, _P, _SHAPE_P, _P],
+                                 ctypes.c_int),
     "g5moe_expert_down": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_swiglu": ([_P, _P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_combine": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),

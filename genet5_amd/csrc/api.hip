@@ -232,6 +232,64 @@ g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
                     "g5moe_expert_gate_up_train");
 }
 
+g5moe_status g5moe_expert_gate_up_train_factors(const void* x, const int32_t* perm,
+                                                const int32_t* offsets, const void* w_gate_up,
+                                                void* ab, void* ws, const g5moe_dropout* dropout,
+                                                const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  DropoutParams drop;
+  G5_CHECK(dropout_params(dropout, &drop));
+  G5_NONNULL(ws);
+  char* w = static_cast<char*>(ws);
+  const hipStream_t st = as_stream(stream);
+  const WorkspaceLayout L = workspace_layout(*shape);
+  const int64_t nk = shape->n_tokens * shape->top_k;
+  G5_CHECK(hip_status(launch_zero16(w + L.h + size_t(nk) * shape->d_ff * 2,
+                                    int64_t(kWgradSlackRows) * shape->d_ff * 2 / 16, st),
+                      "g5moe_expert_gate_up_train_factors (h slack rows)"));
+  if (shape->n_tokens == 0) return G5MOE_OK;
+  G5_NONNULL(x);
+  G5_NONNULL(perm);
+  G5_NONNULL(offsets);
+  G5_NONNULL(w_gate_up);
+  G5_NONNULL(ab);
+  hipError_t err;
+  const uint16_t* xb = gemm_input(x, w, *shape, st, &err);
+  G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train_factors (cast)"));
+  return hip_status(
+      launch_gate_up_ab(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
+                        reinterpret_cast<uint16_t*>(w + L.h), static_cast<uint16_t*>(ab), *shape,
+                        st, drop),
+      "g5moe_expert_gate_up_train_factors");
+}
+
+g5moe_status g5moe_dh_swiglu_backward(const void* dy_pad, int32_t kmax, const int32_t* offsets,
+                                      const void* w_down_t, const void* ab, void* dgu_pad,
+                                      const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (shape->d_ff % 256 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "dh_swiglu_backward: d_ff %d must be a multiple of 256",
+                int(shape->d_ff));
+  if (kmax < 384 || kmax % 192 != 0)
+    return fail(G5MOE_ERR_INVALID_ARG,
+                "dh_swiglu_backward: kmax %d must be a multiple of 192 and >= 384", int(kmax));
+  G5_NONNULL(dgu_pad);
+  G5_NONNULL(offsets);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(dy_pad);
+    G5_NONNULL(w_down_t);
+    G5_NONNULL(ab);
+  }
+  if ((reinterpret_cast<uintptr_t>(dy_pad) | reinterpret_cast<uintptr_t>(w_down_t) |
+       reinterpret_cast<uintptr_t>(ab) | reinterpret_cast<uintptr_t>(dgu_pad)) % 16 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "dh_swiglu_backward: buffers must be 16-byte aligned");
+  return hip_status(launch_dh_swiglu(static_cast<const uint16_t*>(dy_pad), kmax, offsets,
+                                     static_cast<const uint16_t*>(w_down_t),
+                                     static_cast<const uint16_t*>(ab),
+                                     static_cast<uint16_t*>(dgu_pad), *shape, as_stream(stream)),
+                    "g5moe_dh_swiglu_backward");
+}
+
 g5moe_status g5moe_expert_down(const int32_t* offsets, const void* w_down, void* y_perm,
                                void* ws, const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));

@@ -117,6 +117,15 @@ hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t*
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
                           const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
                           hipStream_t st, const DropoutParams* drop = nullptr);
+// Training gate|up for the fused SwiGLU backward: h (with dropout) into h, and the
+// derivative factors A = dh/dg, B = dh/du (dropout folded in) into ab [N*k, 2F].
+hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
+                             const uint16_t* wgu, uint16_t* h, uint16_t* ab,
+                             const g5moe_shape& s, hipStream_t st, const DropoutParams& drop);
+// dGU_pad (per-expert padded, wgrad_rows rows per expert) = (dY_pad Wd_e) * (A | B).
+hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* offsets,
+                            const uint16_t* wd_t, const uint16_t* ab, uint16_t* dgu_pad,
+                            const g5moe_shape& s, hipStream_t st);
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,

@@ -70,9 +70,11 @@ struct GemmArgs {
   int a_rows_per_expert;  // 0: A row of sorted position p is p; > 0: expert e's j-th
                           // row is A row e * a_rows_per_expert + j (per-expert padded
                           // layout; at most a_rows_per_expert rows of each expert are used)
-  // MODE 3 with dropout (the kernel's DROP flag): the mask of g5moe_dropout
+  // MODE 3 / 5 with dropout (the kernel's DROP flag): the mask of g5moe_dropout
   uint32_t drop_seed_lo, drop_seed_hi, drop_thr;
   float drop_scale;
+  const uint16_t* aux;    // MODE 4: the forward's SwiGLU derivative factors [N*k, 2 Nout]
+                          // (packed gate|up order, sorted positions), read in the epilogue
 };
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
@@ -87,9 +89,13 @@ struct TileCoord {
 };
 
 // Rows of expert e the GEMM computes: its sorted positions, capped at the padded
-// layout's per-expert row count.
+// layout's per-expert row count.  WROWS (MODE 4): the weight-gradient kernel's
+// row count wgrad_rows(M_e, kmax) instead, so that the rows it reads past M_e
+// are written too (as zeros).
+template <bool WROWS = false>
 __device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& off, int e) {
   const int cnt = off(e + 1) - off(e);
+  if constexpr (WROWS) return wgrad_rows(cnt, args.a_rows_per_expert);
   return args.a_rows_per_expert > 0 ? min(cnt, args.a_rows_per_expert) : cnt;
 }
 
@@ -115,13 +121,13 @@ __device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& 
 #define G5_B3 1
 #endif
 
-template <int BM, int BN, int GM>
+template <int BM, int BN, int GM, bool WROWS = false>
 __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, const Offsets& off, int u,
                                               TileCoord& tc) {
   const int ntn = args.Nout / BN;
   int e = 0, mt_e = 0;
   for (; e < args.n_experts; ++e) {
-    const int cnt = expert_rows(args, off, e);
+    const int cnt = expert_rows<WROWS>(args, off, e);
     mt_e = (cnt + BM - 1) / BM;
     const int t = mt_e * ntn;
     if (u < t) break;
@@ -135,7 +141,7 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, const Offset
   const int nt = rr / gs;
   tc.e = e;
   tc.p_begin = off(e) + mt * BM;
-  tc.p_end = off(e) + expert_rows(args, off, e);
+  tc.p_end = off(e) + expert_rows<WROWS>(args, off, e);
   tc.a_row = args.a_rows_per_expert > 0 ? e * args.a_rows_per_expert + mt * BM : tc.p_begin;
   tc.n0 = nt * BN;
 }
@@ -158,9 +164,14 @@ constexpr int persist_smem_bytes() {
 // MODE: 0 = A rows in place (down, and the backward GEMMs), 1 = gathered x
 // rows with the SwiGLU epilogue (gate|up), 2 = gathered x rows, raw outputs
 // (the gate|up recompute of the backward), 3 = gathered x rows, raw outputs
-// into C2 and the SwiGLU outputs into C (the training forward's gate|up).
-// DROP (MODE 3 only): dropout on the SwiGLU outputs (the raw products stay
-// unmasked), keyed on each row's assignment perm[p].
+// into C2 and the SwiGLU outputs into C (the training forward's gate|up),
+// 4 = A rows in place with the SwiGLU backward in the epilogue (the dh product
+// times the derivative factors of aux into the per-expert padded dGU), 5 =
+// gathered x rows, the SwiGLU outputs into C and their derivative factors into
+// C2 (the training forward's gate|up for MODE 4).
+// DROP (MODE 3 and 5): dropout on the SwiGLU outputs (MODE 3's raw products stay
+// unmasked; MODE 5's factors carry the mask), keyed on each row's assignment
+// perm[p].
 template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF,
           bool DROP = false>
 __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& off, char* smem,
@@ -188,9 +199,9 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   static_assert(HALF ? 2 * BN == BNF : BN == BNF, "tile width");
   static_assert(S >= 2 && S * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
   static_assert((S - 2) * PER < 64, "vmcnt range");
-  constexpr bool SWIGLU = MODE == 1 || MODE == 3;
+  constexpr bool SWIGLU = MODE == 1 || MODE == 3 || MODE == 5;
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
-  static_assert(!DROP || MODE == 3, "dropout belongs to the training gate|up GEMM");
+  static_assert(!DROP || MODE == 3 || MODE == 5, "dropout belongs to the training gate|up GEMM");
   // Fragment f of the next substeps is read after the f-th MFMA of a substep,
   // so a substep must hold at least as many MFMAs as fragments.
   static_assert(MB * NB >= MB + NB, "fragment prefetch needs MB * NB >= MB + NB");
@@ -201,14 +212,14 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
                 "slot swizzle period");
   // The gate|up GEMMs gather token rows through perm; the others read the
   // expert-contiguous A rows in place.
-  constexpr bool GATHER = MODE != 0;
+  constexpr bool GATHER = MODE != 0 && MODE != 4;
   // Three A stages (MODE 0 with three fragment slots): the epilogue region,
   // which is exactly one A stage (wave w's DMA slice of it is wave w's own
   // region), doubles as A buffer 2, so A is issued three k-steps ahead and B
   // two.  A buffers rotate with the k-step mod 3 (tiles start at 0 mod 3, so
   // every tile's last step reads its A from the epilogue region: the next
   // tile's third A stage goes out after the epilogue), B buffers mod 2.
-  constexpr bool A3 = G5_A3 && MODE == 0 && NSLOT == 3 && S == 2 &&
+  constexpr bool A3 = G5_A3 && (MODE == 0 || MODE == 4) && NSLOT == 3 && S == 2 &&
                       A_BYTES == 4 * kEpiBytesPerWave;
   // Three B stages (the SwiGLU modes, whose weight tiles are the operand that
   // streams from beyond the L2): the same scheme with the roles swapped, B
@@ -220,10 +231,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   auto decode_unit = [&](int i, TileCoord& tc) {
     const int h = un.first + i * un.stride;
     if constexpr (HALF) {
-      decode_tile_u<BM, BNF, GM>(args, off, un.base + (h >> 1), tc);
+      decode_tile_u<BM, BNF, GM, MODE == 4>(args, off, un.base + (h >> 1), tc);
       tc.n0 += (h & 1) * BN;
     } else {
-      decode_tile_u<BM, BNF, GM>(args, off, h, tc);
+      decode_tile_u<BM, BNF, GM, MODE == 4>(args, off, h, tc);
     }
   };
 
@@ -597,6 +608,198 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
       kstep(F_{}, T_{}, P2{}, nk - 1);
     }
 
+    if constexpr (MODE == 5) {
+      // Training gate|up for the fused SwiGLU backward.  Per (gate g, up u) pair,
+      // with s = sigmoid(g) and m the dropout multiplier (scale or 0; 1 without
+      // dropout):
+      //   h = g s u m (into C, as MODE 3 computes it),
+      //   A = u s (1 + g (1 - s)) m (gate column of C2) = d h / d g,
+      //   B = g s m (up column of C2) = d h / d u,
+      // so the backward's dGU is dh * A, dh * B.  Pass j handles token block j:
+      // A and B go through the wave's LDS region (32 rows x 256 bytes, chunk c of
+      // row r at c ^ (r % 16)) to 16-byte row stores, then h (32 rows x 128 bytes,
+      // chunk c of row r at c ^ ((r / 2) % 8)) the same way; the LDS reads of one
+      // stage precede the writes of the next in the wave's instruction order.
+      [[maybe_unused]] uint32_t dkey[DROP ? MB : 1];
+      if constexpr (DROP) {
+        uint32_t av[MB];
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+          av[j] = uint32_t(
+              args.perm[min(cur.p_begin + wm * WTM + 32 * j + tok_l, cur.p_end - 1)]);
+#pragma unroll
+        for (int j = 0; j < MB; ++j)
+          dkey[j] = dropout_row_key(av[j], args.drop_seed_lo, args.drop_seed_hi);
+      }
+      constexpr int OB = NB;         // packed column blocks (gate, up alternating)
+      constexpr int RBY = OB * 64;   // A|B bytes per row
+      constexpr int CR = RBY / 16;
+      constexpr int HRBY = OB * 32;  // h bytes per row
+      constexpr int HCR = HRBY / 16;
+      constexpr int HLPR = 256 / HRBY;
+      static_assert(RBY == 256 && kEpiBytesPerWave / RBY == 32, "one token block per pass");
+      const int col0 = cur.n0 + wn * WTN;
+      const int hcol0 = col0 / 2;
+      const int row = tok_l;
+#pragma unroll
+      for (int j = 0; j < MB; ++j) {
+        uint2 hv[OB / 2][4];
+#pragma unroll
+        for (int ob = 0; ob < OB / 2; ++ob) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            [[maybe_unused]] uint32_t rb[4];
+            if constexpr (DROP) {
+              // h columns hcol0 + 8 (4 ob + q) + 4 half + uu: column pairs cp, cp + 1
+              const uint32_t cp = uint32_t(hcol0 + 8 * (ob * 4 + q) + 4 * half) >> 1;
+              const uint32_t b0 = dropout_pair_bits(dkey[j], cp);
+              const uint32_t b1 = dropout_pair_bits(dkey[j], cp + 1);
+              rb[0] = b0 & 0xffffu;
+              rb[1] = b0 >> 16;
+              rb[2] = b1 & 0xffffu;
+              rb[3] = b1 >> 16;
+            }
+            float hh[4], fa[4], fb[4];
+#pragma unroll
+            for (int uu = 0; uu < 4; ++uu) {
+              const float g = acc[2 * ob][j][4 * q + uu];
+              const float u = acc[2 * ob + 1][j][4 * q + uu];
+              const float sg = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+              const float silu = g * sg;
+              float h = silu * u;
+              float a = u * (sg * (1.0f + g * (1.0f - sg)));
+              float b = silu;
+              if constexpr (DROP) {
+                const bool keep = rb[uu] >= args.drop_thr;
+                h = keep ? h * args.drop_scale : 0.0f;
+                a = keep ? a * args.drop_scale : 0.0f;
+                b = keep ? b * args.drop_scale : 0.0f;
+              }
+              hh[uu] = h;
+              fa[uu] = a;
+              fb[uu] = b;
+            }
+            const int swz = row % CR;
+            *reinterpret_cast<uint2*>(epi + row * RBY + (((2 * ob) * 4 + q) ^ swz) * 16 +
+                                      half * 8) =
+                make_uint2(pack_bf16x2(fa[0], fa[1]), pack_bf16x2(fa[2], fa[3]));
+            *reinterpret_cast<uint2*>(epi + row * RBY + (((2 * ob + 1) * 4 + q) ^ swz) * 16 +
+                                      half * 8) =
+                make_uint2(pack_bf16x2(fb[0], fb[1]), pack_bf16x2(fb[2], fb[3]));
+            hv[ob][q] = make_uint2(pack_bf16x2(hh[0], hh[1]), pack_bf16x2(hh[2], hh[3]));
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < 32 * RBY / 1024; ++it) {
+          const int r = it * (1024 / RBY) + lane / CR;
+          const int c = lane % CR;
+          const uint4 v = *reinterpret_cast<const uint4*>(epi + r * RBY + ((c ^ (r % CR)) * 16));
+          const int p = cur.p_begin + wm * WTM + j * 32 + r;
+          if (p < cur.p_end) store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
+        }
+#pragma unroll
+        for (int ob = 0; ob < OB / 2; ++ob)
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            *reinterpret_cast<uint2*>(epi + row * HRBY +
+                                      (((ob * 4 + q) ^ ((row / HLPR) % HCR)) * 16) + half * 8) =
+                hv[ob][q];
+#pragma unroll
+        for (int it = 0; it < 32 * HRBY / 1024; ++it) {
+          const int r = it * (1024 / HRBY) + lane / HCR;
+          const int c = lane % HCR;
+          const uint4 v = *reinterpret_cast<const uint4*>(
+              epi + r * HRBY + ((c ^ ((r / HLPR) % HCR)) * 16));
+          const int p = cur.p_begin + wm * WTM + j * 32 + r;
+          if (p < cur.p_end) store16_nt(args.C + int64_t(p) * args.ldc + hcol0 + c * 8, v);
+        }
+      }
+    } else if constexpr (MODE == 4) {
+      // The SwiGLU backward on this tile's dh (rounded to bf16, as a stored dh
+      // would be): for row p of expert e and h column f, with A, B the forward's
+      // factors at the packed gate and up columns of f,
+      //   dGU[gate] = bf16(dh * A),  dGU[up] = bf16(dh * B),
+      // written to the per-expert padded row a_row + r; rows from the expert's
+      // count up to the weight gradient's row count get zeros.  dh goes through
+      // the wave's LDS region as in MODE 0; each lane then holds 8 consecutive
+      // columns of one row, the matching 16-byte A and B chunks of aux (loaded
+      // at the start of the pass, over the staging), and writes 16-byte dGU chunks.
+      constexpr int OB = NB;
+      constexpr int RBY = OB * 64;
+      constexpr int CR = RBY / 16;
+      constexpr int ROWS = kEpiBytesPerWave / RBY;
+      constexpr int JP = ROWS / 32;
+      constexpr int LPR = 256 / RBY;
+      constexpr int NIT = ROWS * RBY / 1024;
+      static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
+      const int col0 = cur.n0 + wn * WTN;
+      const int p_valid = off(cur.e + 1);  // rows at or past it are padding
+      const int64_t ld = args.ldc;        // 2 F: dGU and aux rows
+#pragma unroll
+      for (int pass = 0; pass < MB / JP; ++pass) {
+        uint4 va[NIT], vb[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int r = it * (1024 / RBY) + lane / CR;
+          const int f = col0 + (lane % CR) * 8;
+          const int p = cur.p_begin + wm * WTM + pass * ROWS + r;
+          // padding rows read row 0 (valid whenever the launch has rows), unused
+          const int64_t src = int64_t(p < p_valid ? p : 0) * ld + (f >> 5) * 64 + (f & 31);
+          va[it] = *reinterpret_cast<const uint4*>(args.aux + src);
+          vb[it] = *reinterpret_cast<const uint4*>(args.aux + src + 32);
+        }
+#pragma unroll
+        for (int jl = 0; jl < JP; ++jl) {
+          const int j = pass * JP + jl;
+          const int row = jl * 32 + tok_l;
+          const int swz = (row / LPR) % CR;
+#pragma unroll
+          for (int ob = 0; ob < OB; ++ob) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              uint2 o;
+              o.x = pack_bf16x2(acc[ob][j][4 * q], acc[ob][j][4 * q + 1]);
+              o.y = pack_bf16x2(acc[ob][j][4 * q + 2], acc[ob][j][4 * q + 3]);
+              const int c = ob * 4 + q;
+              *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; ++it) {
+          const int r = it * (1024 / RBY) + lane / CR;
+          const int c = lane % CR;
+          const uint4 v = *reinterpret_cast<const uint4*>(
+              epi + r * RBY + ((c ^ ((r / LPR) % CR)) * 16));
+          const int p = cur.p_begin + wm * WTM + pass * ROWS + r;
+          if (p < cur.p_end) {
+            const bool valid = p < p_valid;
+            const uint32_t dv[4] = {v.x, v.y, v.z, v.w};
+            const uint32_t av[4] = {va[it].x, va[it].y, va[it].z, va[it].w};
+            const uint32_t bv[4] = {vb[it].x, vb[it].y, vb[it].z, vb[it].w};
+            uint32_t og[4], ou[4];
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+              const float d0 = __uint_as_float(dv[w] << 16);
+              const float d1 = __uint_as_float(dv[w] & 0xffff0000u);
+              const uint32_t g = pack_bf16x2(d0 * __uint_as_float(av[w] << 16),
+                                             d1 * __uint_as_float(av[w] & 0xffff0000u));
+              const uint32_t u = pack_bf16x2(d0 * __uint_as_float(bv[w] << 16),
+                                             d1 * __uint_as_float(bv[w] & 0xffff0000u));
+              og[w] = valid ? g : 0u;
+              ou[w] = valid ? u : 0u;
+            }
+            const int f = col0 + c * 8;
+            uint16_t* dst = args.C + (int64_t(cur.a_row) + wm * WTM + pass * ROWS + r) * ld +
+                            (f >> 5) * 64 + (f & 31);
+            store16_nt(dst, make_uint4(og[0], og[1], og[2], og[3]));
+            store16_nt(dst + 32, make_uint4(ou[0], ou[1], ou[2], ou[3]));
+          }
+        }
+      }
+    } else
     // DROP (the training forward with dropout): the same epilogue with the
     // SwiGLU outputs masked and scaled.  The kernels without dropout keep the
     // epilogue's statements exactly as they are (else branch): any extra
@@ -906,7 +1109,7 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
   const Offsets off = load_offsets(args.offsets, args.n_experts);
   int total = 0;
   for (int e = 0; e < args.n_experts; ++e) {
-    const int cnt = expert_rows(args, off, e);
+    const int cnt = expert_rows<MODE == 4>(args, off, e);
     total += ((cnt + BM - 1) / BM) * ntn;
   }
   const int ng = gridDim.x;
@@ -1065,6 +1268,66 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false>(pgrid, a, st);
   else
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);
+  return hipGetLastError();
+}
+
+hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
+                             const uint16_t* wgu, uint16_t* h, uint16_t* ab,
+                             const g5moe_shape& s, hipStream_t st, const DropoutParams& drop) {
+  const int64_t nk = s.n_tokens * s.top_k;
+  if (nk == 0) return hipSuccess;
+  GemmArgs a{};
+  a.A = xb;
+  a.perm = perm;
+  a.offsets = offsets;
+  a.B = wgu;
+  a.C = h;
+  a.C2 = ab;
+  a.topk = s.top_k;
+  a.n_experts = s.n_experts;
+  a.K = s.d_model;
+  a.Nout = 2 * s.d_ff;
+  a.ldc = s.d_ff;
+  a.ldc2 = 2 * s.d_ff;
+  if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
+  const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout),
+                                 unsigned(device_cu_count()));
+  if (drop.on) {
+    a.drop_seed_lo = drop.seed_lo;
+    a.drop_seed_hi = drop.seed_hi;
+    a.drop_thr = drop.thr;
+    a.drop_scale = drop.scale;
+    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 5, false, true>(grid, a, st);
+  } else {
+    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 5, false>(grid, a, st);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* offsets,
+                            const uint16_t* wd_t, const uint16_t* ab, uint16_t* dgu_pad,
+                            const g5moe_shape& s, hipStream_t st) {
+  const int E = s.n_experts, d = s.d_model, F = s.d_ff;
+  if (F % 256 != 0 || d % 64 != 0 || d < 128 || kmax < 384 || kmax % 192 != 0)
+    return hipErrorInvalidValue;
+  if (s.n_tokens * s.top_k == 0)  // every expert's rows are padding: zeros
+    return launch_zero16(dgu_pad, int64_t(E) * kmax * 2 * F * 2 / 16, st);
+  GemmArgs a{};
+  a.a_rows_per_expert = kmax;
+  a.A = dy_pad;
+  a.perm = nullptr;
+  a.offsets = offsets;
+  a.B = wd_t;
+  a.C = dgu_pad;
+  a.aux = ab;
+  a.topk = 1;
+  a.n_experts = E;
+  a.K = d;
+  a.Nout = F;
+  a.ldc = 2 * F;
+  const unsigned grid = std::min(grid_bound<256, 256>(int64_t(E) * kmax, E, F),
+                                 unsigned(device_cu_count()));
+  launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 4, true>(grid, a, st);
   return hipGetLastError();
 }
 

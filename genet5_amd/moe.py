@@ -93,6 +93,13 @@ _HOST_OFFSETS: "OrderedDict[int, Tuple[torch.Tensor, torch.cuda.Event]]" = Order
 _HOST_OFFSETS_MAX = 256
 
 
+def _fused_swiglu_backward(w_gate_up: torch.Tensor) -> bool:
+    """Whether the training op keeps the SwiGLU derivative factors (the fused dh +
+    SwiGLU backward, d and F multiples of 256) or the raw gate|up products."""
+    F2, d = w_gate_up.shape[1], w_gate_up.shape[2]
+    return d % 256 == 0 and (F2 // 2) % 256 == 0
+
+
 @torch.library.custom_op("g5moe::moe_forward_train", mutates_args=())
 def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
                           w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
@@ -105,14 +112,16 @@ def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optiona
     (bf16); the kernels read w_gate_up (their packed copy) and w_down, and the
     backward the transposed copies w_gate_up_t [E, d, 2F] and w_down_t [E, F, d].
     The last output is the forward's h [N*k + 384, F] (zero rows past N*k), which
-    the backward's down-weight gradient reads."""
+    the backward's down-weight gradient reads; the one before it the SwiGLU
+    derivative factors (or, for d or F not a multiple of 256, the raw gate|up
+    products), the backward's SwiGLU operand."""
     E = w_router.shape[0]
     host = torch.empty((E + 1,), dtype=torch.int32, pin_memory=True)
     ready = torch.cuda.Event()
     outs = ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias,
                                  offsets_host=host, offsets_ready=ready,
                                  dropout=(dropout_p, seed) if dropout_p > 0 else None,
-                                 return_h=True)
+                                 return_h=True, factors=_fused_swiglu_backward(w_gate_up))
     _HOST_OFFSETS[outs[4].data_ptr()] = (host, ready)
     while len(_HOST_OFFSETS) > _HOST_OFFSETS_MAX:
         _HOST_OFFSETS.popitem(last=False)
@@ -148,9 +157,10 @@ def _train_setup(ctx, inputs, output):
         ctx.host_offsets = _HOST_OFFSETS.pop(offsets.data_ptr(), None)
     except Exception:  # traced (fake) tensors have no storage: read on the device later
         ctx.host_offsets = None
-    # gu: the forward's raw gate|up products, kept so the backward does not
-    # recompute them (894 MB at 36,400 tokens: HBM for time); h: the forward's
-    # SwiGLU outputs, the down-weight gradient's operand (447 MB)
+    # gu: the forward's SwiGLU derivative factors (or raw gate|up products), kept
+    # so the backward does not recompute them (894 MB at 36,400 tokens: HBM for
+    # time); h: the forward's SwiGLU outputs, the down-weight gradient's operand
+    # (447 MB)
     ctx.save_for_backward(x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w,
                           offsets, perm, inv_pos, y_perm, gu, h)
     ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu, h)
@@ -169,8 +179,10 @@ def _train_backward(ctx, dy, dlogits, *unused):
         dy.to(torch.bfloat16).contiguous(), x, w_router, w_gate_up, w_down, ctx.top_k, idx, w,
         offsets, perm, inv_pos, y_perm,
         grad_logits=None if dlogits is None else dlogits.float().contiguous(),
-        w_down_t=w_down_t, w_gate_up_t=w_gate_up_t, gu=gu, offsets_host=offsets_host,
-        dropout=ctx.dropout, h=h, split_gate_up=True)
+        w_down_t=w_down_t, w_gate_up_t=w_gate_up_t, offsets_host=offsets_host, h=h,
+        split_gate_up=True,
+        **(dict(factors=gu) if _fused_swiglu_backward(w_gate_up) else
+           dict(gu=gu, dropout=ctx.dropout)))
     return dx, d_wr, None, d_wg, d_wu, d_wd, None, None, None, None, None, None
 
 

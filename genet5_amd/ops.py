@@ -326,13 +326,16 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
                       w_down: torch.Tensor, top_k: int, bias: Optional[torch.Tensor] = None,
                       offsets_host: Optional[torch.Tensor] = None,
                       offsets_ready: Optional["torch.cuda.Event"] = None,
-                      dropout: Optional[Tuple[float, int]] = None, return_h: bool = False):
+                      dropout: Optional[Tuple[float, int]] = None, return_h: bool = False,
+                      factors: bool = False):
     """The layer forward as stage calls, returning what the backward needs:
     (y, logits fp32 [N, E], topk_idx, topk_w, offsets, perm, inv_pos, y_perm, gu) with
     gu the raw gate|up products bf16 [N*k, 2F] (packed column order), which the
     gate|up GEMM stores beside h (g5moe_expert_gate_up_train) so that the backward
     does not recompute them.  return_h: h (bf16 [N*k + H_SLACK, F], a view of the
     workspace, the rows past N*k zero) is appended, for moe_backward(h=...).
+    factors: the gu slot holds the SwiGLU derivative factors instead of the raw
+    products (g5moe_expert_gate_up_train_factors), for moe_backward(factors=...).
 
     offsets_host (pinned int32 [E + 1] on the host): the expert offsets are copied
     there without blocking as soon as the dispatch has written them, and
@@ -362,8 +365,9 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
     gu = torch.empty((N * top_k, F2), dtype=torch.bfloat16, device=dev)
     y_perm = torch.empty((N * top_k, d), dtype=torch.bfloat16, device=dev)
     S = _stream(dev)
-    _lib.call("g5moe_expert_gate_up_train", _ptr(x2d), _ptr(perm), _ptr(offsets),
-              _ptr(w_gate_up), _ptr(gu), _ptr(ws), _dropout_arg(dropout), ctypes.byref(shape), S)
+    _lib.call("g5moe_expert_gate_up_train_factors" if factors else "g5moe_expert_gate_up_train",
+              _ptr(x2d), _ptr(perm), _ptr(offsets), _ptr(w_gate_up), _ptr(gu), _ptr(ws),
+              _dropout_arg(dropout), ctypes.byref(shape), S)
     _lib.call("g5moe_expert_down", _ptr(offsets), _ptr(w_down), _ptr(y_perm), _ptr(ws),
               ctypes.byref(shape), S)
     y = combine(y_perm, inv_pos, w, x2d.dtype)
@@ -421,7 +425,7 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
                  w_gate_up_t: Optional[torch.Tensor] = None, gu: Optional[torch.Tensor] = None,
                  offsets_host: Optional[torch.Tensor] = None,
                  dropout: Optional[Tuple[float, int]] = None, h: Optional[torch.Tensor] = None,
-                 split_gate_up: bool = False):
+                 split_gate_up: bool = False, factors: Optional[torch.Tensor] = None):
     """Gradients (dx, d_w_router, d_w_gate_up (packed layout), d_w_down) of the layer,
     or with split_gate_up (dx, d_w_router, d_w_gate, d_w_up, d_w_down).
 
@@ -429,6 +433,9 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     gradient then reads it in sorted order (g5moe_weight_grad_sorted_h) instead of
     the SwiGLU backward writing a padded copy, and the gate and up gradients come
     out of the weight-gradient kernel unpacked.
+    factors: the forward's SwiGLU derivative factors (moe_forward_train(...,
+    factors=True), with h): the dh product then computes dGU in its epilogue
+    (g5moe_dh_swiglu_backward) and gu and dropout are not used.
 
     offsets_host: a completed host copy of offsets (moe_forward_train's, after its
     offsets_ready event); without it the offsets are read from the device here,
@@ -483,33 +490,43 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     dlogits = torch.empty((N, E), dtype=torch.float32, device=dev)
     _lib.call("g5moe_router_grad", _ptr(dw), _ptr(topk_w), _ptr(topk_idx), _ptr(grad_logits),
               _ptr(dlogits), ctypes.byref(shape), S)
-    if gu is None:
-        # the forward's gate|up products were not kept: recompute them
-        gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
-        ws = workspace(shape, dev)
-        _lib.call("g5moe_expert_gate_up_raw", _ptr(x2d), _ptr(perm), _ptr(offsets),
-                  _ptr(w_gate_up), _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
-        del ws
-    else:
-        _require(gu, "gu", (N * k, 2 * F), torch.bfloat16, dev)
-    if w_down_t is None:
-        w_down_t = transpose_experts(w_down)            # [E, F, d]
-    if hip_wgrad:
-        dh = grouped_gemm_padded(dy_buf, kmax, N * k, offsets, w_down_t)   # [N*k, F]
-    else:
-        dh = grouped_gemm(dyp, N * k, offsets, w_down_t)
     sorted_h = h is not None and hip_wgrad
     if sorted_h:
         _require(h, "h", (N * k + H_SLACK, F), torch.bfloat16, dev)
-        h_pad = None
-    else:
-        h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
+    if w_down_t is None:
+        w_down_t = transpose_experts(w_down)            # [E, F, d]
     # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
     dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
     dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
-    _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(perm), _ptr(offsets), None,
-              _ptr(h_pad), _ptr(dgu_buf), kmax, _dropout_arg(dropout), ctypes.byref(shape), S)
-    del dh, gu
+    h_pad = None
+    if factors is not None:
+        # the dh product with the SwiGLU backward in its epilogue (the forward's
+        # derivative factors carry the dropout mask)
+        if not (sorted_h and F % 256 == 0):
+            raise ValueError("factors need the forward's h and d, F multiples of 256")
+        _require(factors, "factors", (N * k, 2 * F), torch.bfloat16, dev)
+        _lib.call("g5moe_dh_swiglu_backward", _ptr(dy_buf), kmax, _ptr(offsets),
+                  _ptr(w_down_t), _ptr(factors), _ptr(dgu_buf), ctypes.byref(shape), S)
+    else:
+        if gu is None:
+            # the forward's gate|up products were not kept: recompute them
+            gu = torch.empty((N * k, 2 * F), dtype=torch.bfloat16, device=dev)
+            ws = workspace(shape, dev)
+            _lib.call("g5moe_expert_gate_up_raw", _ptr(x2d), _ptr(perm), _ptr(offsets),
+                      _ptr(w_gate_up), _ptr(gu), _ptr(ws), ctypes.byref(shape), S)
+            del ws
+        else:
+            _require(gu, "gu", (N * k, 2 * F), torch.bfloat16, dev)
+        if hip_wgrad:
+            dh = grouped_gemm_padded(dy_buf, kmax, N * k, offsets, w_down_t)   # [N*k, F]
+        else:
+            dh = grouped_gemm(dyp, N * k, offsets, w_down_t)
+        if not sorted_h:
+            h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
+        _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(perm), _ptr(offsets), None,
+                  _ptr(h_pad), _ptr(dgu_buf), kmax, _dropout_arg(dropout), ctypes.byref(shape),
+                  S)
+        del dh, gu
     if w_gate_up_t is None:
         w_gate_up_t = transpose_experts(w_gate_up)      # [E, d, 2F]
     dxp = grouped_gemm_padded(dgu_buf, kmax, N * k, offsets, w_gate_up_t)  # [N*k, d]

@@ -181,6 +181,21 @@ g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
                                         void* gu, void* ws, const g5moe_dropout* dropout,
                                         const g5moe_shape* shape, void* stream);
 
+/* The training gate|up for the fused SwiGLU backward (g5moe_dh_swiglu_backward):
+ * h into the workspace as g5moe_expert_gate_up_train writes it (bit for bit, with
+ * the same 384 zero rows after it), and in place of the raw products the SwiGLU
+ * derivative factors, ab : bf16 [N*k, 2F] in the packed gate|up column order:
+ *   gate column f:  A = m u s (1 + g (1 - s))   (= dh'/dg)
+ *   up column f:    B = m g s                   (= dh'/du)
+ * with g, u the fp32 products, s = 1 / (1 + exp(-g)) and m the dropout multiplier
+ * of g5moe_dropout (keep ? scale : 0; 1 without dropout), so that the backward
+ * needs neither the mask nor exp.  Replaces keeping `self.wi_0(x)` /
+ * `self.wi_1(x)` for autograd (lib/blocks/_component.py:50). */
+g5moe_status g5moe_expert_gate_up_train_factors(const void* x, const int32_t* perm,
+                                                const int32_t* offsets, const void* w_gate_up,
+                                                void* ab, void* ws, const g5moe_dropout* dropout,
+                                                const g5moe_shape* shape, void* stream);
+
 /* Grouped down GEMM: y_perm[p] = h[p] . Wd_e^T (bf16 out, fp32 accumulate),
  * h read from the workspace written by g5moe_expert_gate_up.  Replaces
  * `self.wo(hidden)` (lib/blocks/_component.py:44, :52).
@@ -310,6 +325,24 @@ g5moe_status g5moe_gate_grad_padded(const void* dy, const void* y_perm, const in
                                     const float* topk_w, const int32_t* offsets, float* dw,
                                     void* dy_pad, int32_t kmax, const g5moe_shape* shape,
                                     void* stream);
+
+/* The dh product and the SwiGLU backward in one launch (the derivative of
+ * LigerSiLUMulFunction's silu(a) * b, lib/blocks/_component.py:31, :50): for
+ * expert e's j-th row, dh = dy_pad[e*kmax + j] . Wd_e (fp32 accumulation, rounded
+ * to bf16 as g5moe_grouped_gemm_padded stores it), and with A, B the factors of
+ * row offsets[e] + j in ab (g5moe_expert_gate_up_train_factors):
+ *   dgu_pad[e*kmax + j][gate f] = bf16(dh[f] * A[f]),
+ *   dgu_pad[e*kmax + j][up f]   = bf16(dh[f] * B[f])   for j < M_e,
+ *   zeros for M_e <= j < max(384, 192 * ceil(M_e / 192)) (the rows
+ *   g5moe_weight_grad reads), rows past those not written.
+ * dy_pad : bf16 [E*kmax + 256, d] (g5moe_gate_grad_padded's);  w_down_t : bf16
+ * [E, F, d] (g5moe_transpose_experts of w_down);  dgu_pad : bf16 [E*kmax + 256, 2F]
+ * (g5moe_grouped_gemm_padded's A operand for dX and g5moe_weight_grad's dgu_pad).
+ * kmax a multiple of 192, >= 384 and >= every M_e; F a multiple of 256; buffers
+ * 16-byte aligned. */
+g5moe_status g5moe_dh_swiglu_backward(const void* dy_pad, int32_t kmax, const int32_t* offsets,
+                                      const void* w_down_t, const void* ab, void* dgu_pad,
+                                      const g5moe_shape* shape, void* stream);
 
 /* Router-logit gradient through the renormalised top-k softmax:
  *   dlogits[t, i_r] = w_r * (dw_r - sum_s w_s dw_s) for the chosen experts,

@@ -466,3 +466,91 @@ def test_router_weight_grad_vs_float64(cuda_device, n, E, d):
     print(f"  n={n} E={E} d={d}: max err/bound {float((err / np.maximum(bound, 1e-30)).max()):.3f}",
           flush=True)
     assert np.all(err <= bound)
+
+
+def _split_packed(t, F):
+    """[rows, 2F] packed gate|up order -> (gate [rows, F], up [rows, F])."""
+    v = t.view(t.shape[0], F // 32, 2, 32)
+    return v[:, :, 0].reshape(t.shape[0], F), v[:, :, 1].reshape(t.shape[0], F)
+
+
+@pytest.mark.parametrize("p", [0.0, 0.2])
+@pytest.mark.parametrize("n,d,F,E,k", [(2048, 768, 3072, 16, 2), (700, 256, 512, 8, 2)])
+def test_gate_up_train_factors(cuda_device, n, d, F, E, k, p):
+    """g5moe_expert_gate_up_train_factors: h bit for bit g5moe_expert_gate_up_train's
+    (same dropout), and the factors A = m u s (1 + g (1 - s)), B = m g s against
+    float64 from the raw products (which are bf16-rounded, the kernel's are not:
+    normwise 1.5e-2 / 4e-3; measured 6e-3 / 2e-3), exactly zero where the mask drops."""
+    from oracle import moe_oracle as mo2
+    print(f"factors n={n} d={d} F={F} E={E} k={k} p={p}", flush=True)
+    inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=21, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    drop = (p, 0x1234_5678_9ABC) if p > 0 else None
+    raw = ops.moe_forward_train(x, wr, wgu, wd, k, dropout=drop, return_h=True)
+    fac = ops.moe_forward_train(x, wr, wgu, wd, k, dropout=drop, return_h=True, factors=True)
+    torch.cuda.synchronize()
+    for i in range(8):  # y, logits, routing, y_perm: the same
+        assert torch.equal(raw[i], fac[i]), i
+    assert torch.equal(raw[9], fac[9])  # h, and its zero slack rows
+    assert not raw[9][n * k:].any()
+    g, u = (t.float().cpu().numpy().astype(np.float64) for t in _split_packed(raw[8], F))
+    a, b = (host(t).astype(np.float64) for t in _split_packed(fac[8], F))
+    perm = raw[5].cpu().numpy()
+    if p > 0:
+        m = mo2.dropout_keep(perm, F, p, drop[1]) * float(mo2.dropout_scale(p))
+    else:
+        m = np.ones_like(g)
+    s = 1.0 / (1.0 + np.exp(-g))
+    a_ref = m * u * s * (1.0 + g * (1.0 - s))
+    b_ref = m * g * s
+    for got, ref, name in ((a, a_ref, "A"), (b, b_ref, "B")):
+        mx, mean = normwise(got, ref)
+        print(f"  {name}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
+        assert mx <= 1.5e-2 and mean <= 4e-3, (name, mx, mean)
+        assert np.all(got[m == 0] == 0), name
+
+
+@pytest.mark.parametrize("counts", [[0, 1, 192, 255, 256, 385, 2000, 4100], [700, 3, 0, 0]])
+def test_dh_swiglu_fused_equals_staged(cuda_device, counts):
+    """g5moe_dh_swiglu_backward against the staged computation: dh from
+    g5moe_grouped_gemm_padded (the same product, stored bf16), times the factors in
+    fp32 with one bf16 rounding (torch) — bit for bit in every expert's rows, zeros
+    in the rows up to the weight gradient's row count, rows past it untouched."""
+    import ctypes
+    from genet5_amd import _lib
+    dev = cuda_device
+    g = torch.Generator(device=dev).manual_seed(3)
+    E, d, F, k = len(counts), 768, 512, 2
+    offsets = np.zeros(E + 1, np.int32)
+    offsets[1:] = np.cumsum(counts)
+    T = int(offsets[-1])
+    t_off = torch.tensor(offsets, dtype=torch.int32, device=dev)
+    kmax = ops.wgrad_kmax(max(counts))
+    dy = torch.randn(T + ops.ROW_PAD, d, device=dev, generator=g).to(torch.bfloat16)
+    dy_buf = torch.zeros(E * kmax + ops.ROW_PAD, d, dtype=torch.bfloat16, device=dev)
+    dy_buf[:E * kmax] = ops.pad_rows(dy, None, t_off, E, kmax, k).view(E * kmax, d)
+    wd_t = (torch.randn(E, F, d, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    fac = torch.randn(T, 2 * F, device=dev, generator=g).to(torch.bfloat16)
+    sentinel = torch.full((E * kmax + ops.ROW_PAD, 2 * F), -7.0, dtype=torch.bfloat16,
+                          device=dev)
+    dgu = sentinel.clone()
+    n_tok = (T + k - 1) // k
+    shape = _lib.make_shape(n_tok, d, F, E, k, _lib.DTYPE_BF16)
+    print(f"  counts={counts} kmax={kmax}", flush=True)
+    _lib.call("g5moe_dh_swiglu_backward", ops._ptr(dy_buf), kmax, ops._ptr(t_off),
+              ops._ptr(wd_t), ops._ptr(fac), ops._ptr(dgu), ctypes.byref(shape),
+              ops._stream(dev))
+    dh = ops.grouped_gemm_padded(dy_buf, kmax, T, t_off, wd_t)  # [T, F] bf16
+    a, b = _split_packed(fac, F)
+    dg = (dh.float() * a.float()).to(torch.bfloat16)
+    du = (dh.float() * b.float()).to(torch.bfloat16)
+    ref = torch.stack([dg.view(T, F // 32, 32), du.view(T, F // 32, 32)], 2).reshape(T, 2 * F)
+    torch.cuda.synchronize()
+    for e, c in enumerate(counts):
+        o0 = int(offsets[e])
+        kr = max(384, 192 * -(-c // 192))
+        rows = dgu[e * kmax: e * kmax + kmax]
+        assert torch.equal(rows[:c], ref[o0:o0 + c]), e
+        assert not rows[c:kr].any(), e
+        assert torch.equal(rows[kr:], sentinel[:kmax - kr]), e
+    assert torch.equal(dgu[E * kmax:], sentinel[E * kmax:])

@@ -74,18 +74,28 @@ def test_gpu_mask_equals_host_restatement(cuda_device, p):
     print(f"  kept {frac:.5f} (expected {q:.5f})", flush=True)
 
 
+@pytest.mark.parametrize("fused", [False, True])
 @pytest.mark.parametrize("n,d,F,E,k,p", [(700, 256, 512, 8, 2, 0.2), (2048, 768, 3072, 16, 2, 0.1)])
-def test_forward_backward_vs_oracle_with_mask(cuda_device, n, d, F, E, k, p):
-    print(f"dropout fwd/bwd n={n} d={d} F={F} E={E} k={k} p={p}", flush=True)
+def test_forward_backward_vs_oracle_with_mask(cuda_device, n, d, F, E, k, p, fused):
+    """fused: the forward keeps the SwiGLU derivative factors (mask folded in) and
+    the backward computes dGU in the dh product's epilogue; otherwise the raw
+    gate|up products and the separate SwiGLU backward regenerating the mask."""
+    print(f"dropout fwd/bwd n={n} d={d} F={F} E={E} k={k} p={p} fused={fused}", flush=True)
     inp = synth.make_layer(n, d_model=d, d_ff=F, n_experts=E, top_k=k, seed=41, dtype="bf16")
     x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
     rng = np.random.default_rng(9)
     dy_np = synth.f32_to_bf16_bits(rng.standard_normal((n, d)).astype(np.float32))
     dy = dev_t(dy_np, cuda_device, True)
-    y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(
-        x, wr, wgu, wd, k, dropout=(p, SEED))
-    grads = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm,
-                             gu=gu, dropout=(p, SEED))
+    if fused:
+        y, logits, idx, w, offsets, perm, inv_pos, y_perm, fac, h = ops.moe_forward_train(
+            x, wr, wgu, wd, k, dropout=(p, SEED), return_h=True, factors=True)
+        grads = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm,
+                                 h=h, factors=fac)
+    else:
+        y, logits, idx, w, offsets, perm, inv_pos, y_perm, gu = ops.moe_forward_train(
+            x, wr, wgu, wd, k, dropout=(p, SEED))
+        grads = ops.moe_backward(dy, x, wr, wgu, wd, k, idx, w, offsets, perm, inv_pos, y_perm,
+                                 gu=gu, dropout=(p, SEED))
     y0 = ops.moe_forward_train(x, wr, wgu, wd, k)[0]
     torch.cuda.synchronize()
     ref_i, _ = oracle.topk_gates_c(oracle.router_logits(inp.x, inp.w_router), k)
