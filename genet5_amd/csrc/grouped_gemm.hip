@@ -45,6 +45,8 @@
 // feature blocks 2j and 2j+1 hold gate and up of the same 32 h columns in the
 // same lanes; silu(g) * u is formed in registers and only h is stored (bf16).
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -75,6 +77,8 @@ struct GemmArgs {
   float drop_scale;
   const uint16_t* aux;    // MODE 4: the forward's SwiGLU derivative factors [N*k, 2 Nout]
                           // (packed gate|up order, sorted positions), read in the epilogue
+  int* claims;            // nullptr, or this launch's {claim, done} counters (zero at
+                          // launch; the last workgroup resets them): the claimed tail
 };
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
@@ -1133,12 +1137,67 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
           Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
     }
   } else {
-    // one pass: the remainder tile of slots s < r is lo + s + q * nslot
-    const int cnt = q + (slot < r ? 1 : 0);
-    if (cnt > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP>(
-          args, off, smem, Units{lo + slot, nslot, cnt, 0});
+    // Static: the remainder tile of slots s < r is lo + s + q * nslot.  With
+    // claims (a claimed tail): every workgroup first runs Q = total / ng - 1
+    // tiles of its XCD's contiguous range (slot-strided as above), and the
+    // remaining total - Q ng tiles (between ng and 2 ng of them) are claimed one
+    // at a time from a counter, so that XCDs that run faster take more of them.
+    // A claim happens between tiles, outside the k-step stream: thread 0 takes
+    // the next index and passes it through LDS (every stage buffer is idle then).
+    const bool claimed = args.claims != nullptr;
+    const int Qs = max(0, total / ng - 1);
+    Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
+    if (claimed) st = Units{Qs * before + slot, nslot, Qs, 0};
+    if (st.count > 0)
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP>(args, off, smem, st);
+    if (claimed) {
+      const int pool = total - Qs * ng;
+      int* const mbox = reinterpret_cast<int*>(smem);
+      for (;;) {
+        __syncthreads();  // every wave is past the previous tile (its DMAs landed)
+        if (threadIdx.x == 0) mbox[0] = atomicAdd(args.claims, 1);
+        __syncthreads();
+        const int u = __builtin_amdgcn_readfirstlane(mbox[0]);
+        __syncthreads();  // every wave has read the index before the stages refill
+        if (u >= pool) break;
+        tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP>(
+            args, off, smem, Units{Qs * ng + u, 1, 1, 0});
+      }
+      // the last workgroup out resets the counters for the slot's next launch
+      if (threadIdx.x == 0 && atomicAdd(args.claims + 1, 1) == ng - 1) {
+        atomicExch(args.claims, 0);
+        atomicExch(args.claims + 1, 0);
+      }
+    }
   }
+}
+
+// Claim counters of the claimed-tail GEMM launches: kClaimSlots pairs {claim,
+// done}, zero at load; each launch takes the next slot (rotating), so launches
+// that overlap on different streams use different counters unless more than
+// kClaimSlots of them are in flight at once.
+constexpr int kClaimSlots = 64;
+__device__ __align__(256) int gemm_tail_claims[2 * kClaimSlots];
+
+// This launch's counter pair on the current device, or nullptr (static
+// schedule) if the symbol lookup fails.
+int* next_claim_slot() {
+  static std::mutex mu;
+  static int* addr[kMaxDevices] = {};
+  static std::atomic<unsigned> next{0};
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
+  int* base;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    if (addr[dev] == nullptr) {
+      void* p = nullptr;
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(gemm_tail_claims)) != hipSuccess) return nullptr;
+      addr[dev] = static_cast<int*>(p);
+    }
+    base = addr[dev];
+  }
+  return base + 2 * (next.fetch_add(1) % kClaimSlots);
 }
 
 }  // namespace
@@ -1254,6 +1313,7 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
+  a.claims = next_claim_slot();
   const bool dropout = drop != nullptr && drop->on;
   if (dropout) {
     if (gu == nullptr) return hipErrorInvalidValue;  // dropout is a training-forward mode
@@ -1292,6 +1352,7 @@ hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int3
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout),
                                  unsigned(device_cu_count()));
+  a.claims = next_claim_slot();
   if (drop.on) {
     a.drop_seed_lo = drop.seed_lo;
     a.drop_seed_hi = drop.seed_hi;
@@ -1377,6 +1438,7 @@ hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout),
                                  unsigned(device_cu_count()));
+  a.claims = next_claim_slot();
   launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 2, false>(grid, a, st);
   return hipGetLastError();
 }
