@@ -1137,14 +1137,17 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
           Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
     }
   } else {
-    // Static: the remainder tile of slots s < r is lo + s + q * nslot.  With
-    // claims (a claimed tail): every workgroup first runs Q = total / ng - 1
-    // tiles of its XCD's contiguous range (slot-strided as above), and the
-    // remaining total - Q ng tiles (between ng and 2 ng of them) are claimed one
-    // at a time from a counter, so that XCDs that run faster take more of them.
-    // A claim happens between tiles, outside the k-step stream: thread 0 takes
-    // the next index and passes it through LDS (every stage buffer is idle then).
-    const bool claimed = args.claims != nullptr;
+    // Static: the remainder tile of slots s < r is lo + s + q * nslot.  Claimed
+    // tail (with claim counters and at least 8 tiles per workgroup): every
+    // workgroup first runs Q = total / ng - 1 tiles of its XCD's contiguous range
+    // (slot-strided as above), and the remaining total - Q ng tiles (between ng
+    // and 2 ng of them) are claimed one at a time from a counter, so that XCDs
+    // that run faster take more of them.  A claim happens between tiles, outside
+    // the k-step stream: thread 0 takes the next index and passes it through LDS
+    // (every stage buffer is idle then).  With a few tiles per workgroup the
+    // claimed tiles' pipeline restarts cost more than the balance gains (3-7 %
+    // slower at 3-5 tiles per CU).
+    const bool claimed = args.claims != nullptr && total >= 8 * ng;
     const int Qs = max(0, total / ng - 1);
     Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
     if (claimed) st = Units{Qs * before + slot, nslot, Qs, 0};
