@@ -516,6 +516,92 @@ __global__ __launch_bounds__(256) void input_grad_kernel(
   }
 }
 
+// The same dx for GeneT5's shape (k = 2, E = 16, bf16), persistent: thread c of a
+// token row owns columns 8c .. 8c + 7 and keeps those columns of all 16 router
+// weight rows in fp32 registers for the whole launch (the per-token kernel above
+// re-reads and converts 256 bytes of them per token); a block walks R rows at a
+// time with the next rows' positions, dX_perm rows and dlogits in flight.  The
+// arithmetic is the per-token kernel's, in the same order.
+template <int D>
+__global__ __launch_bounds__(256) void input_grad_persist_kernel(
+    const uint16_t* __restrict__ dxp, const int32_t* __restrict__ inv_pos,
+    const float* __restrict__ dlogits, const uint16_t* __restrict__ w_router,
+    uint16_t* __restrict__ dx, int64_t n_tokens) {
+  constexpr int CPR = D / 8;        // threads per token row
+  constexpr int R = 256 / CPR;      // rows per block step
+  constexpr int NE = 16;
+  const int c = threadIdx.x % CPR, r = threadIdx.x / CPR;
+  if (r >= R) return;
+  const int c0 = 8 * c;
+  float w[NE][8];
+#pragma unroll
+  for (int e = 0; e < NE; ++e) {
+    const uint4 v = *reinterpret_cast<const uint4*>(w_router + e * D + c0);
+    const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      w[e][2 * j] = bf_lo(vv[j]);
+      w[e][2 * j + 1] = bf_hi(vv[j]);
+    }
+  }
+  const int64_t step = int64_t(gridDim.x) * R;
+  int64_t t = int64_t(blockIdx.x) * R + r;
+  if (t >= n_tokens) return;
+  // loads of token t: its two positions, then their rows and its dlogits row
+  struct In {
+    int32_t p0, p1;
+    uint4 v0, v1;
+    float4 g[NE / 4];
+  };
+  auto load = [&](int64_t tt, In& in) __attribute__((always_inline)) {
+    const int2 pp = *reinterpret_cast<const int2*>(inv_pos + 2 * tt);
+    in.p0 = pp.x;
+    in.p1 = pp.y;
+    in.v0 = in.p0 >= 0 ? *reinterpret_cast<const uint4*>(dxp + int64_t(in.p0) * D + c0)
+                       : make_uint4(0, 0, 0, 0);
+    in.v1 = in.p1 >= 0 ? *reinterpret_cast<const uint4*>(dxp + int64_t(in.p1) * D + c0)
+                       : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int q = 0; q < NE / 4; ++q)
+      in.g[q] = *reinterpret_cast<const float4*>(dlogits + tt * NE + 4 * q);
+  };
+  In cur;
+  load(t, cur);
+  for (;;) {
+    const int64_t tn = t + step;
+    In nxt;
+    const bool more = tn < n_tokens;
+    load(more ? tn : t, nxt);  // unconditional (an in-bounds repeat at the end)
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.f;
+    auto add_row = [&](const uint4& v) __attribute__((always_inline)) {
+      const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        acc[2 * j] += bf_lo(vv[j]);
+        acc[2 * j + 1] += bf_hi(vv[j]);
+      }
+    };
+    if (cur.p0 >= 0) add_row(cur.v0);
+    if (cur.p1 >= 0) add_row(cur.v1);
+    const float gv[NE] = {cur.g[0].x, cur.g[0].y, cur.g[0].z, cur.g[0].w,
+                          cur.g[1].x, cur.g[1].y, cur.g[1].z, cur.g[1].w,
+                          cur.g[2].x, cur.g[2].y, cur.g[2].z, cur.g[2].w,
+                          cur.g[3].x, cur.g[3].y, cur.g[3].z, cur.g[3].w};
+#pragma unroll
+    for (int e = 0; e < NE; ++e)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(gv[e], w[e][j], acc[j]);
+    *reinterpret_cast<uint4*>(dx + t * D + c0) =
+        make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
+                   pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
+    if (!more) break;
+    t = tn;
+    cur = nxt;
+  }
+}
+
 // W [E, R, C] -> WT [E, C, R] (bf16), 64 x 64 tiles through LDS; R and C are
 // multiples of 64.
 __global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restrict__ w,
@@ -628,6 +714,26 @@ hipError_t launch_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const 
                              hipStream_t st) {
   const int64_t work = s.n_tokens * (s.d_model / 8);
   if (work == 0) return hipSuccess;
+  if (s.x_dtype == G5MOE_DTYPE_BF16 && s.top_k == 2 && s.n_experts == 16) {
+    // GeneT5's shape: the persistent kernel (router weights held in registers)
+    auto go_p = [&](auto d_c) {
+      constexpr int D = decltype(d_c)::value;
+      constexpr int R = 256 / (D / 8);
+      const int64_t blocks = (s.n_tokens + R - 1) / R;
+      const unsigned grid =
+          unsigned(std::min<int64_t>(blocks, int64_t(4) * device_cu_count()));
+      hipLaunchKernelGGL(input_grad_persist_kernel<D>, dim3(grid), dim3(R * (D / 8)), 0, st, dxp,
+                         inv_pos, dlogits, static_cast<const uint16_t*>(w_router),
+                         static_cast<uint16_t*>(dx), s.n_tokens);
+    };
+    switch (s.d_model) {
+      case 128: go_p(std::integral_constant<int, 128>{}); return hipGetLastError();
+      case 256: go_p(std::integral_constant<int, 256>{}); return hipGetLastError();
+      case 512: go_p(std::integral_constant<int, 512>{}); return hipGetLastError();
+      case 768: go_p(std::integral_constant<int, 768>{}); return hipGetLastError();
+      default: break;
+    }
+  }
   const unsigned grid = unsigned((work + 255) / 256);
   auto go = [&](auto f32_c, auto topk_c, auto ne_c) {
     hipLaunchKernelGGL((input_grad_kernel<decltype(f32_c)::value, decltype(topk_c)::value,

@@ -21,6 +21,7 @@ from .moe_oracle import (  # noqa: F401
     dispatch,
     dispatch_c,
     expert_forward,
+    input_grad_c,
     moe_backward,
     moe_forward,
     router_logits,

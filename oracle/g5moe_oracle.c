@@ -190,6 +190,31 @@ int g5o_add_rmsnorm(const void* x_add, const void* res, int dtype, const float* 
   return 0;
 }
 
+/* Input gradient (g5moe_input_grad): for token t and column j, in fp32,
+ *   acc = 0; acc += dxp[inv_pos[t*k+s]][j] for s = 0 .. k-1 (skipping p < 0);
+ *   acc = fmaf(dl[t][e], wr[e][j], acc) for e = 0 .. E-1;
+ * out[t][j] = T(acc).  dxp bf16 bits [N*k, d]; dl fp32 [N, E]; wr and out in
+ * dtype T (0 = bf16 bits, 1 = fp32). */
+int g5o_input_grad(const uint16_t* dxp, const int32_t* inv_pos, const float* dl,
+                   const void* wr, int dtype, int64_t n, int d, int k, int n_experts,
+                   void* out) {
+  if (dtype != 0 && dtype != 1) return 1;
+  for (int64_t t = 0; t < n; ++t) {
+    for (int j = 0; j < d; ++j) {
+      float acc = 0.0f;
+      for (int s = 0; s < k; ++s) {
+        const int32_t p = inv_pos[(size_t)t * k + s];
+        if (p < 0) continue;
+        acc = acc + bf16_to_f32(dxp[(size_t)p * d + j]);
+      }
+      for (int e = 0; e < n_experts; ++e)
+        acc = fmaf(dl[(size_t)t * n_experts + e], load_elem(wr, dtype, (size_t)e * d + j), acc);
+      store_elem(out, dtype, (size_t)t * d + j, acc);
+    }
+  }
+  return 0;
+}
+
 /* Combine (residual == NULL) or combine added into the residual stream.
  * y_perm: bf16 bits [N*k, d]; inv_pos int32 [N*k]; w fp32 [N, k]. */
 int g5o_combine(const uint16_t* y_perm, const int32_t* inv_pos, const float* w,

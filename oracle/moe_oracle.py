@@ -45,6 +45,11 @@ combine_c
     `hidden_states + ff_output * alpha` (lib/blocks/encoder.py:89).  Pins:
     exact-rational fma restatement; k = 1, w = 1 returns y_perm bit for bit;
     the residual composition equals torch's own bf16 ops (CPU) on y_moe.
+input_grad_c
+    The C restatement of g5moe_input_grad (dX_perm rows added in slot order,
+    then fmaf over experts in order, one rounding).  Pins: an exact-rational
+    restatement (each addition and fma rounded once to fp32) on small inputs,
+    including skipped positions; with zero dlogits it is the slot sum.
 moe_backward
     Float64 textbook backward of the layer for fixed routing indices: gate
     gradient dw = dy . Y, dY = w dy, dh = dY Wd_e, SwiGLU derivative
@@ -112,8 +117,10 @@ def _clib():
                                       ctypes.c_int, P, P, P]
         L.g5o_combine.argtypes = [P, P, P, P, ctypes.c_float, ctypes.c_int, ctypes.c_int64,
                                   ctypes.c_int, ctypes.c_int, P]
+        L.g5o_input_grad.argtypes = [P, P, P, P, ctypes.c_int, ctypes.c_int64, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_int, P]
         for f in (L.g5o_router_logits_f32, L.g5o_router_logits_bf16, L.g5o_topk, L.g5o_dispatch,
-                  L.g5o_add_rmsnorm, L.g5o_combine):
+                  L.g5o_add_rmsnorm, L.g5o_combine, L.g5o_input_grad):
             f.restype = ctypes.c_int
         _LIB = L
     return _LIB
@@ -457,6 +464,26 @@ def add_rmsnorm_np(residual_f32: np.ndarray, weight: np.ndarray, eps: float,
     rstd = np.float32(1.0) / np.sqrt(ss / np.float32(d) + np.float32(eps))
     normed = round_bf16((s * rstd[:, None]) * np.asarray(weight, np.float32)[None, :])
     return normed, (s if x_add_f32 is not None else None)
+
+
+def input_grad_c(dxp_bits: np.ndarray, inv_pos: np.ndarray, dlogits: np.ndarray,
+                 w_router: np.ndarray, out_dtype: str = "bf16") -> np.ndarray:
+    """C restatement of g5moe_input_grad: per column, the dX_perm rows added in slot
+    order from 0 (rows with a negative position skipped), then fmaf of dlogits and
+    the router weight in expert order, one rounding to out_dtype.  dxp as uint16
+    bf16 bits [N*k, d]; w_router and the result as uint16 bits ("bf16") or fp32."""
+    dl = np.ascontiguousarray(dlogits, np.float32)
+    N, E = dl.shape
+    ip = np.ascontiguousarray(inv_pos, np.int32).reshape(N, -1)
+    k = ip.shape[1]
+    xp = np.ascontiguousarray(dxp_bits, np.uint16)
+    d = xp.shape[1]
+    code = 0 if out_dtype == "bf16" else 1
+    wr = np.ascontiguousarray(w_router, np.uint16 if code == 0 else np.float32)
+    out = np.empty((N, d), np.uint16 if code == 0 else np.float32)
+    if _clib().g5o_input_grad(_p(xp), _p(ip), _p(dl), _p(wr), code, N, d, k, E, _p(out)) != 0:
+        raise ValueError("bad dtype")
+    return out
 
 
 def combine_c(y_perm_bits: np.ndarray, inv_pos: np.ndarray, topk_w: np.ndarray,

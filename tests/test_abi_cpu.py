@@ -154,6 +154,24 @@ def test_fake_impl_traces_shape():
         assert y.shape == x.shape and y.dtype == x.dtype
 
 
+def test_training_op_fake_impl_shapes():
+    """The training op's fake implementation (torch.compile traces it) gives the
+    real op's ten outputs: y, logits, routing, y_perm, the SwiGLU operand for the
+    backward [N*k, 2F] and the forward's h with its 384 slack rows."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+    from genet5_amd.moe import _moe_forward_train_op
+    N, d, F, E, k = 10, 768, 3072, 16, 2
+    with FakeTensorMode():
+        b = dict(dtype=torch.bfloat16)
+        outs = _moe_forward_train_op(
+            torch.empty(N, d, **b), torch.empty(E, d, **b), None, torch.empty(E, F, d, **b),
+            torch.empty(E, F, d, **b), torch.empty(E, d, F, **b), torch.empty(E, 2 * F, d, **b),
+            torch.empty(E, d, 2 * F, **b), torch.empty(E, F, d, **b), k, 0.1, 123)
+        shapes = [tuple(t.shape) for t in outs]
+    assert shapes == [(N, d), (N, E), (N, k), (N, k), (E + 1,), (N * k,), (N * k,), (N * k, d),
+                      (N * k, 2 * F), (N * k + ops.H_SLACK, F)]
+
+
 @pytest.mark.parametrize("args,code,msg", [
     (dict(n=-1), 1, "n_rows"),
     (dict(dtype=3), 1, "dtype"),

@@ -554,3 +554,30 @@ def test_dh_swiglu_fused_equals_staged(cuda_device, counts):
         assert not rows[c:kr].any(), e
         assert torch.equal(rows[kr:], sentinel[:kmax - kr]), e
     assert torch.equal(dgu[E * kmax:], sentinel[E * kmax:])
+
+
+@pytest.mark.parametrize("n,d,E,k", [(36400, 768, 16, 2), (4097, 768, 16, 2), (1, 768, 16, 2),
+                                     (777, 256, 16, 2), (300, 128, 16, 2), (500, 512, 8, 2),
+                                     (333, 768, 16, 1)])
+def test_input_grad_bit_exact(cuda_device, n, d, E, k):
+    """g5moe_input_grad against the C restatement (oracle.input_grad_c, pinned by
+    exact rationals) bit for bit: the persistent kernel (k = 2, E = 16, bf16:
+    router weights held in registers, rows walked with prefetch, ragged last
+    block) and the per-token kernel (other shapes), with skipped positions."""
+    import ctypes
+    from genet5_amd import _lib
+    dev = cuda_device
+    g = torch.Generator(device=dev).manual_seed(n + d)
+    dxp = torch.randn(n * k, d, device=dev, generator=g).to(torch.bfloat16)
+    inv = torch.randperm(n * k, device=dev, generator=g).to(torch.int32)
+    inv[::7] = -1
+    dl = torch.randn(n, E, device=dev, generator=g) * 0.1
+    wr = torch.randn(E, d, device=dev, generator=g).to(torch.bfloat16)
+    dx = torch.empty(n, d, dtype=torch.bfloat16, device=dev)
+    shape = _lib.make_shape(n, d, 512, E, k, _lib.DTYPE_BF16)
+    _lib.call("g5moe_input_grad", ops._ptr(dxp), ops._ptr(inv), ops._ptr(dl), ops._ptr(wr),
+              ops._ptr(dx), ctypes.byref(shape), ops._stream(dev))
+    torch.cuda.synchronize()
+    bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = oracle.input_grad_c(bits(dxp), inv.cpu().numpy(), dl.cpu().numpy(), bits(wr))
+    np.testing.assert_array_equal(bits(dx), ref)

@@ -183,3 +183,41 @@ def test_combine_residual_equals_torch_composition(alpha):
     out32 = oracle.combine_c(y_perm, inv, w, res, alpha, out_dtype="f32")
     ref32 = torch.from_numpy(res) + torch.from_numpy(y32) * np.float32(alpha)
     np.testing.assert_array_equal(out32.view(np.uint32), ref32.numpy().view(np.uint32))
+
+
+def test_input_grad_c_matches_exact_rational():
+    """oracle.input_grad_c: each slot addition and each fma rounded once to fp32, in
+    slot then expert order (a skipped position included); fp32 and bf16 outputs."""
+    rng = np.random.default_rng(4)
+    n, d, k, E = 3, 64, 2, 5
+    dxp = bf16_bits(rng.standard_normal((n * k, d)).astype(np.float32))
+    inv = rng.permutation(n * k).astype(np.int32)
+    inv[3] = -1
+    dl = (rng.standard_normal((n, E)) * 0.1).astype(np.float32)
+    wr = rng.standard_normal((E, d)).astype(np.float32)
+    got = oracle.input_grad_c(dxp, inv, dl, wr, out_dtype="f32")
+    xp = mo.bf16_to_f32(dxp)
+    for t in range(n):
+        for j in range(d):
+            acc = np.float32(0)
+            for s in range(k):
+                p = inv[t * k + s]
+                if p >= 0:
+                    acc = add_exact(acc, xp[p, j])
+            for e in range(E):
+                acc = fma_exact(dl[t, e], wr[e, j], acc)
+            assert got[t, j].view(np.uint32) == np.float32(acc).view(np.uint32), (t, j)
+    wb = bf16_bits(wr)
+    gb = oracle.input_grad_c(dxp, inv, dl, wb, out_dtype="bf16")
+    g32 = oracle.input_grad_c(dxp, inv, dl, mo.bf16_to_f32(wb), out_dtype="f32")
+    np.testing.assert_array_equal(gb, bf16_bits(g32))
+
+
+def test_input_grad_c_without_logits_is_slot_sum():
+    rng = np.random.default_rng(5)
+    dxp = bf16_bits(rng.standard_normal((40, 128)).astype(np.float32))
+    inv = rng.permutation(40).astype(np.int32)
+    out = oracle.input_grad_c(dxp, inv, np.zeros((20, 16), np.float32),
+                              np.ones((16, 128), np.float32), out_dtype="f32")
+    xp = mo.bf16_to_f32(dxp)[inv].reshape(20, 2, 128)
+    np.testing.assert_array_equal(out, xp[:, 0] + xp[:, 1])
