@@ -24,6 +24,7 @@ EXPORTED = (
     "g5moe_version",
     "g5moe_workspace_size",
     "g5moe_pack_gate_up",
+    "g5moe_pack_gate_up_transposed",
     "g5moe_router_topk",
     "g5moe_dispatch",
     "g5moe_dispatch_noalloc",
@@ -127,6 +128,7 @@ _SIGS = {
     "g5moe_version": ([], ctypes.c_int32),
     "g5moe_workspace_size": ([_SHAPE_P, ctypes.POINTER(ctypes.c_size_t)], ctypes.c_int),
     "g5moe_pack_gate_up": ([_P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_pack_gate_up_transposed": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_router_topk": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_dispatch": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_dispatch_noalloc": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),

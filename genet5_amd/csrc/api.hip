@@ -126,6 +126,24 @@ g5moe_status g5moe_pack_gate_up(const void* w_gate, const void* w_up, void* w_ga
                     "g5moe_pack_gate_up");
 }
 
+g5moe_status g5moe_pack_gate_up_transposed(const void* w_gate, const void* w_up,
+                                           void* w_gate_up, void* w_gate_up_t,
+                                           const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(w_gate);
+  G5_NONNULL(w_up);
+  G5_NONNULL(w_gate_up_t);
+  if (shape->d_model % 64 != 0)
+    return fail(G5MOE_ERR_UNSUPPORTED, "pack_gate_up_transposed: d_model %d not a multiple of 64",
+                int(shape->d_model));
+  return hip_status(launch_pack_gate_up_t(static_cast<const uint16_t*>(w_gate),
+                                          static_cast<const uint16_t*>(w_up),
+                                          static_cast<uint16_t*>(w_gate_up),
+                                          static_cast<uint16_t*>(w_gate_up_t), *shape,
+                                          as_stream(stream)),
+                    "g5moe_pack_gate_up_transposed");
+}
+
 g5moe_status g5moe_router_topk(const void* x, const void* w_router, const float* bias,
                                int32_t* topk_idx, float* topk_w, float* logits,
                                const g5moe_shape* shape, void* stream) {

@@ -626,7 +626,45 @@ __global__ __launch_bounds__(256) void transpose_kernel(const uint16_t* __restri
   }
 }
 
+// Packed gate|up and its per-expert transpose in one pass over gate and up:
+// block (x, y, e) moves packed rows [64y, 64y + 64) (gate rows 32y .. 32y + 31,
+// then the matching up rows) by columns [64x, 64x + 64): the rows straight into
+// w_gate_up [E, 2F, d] (when given), and through LDS into w_gate_up_t [E, d, 2F].
+__global__ __launch_bounds__(256) void pack_gate_up_t_kernel(
+    const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu, uint16_t* __restrict__ wgu,
+    uint16_t* __restrict__ wgu_t, int F, int d) {
+  __shared__ uint16_t tile[64][66];
+  const int e = blockIdx.z;
+  const int rb = blockIdx.y, c0 = blockIdx.x * 64;
+  const int64_t F2 = 2 * int64_t(F);
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = ty + 4 * i;  // packed row 64 rb + r
+    const uint16_t* src = (r < 32 ? wg : wu) + (int64_t(e) * F + 32 * rb + (r & 31)) * d;
+    const uint16_t v = src[c0 + tx];
+    tile[r][tx] = v;
+    if (wgu != nullptr) wgu[(int64_t(e) * F2 + 64 * rb + r) * d + c0 + tx] = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int c = ty + 4 * i;
+    wgu_t[(int64_t(e) * d + c0 + c) * F2 + 64 * rb + tx] = tile[tx][c];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_pack_gate_up_t(const uint16_t* wg, const uint16_t* wu, uint16_t* wgu,
+                                 uint16_t* wgu_t, const g5moe_shape& s, hipStream_t st) {
+  if (s.n_experts == 0) return hipSuccess;
+  if (s.d_model % 64 != 0 || s.d_ff % 32 != 0) return hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_gate_up_t_kernel,
+                     dim3(unsigned(s.d_model / 64), unsigned(s.d_ff / 32), unsigned(s.n_experts)),
+                     dim3(256), 0, st, wg, wu, wgu, wgu_t, s.d_ff, s.d_model);
+  return hipGetLastError();
+}
 
 hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const int32_t* inv_pos,
                             const float* topk_w, float* dw, uint16_t* dyp,

@@ -177,6 +177,9 @@ hipError_t launch_combine(const uint16_t* y_perm, const int32_t* inv_pos, const 
                           void* y, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_pack_gate_up(const uint16_t* wg, const uint16_t* wu, uint16_t* wgu,
                                const g5moe_shape& s, hipStream_t st);
+// the packed gate|up (wgu, may be nullptr) and its per-expert transpose wgu_t
+hipError_t launch_pack_gate_up_t(const uint16_t* wg, const uint16_t* wu, uint16_t* wgu,
+                                 uint16_t* wgu_t, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_cast_f32_bf16(const float* x, uint16_t* xb, int64_t n, hipStream_t st);
 hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t* v, uint16_t* o,
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,

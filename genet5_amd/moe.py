@@ -268,9 +268,15 @@ class MoEFeedForward(nn.Module):
                 wg = self.w_gate.detach().to(torch.bfloat16).contiguous()
                 wu = self.w_up.detach().to(torch.bfloat16).contiguous()
                 wd = self.w_down.detach().to(torch.bfloat16).contiguous()
-                self._packed = (ops.pack_gate_up(wg, wu), wd)
+                if transposed:
+                    # the packed copy and its transpose in one pass over gate and up
+                    wgu, wgu_t = ops.pack_gate_up_transposed(wg, wu)
+                    self._packed = (wgu, wd)
+                    self._transposed = (wgu_t, ops.transpose_experts(wd))
+                else:
+                    self._packed = (ops.pack_gate_up(wg, wu), wd)
+                    self._transposed = None
             self._packed_key = key
-            self._transposed = None
         if not transposed:
             return self._packed
         if self._transposed is None:

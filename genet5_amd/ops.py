@@ -79,6 +79,20 @@ def pack_gate_up(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def pack_gate_up_transposed(w_gate: torch.Tensor, w_up: torch.Tensor):
+    """(pack_gate_up(w_gate, w_up), its per-expert transpose [E, d, 2F]) in one pass."""
+    dev = _check_device(w_gate)
+    E, F, d = w_gate.shape
+    _require(w_gate, "w_gate", (E, F, d), torch.bfloat16, dev)
+    _require(w_up, "w_up", (E, F, d), torch.bfloat16, dev)
+    out = torch.empty((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
+    out_t = torch.empty((E, d, 2 * F), dtype=torch.bfloat16, device=dev)
+    shape = _lib.make_shape(0, d, F, E, 1, _lib.DTYPE_BF16)
+    _lib.call("g5moe_pack_gate_up_transposed", _ptr(w_gate), _ptr(w_up), _ptr(out), _ptr(out_t),
+              ctypes.byref(shape), _stream(dev))
+    return out, out_t
+
+
 def router_topk(x2d: torch.Tensor, w_router: torch.Tensor, top_k: int,
                 bias: Optional[torch.Tensor] = None, return_logits: bool = False):
     """Router on [N, d] -> (topk_idx int32 [N, k], topk_w fp32 [N, k][, logits fp32 [N, E]])."""

@@ -88,6 +88,15 @@ g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes);
 g5moe_status g5moe_pack_gate_up(const void* w_gate, const void* w_up, void* w_gate_up,
                                 const g5moe_shape* shape, void* stream);
 
+/* g5moe_pack_gate_up and the packed weight's per-expert transpose in one pass over
+ * w_gate and w_up (the backward's dX product reads the transpose):
+ *   w_gate_up : bf16 [E, 2F, d] out, or NULL (only the transpose);
+ *   w_gate_up_t : bf16 [E, d, 2F] out, w_gate_up_t[e][c][r] = w_gate_up[e][r][c].
+ * d a multiple of 64.  No reference counterpart (a layout step of this library). */
+g5moe_status g5moe_pack_gate_up_transposed(const void* w_gate, const void* w_up,
+                                           void* w_gate_up, void* w_gate_up_t,
+                                           const g5moe_shape* shape, void* stream);
+
 /* Router: fp32 logits, top-k with a lower-index tie-break, renormalised gates.
  * New stage (the reference has no router; README.md:12 "16 experts top-2").
  *   x        : [N, d] in x_dtype          w_router : [E, d] in x_dtype

@@ -581,3 +581,26 @@ def test_input_grad_bit_exact(cuda_device, n, d, E, k):
     bits = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
     ref = oracle.input_grad_c(bits(dxp), inv.cpu().numpy(), dl.cpu().numpy(), bits(wr))
     np.testing.assert_array_equal(bits(dx), ref)
+
+
+@pytest.mark.parametrize("E,F,d", [(16, 3072, 768), (3, 128, 128), (2, 512, 256)])
+def test_pack_gate_up_transposed(cuda_device, E, F, d):
+    """g5moe_pack_gate_up_transposed: the packed weight bit for bit g5moe_pack_gate_up's,
+    and the transpose bit for bit g5moe_transpose_experts of it; with a NULL packed
+    output only the transpose is written."""
+    import ctypes
+    from genet5_amd import _lib
+    g = torch.Generator(device=cuda_device).manual_seed(E * F)
+    wg = torch.randn(E, F, d, device=cuda_device, generator=g).to(torch.bfloat16)
+    wu = torch.randn(E, F, d, device=cuda_device, generator=g).to(torch.bfloat16)
+    wgu, wgu_t = ops.pack_gate_up_transposed(wg, wu)
+    ref = ops.pack_gate_up(wg, wu)
+    ref_t = ops.transpose_experts(ref)
+    only_t = torch.empty_like(wgu_t)
+    shape = _lib.make_shape(0, d, F, E, 1, _lib.DTYPE_BF16)
+    _lib.call("g5moe_pack_gate_up_transposed", ops._ptr(wg), ops._ptr(wu), None,
+              ops._ptr(only_t), ctypes.byref(shape), ops._stream(cuda_device))
+    torch.cuda.synchronize()
+    assert torch.equal(wgu, ref)
+    assert torch.equal(wgu_t, ref_t)
+    assert torch.equal(only_t, ref_t)
