@@ -595,6 +595,11 @@ def main():
         del src, dst
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(inp, min(args.cpu_sample_tokens, N))
+        if cfg == 2 and args.shard is None:
+            # the same oracle on the whole of config 1 (2,048 tokens, the reference's
+            # CPU-runnable case), beside the config-2 sample
+            c1 = cpu_baseline(synth.make_config(1, seed=0), 2048)
+            out["cpu_baseline"]["config1"] = {k: c1[k] for k in ("value", "unit", "sample")}
     print(json.dumps(out), flush=True)
 
 

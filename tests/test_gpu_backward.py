@@ -604,3 +604,37 @@ def test_pack_gate_up_transposed(cuda_device, E, F, d):
     assert torch.equal(wgu, ref)
     assert torch.equal(wgu_t, ref_t)
     assert torch.equal(only_t, ref_t)
+
+
+def test_module_autograd_skewed_routing_vs_oracle(cuda_device):
+    """The module's training path (factor-storing forward, fused dh + SwiGLU backward,
+    sorted-h weight gradient) under skewed routing — a direction shared by the
+    tokens and one expert's router row, so that this expert takes about half of
+    the assignments and others few — against the float64 oracle backward."""
+    torch.manual_seed(17)
+    d, F, E, k, n = 768, 3072, 16, 2, 3000
+    m = MoEFeedForward(d, F, 0.0, num_experts=E, top_k=k).to(cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        for p in (m.w_gate, m.w_up, m.w_down):
+            p.normal_(0, 0.02)
+        m.router.weight.normal_(0, 0.05)
+        # a direction shared by the tokens and expert 3's router row
+        sgn = torch.randint(0, 2, (d,), device=cuda_device).float() * 2 - 1
+        m.router.weight[3] += (0.03 * sgn).to(torch.bfloat16)
+    x = (torch.randn(n, d, device=cuda_device) + 0.3 * sgn).to(torch.bfloat16).requires_grad_(True)
+    R = torch.randn(n, d, device=cuda_device)
+    y = m(x)
+    (y.float() * R).sum().backward()
+    bits = lambda t: t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    xb, wrb = bits(x), bits(m.router.weight)
+    idx, _ = oracle.topk_gates_c(oracle.router_logits(xb, wrb), k)
+    counts = np.bincount(idx.reshape(-1), minlength=E)
+    print(f"  counts {counts.tolist()}", flush=True)
+    assert counts.max() > 0.4 * n * k
+    ref = oracle.moe_backward(xb, wrb, bits(m.w_gate), bits(m.w_up), bits(m.w_down), idx,
+                              synth.f32_to_bf16_bits(R.cpu().numpy()))
+    check("x.grad", host(x.grad), ref["dx"])
+    check("router.grad", host(m.router.weight.grad), ref["d_w_router"])
+    check("w_gate.grad", host(m.w_gate.grad), ref["d_w_gate"])
+    check("w_up.grad", host(m.w_up.grad), ref["d_w_up"])
+    check("w_down.grad", host(m.w_down.grad), ref["d_w_down"])
