@@ -536,6 +536,34 @@ def main():
         and np.array_equal(r.perm.cpu().numpy(), rp)
         and np.array_equal(r.inv_pos.cpu().numpy(), ri))
 
+    # the same layer forward (one g5moe_forward call) captured once in a HIP graph and
+    # replayed: how a serving loop would run it (no launch overhead per kernel); a
+    # side figure — `value` stays the stage-by-stage loop above
+    graph_ms = None
+    try:
+        gs = torch.cuda.Stream(dev)
+        gs.wait_stream(torch.cuda.current_stream(dev))
+        with torch.cuda.stream(gs):
+            ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf)
+        torch.cuda.current_stream(dev).wait_stream(gs)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf)
+        for _ in range(args.warmup):
+            graph.replay()
+        g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        g0.record()
+        for _ in range(args.steps):
+            graph.replay()
+        g1.record()
+        torch.cuda.synchronize()
+        graph_ms = g0.elapsed_time(g1) / args.steps
+        del graph
+    except RuntimeError as exc:  # capture unavailable: report it instead of a number
+        graph_ms = f"capture failed: {exc}"
+
     # calibrated HBM bytes per gate|up launch, measured at config 2 (null elsewhere)
     traffic = None
     tf_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -585,6 +613,7 @@ def main():
             "flop_per_launch": flops_gu,
         },
         "routing_bit_exact_vs_oracle": routing_exact,
+        "graph_ms_per_step": graph_ms,
     }
     if args.calibrate_copy:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
