@@ -197,3 +197,44 @@ def test_backward_has_no_host_sync(cuda_device):
     assert torch.equal(y, y2)
     for a, b in zip(g_nosync, g_dev):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("d,F,E,k", [(512, 384, 4, 3), (128, 256, 8, 2), (768, 3072, 16, 2)])
+def test_module_training_with_dropout_vs_oracle(cuda_device, d, F, E, k):
+    """The module's training path with dropout against the float64 oracle backward
+    under the same mask (the module's seed is its first draw from torch's generator
+    after manual_seed): for shapes the fused kernels do not take (d or F not a
+    multiple of 256: raw gate|up products kept, the separate SwiGLU backward
+    regenerating the mask, weight gradients as batched products) and for GeneT5's
+    (the mask folded into the forward's SwiGLU factors, the fused dh + SwiGLU
+    backward, the sorted-h weight gradient)."""
+    from genet5_amd.moe import MoEFeedForward
+    n, p = 600, 0.2
+    torch.manual_seed(4)
+    m = MoEFeedForward(d, F, p, num_experts=E, top_k=k).to(cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        for prm in (m.w_gate, m.w_up, m.w_down):
+            prm.normal_(0, 0.05)
+        m.router.weight.normal_(0, 0.05)
+    m.train()
+    x = torch.randn(n, d, device=cuda_device).to(torch.bfloat16).requires_grad_(True)
+    R = torch.randn(n, d, device=cuda_device)
+    torch.manual_seed(123)
+    seed = int(torch.randint(0, 2 ** 62, (1,)).item())
+    torch.manual_seed(123)
+    y = m(x)
+    (y.float() * R).sum().backward()
+    bits = lambda t: t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+    xb, wrb = bits(x), bits(m.router.weight)
+    idx, _ = oracle.topk_gates_c(oracle.router_logits(xb, wrb), k)
+    keep = mo.dropout_keep(np.arange(n * k), F, p, seed)
+    ref = oracle.moe_backward(xb, wrb, bits(m.w_gate), bits(m.w_up), bits(m.w_down), idx,
+                              synth.f32_to_bf16_bits(R.cpu().numpy()), keep=keep,
+                              scale=float(mo.dropout_scale(p)))
+    print(f"module with dropout d={d} F={F} E={E} k={k}", flush=True)
+    check("y", host(y), ref["y"])
+    check("x.grad", host(x.grad), ref["dx"])
+    check("router.grad", host(m.router.weight.grad), ref["d_w_router"])
+    check("w_gate.grad", host(m.w_gate.grad), ref["d_w_gate"])
+    check("w_up.grad", host(m.w_up.grad), ref["d_w_up"])
+    check("w_down.grad", host(m.w_down.grad), ref["d_w_down"])
