@@ -226,7 +226,7 @@ def bench_config5(args) -> dict:
     sl = layer0.self_attn.slopes_on(dev)
     att = {}
     for name, skip in (("skip", True), ("dense", False)):
-        f = lambda: attn_mod.attn_varlen_fwd(q, k, v, cu, 4550, 0.125, sl, skip_negligible=skip)
+        f = lambda: attn_mod.attn_varlen_fwd(q, k, v, cu, 4550, 0.125, sl, key_bounds=skip)
         for _ in range(3):
             f()
         torch.cuda.synchronize()

@@ -67,15 +67,19 @@ def _check_qkv(t: torch.Tensor, name: str, total: int, heads: int, dev: torch.de
 def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                     cu_seqlens: torch.Tensor, max_seqlen: int, softmax_scale: float,
                     alibi_slopes: Optional[torch.Tensor] = None, return_lse: bool = False,
-                    skip_negligible: bool = True):
+                    key_bounds: bool = True):
     """g5moe_attn_varlen_fwd on the current stream.  q [T, H, 64], k/v [T, Hkv, 64]
     bf16 (head dims contiguous, other strides free); cu_seqlens int32 [n + 1] on
     the GPU; alibi_slopes fp32 [H] or None.  Returns out [T, H, 64] (and the
     natural-log softmax_lse [H, T] fp32 when return_lse).
 
-    skip_negligible (with ALiBi): leave out the key blocks whose probabilities are
-    provably below 2^-64 of each row's largest (a key-norm bound against the ALiBi
-    distance); the result equals the dense computation to fp32 rounding."""
+    key_bounds: give the kernel a workspace for per-64-key-block norm maxima (one
+    pre-pass over k).  With them it (a) leaves out, under ALiBi, the key blocks whose
+    probabilities are provably below 2^-64 of each row's largest (a key-norm bound
+    against the ALiBi distance), and (b) uses a fixed per-query reference maximum
+    instead of the online running maximum where the bounds keep every score term
+    within 32 of zero (base 2).  The result equals the plain online computation over
+    every block (key_bounds=False) to fp32 rounding of the probabilities."""
     dev = _check_device(q)
     T, H = q.shape[0], q.shape[1]
     Hkv = k.shape[1] if k.dim() == 3 else -1
@@ -99,7 +103,7 @@ def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
         out.stride(0), out.stride(1))
     ws = None
-    if skip_negligible and alibi_slopes is not None:
+    if key_bounds:
         n = ctypes.c_size_t(0)
         _lib.call("g5moe_attn_workspace_size", ctypes.byref(shape), ctypes.byref(n))
         ws = torch.empty(int(n.value), dtype=torch.uint8, device=dev)
@@ -111,16 +115,22 @@ def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
 @torch.library.custom_op("g5moe::attn_varlen_fwd", mutates_args=())
 def _attn_op(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens: torch.Tensor,
-             max_seqlen: int, softmax_scale: float, alibi_slopes: Optional[torch.Tensor]
-             ) -> Tuple[torch.Tensor, torch.Tensor]:
-    return attn_varlen_fwd(q, k, v, cu_seqlens, max_seqlen, softmax_scale, alibi_slopes,
-                           return_lse=True)
+             max_seqlen: int, softmax_scale: float, alibi_slopes: Optional[torch.Tensor],
+             return_lse: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """(out, softmax_lse [H, T]) with return_lse, else (out, an empty [0] tensor): the
+    kernel keeps the fp32 row sums lse needs only when it is asked for."""
+    if return_lse:
+        return attn_varlen_fwd(q, k, v, cu_seqlens, max_seqlen, softmax_scale, alibi_slopes,
+                               return_lse=True)
+    out = attn_varlen_fwd(q, k, v, cu_seqlens, max_seqlen, softmax_scale, alibi_slopes)
+    return out, out.new_empty((0,), dtype=torch.float32)
 
 
 @_attn_op.register_fake
-def _(q, k, v, cu_seqlens, max_seqlen, softmax_scale, alibi_slopes):
+def _(q, k, v, cu_seqlens, max_seqlen, softmax_scale, alibi_slopes, return_lse):
     T, H, D = q.shape
-    return q.new_empty((T, H, D)), q.new_empty((H, T), dtype=torch.float32)
+    lse_shape = (H, T) if return_lse else (0,)
+    return q.new_empty((T, H, D)), q.new_empty(lse_shape, dtype=torch.float32)
 
 
 def _no_backward(ctx, *grads):
@@ -161,7 +171,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
         raise NotImplementedError("the HIP attention kernel is forward-only; call it under "
                                   "torch.no_grad()")
     out, lse = _attn_op(q, k, v, cu_seqlens_q, int(max_seqlen_q), float(softmax_scale),
-                        alibi_slopes)
+                        alibi_slopes, bool(return_attn_probs))
     return (out, lse, None) if return_attn_probs else out
 
 

@@ -42,13 +42,27 @@
 // queries; the skipped probability mass is below 2^-51 of each row's sum, so
 // the result equals the dense computation to fp32 rounding.
 //
-// Softmax in base 2: t = s * scale * log2(e) + bias * log2(e), p = 2^(t - m).
-// On a key block that lies entirely on one side of every query of the wave
-// and inside the sequence, bias = c_blk +/- c_r with c_r = -slope * log2(e) *
-// (key offset inside the block) held in registers and c_blk a per-lane
-// scalar, so the bias costs nothing beyond the score's own fused
-// multiply-add; blocks that straddle the diagonal or the sequence end take the
-// exact per-element |i - j| path with masking.
+// Softmax in base 2: t = s * scale * log2(e) + bias * log2(e).  Two loops:
+//
+// * Reference maximum (with key norms, a positive scale, a non-negative slope
+//   and every |s * sc| of the workgroup within 32): p = 2^(t - mref) with the
+//   lane's fixed upper bound mref = sc * |q| * KM >= t.  The row's largest term
+//   is at least its diagonal's, >= -mref, so no probability that matters
+//   underflows and no running maximum or rescaling is needed.  On a key block
+//   wholly on one side of the wave's queries (and inside the sequence) the
+//   ALiBi bias and -mref enter the score product as one more MFMA k-chunk
+//   (key offsets against bf16 splits of the slope and of the lane's
+//   constant), so a probability costs one multiply and one exp; the row sums
+//   that normalise the output come from an all-ones MFMA operand against P^T
+//   (the sums of the bf16 probabilities the output product weights; the fp32
+//   sums are kept only when softmax_lse is asked for).
+// * Online (otherwise): running maximum, rescaled output and row sum.  On a
+//   one-sided block bias = c_blk +/- c_r with c_r = -slope * log2(e) * (key
+//   offset inside the block) held in registers and c_blk a per-lane scalar,
+//   so the bias costs nothing beyond the score's own fused multiply-add.
+//
+// Blocks that straddle the diagonal or the sequence end take the exact
+// per-element |i - j| path with masking in both loops.
 #include "g5moe_internal.h"
 
 namespace g5moe {
@@ -64,6 +78,7 @@ constexpr int kBKV = 64;   // keys per LDS block
 constexpr int kRowBytes = kHeadDim * 2 + 16;      // 144: padded K row / V^T row
 constexpr int kTileBytes = kBKV * kRowBytes;      // 9 KB
 constexpr float kSkipMargin = 64.0f;              // skipped keys have p < 2^-64
+constexpr float kFixedGap = 64.0f;                // reference-max loop: row maximum >= 2^-64
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -93,6 +108,8 @@ __device__ __forceinline__ int vt_pos(int r) {
   return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
 }
 
+// LSE: softmax_lse is written (a.lse != nullptr).
+template <bool LSE>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16))) char smem[2][2][kTileBytes];  // [buffer][K, V^T]
@@ -131,10 +148,15 @@ void attn_fwd_kernel(AttnArgs a) {
     }
   }
   // Key blocks this workgroup visits: [n_lo, n_hi] (all of them without ALiBi
-  // or without key norms).
+  // or without key norms).  With key norms, `fixed` selects the reference-max
+  // loop when every score term s * sc of the workgroup is provably within
+  // kFixedGap / 2 of zero; mref is then this lane's upper bound on its row's
+  // largest term.
   const int nblk = (L + kBKV - 1) / kBKV;
   int n_lo = 0, n_hi = nblk - 1;
-  if (a.kmax != nullptr && sl > 0.0f) {
+  bool fixed = false;
+  float mref = 0.0f;
+  if (a.kmax != nullptr) {
     __shared__ float red[8];
     // largest key norm over the 64-token blocks that cover the sequence
     float km = 0.0f;
@@ -151,6 +173,7 @@ void attn_fwd_kernel(AttnArgs a) {
         ss = __builtin_fmaf(x, x, ss);
       }
     ss += __shfl_xor(ss, 32, 64);
+    const float ss_own = ss;  // this lane's squared query norm
 #pragma unroll
     for (int bit = 16; bit >= 1; bit >>= 1) ss = __builtin_fmaxf(ss, __shfl_xor(ss, bit, 64));
     if (lane == 0) {
@@ -160,22 +183,22 @@ void attn_fwd_kernel(AttnArgs a) {
     __syncthreads();
     const float nq2 = __builtin_fmaxf(__builtin_fmaxf(red[0], red[1]), __builtin_fmaxf(red[2], red[3]));
     const float kmx = __builtin_fmaxf(__builtin_fmaxf(red[4], red[5]), __builtin_fmaxf(red[6], red[7]));
-    const float w = (2.0f * sc * __builtin_sqrtf(nq2) * kmx + kSkipMargin) / sl;
-    if (w < 1.0e9f) {  // false for inf / NaN: visit every block
-      const int wi = int(w);
-      const int q_hi = min(q0 + kBQ, L) - 1;
-      n_lo = max(0, (q0 - wi) / kBKV);
-      n_hi = min(nblk - 1, (q_hi + wi) / kBKV);
+    // |s * sc| <= bound for every query of the workgroup and key of the sequence
+    const float bound = __builtin_fabsf(sc) * __builtin_sqrtf(nq2) * kmx;
+    if (sl > 0.0f) {
+      const float w = (2.0f * bound + kSkipMargin) / sl;
+      if (w < 1.0e9f) {  // false for inf / NaN: visit every block
+        const int wi = int(w);
+        const int q_hi = min(q0 + kBQ, L) - 1;
+        n_lo = max(0, (q0 - wi) / kBKV);
+        n_hi = min(nblk - 1, (q_hi + wi) / kBKV);
+      }
     }
+    // bound is the same in every lane (red); false for inf / NaN
+    fixed = __builtin_amdgcn_readfirstlane(
+                int(sc > 0.0f && sl >= 0.0f && 2.0f * bound <= kFixedGap)) != 0;
+    mref = sc * __builtin_sqrtf(ss_own) * kmx;
   }
-
-  // c_r = -slope * log2(e) * (offset of element r's key inside the block)
-  float ck[2][16];
-#pragma unroll
-  for (int b = 0; b < 2; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r)
-      ck[b][r] = -sl * float(32 * b + 8 * (r >> 2) + 4 * half + (r & 3));
 
   // Tile loaders.  K: thread t moves rows (t >> 3) and (t >> 3) + 32, chunk t & 7
   // (eight threads per 128-byte row).  V: thread t moves key t & 63, chunks
@@ -185,55 +208,55 @@ void attn_fwd_kernel(AttnArgs a) {
   const int v_key = tid & 63, v_chunk = tid >> 6;
   const uint16_t* kbase = a.k + int64_t(s0) * a.k_tok + hk * a.k_head;
   const uint16_t* vbase = a.v + int64_t(s0) * a.v_tok + hk * a.v_head;
+  // per-lane element offsets inside a tile (the tile's base is block-uniform)
+  const int64_t k_off0 = int64_t(k_row) * a.k_tok + k_chunk * 8;
+  const int64_t k_off1 = k_off0 + 32 * a.k_tok;
+  const int64_t v_off = int64_t(v_key) * a.v_tok + v_chunk * 8;
   u32x4 kreg[2], vreg[2];
-  auto load_tile = [&](int j0) {
+  auto load_k = [&](int j0) __attribute__((always_inline)) {
+    const uint16_t* kt = kbase + int64_t(j0) * a.k_tok;
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int kr = j0 + k_row + 32 * i;
-      kreg[i] = kr < L ? *reinterpret_cast<const u32x4*>(kbase + int64_t(kr) * a.k_tok + k_chunk * 8)
-                       : u32x4{0, 0, 0, 0};
-      const int vr = j0 + v_key;
-      vreg[i] = vr < L ? *reinterpret_cast<const u32x4*>(vbase + int64_t(vr) * a.v_tok +
-                                                        (v_chunk + 4 * i) * 8)
+      kreg[i] = kr < L ? *reinterpret_cast<const u32x4*>(kt + (i == 0 ? k_off0 : k_off1))
                        : u32x4{0, 0, 0, 0};
     }
   };
-  auto store_tile = [&](int buf) {
-    char* Ks = smem[buf][0];
-    char* Vs = smem[buf][1];
-    char* vrow = Vs + v_chunk * 8 * kRowBytes + vt_pos(v_key) * 2;
+  auto load_v = [&](int j0) __attribute__((always_inline)) {
+    const uint16_t* vt = vbase + int64_t(j0) * a.v_tok;
+    const int vr = j0 + v_key;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int kr = k_row + 32 * i;
-      *reinterpret_cast<u32x4*>(Ks + lds_off(kr, k_chunk)) = kreg[i];
+    for (int i = 0; i < 2; ++i)
+      vreg[i] = vr < L ? *reinterpret_cast<const u32x4*>(vt + v_off + 32 * i)
+                       : u32x4{0, 0, 0, 0};
+  };
+  auto store_k = [&](int buf) __attribute__((always_inline)) {
+    char* Ks = smem[buf][0];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      *reinterpret_cast<u32x4*>(Ks + lds_off(k_row + 32 * i, k_chunk)) = kreg[i];
+  };
+  auto store_v = [&](int buf) __attribute__((always_inline)) {
+    char* vrow = smem[buf][1] + v_chunk * 8 * kRowBytes + vt_pos(v_key) * 2;
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint16_t val = uint16_t(vreg[i][e >> 1] >> ((e & 1) * 16));
         *reinterpret_cast<uint16_t*>(vrow + (32 * i + e) * kRowBytes) = val;
       }
-    }
   };
-
-  f32x16 o[2];
-  const f32x16 zero16 = {};
-  o[0] = zero16;
-  o[1] = zero16;
-  float m = -__builtin_inff();
-  float l = 0.0f;
-
-  load_tile(n_lo * kBKV);
-  store_tile(n_lo & 1);
-  __syncthreads();
-
-  for (int n = n_lo; n <= n_hi; ++n) {
-    const int buf = n & 1;
-    const int j0 = n * kBKV;
-    if (n < n_hi) load_tile(j0 + kBKV);
-    const char* Ks = smem[buf][0];
-    const char* Vs = smem[buf][1];
-
-    // S^T = K . Q^T for the two 32-key halves of the block
-    f32x16 s[2];
+  auto load_tile = [&](int j0) __attribute__((always_inline)) {
+    load_k(j0);
+    load_v(j0);
+  };
+  auto store_tile = [&](int buf) __attribute__((always_inline)) {
+    store_k(buf);
+    store_v(buf);
+  };
+  // S^T = K . Q^T for the two 32-key halves of the block
+  auto scores = [&](const char* Ks, f32x16* s) __attribute__((always_inline)) {
+    const f32x16 zero16 = {};
 #pragma unroll
     for (int b = 0; b < 2; ++b) {
 #pragma unroll
@@ -244,74 +267,20 @@ void attn_fwd_kernel(AttnArgs a) {
                                                        0, 0);
       }
     }
-
-    // t = s * sc + bias (base 2), block maximum, rescale, probabilities
-    const bool inside = j0 + kBKV <= L;
-    const bool after = inside && j0 > wq_hi;           // every key > every query
-    const bool before = inside && j0 + kBKV - 1 < wq_lo;  // every key < every query
-    float cblk;
-    float t[2][16];
-    if (after) {
-      cblk = -sl * float(j0 - iq);
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) t[b][r] = __builtin_fmaf(s[b][r], sc, ck[b][r]);
-    } else if (before) {
-      cblk = -sl * float(iq - j0);
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) t[b][r] = __builtin_fmaf(s[b][r], sc, -ck[b][r]);
-    } else {
-      cblk = 0.0f;
-      const float di = float(iq - j0);
-#pragma unroll
-      for (int b = 0; b < 2; ++b)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kr = 32 * b + 8 * (r >> 2) + 4 * half + (r & 3);
-          const float bias = -sl * __builtin_fabsf(di - float(kr));
-          t[b][r] = j0 + kr < L ? __builtin_fmaf(s[b][r], sc, bias) : -__builtin_inff();
-        }
-    }
-    float mx = t[0][0];
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, t[b][r]);
-    mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = __builtin_fmaxf(m, mx + cblk);
-    const float alpha = __builtin_amdgcn_exp2f(m - m_new);
-    m = m_new;
-    const float mm = m_new - cblk;
-    float psum = 0.0f;
-    uint32_t pk[2][8];
-#pragma unroll
-    for (int b = 0; b < 2; ++b)
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(t[b][r] - mm);
-        const float p1 = __builtin_amdgcn_exp2f(t[b][r + 1] - mm);
-        psum += p0;
-        psum += p1;
-        pk[b][r >> 1] = pack_bf16x2(p0, p1);
-      }
-    l = l * alpha + psum;
-    if (__ballot(alpha != 1.0f) != 0) {
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[mb][r] *= alpha;
-    }
-
-    // O^T += V^T . P^T over the four 16-key chunks (chunk c = key block c / 2,
-    // elements 8 (c % 2) .. +8)
+  };
+  // P^T operand of 16-key chunk c (chunk c = key block c / 2, elements
+  // 8 (c % 2) .. +8): the lane's own probabilities, no data movement
+  auto p_chunk = [&](const uint32_t (*pk)[8], int c) __attribute__((always_inline)) -> bf16x8 {
+    const u32x4 praw = {pk[c >> 1][4 * (c & 1) + 0], pk[c >> 1][4 * (c & 1) + 1],
+                        pk[c >> 1][4 * (c & 1) + 2], pk[c >> 1][4 * (c & 1) + 3]};
+    return __builtin_bit_cast(bf16x8, praw);
+  };
+  // O^T += V^T . P^T over the four 16-key chunks
+  auto out_product = [&](const char* Vs, const uint32_t (*pk)[8], f32x16* o)
+      __attribute__((always_inline)) {
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const u32x4 praw = {pk[c >> 1][4 * (c & 1) + 0], pk[c >> 1][4 * (c & 1) + 1],
-                          pk[c >> 1][4 * (c & 1) + 2], pk[c >> 1][4 * (c & 1) + 3]};
-      const bf16x8 pf = __builtin_bit_cast(bf16x8, praw);
+      const bf16x8 pf = p_chunk(pk, c);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         const bf16x8 vf =
@@ -319,13 +288,214 @@ void attn_fwd_kernel(AttnArgs a) {
         o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[mb], 0, 0, 0);
       }
     }
+  };
+  // Exact per-element bias and sequence-end mask of a block that straddles the
+  // wave's queries or the sequence end: t = s * sc - sl * |i - j|, -inf past L.
+  auto exact_terms = [&](const f32x16* s, int j0, float (*t)[16]) __attribute__((always_inline)) {
+    const float di = float(iq - j0);
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kr = 32 * b + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float bias = -sl * __builtin_fabsf(di - float(kr));
+        t[b][r] = j0 + kr < L ? __builtin_fmaf(s[b][r], sc, bias) : -__builtin_inff();
+      }
+  };
 
-    if (n < n_hi) store_tile(buf ^ 1);
-    __syncthreads();
+  f32x16 o[2];
+  {
+    const f32x16 zero16 = {};
+    o[0] = zero16;
+    o[1] = zero16;
+  }
+  float m, l_tot, l_lse;  // reference maximum, normalising sum, fp32 sum for lse
+
+  load_tile(n_lo * kBKV);
+  store_tile(n_lo & 1);
+  __syncthreads();
+
+  if (fixed) {
+    // Reference-max loop: p = 2^(t - mref) with the lane's fixed bound mref
+    // (t <= mref because the bias is <= 0; the row's largest term is at least
+    // its diagonal's, >= -mref, so p_max >= 2^-kFixedGap): no running maximum,
+    // no rescaling.  On a block wholly on one side of the wave's queries the
+    // bias and -mref ride in the score product as one more 16-deep MFMA
+    // chunk: key rows K' = [kr, kr, kr, 1, 1, 1, 0, 0] (kr the key's offset
+    // inside the block, exact in bf16) against query columns Q' = [-+u1, -+u2,
+    // -+u3, c1, c2, c3, 0, 0], where u1 + u2 + u3 = u = sl / sc (the slope in
+    // units of raw scores) and c1 + c2 + c3 = c = -u * |j0 - i| - mref / sc
+    // are bf16 splits (exact to fp32 precision; bf16 products are exact in
+    // the fp32 accumulation), so the accumulator holds s + (bias - mref) / sc
+    // and p = 2^(acc * sc).  The row sums come from the matrix cores too: an
+    // all-ones A operand against P^T adds sum_k bf16(p) to every element of
+    // lacc (the same bf16 probabilities the output product weights).
+    auto bf16r = [](float x) __attribute__((always_inline)) -> float { return float(__bf16(x)); };
+    const float u = sl / sc;
+    const float u1 = bf16r(u), u2 = bf16r(u - u1), u3 = bf16r(u - u1 - u2);
+    const float mref_s = mref / sc;
+    const __bf16 bz = __bf16(0.0f), b1 = __bf16(1.0f);
+    bf16x8 kx[2];
+#pragma unroll
+    for (int b = 0; b < 2; ++b) {
+      const __bf16 kr = __bf16(float(32 * b + col));
+      const bf16x8 v = {kr, kr, kr, b1, b1, b1, bz, bz};
+      const bf16x8 zv = {bz, bz, bz, bz, bz, bz, bz, bz};
+      kx[b] = half == 0 ? v : zv;
+    }
+    const bf16x8 ones = {b1, b1, b1, b1, b1, b1, b1, b1};
+    f32x16 lacc = {};
+    // softmax_lse wants the fp32 sum of the probabilities (lacc sums their bf16
+    // roundings, which the output product weights)
+    constexpr bool want_lse = LSE;
+    float psum = 0.0f;
+
+    for (int n = n_lo; n <= n_hi; ++n) {
+      const int buf = n & 1;
+      const int j0 = n * kBKV;
+      if (n < n_hi) load_tile(j0 + kBKV);
+      const char* Ks = smem[buf][0];
+      const char* Vs = smem[buf][1];
+      f32x16 s[2];
+      scores(Ks, s);
+
+      const bool inside = j0 + kBKV <= L;
+      const bool after = inside && j0 > wq_hi;              // every key > every query
+      const bool before = inside && j0 + kBKV - 1 < wq_lo;  // every key < every query
+      uint32_t pk[2][8];
+      // without ALiBi (u = 0) every block inside the sequence takes the chunk
+      if (after || before || (inside && sl == 0.0f)) {
+        const float c = -u * float(after ? j0 - iq : iq - j0) - mref_s;
+        const float c1 = bf16r(c), c2 = bf16r(c - c1), c3 = bf16r(c - c1 - c2);
+        const float su = after ? -1.0f : 1.0f;
+        const bf16x8 qv = {__bf16(su * u1), __bf16(su * u2), __bf16(su * u3), __bf16(c1),
+                           __bf16(c2),      __bf16(c3),      bz,              bz};
+        const bf16x8 zv = {bz, bz, bz, bz, bz, bz, bz, bz};
+        const bf16x8 qx = half == 0 ? qv : zv;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+          s[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kx[b], qx, s[b], 0, 0, 0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(s[b][r] * sc);
+            const float p1 = __builtin_amdgcn_exp2f(s[b][r + 1] * sc);
+            if constexpr (want_lse) {
+              psum += p0;
+              psum += p1;
+            }
+            pk[b][r >> 1] = pack_bf16x2(p0, p1);
+          }
+      } else {
+        float t[2][16];
+        exact_terms(s, j0, t);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; r += 2) {
+            const float p0 = __builtin_amdgcn_exp2f(t[b][r] - mref);
+            const float p1 = __builtin_amdgcn_exp2f(t[b][r + 1] - mref);
+            if constexpr (want_lse) {
+              psum += p0;
+              psum += p1;
+            }
+            pk[b][r >> 1] = pack_bf16x2(p0, p1);
+          }
+      }
+      out_product(Vs, pk, o);
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+        lacc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ones, p_chunk(pk, c), lacc, 0, 0, 0);
+
+      if (n < n_hi) store_tile(buf ^ 1);
+      __syncthreads();
+    }
+    m = mref;
+    l_tot = lacc[0];
+    l_lse = psum + __shfl_xor(psum, 32, 64);
+  } else {
+    // Online softmax: running maximum m, rescaled output and sum.
+    // c_r = -slope * log2(e) * (offset of element r's key inside the block)
+    float ck[2][16];
+#pragma unroll
+    for (int b = 0; b < 2; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        ck[b][r] = -sl * float(32 * b + 8 * (r >> 2) + 4 * half + (r & 3));
+    m = -__builtin_inff();
+    float l = 0.0f;
+
+    for (int n = n_lo; n <= n_hi; ++n) {
+      const int buf = n & 1;
+      const int j0 = n * kBKV;
+      if (n < n_hi) load_tile(j0 + kBKV);
+      const char* Ks = smem[buf][0];
+      const char* Vs = smem[buf][1];
+      f32x16 s[2];
+      scores(Ks, s);
+
+      // t = s * sc + bias (base 2), block maximum, rescale, probabilities
+      const bool inside = j0 + kBKV <= L;
+      const bool after = inside && j0 > wq_hi;              // every key > every query
+      const bool before = inside && j0 + kBKV - 1 < wq_lo;  // every key < every query
+      float cblk;
+      float t[2][16];
+      if (after) {
+        cblk = -sl * float(j0 - iq);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) t[b][r] = __builtin_fmaf(s[b][r], sc, ck[b][r]);
+      } else if (before) {
+        cblk = -sl * float(iq - j0);
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) t[b][r] = __builtin_fmaf(s[b][r], sc, -ck[b][r]);
+      } else {
+        cblk = 0.0f;
+        exact_terms(s, j0, t);
+      }
+      float mx = t[0][0];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, t[b][r]);
+      mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+      const float m_new = __builtin_fmaxf(m, mx + cblk);
+      const float alpha = __builtin_amdgcn_exp2f(m - m_new);
+      m = m_new;
+      const float mm = m_new - cblk;
+      float psum = 0.0f;
+      uint32_t pk[2][8];
+#pragma unroll
+      for (int b = 0; b < 2; ++b)
+#pragma unroll
+        for (int r = 0; r < 16; r += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(t[b][r] - mm);
+          const float p1 = __builtin_amdgcn_exp2f(t[b][r + 1] - mm);
+          psum += p0;
+          psum += p1;
+          pk[b][r >> 1] = pack_bf16x2(p0, p1);
+        }
+      l = l * alpha + psum;
+      if (__ballot(alpha != 1.0f) != 0) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[mb][r] *= alpha;
+      }
+      out_product(Vs, pk, o);
+
+      if (n < n_hi) store_tile(buf ^ 1);
+      __syncthreads();
+    }
+    l_tot = l + __shfl_xor(l, 32, 64);
+    l_lse = l_tot;
   }
 
   // normalise and store: lane holds query iq, dims 32mb + 8q + 4half + u
-  const float l_tot = l + __shfl_xor(l, 32, 64);
   if (iq < L) {
     const float inv = 1.0f / l_tot;
     uint16_t* op = a.o + int64_t(s0 + iq) * a.o_tok + hq * a.o_head + 4 * half;
@@ -338,8 +508,8 @@ void attn_fwd_kernel(AttnArgs a) {
         w.y = pack_bf16x2(o[mb][4 * q + 2] * inv, o[mb][4 * q + 3] * inv);
         *reinterpret_cast<uint2*>(op + 32 * mb + 8 * q) = w;
       }
-    if (a.lse != nullptr && half == 0)
-      a.lse[int64_t(hq) * a.total + s0 + iq] = (m + __builtin_log2f(l_tot)) * kLn2;
+    if (LSE && half == 0)
+      a.lse[int64_t(hq) * a.total + s0 + iq] = (m + __builtin_log2f(l_lse)) * kLn2;
   }
 }
 
@@ -390,9 +560,10 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
                            const int32_t* cu_seqlens, const float* slopes, float softmax_scale,
                            float* lse, float* kmax_ws, const g5moe_attn_shape& s,
                            hipStream_t st) {
-  const bool skip = kmax_ws != nullptr && slopes != nullptr && s.total_tokens > 0;
+  // key-norm bounds: block skipping (with ALiBi) and the reference-max loop
+  const bool bounds = kmax_ws != nullptr && s.total_tokens > 0;
   const int n_kblk = int((s.total_tokens + 63) / 64);
-  if (skip) {
+  if (bounds) {
     hipLaunchKernelGGL(key_norm_max_kernel, dim3(unsigned(n_kblk), unsigned(s.n_kv_heads)),
                        dim3(256), 0, st, k, s.k_token_stride, s.k_head_stride, s.total_tokens,
                        n_kblk, kmax_ws);
@@ -417,12 +588,15 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
   a.sc = softmax_scale * kLog2e;
   a.slopes = slopes;
   a.lse = lse;
-  a.kmax = skip ? kmax_ws : nullptr;
+  a.kmax = bounds ? kmax_ws : nullptr;
   a.n_kblk = n_kblk;
   a.total = s.total_tokens;
   const dim3 grid(unsigned((s.max_seqlen + kBQ - 1) / kBQ), unsigned(s.n_heads),
                   unsigned(s.n_seqs));
-  hipLaunchKernelGGL(attn_fwd_kernel, grid, dim3(256), 0, st, a);
+  if (lse != nullptr)
+    hipLaunchKernelGGL(attn_fwd_kernel<true>, grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(attn_fwd_kernel<false>, grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 

@@ -499,7 +499,7 @@ typedef struct g5moe_attn_shape {
   int64_t o_token_stride, o_head_stride;
 } g5moe_attn_shape;
 
-/* Bytes of workspace g5moe_attn_varlen_fwd uses for block skipping
+/* Bytes of workspace g5moe_attn_varlen_fwd uses for its key-norm bounds
  * (n_kv_heads * ceil(total_tokens / 64) fp32 key-norm maxima, 256-byte
  * aligned). */
 g5moe_status g5moe_attn_workspace_size(const g5moe_attn_shape* shape, size_t* bytes);
@@ -512,12 +512,19 @@ g5moe_status g5moe_attn_workspace_size(const g5moe_attn_shape* shape, size_t* by
  *   alibi_slopes : fp32 [n_heads] or NULL (no bias);
  *   softmax_lse : fp32 [n_heads, total_tokens] out (natural-log sum of the
  *   exponentials of each row, flash-attn's softmax_lse), or NULL;
- *   ws : g5moe_attn_workspace_size() bytes, or NULL.  With ALiBi and a
- *   workspace, key blocks whose every probability is provably below 2^-64 of
- *   the row's largest (Cauchy-Schwarz on the key and query norms against the
- *   ALiBi distance) are not computed: the skipped mass is below 2^-51 of each
- *   row's sum, so the result equals the dense computation (ws = NULL) to fp32
- *   rounding.
+ *   ws : g5moe_attn_workspace_size() bytes, or NULL.  With a workspace a
+ *   pre-pass writes the largest key norm of every 64-token block, and
+ *   (a) with ALiBi, key blocks whose every probability is provably below 2^-64
+ *   of the row's largest (Cauchy-Schwarz on the key and query norms against
+ *   the ALiBi distance) are not computed: the skipped mass is below 2^-51 of
+ *   each row's sum;
+ *   (b) where the same bounds keep |q.k * softmax_scale * log2(e)| <= 32 for a
+ *   128-query block (softmax_scale > 0, slopes >= 0), the block's softmax uses
+ *   a fixed per-query upper bound as its reference maximum instead of a running
+ *   one, and normalises by the sum of the bf16 probabilities the output product
+ *   weights (softmax_lse keeps the fp32 sum).
+ *   The result equals the plain online computation (ws = NULL) to the rounding
+ *   of the bf16 probabilities.
  * Scores, softmax and the output sum are fp32; the probabilities enter the
  * output product as bf16 (as in flash-attn); one rounding to bf16 at the end.
  * The summation order is fixed, so results are deterministic. */
