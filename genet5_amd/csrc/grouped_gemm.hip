@@ -272,7 +272,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   // is issued.  Positions past the expert's end repeat its last row.  Wave w
   // reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile: slot j's rows
   // (w * AI + j) * RPB + lrow.
-  static_assert(AI * RPB == 64, "one 64-row perm block per wave");
+  static_assert(!GATHER || AI * RPB == 64, "one 64-row perm block per wave");
   char* epi = smem + S * STAGE + wave * kEpiBytesPerWave;
   // rows_fill: byte offsets of the gathered rows of the tile whose stages
   // the refills load (the current tile, then the next from its first stage).
@@ -1395,6 +1395,15 @@ hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* off
   return hipGetLastError();
 }
 
+// Small M (a shard's share of the tokens: one wave of 256-row tiles or less for
+// the CUs): 128-row m-tiles, twice the tiles at half the work each, and less
+// padding past each expert's last row.  The row count is the host's N * k (the
+// per-expert counts stay on the device), so the test is on the full-tile count
+// the rows would give if packed.
+inline bool small_m(int64_t rows, int nout, unsigned ncu) {
+  return (rows / 256) * (nout / 256) < int64_t(3 * ncu / 2);
+}
+
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st) {
   const int64_t nk = s.n_tokens * s.top_k;
@@ -1412,7 +1421,10 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.ldc = s.d_model;
   if (a.K < G5_DN_STAGES * G5_DN_BK) return hipErrorInvalidValue;
   const unsigned ncu = unsigned(device_cu_count());
-  if (a.Nout % 256 == 0) {
+  if (a.Nout % 256 == 0 && small_m(nk, a.Nout, ncu)) {
+    const unsigned grid = std::min(grid_bound<128, 256>(nk, s.n_experts, a.Nout), ncu);
+    launch_persist<128, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);
+  } else if (a.Nout % 256 == 0) {
     const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout), ncu);
     launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, true>(grid, a, st);
   } else {
@@ -1465,7 +1477,10 @@ hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const ui
   a.Nout = Nout;
   a.ldc = Nout;
   const unsigned ncu = unsigned(device_cu_count());
-  if (Nout % 256 == 0) {
+  if (Nout % 256 == 0 && small_m(rows, Nout, ncu)) {
+    const unsigned grid = std::min(grid_bound<128, 256>(rows, n_experts, Nout), ncu);
+    launch_persist<128, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);
+  } else if (Nout % 256 == 0) {
     const unsigned grid = std::min(grid_bound<256, 256>(rows, n_experts, Nout), ncu);
     launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, true>(grid, a, st);
   } else {

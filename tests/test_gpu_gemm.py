@@ -2,13 +2,16 @@
 and the backward's dh / dX products) across its pipeline variants: two fragment
 slots (k-steps not a multiple of 3), three slots with the third A stage in the
 epilogue region (k-steps a multiple of 3, at least 6), 128- and 256-column tiles,
-the n-half tail, experts with no rows, partial last tiles and workgroups that run
-many tiles in a row.
+the n-half tail, 128-row tiles (launches whose rows give fewer than 1.5 full
+256 x 256 tiles per CU), experts with no rows, partial last tiles and workgroups
+that run many tiles in a row.
 
 Two checks per case.  (1) Each expert launched alone gives the same bits as the
 full launch: an output element's MFMA chain runs over k in one fixed order whatever
-workgroup, tile slot or stage buffer computes it, so a stage that lands in the wrong
-buffer, a stale refill or a skipped tile breaks equality.  (2) Every expert's rows
+workgroup, tile slot, stage buffer or tile height computes it, so a stage that lands
+in the wrong buffer, a stale refill or a skipped tile breaks equality (a small
+expert's solo launch takes 128-row tiles where the full launch may take 256-row
+ones).  (2) Every expert's rows
 match a float32 torch product of the same bf16 operands (rtol = atol = 2e-2 on
 unit-scale outputs)."""
 import numpy as np
@@ -28,6 +31,7 @@ def _offsets(counts, device):
 
 @pytest.mark.parametrize("K,n_out,counts", [
     (384, 256, [40000, 0, 257, 9000]),         # nk = 6: shortest three-stage tile
+    (384, 256, [100000, 0, 257, 9000]),        # 256-row tiles, solos of 257 / 9000: 128
     (576, 768, [0, 1, 255, 256, 4097, 30000]),  # nk = 9, three n-tiles, half tail
     (448, 256, [12000, 3, 700]),               # nk = 7: two fragment slots
     (128, 128, [5000, 0, 999]),                # nk = 2, 128-column tiles
