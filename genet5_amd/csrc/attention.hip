@@ -194,9 +194,11 @@ void attn_fwd_kernel(AttnArgs a) {
         n_hi = min(nblk - 1, (q_hi + wi) / kBKV);
       }
     }
-    // bound is the same in every lane (red); false for inf / NaN
-    fixed = __builtin_amdgcn_readfirstlane(
-                int(sc > 0.0f && sl >= 0.0f && 2.0f * bound <= kFixedGap)) != 0;
+    // bound is the same in every lane (red); false for inf / NaN.  sl < 2^60 sc
+    // keeps the slope in units of raw scores (u = sl / sc) and its products
+    // with key offsets and distances (< 2^31) finite.
+    fixed = __builtin_amdgcn_readfirstlane(int(sc > 0.0f && sl >= 0.0f && sl < sc * 0x1p60f &&
+                                               2.0f * bound <= kFixedGap)) != 0;
     mref = sc * __builtin_sqrtf(ss_own) * kmx;
   }
 
