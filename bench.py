@@ -9,8 +9,8 @@ Prints ONE JSON line.  `value` is tokens/s of the whole layer; `roofline` is
 for the dominant kernel (the grouped gate|up GEMM), its average launch time
 taken from HIP events recorded between the stages, on the stream they run on,
 inside the timed loop.  `cpu_baseline` times the CPU oracle (fp32,
-numpy/BLAS) on a bounded token sample of the same workload on this host's
-cores.
+numpy/BLAS) on the same workload (all of its tokens unless --cpu-sample-tokens
+bounds it) on this host's cores, and config 1 beside it.
 """
 from __future__ import annotations
 
@@ -39,7 +39,8 @@ def parse():
                          "autograd backward, with a per-stage breakdown")
     ap.add_argument("--dropout", type=float, default=0.1,
                     help="--train: dropout on the expert hidden state (GeneT5 trains with 0.1)")
-    ap.add_argument("--cpu-sample-tokens", type=int, default=8192)
+    ap.add_argument("--cpu-sample-tokens", type=int, default=0,
+                    help="tokens of the workload the CPU baseline runs (0: all of them)")
     ap.add_argument("--shard", choices=("dp8", "ep8"), default=None,
                     help="one GPU's share of config 2 sharded over 8 GPUs: dp8 = 4,550 tokens "
                          "with all 16 experts (about 569 rows per expert), ep8 = the 2 experts "
@@ -75,7 +76,8 @@ def blas_threads() -> int:
 
 
 def cpu_baseline(inp, n_sample: int) -> dict:
-    """Oracle (fp32 numpy/BLAS) on the first n_sample tokens of the workload."""
+    """Oracle (fp32 numpy/BLAS) on the first n_sample tokens of the workload (all of
+    them by default: config 2 takes about 1.3 s per run on a 16-thread host)."""
     import oracle
     from genet5_amd import synth
     x = inp.x[:n_sample]
@@ -95,8 +97,9 @@ def cpu_baseline(inp, n_sample: int) -> dict:
         "unit": "tokens/s",
         "cores": blas_threads(),
         "kind": "port",
-        "sample": (f"oracle.moe_forward (C router + numpy fp32 BLAS experts) on the first "
-                   f"{n_sample} tokens of the same workload, median of 3 after 1 warm-up, "
+        "sample": (f"oracle.moe_forward (C router + numpy fp32 BLAS experts) on "
+                   + ("all " if n_sample == inp.x.shape[0] else "the first ")
+                   + f"{n_sample} tokens of the same workload, median of 3 after 1 warm-up, "
                    f"{t * 1e3:.1f} ms per run; host {cpu_info()}, os.cpu_count()={os.cpu_count()}"),
         "expert_tflops": 6 * 768 * 3072 * n_sample * inp.top_k / t / 1e12,
     }
@@ -623,10 +626,11 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(inp, min(args.cpu_sample_tokens, N))
+        n_cpu = N if args.cpu_sample_tokens <= 0 else min(args.cpu_sample_tokens, N)
+        out["cpu_baseline"] = cpu_baseline(inp, n_cpu)
         if cfg == 2 and args.shard is None:
             # the same oracle on the whole of config 1 (2,048 tokens, the reference's
-            # CPU-runnable case), beside the config-2 sample
+            # CPU-runnable case), beside config 2
             c1 = cpu_baseline(synth.make_config(1, seed=0), 2048)
             out["cpu_baseline"]["config1"] = {k: c1[k] for k in ("value", "unit", "sample")}
     print(json.dumps(out), flush=True)
