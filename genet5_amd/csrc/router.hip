@@ -25,7 +25,8 @@
 //
 // Schedule.  Persistent: at most two resident workgroups per CU; each wave pair
 // owns a contiguous range of tokens per round, walks it in 4-token batches with
-// the next batch's rows in flight while the current one computes (row
+// the next batch's rows in flight while the current one computes (MODE 2, with
+// two rows per token, loads each batch where it computes it instead) (row
 // addresses are scalar: the wave index is made uniform), and stages the logits
 // in LDS; one thread per token then does the top-k scan and the gates.  The
 // weights are loaded into registers once per wave.
@@ -168,6 +169,31 @@ struct NormArgs {
   void* normed_out;    // normed rows (the MoE input)
 };
 
+// Full xor butterfly in the contract's order (lane bits 5, 4, 3, 2, 1, 0): every
+// lane ends with the same sum, bit for bit.  Bits 5 and 4 swap a value with
+// itself (v_permlane32_swap / v_permlane16_swap: own + partner in one half,
+// partner + own in the other).  Bits 3..0 use DPP row rotates: row_ror:R hands
+// lane l the value of lane (l - R) mod 16, which differs from l ^ R only in row
+// bits above R (the borrow), over which the partial sums are already symmetric,
+// so it carries the xor partner's value.  No LDS (a __shfl_xor would be a
+// ds_bpermute per level).
+template <int R>
+__device__ __forceinline__ float row_ror(float v) {
+  return __uint_as_float(
+      __builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x120 + R, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float butterfly_sum64(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  v = v + row_ror<8>(v);
+  v = v + row_ror<4>(v);
+  v = v + row_ror<2>(v);
+  v = v + row_ror<1>(v);
+  return v;
+}
+
 // Plain (residual add +) RMSNorm with the fused variant's arithmetic, so its
 // normed rows equal the ones g5moe_add_rmsnorm_router writes bit for bit: one
 // wave per row, lane c holding columns [c*L, c*L + L), kRowsPerWave rows per
@@ -207,9 +233,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const XT* __restrict__ x,
     ss[m] = acc;
   }
 #pragma unroll
-  for (int bit = 32; bit >= 1; bit >>= 1)
-#pragma unroll
-    for (int m = 0; m < kRowsPerWave; ++m) ss[m] = ss[m] + __shfl_xor(ss[m], bit, 64);
+  for (int m = 0; m < kRowsPerWave; ++m) ss[m] = butterfly_sum64(ss[m]);
 #pragma unroll
   for (int m = 0; m < kRowsPerWave; ++m) {
     if (row0 + m >= n_rows) break;
@@ -433,9 +457,7 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           ss[m] = acc;
         }
 #pragma unroll
-        for (int bit = 32; bit >= 1; bit >>= 1)
-#pragma unroll
-          for (int m = 0; m < kTokBatch; ++m) ss[m] = ss[m] + __shfl_xor(ss[m], bit, 64);
+        for (int m = 0; m < kTokBatch; ++m) ss[m] = butterfly_sum64(ss[m]);
 #pragma unroll
         for (int m = 0; m < kTokBatch; ++m) {
           const float rstd = 1.0f / __builtin_sqrtf(ss[m] / float(D) + na.eps);
@@ -486,12 +508,23 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     // token, so a batch past the range is a harmless reload): a load under a
     // branch makes the compiler's wait counts assume it may be missing, and the
     // current batch's waits then also wait for the prefetch.
-    load_batch(ra, 0);
-    for (int b = 0; b < nb; b += 2) {
-      load_batch(rb, b + 1);
-      compute_batch(ra, b);
-      load_batch(ra, b + 2);
-      if (b + 1 < nb) compute_batch(rb, b + 1);
+    if constexpr (MODE == 2) {
+      // two rows per token: with a second row buffer the kernel needs 280
+      // VGPRs (one wave per SIMD); without it 225, and two waves per SIMD hide
+      // the loads better (add + RMSNorm + router 74 us instead of 83 at 45,500
+      // tokens)
+      for (int b = 0; b < nb; ++b) {
+        load_batch(ra, b);
+        compute_batch(ra, b);
+      }
+    } else {
+      load_batch(ra, 0);
+      for (int b = 0; b < nb; b += 2) {
+        load_batch(rb, b + 1);
+        compute_batch(ra, b);
+        load_batch(ra, b + 2);
+        if (b + 1 < nb) compute_batch(rb, b + 1);
+      }
     }
     __syncthreads();
 
