@@ -105,6 +105,54 @@ def cpu_baseline(inp, n_sample: int) -> dict:
     }
 
 
+def torch_eager_gpu(x, wr, bias, w_gate, w_up, w_down, k, ref_y, steps=10, warmup=3) -> dict:
+    """The layer as PyTorch code would write it on the same GPU: the reference's
+    FeedForward (lib/blocks/_component.py:48-52: silu(wi_0(x)) * wi_1(x), then wo)
+    per expert over its routed rows, an fp32 router with torch.softmax / torch.topk,
+    and an index_add combine.  bf16 weights and activations through F.linear
+    (hipBLASLt); the per-expert row lists cost a host synchronisation each
+    (nonzero), as in any such loop.  Reported beside the HIP layer, with the
+    largest difference between the two outputs."""
+    import torch
+    import torch.nn.functional as Fn
+    E = w_gate.shape[0]
+
+    def fwd():
+        logits = x.float() @ wr.float().t()
+        if bias is not None:
+            logits = logits + bias
+        wts, idx = torch.topk(torch.softmax(logits, dim=-1), k, dim=-1)
+        wts = wts / wts.sum(-1, keepdim=True)
+        y = torch.zeros(x.shape, dtype=torch.float32, device=x.device)
+        for e in range(E):
+            tok, slot = (idx == e).nonzero(as_tuple=True)
+            if tok.numel() == 0:
+                continue
+            xe = x[tok]
+            h = Fn.silu(Fn.linear(xe, w_gate[e])) * Fn.linear(xe, w_up[e])
+            y.index_add_(0, tok, Fn.linear(h, w_down[e]).float() * wts[tok, slot, None])
+        return y.to(x.dtype)
+
+    for _ in range(warmup):
+        out = fwd()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        out = fwd()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    err = (out.float() - ref_y.float()).abs()
+    ref_abs = ref_y.float().abs()
+    return {"ms_per_step": ms, "tokens_per_s": x.shape[0] / (ms * 1e-3),
+            # a token whose top-2 is a near tie may pick another expert in fp32
+            # torch than in the fixed-order router: the mean is the comparison
+            "mean_rel_diff_vs_hip": err.mean().item() / ref_abs.mean().item(),
+            "max_rel_diff_vs_hip": err.max().item() / ref_abs.max().item(),
+            "what": "PyTorch eager on this GPU: fp32 router + softmax/topk, per-expert "
+                    "F.linear SwiGLU MLP over the routed rows (bf16, hipBLASLt), index_add "
+                    f"combine; {steps} steps after {warmup} warm-up"}
+
+
 def timed(fn, steps: int, warmup: int) -> float:
     import torch
     for _ in range(warmup):
@@ -465,6 +513,7 @@ def main():
     x, wr, bias = tt["x"], tt["w_router"], tt["bias"]
     wgu = ops.pack_gate_up(tt["w_gate"], tt["w_up"])
     wd = tt["w_down"]
+    w_gate_sep, w_up_sep = tt["w_gate"], tt["w_up"]  # the eager-PyTorch comparison's
     del tt
     buf = ops.ForwardBuffers(N, d, F, E, k, x.dtype, dev)
     torch.cuda.synchronize()
@@ -567,6 +616,11 @@ def main():
     except RuntimeError as exc:  # capture unavailable: report it instead of a number
         graph_ms = f"capture failed: {exc}"
 
+    # the same layer as eager PyTorch code on this GPU (context for `value`)
+    y_hip = ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf).clone()
+    torch.cuda.synchronize()
+    torch_gpu = torch_eager_gpu(x, wr, bias, w_gate_sep, w_up_sep, wd, k, y_hip)
+
     # calibrated HBM bytes per gate|up launch, measured at config 2 (null elsewhere)
     traffic = None
     tf_path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
@@ -617,6 +671,7 @@ def main():
         },
         "routing_bit_exact_vs_oracle": routing_exact,
         "graph_ms_per_step": graph_ms,
+        "torch_eager_gpu": torch_gpu,
     }
     if args.calibrate_copy:
         src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)  # 256 MiB
