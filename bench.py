@@ -105,33 +105,40 @@ def cpu_baseline(inp, n_sample: int) -> dict:
     }
 
 
-def torch_eager_gpu(x, wr, bias, w_gate, w_up, w_down, k, ref_y, steps=10, warmup=3) -> dict:
-    """The layer as PyTorch code would write it on the same GPU: the reference's
-    FeedForward (lib/blocks/_component.py:48-52: silu(wi_0(x)) * wi_1(x), then wo)
-    per expert over its routed rows, an fp32 router with torch.softmax / torch.topk,
-    and an index_add combine.  bf16 weights and activations through F.linear
-    (hipBLASLt); the per-expert row lists cost a host synchronisation each
-    (nonzero), as in any such loop.  Reported beside the HIP layer, with the
-    largest difference between the two outputs."""
+def eager_layer(x, wr, bias, w_gate, w_up, w_down, k, dropout=0.0):
+    """The layer as PyTorch code would write it: the reference's FeedForward
+    (lib/blocks/_component.py:48-52: silu(wi_0(x)) * wi_1(x), dropout on that
+    product in training, then wo) per expert over its routed rows, an fp32 router
+    with torch.softmax / torch.topk, and an index_add combine.  bf16 weights and
+    activations through F.linear (hipBLASLt); the per-expert row lists cost a host
+    synchronisation each (nonzero), as in any such loop."""
     import torch
     import torch.nn.functional as Fn
-    E = w_gate.shape[0]
+    logits = x.float() @ wr.float().t()
+    if bias is not None:
+        logits = logits + bias
+    wts, idx = torch.topk(torch.softmax(logits, dim=-1), k, dim=-1)
+    wts = wts / wts.sum(-1, keepdim=True)
+    y = torch.zeros(x.shape, dtype=torch.float32, device=x.device)
+    for e in range(w_gate.shape[0]):
+        tok, slot = (idx == e).nonzero(as_tuple=True)
+        if tok.numel() == 0:
+            continue
+        xe = x[tok]
+        h = Fn.silu(Fn.linear(xe, w_gate[e])) * Fn.linear(xe, w_up[e])
+        if dropout > 0.0:
+            h = Fn.dropout(h, dropout, training=True)
+        y = y.index_add(0, tok, Fn.linear(h, w_down[e]).float() * wts[tok, slot, None])
+    return y.to(x.dtype)
+
+
+def torch_eager_gpu(x, wr, bias, w_gate, w_up, w_down, k, ref_y, steps=10, warmup=3) -> dict:
+    """eager_layer on the same GPU and tensors, beside the HIP layer, with the
+    difference between the two outputs."""
+    import torch
 
     def fwd():
-        logits = x.float() @ wr.float().t()
-        if bias is not None:
-            logits = logits + bias
-        wts, idx = torch.topk(torch.softmax(logits, dim=-1), k, dim=-1)
-        wts = wts / wts.sum(-1, keepdim=True)
-        y = torch.zeros(x.shape, dtype=torch.float32, device=x.device)
-        for e in range(E):
-            tok, slot = (idx == e).nonzero(as_tuple=True)
-            if tok.numel() == 0:
-                continue
-            xe = x[tok]
-            h = Fn.silu(Fn.linear(xe, w_gate[e])) * Fn.linear(xe, w_up[e])
-            y.index_add_(0, tok, Fn.linear(h, w_down[e]).float() * wts[tok, slot, None])
-        return y.to(x.dtype)
+        return eager_layer(x, wr, bias, w_gate, w_up, w_down, k)
 
     for _ in range(warmup):
         out = fwd()
@@ -151,6 +158,34 @@ def torch_eager_gpu(x, wr, bias, w_gate, w_up, w_down, k, ref_y, steps=10, warmu
             "what": "PyTorch eager on this GPU: fp32 router + softmax/topk, per-expert "
                     "F.linear SwiGLU MLP over the routed rows (bf16, hipBLASLt), index_add "
                     f"combine; {steps} steps after {warmup} warm-up"}
+
+
+def torch_eager_gpu_train(x, wr, w_gate, w_up, w_down, k, dy, dropout, steps=5,
+                          warmup=2) -> dict:
+    """eager_layer's forward and autograd backward (parameter and input gradients)
+    on the same GPU, as PyTorch training code would run the layer."""
+    import torch
+    params = [t.detach().clone().requires_grad_(True) for t in (wr, w_gate, w_up, w_down)]
+    xr = x.detach().clone().requires_grad_(True)
+
+    def step():
+        for t in params + [xr]:
+            t.grad = None
+        y = eager_layer(xr, params[0], None, params[1], params[2], params[3], k, dropout)
+        y.backward(dy)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    return {"ms_per_step": ms, "tokens_per_s": x.shape[0] / (ms * 1e-3),
+            "what": "PyTorch eager forward + autograd backward of the same layer on this "
+                    f"GPU (bf16 parameters, dropout {dropout}); {steps} steps after "
+                    f"{warmup} warm-up"}
 
 
 def timed(fn, steps: int, warmup: int) -> float:
@@ -459,6 +494,8 @@ def bench_train(args) -> dict:
     ms_p0 = run(args.steps, 2, True)
     m.dropout = p_saved
     bd = train_stage_breakdown(args)
+    eager = torch_eager_gpu_train(x, tt["w_router"], tt["w_gate"], tt["w_up"], tt["w_down"], k,
+                                  dy, args.dropout)
     g = 2 * d * F * N * k
     return {
         "metric": "MoE layer training step (forward + backward) tokens/s, 36.4k tok, 16e top-2",
@@ -473,6 +510,7 @@ def bench_train(args) -> dict:
         "dropout_zero_ms_per_step": ms_p0,
         "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
         "breakdown": bd,
+        "torch_eager_gpu": eager,
         "note": "every stage is this library's HIP kernels; the backward reads the expert "
                 "offsets from the forward's pinned host copy (no host synchronisation); "
                 "weight-gradient products in one g5moe_weight_grad launch over per-expert "
