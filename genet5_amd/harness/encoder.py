@@ -11,12 +11,14 @@ Reference shapes followed:
     HIP varlen ALiBi kernel (genet5_amd.attention); backend "torch" keeps the
     PyTorch SDPA composition as the reference.
   * Attention projections q/k/v/o bias-free (lib/blocks/_sdpa_att.py:68-71),
-    bidirectional, scale 1/sqrt(head_dim).  No reference backend adds a
-    positional bias; following the DNABERT-2 lineage this one adds
+    bidirectional, scale 1/sqrt(head_dim).  No reference attention backend adds
+    a positional bias (lib/blocks/_sdpa_att.py, _flash_att.py); following the
+    DNABERT-2 lineage this one adds
     symmetric ALiBi, bias[h, i, j] = -slope_h * |i - j|, with the slopes of
     Press et al. (2022), "Train Short, Test Long".  Packed inputs with
     cu_seqlens attend within each sequence only (a block-diagonal mask per
-    row, unlike the reference SDPA fallback's global-offset mask).
+    row, unlike the global-offset mask of the reference SDPA fallback,
+    lib/blocks/_sdpa_att.py:36-43).
   * diffusion_generate (lib/inference/diffusion_engine.py:18-95): linear unmask
     schedule, mask/pad logits suppressed, argmax (temperature 0) or sampling,
     confidence = log-prob of the prediction (strategy "confidence") or the gap
