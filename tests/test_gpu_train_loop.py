@@ -48,6 +48,7 @@ def test_adamw_training_matches_eager_reference(cuda_device):
         m.w_down.copy_(torch.randn(E, d, Fd, device=cuda_device) * Fd ** -0.5)
     ref = [p.detach().clone().requires_grad_(True)
            for p in (m.router.weight, m.w_gate, m.w_up, m.w_down)]
+    init = [p.detach().clone() for p in ref]
     m.train()
 
     g = torch.Generator(device=cuda_device).manual_seed(1)
@@ -78,7 +79,8 @@ def test_adamw_training_matches_eager_reference(cuda_device):
     assert loss_r[-1] < 0.5 * loss_r[0], loss_r
     for i, (a, b) in enumerate(zip(loss_m, loss_r)):
         assert abs(a - b) <= 0.01 * b, (i, a, b)
-    # the optimizer moved every parameter of the module (none was left behind by a
-    # stale cache or a missing gradient)
-    for p, p0 in zip((m.router.weight, m.w_gate, m.w_up, m.w_down), ref):
+    # every parameter of the module got a finite gradient and moved (none was left
+    # behind by a stale cache or a missing gradient)
+    for p, p0 in zip((m.router.weight, m.w_gate, m.w_up, m.w_down), init):
         assert p.grad is not None and torch.isfinite(p.grad.float()).all()
+        assert not torch.equal(p.detach(), p0)
