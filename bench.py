@@ -153,8 +153,8 @@ def torch_eager_gpu(x, wr, bias, w_gate, w_up, w_down, k, ref_y, steps=10, warmu
     return {"ms_per_step": ms, "tokens_per_s": x.shape[0] / (ms * 1e-3),
             # a token whose top-2 is a near tie may pick another expert in fp32
             # torch than in the fixed-order router: the mean is the comparison
-            "mean_rel_diff_vs_hip": err.mean().item() / ref_abs.mean().item(),
-            "max_rel_diff_vs_hip": err.max().item() / ref_abs.max().item(),
+            "mean_rel_diff_vs_hip": err.mean().item() / max(ref_abs.mean().item(), 1e-30),
+            "max_rel_diff_vs_hip": err.max().item() / max(ref_abs.max().item(), 1e-30),
             "what": "PyTorch eager on this GPU: fp32 router + softmax/topk, per-expert "
                     "F.linear SwiGLU MLP over the routed rows (bf16, hipBLASLt), index_add "
                     f"combine; {steps} steps after {warmup} warm-up"}
