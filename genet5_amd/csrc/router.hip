@@ -33,8 +33,9 @@
 //
 // Cost.  The E*d fused multiply-adds per token are the floor: N*E*d = 447M
 // FMAs at N = 36,400, about 11-14 us of VALU time on 256 CUs at 2.0-2.4 GHz
-// (the contract's order rules out the matrix cores, and packed fp32 FMAs are
-// not used); reading x (55.9 MB) takes about 7 us at 8 TB/s, so the kernel is
+// (the contract's order rules out the matrix cores, packed fp32 FMAs are not
+// used, and v_dot2c_f32_bf16 is not correctly rounded, so it cannot carry the
+// contract); reading x (55.9 MB) takes about 7 us at 8 TB/s, so the kernel is
 // VALU-bound.  NaN payloads are outside the contract: a level adds own +
 // partner in one lane and partner + own in the other, equal for every
 // non-NaN value.
