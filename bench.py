@@ -10,7 +10,9 @@ for the dominant kernel (the grouped gate|up GEMM), its average launch time
 taken from HIP events recorded between the stages, on the stream they run on,
 inside the timed loop.  `cpu_baseline` times the CPU oracle (fp32,
 numpy/BLAS) on the same workload (all of its tokens unless --cpu-sample-tokens
-bounds it) on this host's cores, and config 1 beside it.
+bounds it) on this host's cores, and config 1 beside it; `torch_eager_gpu` times
+the same layer written as eager PyTorch on the same GPU (the reference's
+FeedForward body per expert), for context.
 """
 from __future__ import annotations
 
