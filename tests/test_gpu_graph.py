@@ -44,3 +44,36 @@ def test_forward_graph_replays_equal_eager(cuda_device, n):
         want = y_a if rep % 2 == 0 else y_b
         assert torch.equal(y, want), f"replay {rep}"
         del junk
+
+
+def test_module_forward_graph_replays_equal_eager(cuda_device):
+    """The drop-in module itself under capture (inference: no grad, eval mode), as a
+    serving loop or torch.cuda.graphs-based runtime would use it: outputs and
+    workspace come from the caching allocator's graph pool, and the weight caches
+    are built before capture.  Replays follow in-place input changes."""
+    from genet5_amd.moe import MoEFeedForward
+    d, F, E, k, n = 768, 3072, 16, 2, 4550
+    print(f"module graph capture n={n}", flush=True)
+    torch.manual_seed(0)
+    m = MoEFeedForward(d, F, 0.1, num_experts=E, top_k=k).to(cuda_device).to(torch.bfloat16)
+    m.eval()
+    g = torch.Generator(device=cuda_device).manual_seed(4)
+    x1 = torch.randn(2, n // 2, d, device=cuda_device, generator=g).to(torch.bfloat16)
+    x2 = torch.randn(2, n // 2, d, device=cuda_device, generator=g).to(torch.bfloat16)
+    with torch.no_grad():
+        y1, y2 = m(x1).clone(), m(x2).clone()
+        xin = x1.clone()
+        s = torch.cuda.Stream(cuda_device)
+        s.wait_stream(torch.cuda.current_stream(cuda_device))
+        with torch.cuda.stream(s):
+            m(xin)
+        torch.cuda.current_stream(cuda_device).wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            y = m(xin)
+        for rep in range(4):
+            xin.copy_(x1 if rep % 2 == 0 else x2)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y, y1 if rep % 2 == 0 else y2), f"replay {rep}"
