@@ -253,10 +253,13 @@ class MoEFeedForward(nn.Module):
         operands), cached by the parameters' versions: rebuilt only when a weight
         changes, so forwards and backwards between two optimizer steps (gradient
         accumulation) share one copy.  Under torch.compile the cache (Python-side
-        state) is bypassed and the copies are made by custom ops on every call."""
+        state) is bypassed and the copies are made by custom ops on every call, from
+        detached parameters: the copies are kernel operands, and the gradients reach
+        the parameters through the training op's own inputs."""
         if torch.compiler.is_compiling():
-            wgu = _pack_gate_up_op(self.w_gate.to(torch.bfloat16), self.w_up.to(torch.bfloat16))
-            wd = self.w_down.to(torch.bfloat16)
+            wgu = _pack_gate_up_op(self.w_gate.detach().to(torch.bfloat16),
+                                   self.w_up.detach().to(torch.bfloat16))
+            wd = self.w_down.detach().to(torch.bfloat16)
             if not transposed:
                 return wgu, wd
             return wgu, wd, _transpose_experts_op(wgu), _transpose_experts_op(wd)

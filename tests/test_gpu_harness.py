@@ -371,3 +371,36 @@ def test_upcycled_checkpoint_layer_equals_dense(cuda_device):
         mx, mean = normwise(y.cpu().numpy(), dense.cpu().numpy())
         print(f"upcycled layer {i}: max_rel={mx:.3e} mean_rel={mean:.3e}", flush=True)
         assert mx <= 2e-2 and mean <= 4e-3, (i, mx, mean)
+
+
+@pytest.mark.parametrize("dropout", [0.0, 0.1])
+def test_module_training_step_under_torch_compile(cuda_device, dropout):
+    """GeneT5 compiles its encoder for training (torch.compile(model.encoder)): the
+    module's training op, its fake implementation and the autograd backward trace
+    under dynamo + AOT autograd (aot_eager backend), and the compiled step gives
+    the eager step's output and gradients bit for bit (same seed for the dropout
+    mask: torch.manual_seed before each)."""
+    print(f"compile training dropout={dropout}", flush=True)
+    torch.manual_seed(0)
+    m = MoEFeedForward(128, 256, dropout, num_experts=4).to(cuda_device).to(torch.bfloat16)
+    m.train()
+    x = torch.randn(96, 128, device=cuda_device).to(torch.bfloat16)
+    dy = torch.randn(96, 128, device=cuda_device).to(torch.bfloat16)
+
+    def step(fn):
+        m.zero_grad(set_to_none=True)
+        xr = x.clone().requires_grad_(True)
+        torch.manual_seed(123)
+        y = fn(xr)
+        y.backward(dy)
+        return y.detach(), xr.grad, [p.grad.clone() for p in
+                                     (m.router.weight, m.w_gate, m.w_up, m.w_down)]
+
+    y0, dx0, g0 = step(m)
+    f = torch.compile(m, backend="aot_eager")
+    y1, dx1, g1 = step(f)
+    torch.cuda.synchronize()
+    assert torch.equal(y0, y1)
+    assert torch.equal(dx0, dx1)
+    for a, b in zip(g0, g1):
+        assert torch.equal(a, b)
