@@ -572,7 +572,7 @@ g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int
     return fail(G5MOE_ERR_INVALID_ARG, "pad_transpose: cols %d must be a positive multiple of "
                 "64 and kmax %d a multiple of 8 >= 0", int(cols), int(kmax));
   if (kmax == 0) return G5MOE_OK;
-  G5_NONNULL(src);
+  if (shape->n_tokens > 0) G5_NONNULL(src);  // no tokens: every row is a zero row
   G5_NONNULL(offsets);
   G5_NONNULL(out);
   if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
@@ -592,7 +592,7 @@ g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t*
                 "pad_rows: cols %d must be a positive multiple of 8 and kmax %d >= 0", int(cols),
                 int(kmax));
   if (kmax == 0) return G5MOE_OK;
-  G5_NONNULL(src);
+  if (shape->n_tokens > 0) G5_NONNULL(src);  // no tokens: every row is a zero row
   G5_NONNULL(offsets);
   G5_NONNULL(out);
   if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)

@@ -618,8 +618,9 @@ def pad_rows(src: torch.Tensor, perm: Optional[torch.Tensor], offsets: torch.Ten
         raise TypeError("pad_rows takes a contiguous bf16 source")
     _require(offsets, "offsets", (n_experts + 1,), torch.int32, dev)
     out = torch.empty((n_experts, kmax, cols), dtype=torch.bfloat16, device=dev)
-    shape = _lib.make_shape(max(1, src.shape[0] // top_k), 256, 256, n_experts, top_k,
-                            _lib.DTYPE_BF16)
+    # n_tokens: the source's row count (0 for an empty batch, when every output
+    # row is a zero row); the kernel itself reads offsets and perm
+    shape = _lib.make_shape(src.shape[0], 256, 256, n_experts, top_k, _lib.DTYPE_BF16)
     _lib.call("g5moe_pad_rows", _ptr(src), _ptr(perm), _ptr(offsets), _ptr(out), cols, kmax,
               ctypes.byref(shape), _stream(dev))
     return out

@@ -398,7 +398,8 @@ g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t
  * e's j-th sorted position, 0 for j >= M_e.  The row of sorted position p is
  * src row p (perm == NULL: dY) or src row perm[p] / k (the gathered x row).
  *   src : bf16 [rows, cols];  out : bf16 [E, cols, kmax];  cols multiple of 64,
- *   kmax multiple of 8; src and out 16-byte aligned. */
+ *   kmax multiple of 8; src and out 16-byte aligned.  shape->n_tokens 0 (an
+ *   empty batch, every offset 0) allows src NULL: out is all zeros. */
 g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int32_t* offsets,
                                  void* out, int32_t cols, int32_t kmax,
                                  const g5moe_shape* shape, void* stream);
@@ -408,7 +409,8 @@ g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int
  * p is src row p (perm == NULL: dY) or src row perm[p] / k (the gathered x
  * row).  These are g5moe_weight_grad's token-major operands.
  *   src : bf16 [rows, cols];  out : bf16 [E, kmax, cols];  cols multiple of 8,
- *   kmax >= 0; src and out 16-byte aligned. */
+ *   kmax >= 0; src and out 16-byte aligned.  shape->n_tokens 0 (an empty
+ *   batch, every offset 0) allows src NULL: out is all zeros. */
 g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t* offsets,
                             void* out, int32_t cols, int32_t kmax, const g5moe_shape* shape,
                             void* stream);
