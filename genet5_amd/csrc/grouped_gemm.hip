@@ -87,6 +87,39 @@ __device__ __forceinline__ float silu_mul(float g, float u) {
   return g * __builtin_amdgcn_rcpf(1.0f + __expf(-g)) * u;
 }
 
+// Writes one staged pass of a wave's epilogue region to global memory: ROWS
+// token rows of RBY bytes, chunk c of row r at c ^ ((r / (256 / RBY)) % (RBY /
+// 16)), row r to dst + (p0 + r) * ld for the rows p0 + r < p_end, as 16-byte
+// non-temporal stores, RBY / 16 lanes per row.  Every LDS read is issued before
+// the first store, so their latencies overlap instead of one read waiting
+// before each store; a pass whose rows are all valid stores without per-row
+// branches.
+template <int ROWS, int RBY>
+__device__ __forceinline__ void store_pass(const char* epi, uint16_t* dst, int64_t ld, int p0,
+                                           int p_end, int lane) {
+  constexpr int CR = RBY / 16;
+  constexpr int LPR = 256 / RBY;
+  constexpr int RPI = 1024 / RBY;  // rows per 1 KB wave instruction
+  constexpr int NIT = ROWS * RBY / 1024;
+  const int c = lane % CR;
+  const int r0 = lane / CR;
+  uint4 v[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int r = it * RPI + r0;
+    v[it] = *reinterpret_cast<const uint4*>(epi + r * RBY + ((c ^ ((r / LPR) % CR)) * 16));
+  }
+  uint16_t* row0 = dst + (int64_t(p0) + r0) * ld + c * 8;
+  if (p0 + ROWS <= p_end) {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it) store16_nt(row0 + it * RPI * ld, v[it]);
+  } else {
+#pragma unroll
+    for (int it = 0; it < NIT; ++it)
+      if (p0 + it * RPI + r0 < p_end) store16_nt(row0 + it * RPI * ld, v[it]);
+  }
+}
+
 struct TileCoord {
   int e, p_begin, p_end, n0;
   int a_row;  // A row of position p_begin (non-gathered A)
@@ -694,14 +727,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
             __builtin_amdgcn_sched_barrier(0);
           }
         }
-#pragma unroll
-        for (int it = 0; it < 32 * RBY / 1024; ++it) {
-          const int r = it * (1024 / RBY) + lane / CR;
-          const int c = lane % CR;
-          const uint4 v = *reinterpret_cast<const uint4*>(epi + r * RBY + ((c ^ (r % CR)) * 16));
-          const int p = cur.p_begin + wm * WTM + j * 32 + r;
-          if (p < cur.p_end) store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
-        }
+        store_pass<32, RBY>(epi, args.C2 + col0, args.ldc2, cur.p_begin + wm * WTM + j * 32,
+                            cur.p_end, lane);
 #pragma unroll
         for (int ob = 0; ob < OB / 2; ++ob)
 #pragma unroll
@@ -709,15 +736,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
             *reinterpret_cast<uint2*>(epi + row * HRBY +
                                       (((ob * 4 + q) ^ ((row / HLPR) % HCR)) * 16) + half * 8) =
                 hv[ob][q];
-#pragma unroll
-        for (int it = 0; it < 32 * HRBY / 1024; ++it) {
-          const int r = it * (1024 / HRBY) + lane / HCR;
-          const int c = lane % HCR;
-          const uint4 v = *reinterpret_cast<const uint4*>(
-              epi + r * HRBY + ((c ^ ((r / HLPR) % HCR)) * 16));
-          const int p = cur.p_begin + wm * WTM + j * 32 + r;
-          if (p < cur.p_end) store16_nt(args.C + int64_t(p) * args.ldc + hcol0 + c * 8, v);
-        }
+        store_pass<32, HRBY>(epi, args.C + hcol0, args.ldc, cur.p_begin + wm * WTM + j * 32,
+                             cur.p_end, lane);
       }
     } else if constexpr (MODE == 4) {
       // The SwiGLU backward on this tile's dh (rounded to bf16, as a stored dh
@@ -860,16 +880,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
               }
             }
           }
-#pragma unroll
-          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
-            const int row = it * (1024 / RBY) + lane / CR;
-            const int c = lane % CR;
-            const uint4 v = *reinterpret_cast<const uint4*>(
-                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
-            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
-            if (p < cur.p_end)
-              store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
-          }
+          store_pass<ROWS, RBY>(epi, args.C2 + col0, args.ldc2,
+                                cur.p_begin + wm * WTM + pass * ROWS, cur.p_end, lane);
         }
       }
       if constexpr (MODE == 3) {
@@ -922,18 +934,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
               }
             }
           }
-#pragma unroll
-          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
-            const int row = it * (1024 / RBY) + lane / CR;
-            const int c = lane % CR;
-            const uint4 v = *reinterpret_cast<const uint4*>(
-                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
-            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
-            if (p < cur.p_end)
-              // non-temporal: the outputs are the next kernel's, and the L2 is
-              // left to the operand tiles (training forward 3 % faster)
-              store16_nt(args.C + int64_t(p) * args.ldc + col0 + c * 8, v);
-          }
+          // non-temporal stores: the outputs are the next kernel's, and the L2
+          // is left to the operand tiles (training forward 3 % faster)
+          store_pass<ROWS, RBY>(epi, args.C + col0, args.ldc,
+                                cur.p_begin + wm * WTM + pass * ROWS, cur.p_end, lane);
         }
       }
 
@@ -980,16 +984,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
               }
             }
           }
-#pragma unroll
-          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
-            const int row = it * (1024 / RBY) + lane / CR;
-            const int c = lane % CR;
-            const uint4 v = *reinterpret_cast<const uint4*>(
-                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
-            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
-            if (p < cur.p_end)
-              store16_nt(args.C2 + int64_t(p) * args.ldc2 + col0 + c * 8, v);
-          }
+          store_pass<ROWS, RBY>(epi, args.C2 + col0, args.ldc2,
+                                cur.p_begin + wm * WTM + pass * ROWS, cur.p_end, lane);
         }
       }
       if constexpr (MODE == 3) {
@@ -1038,18 +1034,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
               }
             }
           }
-#pragma unroll
-          for (int it = 0; it < ROWS * RBY / 1024; ++it) {
-            const int row = it * (1024 / RBY) + lane / CR;
-            const int c = lane % CR;
-            const uint4 v = *reinterpret_cast<const uint4*>(
-                epi + row * RBY + ((c ^ ((row / LPR) % CR)) * 16));
-            const int p = cur.p_begin + wm * WTM + pass * ROWS + row;
-            if (p < cur.p_end)
-              // non-temporal: the outputs are the next kernel's, and the L2 is
-              // left to the operand tiles (training forward 3 % faster)
-              store16_nt(args.C + int64_t(p) * args.ldc + col0 + c * 8, v);
-          }
+          // non-temporal stores: the outputs are the next kernel's, and the L2
+          // is left to the operand tiles (training forward 3 % faster)
+          store_pass<ROWS, RBY>(epi, args.C + col0, args.ldc,
+                                cur.p_begin + wm * WTM + pass * ROWS, cur.p_end, lane);
         }
       }
 
