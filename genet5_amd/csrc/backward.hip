@@ -654,15 +654,103 @@ __global__ __launch_bounds__(256) void pack_gate_up_t_kernel(
   }
 }
 
+// The 16-byte forms of the two transposes above, for 16-byte aligned pointers.
+// A 64 x 64 tile goes through LDS as bf16 pairs (element (r, c) in the low or
+// high half of dword c / 2 of row r, rows 33 dwords apart): each thread loads
+// two 16-byte row chunks and stores them as four dwords, then reads the 8 dwords
+// (rows 8q .. 8q + 7, dword column cc) that hold chunk q of output rows 2 cc and
+// 2 cc + 1 — across a wave's 64 lanes those reads hit 64 distinct banks — and
+// writes both rows' 16-byte chunks; 8 lanes cover one 128-byte row segment.
+__device__ __forceinline__ void tile_store_rows(uint32_t (*tile)[33], int r, int q,
+                                                const uint4& v) {
+  tile[r][4 * q] = v.x;
+  tile[r][4 * q + 1] = v.y;
+  tile[r][4 * q + 2] = v.z;
+  tile[r][4 * q + 3] = v.w;
+}
+
+// Output rows 2 cc (low halves) and 2 cc + 1 (high halves), chunk q.
+__device__ __forceinline__ void tile_read_cols(uint32_t (*tile)[33], int cc, int q, uint4& lo,
+                                               uint4& hi) {
+  uint32_t d[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) d[j] = tile[8 * q + j][cc];
+  uint32_t l[4], h[4];
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    l[m] = (d[2 * m] & 0xffffu) | (d[2 * m + 1] << 16);
+    h[m] = (d[2 * m] >> 16) | (d[2 * m + 1] & 0xffff0000u);
+  }
+  lo = make_uint4(l[0], l[1], l[2], l[3]);
+  hi = make_uint4(h[0], h[1], h[2], h[3]);
+}
+
+__global__ __launch_bounds__(256) void transpose16_kernel(const uint16_t* __restrict__ w,
+                                                          uint16_t* __restrict__ wt, int R,
+                                                          int C) {
+  __shared__ uint32_t tile[64][33];
+  const int e = blockIdx.z;
+  const int r0 = blockIdx.y * 64, c0 = blockIdx.x * 64;
+  const uint16_t* src = w + int64_t(e) * R * C;
+  uint16_t* dst = wt + int64_t(e) * R * C;
+  const int t = threadIdx.x;
+  const int q = t & 7;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (t >> 3) + 32 * i;
+    tile_store_rows(tile, r, q,
+                    *reinterpret_cast<const uint4*>(src + int64_t(r0 + r) * C + c0 + 8 * q));
+  }
+  __syncthreads();
+  const int cc = t >> 3;
+  uint4 lo, hi;
+  tile_read_cols(tile, cc, q, lo, hi);
+  *reinterpret_cast<uint4*>(dst + int64_t(c0 + 2 * cc) * R + r0 + 8 * q) = lo;
+  *reinterpret_cast<uint4*>(dst + int64_t(c0 + 2 * cc + 1) * R + r0 + 8 * q) = hi;
+}
+
+__global__ __launch_bounds__(256) void pack_gate_up_t16_kernel(
+    const uint16_t* __restrict__ wg, const uint16_t* __restrict__ wu, uint16_t* __restrict__ wgu,
+    uint16_t* __restrict__ wgu_t, int F, int d) {
+  __shared__ uint32_t tile[64][33];
+  const int e = blockIdx.z;
+  const int rb = blockIdx.y, c0 = blockIdx.x * 64;
+  const int64_t F2 = 2 * int64_t(F);
+  const int t = threadIdx.x;
+  const int q = t & 7;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (t >> 3) + 32 * i;  // packed row 64 rb + r: gate rows first, then up
+    const uint16_t* src = (r < 32 ? wg : wu) + (int64_t(e) * F + 32 * rb + (r & 31)) * d;
+    const uint4 v = *reinterpret_cast<const uint4*>(src + c0 + 8 * q);
+    tile_store_rows(tile, r, q, v);
+    if (wgu != nullptr)
+      *reinterpret_cast<uint4*>(wgu + (int64_t(e) * F2 + 64 * rb + r) * d + c0 + 8 * q) = v;
+  }
+  __syncthreads();
+  const int cc = t >> 3;
+  uint4 lo, hi;
+  tile_read_cols(tile, cc, q, lo, hi);
+  *reinterpret_cast<uint4*>(wgu_t + (int64_t(e) * d + c0 + 2 * cc) * F2 + 64 * rb + 8 * q) = lo;
+  *reinterpret_cast<uint4*>(wgu_t + (int64_t(e) * d + c0 + 2 * cc + 1) * F2 + 64 * rb + 8 * q) =
+      hi;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 }  // namespace
 
 hipError_t launch_pack_gate_up_t(const uint16_t* wg, const uint16_t* wu, uint16_t* wgu,
                                  uint16_t* wgu_t, const g5moe_shape& s, hipStream_t st) {
   if (s.n_experts == 0) return hipSuccess;
   if (s.d_model % 64 != 0 || s.d_ff % 32 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(pack_gate_up_t_kernel,
-                     dim3(unsigned(s.d_model / 64), unsigned(s.d_ff / 32), unsigned(s.n_experts)),
-                     dim3(256), 0, st, wg, wu, wgu, wgu_t, s.d_ff, s.d_model);
+  const dim3 grid(unsigned(s.d_model / 64), unsigned(s.d_ff / 32), unsigned(s.n_experts));
+  if (aligned16(wg) && aligned16(wu) && aligned16(wgu) && aligned16(wgu_t))
+    hipLaunchKernelGGL(pack_gate_up_t16_kernel, grid, dim3(256), 0, st, wg, wu, wgu, wgu_t,
+                       s.d_ff, s.d_model);
+  else
+    hipLaunchKernelGGL(pack_gate_up_t_kernel, grid, dim3(256), 0, st, wg, wu, wgu, wgu_t,
+                       s.d_ff, s.d_model);
   return hipGetLastError();
 }
 
@@ -836,8 +924,11 @@ hipError_t launch_transpose_experts(const uint16_t* w, uint16_t* wt, int E, int 
                                     hipStream_t st) {
   if (E == 0 || R == 0 || C == 0) return hipSuccess;
   if (R % 64 != 0 || C % 64 != 0) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(transpose_kernel, dim3(unsigned(C / 64), unsigned(R / 64), unsigned(E)),
-                     dim3(256), 0, st, w, wt, R, C);
+  const dim3 grid(unsigned(C / 64), unsigned(R / 64), unsigned(E));
+  if (aligned16(w) && aligned16(wt))
+    hipLaunchKernelGGL(transpose16_kernel, grid, dim3(256), 0, st, w, wt, R, C);
+  else
+    hipLaunchKernelGGL(transpose_kernel, grid, dim3(256), 0, st, w, wt, R, C);
   return hipGetLastError();
 }
 

@@ -604,6 +604,51 @@ def test_pack_gate_up_transposed(cuda_device, E, F, d):
     assert torch.equal(wgu, ref)
     assert torch.equal(wgu_t, ref_t)
     assert torch.equal(only_t, ref_t)
+    # against torch: 32-row blocks of gate then up rows per expert, and its transpose
+    packed = torch.cat([wg.view(E, F // 32, 32, d), wu.view(E, F // 32, 32, d)], dim=2)
+    packed = packed.view(E, 2 * F, d)
+    assert torch.equal(wgu, packed)
+    assert torch.equal(wgu_t, packed.transpose(1, 2).contiguous())
+    # operands and outputs at an odd element offset (2-byte aligned): the same bits
+    # through the kernel that makes 2-byte accesses
+    n = E * F * d
+
+    def odd(t):
+        buf = torch.empty(t.numel() + 1, dtype=torch.bfloat16, device=cuda_device)
+        v = buf[1:].view(t.shape)
+        v.copy_(t)
+        return v
+
+    wg_o, wu_o = odd(wg), odd(wu)
+    wgu_o, wgu_t_o = odd(torch.zeros_like(wgu)), odd(torch.zeros_like(wgu_t))
+    assert wg_o.data_ptr() % 16 != 0 and wgu_t_o.data_ptr() % 16 != 0 and n > 0
+    _lib.call("g5moe_pack_gate_up_transposed", ops._ptr(wg_o), ops._ptr(wu_o), ops._ptr(wgu_o),
+              ops._ptr(wgu_t_o), ctypes.byref(shape), ops._stream(cuda_device))
+    torch.cuda.synchronize()
+    assert torch.equal(wgu_o, packed)
+    assert torch.equal(wgu_t_o, wgu_t)
+
+
+@pytest.mark.parametrize("E,R,C", [(16, 3072, 768), (16, 768, 3072), (3, 128, 192), (1, 64, 64)])
+def test_transpose_experts_equals_torch(cuda_device, E, R, C):
+    """g5moe_transpose_experts bit for bit torch's transpose(1, 2), with 16-byte
+    aligned tensors (the kernel with 16-byte accesses) and with the source and the
+    output at an odd element offset (the kernel with 2-byte accesses)."""
+    from genet5_amd import _lib
+    g = torch.Generator(device=cuda_device).manual_seed(R + C)
+    w = torch.randn(E, R, C, device=cuda_device, generator=g).to(torch.bfloat16)
+    ref = w.transpose(1, 2).contiguous()
+    assert torch.equal(ops.transpose_experts(w), ref)
+    wbuf = torch.empty(E * R * C + 1, dtype=torch.bfloat16, device=cuda_device)
+    obuf = torch.zeros(E * R * C + 1, dtype=torch.bfloat16, device=cuda_device)
+    w_o, out_o = wbuf[1:].view(E, R, C), obuf[1:].view(E, C, R)
+    w_o.copy_(w)
+    assert w_o.data_ptr() % 16 != 0 and out_o.data_ptr() % 16 != 0
+    _lib.call("g5moe_transpose_experts", ops._ptr(w_o), ops._ptr(out_o), E, R, C,
+              ops._stream(cuda_device))
+    torch.cuda.synchronize()
+    assert torch.equal(out_o, ref)
+    assert obuf[0].item() == 0  # nothing written before the output
 
 
 def test_module_autograd_skewed_routing_vs_oracle(cuda_device):
