@@ -75,8 +75,13 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kHeadDim = 64;
 constexpr int kBQ = 128;   // queries per workgroup (32 per wave)
 constexpr int kBKV = 64;   // keys per LDS block
-constexpr int kRowBytes = kHeadDim * 2 + 16;      // 144: padded K row / V^T row
+constexpr int kRowBytes = kHeadDim * 2 + 16;      // 144: padded K row
 constexpr int kTileBytes = kBKV * kRowBytes;      // 9 KB
+// V rows (one key each) 192 bytes apart: the four keys a transposing read's
+// 16-lane group covers start at a multiple of 4, so their 64-byte row pieces
+// land in four distinct quarters of the 64 banks.
+constexpr int kVRowBytes = kHeadDim * 2 + 64;
+constexpr int kVTileBytes = kBKV * kVRowBytes;    // 12 KB
 constexpr float kSkipMargin = 64.0f;              // skipped keys have p < 2^-64
 constexpr float kFixedGap = 64.0f;                // reference-max loop: row maximum >= 2^-64
 constexpr float kLog2e = 1.4426950408889634f;
@@ -103,16 +108,23 @@ struct AttnArgs {
 // Byte offset of 16-byte chunk c of LDS row r.
 __device__ __forceinline__ int lds_off(int row, int chunk) { return row * kRowBytes + chunk * 16; }
 
-// Position of key r (0..63) inside V^T's row: bits 2 and 3 swapped.
-__device__ __forceinline__ int vt_pos(int r) {
-  return (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4* lds_i16x4_p;
+
+// ds_read_b64_tr_b16 (gfx950): within each 16-lane group the lanes' 64-bit
+// chunks form a 16 x 4 matrix (lane k's chunk is row k), and lane i receives
+// element i % 4 of rows i / 4, 4 + i / 4, 8 + i / 4 and 12 + i / 4.
+__device__ __forceinline__ i16x4 read_tr(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(reinterpret_cast<lds_i16x4_p>(
+      uintptr_t((__attribute__((address_space(3))) const char*)p)));
 }
 
 // LSE: softmax_lse is written (a.lse != nullptr).
 template <bool LSE>
 __global__ __attribute__((amdgpu_flat_work_group_size(256, 256), amdgpu_waves_per_eu(2)))
 void attn_fwd_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) char smem[2][2][kTileBytes];  // [buffer][K, V^T]
+  __shared__ __attribute__((aligned(16))) char ksm[2][kTileBytes];   // K rows
+  __shared__ __attribute__((aligned(16))) char vsm[2][kVTileBytes];  // V rows
 
   const int z = blockIdx.z;
   const int hq = blockIdx.y;
@@ -202,18 +214,17 @@ void attn_fwd_kernel(AttnArgs a) {
     mref = sc * __builtin_sqrtf(ss_own) * kmx;
   }
 
-  // Tile loaders.  K: thread t moves rows (t >> 3) and (t >> 3) + 32, chunk t & 7
-  // (eight threads per 128-byte row).  V: thread t moves key t & 63, chunks
-  // (t >> 6) and (t >> 6) + 4, and writes them transposed.  Rows past the
-  // sequence end are zero (masked keys then meet finite values only).
+  // Tile loaders: thread t moves rows (t >> 3) and (t >> 3) + 32, chunk t & 7
+  // (eight threads per 128-byte row), of K and of V.  Rows past the sequence
+  // end are zero (masked keys then meet finite values only).
   const int k_row = tid >> 3, k_chunk = tid & 7;
-  const int v_key = tid & 63, v_chunk = tid >> 6;
   const uint16_t* kbase = a.k + int64_t(s0) * a.k_tok + hk * a.k_head;
   const uint16_t* vbase = a.v + int64_t(s0) * a.v_tok + hk * a.v_head;
   // per-lane element offsets inside a tile (the tile's base is block-uniform)
   const int64_t k_off0 = int64_t(k_row) * a.k_tok + k_chunk * 8;
   const int64_t k_off1 = k_off0 + 32 * a.k_tok;
-  const int64_t v_off = int64_t(v_key) * a.v_tok + v_chunk * 8;
+  const int64_t v_off0 = int64_t(k_row) * a.v_tok + k_chunk * 8;
+  const int64_t v_off1 = v_off0 + 32 * a.v_tok;
   u32x4 kreg[2], vreg[2];
   auto load_k = [&](int j0) __attribute__((always_inline)) {
     const uint16_t* kt = kbase + int64_t(j0) * a.k_tok;
@@ -226,27 +237,24 @@ void attn_fwd_kernel(AttnArgs a) {
   };
   auto load_v = [&](int j0) __attribute__((always_inline)) {
     const uint16_t* vt = vbase + int64_t(j0) * a.v_tok;
-    const int vr = j0 + v_key;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      vreg[i] = vr < L ? *reinterpret_cast<const u32x4*>(vt + v_off + 32 * i)
+    for (int i = 0; i < 2; ++i) {
+      const int vr = j0 + k_row + 32 * i;
+      vreg[i] = vr < L ? *reinterpret_cast<const u32x4*>(vt + (i == 0 ? v_off0 : v_off1))
                        : u32x4{0, 0, 0, 0};
+    }
   };
   auto store_k = [&](int buf) __attribute__((always_inline)) {
-    char* Ks = smem[buf][0];
+    char* Ks = ksm[buf];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
       *reinterpret_cast<u32x4*>(Ks + lds_off(k_row + 32 * i, k_chunk)) = kreg[i];
   };
   auto store_v = [&](int buf) __attribute__((always_inline)) {
-    char* vrow = smem[buf][1] + v_chunk * 8 * kRowBytes + vt_pos(v_key) * 2;
+    char* Vs = vsm[buf];
 #pragma unroll
     for (int i = 0; i < 2; ++i)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t val = uint16_t(vreg[i][e >> 1] >> ((e & 1) * 16));
-        *reinterpret_cast<uint16_t*>(vrow + (32 * i + e) * kRowBytes) = val;
-      }
+      *reinterpret_cast<u32x4*>(Vs + (k_row + 32 * i) * kVRowBytes + k_chunk * 16) = vreg[i];
   };
   auto load_tile = [&](int j0) __attribute__((always_inline)) {
     load_k(j0);
@@ -277,7 +285,13 @@ void attn_fwd_kernel(AttnArgs a) {
                         pk[c >> 1][4 * (c & 1) + 2], pk[c >> 1][4 * (c & 1) + 3]};
     return __builtin_bit_cast(bf16x8, praw);
   };
-  // O^T += V^T . P^T over the four 16-key chunks
+  // O^T += V^T . P^T over the four 16-key chunks.  The V^T operand of lane
+  // (col, half) for chunk c is head dim 32 mb + col at the keys its P^T elements
+  // hold, 16 c + 4 half + {0..3, 8..11}: two transposing reads of four keys
+  // each, lane k of a 16-lane group addressing key (k / 4) of the four and the
+  // four dims from 4 (k % 4) of the group's 16.
+  const int v_lane = (4 * half + ((lane & 15) >> 2)) * kVRowBytes +
+                     (16 * ((lane >> 4) & 1) + 4 * (lane & 3)) * 2;
   auto out_product = [&](const char* Vs, const uint32_t (*pk)[8], f32x16* o)
       __attribute__((always_inline)) {
 #pragma unroll
@@ -285,8 +299,11 @@ void attn_fwd_kernel(AttnArgs a) {
       const bf16x8 pf = p_chunk(pk, c);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        const bf16x8 vf =
-            *reinterpret_cast<const bf16x8*>(Vs + lds_off(32 * mb + col, 2 * c + half));
+        const char* vp = Vs + v_lane + 16 * c * kVRowBytes + 64 * mb;
+        const i16x4 lo = read_tr(vp);
+        const i16x4 hi = read_tr(vp + 8 * kVRowBytes);
+        const i16x4 vv[2] = {lo, hi};
+        const bf16x8 vf = __builtin_bit_cast(bf16x8, vv);
         o[mb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf, o[mb], 0, 0, 0);
       }
     }
@@ -356,8 +373,8 @@ void attn_fwd_kernel(AttnArgs a) {
       const int buf = n & 1;
       const int j0 = n * kBKV;
       if (n < n_hi) load_tile(j0 + kBKV);
-      const char* Ks = smem[buf][0];
-      const char* Vs = smem[buf][1];
+      const char* Ks = ksm[buf];
+      const char* Vs = vsm[buf];
       f32x16 s[2];
       scores(Ks, s);
 
@@ -432,8 +449,8 @@ void attn_fwd_kernel(AttnArgs a) {
       const int buf = n & 1;
       const int j0 = n * kBKV;
       if (n < n_hi) load_tile(j0 + kBKV);
-      const char* Ks = smem[buf][0];
-      const char* Vs = smem[buf][1];
+      const char* Ks = ksm[buf];
+      const char* Vs = vsm[buf];
       f32x16 s[2];
       scores(Ks, s);
 
