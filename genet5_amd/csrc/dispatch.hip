@@ -55,7 +55,7 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_rank_kernel(
     for (int w = 0; w < wave; ++w) r += wcnt[w][e];
   }
   if (a < nk) rank[a] = r;
-  if (threadIdx.x < n_experts) {
+  if (int(threadIdx.x) < n_experts) {
     int c = 0;
     for (int w = 0; w < kWaves; ++w) c += wcnt[w][threadIdx.x];
     blk_counts[int64_t(blockIdx.x) * n_experts + threadIdx.x] = c;
