@@ -98,7 +98,9 @@ g5moe_status g5moe_pack_gate_up(const void* w_gate, const void* w_up, void* w_ga
  * w_gate and w_up (the backward's dX product reads the transpose):
  *   w_gate_up : bf16 [E, 2F, d] out, or NULL (only the transpose);
  *   w_gate_up_t : bf16 [E, d, 2F] out, w_gate_up_t[e][c][r] = w_gate_up[e][r][c].
- * d a multiple of 64.  No reference counterpart (a layout step of this library). */
+ * d a multiple of 64.  Any 2-byte alignment; with every pointer 16-byte aligned
+ * the copy moves 16 bytes per access (about twice as fast), with the same
+ * result.  No reference counterpart (a layout step of this library). */
 g5moe_status g5moe_pack_gate_up_transposed(const void* w_gate, const void* w_up,
                                            void* w_gate_up, void* w_gate_up_t,
                                            const g5moe_shape* shape, void* stream);
@@ -295,7 +297,9 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
 
 /* W [E, rows, cols] bf16 -> W^T [E, cols, rows] (per-expert transpose; the
  * backward's products need Wd^T [E, F, d] and the packed gate|up's transpose
- * [E, d, 2F]).  rows and cols are multiples of 64. */
+ * [E, d, 2F]).  rows and cols are multiples of 64.  Any 2-byte alignment; with
+ * both pointers 16-byte aligned the copy moves 16 bytes per access, with the
+ * same result. */
 g5moe_status g5moe_transpose_experts(const void* w, void* w_t, int32_t n_experts, int32_t rows,
                                      int32_t cols, void* stream);
 
