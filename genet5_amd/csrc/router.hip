@@ -17,19 +17,20 @@
 // reduces them with a reduce-scatter butterfly — at the xor-32 step every lane
 // keeps 16 of its 32 values and adds the partner's copy of those 16, then
 // 16 -> 8 at xor-16, ..., 2 -> 1 at xor-2, and a plain xor-1 butterfly.  Each
-// sum is therefore the pairwise tree of the contract; lanes 2m and 2m+1 end up
-// holding the logit of (token m >> 3, expert m & 7).  The exchanges use no LDS:
+// sum is therefore the pairwise tree of the contract; with 2-token batches the
+// lanes 4m .. 4m+3 end up holding the logit of (token m >> 3, expert m & 7)
+// (4-token batches: lanes 2m and 2m+1).  The exchanges use no LDS:
 // the xor-32 and xor-16 levels are gfx950's v_permlane32_swap and
 // v_permlane16_swap, the others DPP row rotates and a quad permute folded into
 // the adds.
 //
-// Schedule.  Persistent: at most two resident workgroups per CU; each wave pair
-// owns a contiguous range of tokens per round, walks it in 4-token batches with
-// the next batch's rows in flight while the current one computes (MODE 2, with
-// two rows per token, loads each batch where it computes it instead) (row
-// addresses are scalar: the wave index is made uniform), and stages the logits
-// in LDS; one thread per token then does the top-k scan and the gates.  The
-// weights are loaded into registers once per wave.
+// Schedule.  Persistent: at most the resident workgroups per CU (three for
+// MODE 0, two for MODES 1 / 2); each wave pair owns a contiguous range of tokens
+// per round, walks it in 2-token batches with the next batch's rows in flight
+// while the current one computes (row addresses are scalar: the wave index is
+// made uniform), and stages the logits in LDS; one thread per token then does
+// the top-k scan and the gates.  The weights are loaded into registers once per
+// wave.
 //
 // Cost.  The E*d fused multiply-adds per token are the floor: N*E*d = 447M
 // FMAs at N = 36,400, about 11-14 us of VALU time on 256 CUs at 2.0-2.4 GHz
@@ -65,7 +66,7 @@ namespace {
 
 constexpr int kRouterThreads = 256;
 constexpr int kHalfExperts = 8;           // experts per wave
-constexpr int kTokBatch = 4;              // tokens reduced together
+constexpr int kTokBatch = 4;              // tokens reduced together (the widest batch)
 
 template <typename XT, int L>
 struct RowLoader;
@@ -307,19 +308,21 @@ __device__ __forceinline__ void to_floats(const RawRow<XT, L>& r, float (&v)[L])
 // partner's copy of it in the two results, whose sum is the pairwise sum of the
 // contract (own + partner in low lanes, partner + own in high lanes: the same
 // value for every non-NaN input, fp addition being commutative).
+template <int HALF>
 __device__ __forceinline__ void rs_swap32(float* p) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
+  for (int i = 0; i < HALF; ++i) {
     const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(p[i]),
-                                                    __float_as_uint(p[16 + i]), false, false);
+                                                    __float_as_uint(p[HALF + i]), false, false);
     p[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 }
+template <int HALF>
 __device__ __forceinline__ void rs_swap16(float* p) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
+  for (int i = 0; i < HALF; ++i) {
     const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(p[i]),
-                                                    __float_as_uint(p[8 + i]), false, false);
+                                                    __float_as_uint(p[HALF + i]), false, false);
     p[i] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
   }
 }
@@ -351,6 +354,13 @@ __device__ __forceinline__ void rs_dpp(float* p, int lane) {
   }
 }
 
+// MODE 2 with the next batch's rows prefetched (a second row buffer): 216
+// VGPRs at 2-token batches, still two waves per SIMD.  At 4-token batches the
+// second buffer cost the second wave (280 VGPRs; 83 us against 74 without it).
+#ifndef G5_ROUTER_M2_PREFETCH
+#define G5_ROUTER_M2_PREFETCH 1
+#endif
+
 // Tokens a wave pair handles per round (the logit staging in LDS).
 constexpr int kMaxPairTokens = 64;
 
@@ -359,11 +369,11 @@ constexpr int kMaxPairTokens = 64;
 //
 // Persistent schedule: the grid is at most the resident block count; in each
 // round wave pair q of the grid owns the contiguous token range [base + q *
-// tpp, base + (q + 1) * tpp), walks it in batches of 4 tokens with the next
+// tpp, base + (q + 1) * tpp), walks it in batches of TB tokens with the next
 // batch's rows loaded while the current one computes, and stages the logits in
 // LDS; after a block barrier one thread per token does the top-k scan.  The
 // weights are loaded into registers once per wave.
-template <typename XT, int L, int MODE>
+template <typename XT, int L, int MODE, int TB = kTokBatch>
 __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     const XT* __restrict__ x, const XT* __restrict__ wr, const float* __restrict__ bias,
     int64_t n_tokens, int n_experts, int top_k, int32_t* __restrict__ topk_idx,
@@ -398,37 +408,39 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
 
   // the bias of the expert this lane's logits belong to (loaded once: a load in
   // the batch loop would make its waits cover the prefetched rows)
-  const int e_lane = e0 + ((lane >> 1) & 7);
+  // lane bits above SH index the reduced sums (see compute_batch)
+  constexpr int SH = TB == 4 ? 1 : 2;
+  const int e_lane = e0 + ((lane >> SH) & 7);
   const float bias_e = (bias != nullptr && e_lane < n_experts) ? bias[e_lane] : 0.f;
 
   const int64_t round_tokens = int64_t(gridDim.x) * 2 * tpp;
   const int64_t pid = int64_t(blockIdx.x) * 2 + pair;
   constexpr int NX = MODE == 2 ? 2 : 1;  // rows loaded per token (x, and x_add)
-  RawRow<XT, L> ra[NX][kTokBatch], rb[NX][kTokBatch];
+  RawRow<XT, L> ra[NX][TB], rb[NX][TB];
 
   for (int64_t base = 0; base < n_tokens; base += round_tokens) {
     const int64_t t0 = base + pid * tpp;
     const int64_t t1 = min(t0 + int64_t(tpp), n_tokens);
-    const int nb = t1 > t0 ? int((t1 - t0 + kTokBatch - 1) / kTokBatch) : 0;
+    const int nb = t1 > t0 ? int((t1 - t0 + TB - 1) / TB) : 0;
     float* lgp = &lg[pair * kMaxPairTokens][0];
 
     // rows of batch b (rows past the end are computed, not stored)
-    auto load_batch = [&](RawRow<XT, L> (&r)[NX][kTokBatch], int b) {
+    auto load_batch = [&](RawRow<XT, L> (&r)[NX][TB], int b) {
 #pragma unroll
-      for (int m = 0; m < kTokBatch; ++m) {
-        const int64_t t = min(t0 + b * kTokBatch + m, n_tokens - 1);
+      for (int m = 0; m < TB; ++m) {
+        const int64_t t = min(t0 + b * TB + m, n_tokens - 1);
         load_raw<XT, L>(x + size_t(t) * D + lane * L, r[0][m]);
         if constexpr (MODE == 2)
           load_raw<XT, L>(static_cast<const XT*>(na.x_add) + size_t(t) * D + lane * L,
                           r[NX - 1][m]);
       }
     };
-    auto compute_batch = [&](const RawRow<XT, L> (&r)[NX][kTokBatch], int b) {
-      const int64_t tb = t0 + b * kTokBatch;
-      float p[kTokBatch * kHalfExperts];
+    auto compute_batch = [&](const RawRow<XT, L> (&r)[NX][TB], int b) {
+      const int64_t tb = t0 + b * TB;
+      float p[TB * kHalfExperts];
       if constexpr (MODE == 0) {
 #pragma unroll
-        for (int m = 0; m < kTokBatch; ++m) {
+        for (int m = 0; m < TB; ++m) {
           float xv[L];
           to_floats<XT, L>(r[0][m], xv);
 #pragma unroll
@@ -440,9 +452,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           }
         }
       } else {
-        float xv[kTokBatch][L], ss[kTokBatch];
+        float xv[TB][L], ss[TB];
 #pragma unroll
-        for (int m = 0; m < kTokBatch; ++m) {
+        for (int m = 0; m < TB; ++m) {
           to_floats<XT, L>(r[0][m], xv[m]);
           if constexpr (MODE == 2) {
             float xa[L];
@@ -458,9 +470,9 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           ss[m] = acc;
         }
 #pragma unroll
-        for (int m = 0; m < kTokBatch; ++m) ss[m] = butterfly_sum64(ss[m]);
+        for (int m = 0; m < TB; ++m) ss[m] = butterfly_sum64(ss[m]);
 #pragma unroll
-        for (int m = 0; m < kTokBatch; ++m) {
+        for (int m = 0; m < TB; ++m) {
           const float rstd = 1.0f / __builtin_sqrtf(ss[m] / float(D) + na.eps);
           const bool store = half == 0 && tb + m < n_tokens;
           if constexpr (MODE == 2) {
@@ -484,36 +496,39 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           }
         }
       }
-      rs_swap32(p);
-      rs_swap16(p);
-      rs_dpp<4, 8>(p, lane);
-      rs_dpp<2, 4>(p, lane);
-      rs_dpp<1, 2>(p, lane);
-      // the last level is a plain butterfly: lanes 2m and 2m + 1 both get the sum
-      // (quad_perm [1,0,3,2] hands every lane its xor-1 partner; a per-lane choice
-      // between two rotates would become a branch, and a DPP read from a lane
-      // the branch has masked off returns 0)
+      static_assert(TB == 4 || TB == 2, "token batch");
+      constexpr int NV = TB * kHalfExperts;  // sums per lane before the reduction
+      rs_swap32<NV / 2>(p);
+      rs_swap16<NV / 4>(p);
+      rs_dpp<NV / 8, 8>(p, lane);
+      rs_dpp<NV / 16, 4>(p, lane);
+      if constexpr (TB == 4) rs_dpp<1, 2>(p, lane);
+      // the last levels are plain butterflies: every lane of a group gets the sum
+      // (quad_perm [2,3,0,1] / [1,0,3,2] hand every lane its xor-2 / xor-1
+      // partner; a per-lane choice between two rotates would become a branch,
+      // and a DPP read from a lane the branch has masked off returns 0)
+      if constexpr (TB == 2)
+        p[0] = p[0] + __uint_as_float(__builtin_amdgcn_update_dpp(
+                          0u, __float_as_uint(p[0]), 0x4E, 0xf, 0xf, false));
       p[0] = p[0] + __uint_as_float(__builtin_amdgcn_update_dpp(0u, __float_as_uint(p[0]), 0xB1,
                                                                 0xf, 0xf, false));
-      // lane holds value index v = 16*b5 + 8*b4 + 4*b3 + 2*b2 + b1 of its bits,
-      // i.e. token m = v >> 3, expert e0 + (v & 7).
-      const int v = lane >> 1;
+      // lane holds value index v of its high bits (TB = 4: v = 16*b5 + 8*b4 +
+      // 4*b3 + 2*b2 + b1; TB = 2: v = 8*b5 + 4*b4 + 2*b3 + b2), i.e. token
+      // m = v >> 3, expert e0 + (v & 7).
+      const int v = lane >> SH;
       const int m = v >> 3, e = e0 + (v & 7);
-      if ((lane & 1) == 0 && e < n_experts && tb + m < n_tokens) {
+      if ((lane & ((1 << SH) - 1)) == 0 && e < n_experts && tb + m < n_tokens) {
         float val = p[0];
         if (bias != nullptr) val = val + bias_e;
-        lgp[(b * kTokBatch + m) * (kMaxExperts + 1) + e] = val;
+        lgp[(b * TB + m) * (kMaxExperts + 1) + e] = val;
       }
     };
     // The next batch's loads go out unconditionally (rows clamped to the last
     // token, so a batch past the range is a harmless reload): a load under a
     // branch makes the compiler's wait counts assume it may be missing, and the
     // current batch's waits then also wait for the prefetch.
-    if constexpr (MODE == 2) {
-      // two rows per token: with a second row buffer the kernel needs 280
-      // VGPRs (one wave per SIMD); without it 225, and two waves per SIMD hide
-      // the loads better (add + RMSNorm + router 74 us instead of 83 at 45,500
-      // tokens)
+    if constexpr (MODE == 2 && !G5_ROUTER_M2_PREFETCH) {
+      // two rows per token, one row buffer
       for (int b = 0; b < nb; ++b) {
         load_batch(ra, b);
         compute_batch(ra, b);
@@ -585,22 +600,39 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
   }
 }
 
+// Tokens per reduced batch (2 or 4) for MODE 0 and for MODES 1 / 2, and the
+// resident blocks per CU MODE 0 is launched for.  2-token batches need fewer
+// registers (MODE 0: 167 VGPRs, three waves per SIMD, against 197 and two with
+// 4-token batches; MODES 1 / 2 leave room for MODE 2's second row buffer):
+// router 30.1-30.2 us against 31.2-31.4 at config 2, add + RMSNorm + router
+// 71-72 against 76-80 at config 4 (two rounds in one session).
+#ifndef G5_ROUTER_TB0
+#define G5_ROUTER_TB0 2
+#endif
+#ifndef G5_ROUTER_TB12
+#define G5_ROUTER_TB12 2
+#endif
+#ifndef G5_ROUTER_BPC0
+#define G5_ROUTER_BPC0 3
+#endif
+
 template <typename XT, int MODE>
 hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* idx, float* w,
                         float* logits, const NormArgs& na, const g5moe_shape& s,
                         hipStream_t st) {
+  constexpr int TB = MODE == 0 ? G5_ROUTER_TB0 : G5_ROUTER_TB12;
   const int64_t n = s.n_tokens;
-  // at most two resident blocks per CU (each wave holds its 8 experts' weights
-  // and two batches of rows in registers), at least one 4-token batch per pair
-  const int64_t max_grid = 2 * int64_t(device_cu_count());
+  // at most the resident blocks per CU (each wave holds its 8 experts' weights
+  // and two batches of rows in registers), at least one batch per pair
+  const int64_t max_grid = int64_t(MODE == 0 ? G5_ROUTER_BPC0 : 2) * int64_t(device_cu_count());
   const int64_t grid = std::max<int64_t>(
-      1, std::min<int64_t>(max_grid, (n + 2 * kTokBatch - 1) / (2 * kTokBatch)));
+      1, std::min<int64_t>(max_grid, (n + 2 * TB - 1) / (2 * TB)));
   int64_t tpp = (n + 2 * grid - 1) / (2 * grid);
-  tpp = std::min<int64_t>(kMaxPairTokens, (tpp + kTokBatch - 1) / kTokBatch * kTokBatch);
+  tpp = std::min<int64_t>(kMaxPairTokens, (tpp + TB - 1) / TB * TB);
   const int L = s.d_model / 64;
 #define G5_ROUTER_CASE(LL)                                                                  \
   case LL:                                                                                  \
-    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE>), dim3(unsigned(grid)),             \
+    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE, TB>), dim3(unsigned(grid)),         \
                        dim3(kRouterThreads), 0, st, x, wr, bias, n, s.n_experts, s.top_k,    \
                        idx, w, logits, na, int(tpp));                                        \
     break;
