@@ -520,7 +520,7 @@ __global__ __launch_bounds__(256) void input_grad_kernel(
 // token row owns columns 8c .. 8c + 7 and keeps those columns of all 16 router
 // weight rows in fp32 registers for the whole launch (the per-token kernel above
 // re-reads and converts 256 bytes of them per token); a block walks R rows at a
-// time with the next rows' positions, dX_perm rows and dlogits in flight.  The
+// time with later rows' positions, dX_perm rows and dlogits in flight.  The
 // arithmetic is the per-token kernel's, in the same order.
 template <int D>
 __global__ __launch_bounds__(256) void input_grad_persist_kernel(
@@ -547,58 +547,83 @@ __global__ __launch_bounds__(256) void input_grad_persist_kernel(
   const int64_t step = int64_t(gridDim.x) * R;
   int64_t t = int64_t(blockIdx.x) * R + r;
   if (t >= n_tokens) return;
-  // loads of token t: its two positions, then their rows and its dlogits row
-  struct In {
-    int32_t p0, p1;
-    uint4 v0, v1;
-    float4 g[NE / 4];
+  // Software pipeline over this thread's tokens t, t + step, ...: a token's
+  // positions are loaded three tokens before its rows, and its rows and dlogits
+  // two tokens before its arithmetic, in three register slots used in rotation
+  // (the loop is unrolled by three, so no slot is copied: copying a register
+  // whose load is in flight would wait for it).  A row's load never waits for
+  // its position's.  Negative positions load row 0 and add zeros (no load
+  // under a branch).  Past the last token the loads repeat token t.
+  auto ahead = [&](int64_t tt) { return tt < n_tokens ? tt : t; };
+  auto load_pos = [&](int64_t tt) __attribute__((always_inline)) {
+    return *reinterpret_cast<const int2*>(inv_pos + 2 * tt);
   };
-  auto load = [&](int64_t tt, In& in) __attribute__((always_inline)) {
-    const int2 pp = *reinterpret_cast<const int2*>(inv_pos + 2 * tt);
-    in.p0 = pp.x;
-    in.p1 = pp.y;
-    in.v0 = in.p0 >= 0 ? *reinterpret_cast<const uint4*>(dxp + int64_t(in.p0) * D + c0)
-                       : make_uint4(0, 0, 0, 0);
-    in.v1 = in.p1 >= 0 ? *reinterpret_cast<const uint4*>(dxp + int64_t(in.p1) * D + c0)
-                       : make_uint4(0, 0, 0, 0);
+  auto load_rows = [&](const int2 pp, uint4& v0, uint4& v1) __attribute__((always_inline)) {
+    v0 = *reinterpret_cast<const uint4*>(dxp + int64_t(max(pp.x, 0)) * D + c0);
+    v1 = *reinterpret_cast<const uint4*>(dxp + int64_t(max(pp.y, 0)) * D + c0);
+  };
+  auto load_g = [&](int64_t tt, float4 (&g)[NE / 4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < NE / 4; ++q)
-      in.g[q] = *reinterpret_cast<const float4*>(dlogits + tt * NE + 4 * q);
+      g[q] = *reinterpret_cast<const float4*>(dlogits + tt * NE + 4 * q);
   };
-  In cur;
-  load(t, cur);
-  for (;;) {
-    const int64_t tn = t + step;
-    In nxt;
-    const bool more = tn < n_tokens;
-    load(more ? tn : t, nxt);  // unconditional (an in-bounds repeat at the end)
+  auto compute = [&](int64_t tt, const int2 pp, const uint4& v0, const uint4& v1,
+                     const float4 (&g)[NE / 4]) __attribute__((always_inline)) {
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.f;
-    auto add_row = [&](const uint4& v) __attribute__((always_inline)) {
+    auto add_row = [&](const uint4& v, bool on) __attribute__((always_inline)) {
       const uint32_t vv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        acc[2 * j] += bf_lo(vv[j]);
-        acc[2 * j + 1] += bf_hi(vv[j]);
+        // a skipped slot adds nothing (acc + 0 would turn -0 into +0)
+        acc[2 * j] = on ? acc[2 * j] + bf_lo(vv[j]) : acc[2 * j];
+        acc[2 * j + 1] = on ? acc[2 * j + 1] + bf_hi(vv[j]) : acc[2 * j + 1];
       }
     };
-    if (cur.p0 >= 0) add_row(cur.v0);
-    if (cur.p1 >= 0) add_row(cur.v1);
-    const float gv[NE] = {cur.g[0].x, cur.g[0].y, cur.g[0].z, cur.g[0].w,
-                          cur.g[1].x, cur.g[1].y, cur.g[1].z, cur.g[1].w,
-                          cur.g[2].x, cur.g[2].y, cur.g[2].z, cur.g[2].w,
-                          cur.g[3].x, cur.g[3].y, cur.g[3].z, cur.g[3].w};
+    add_row(v0, pp.x >= 0);
+    add_row(v1, pp.y >= 0);
+    const float gv[NE] = {g[0].x, g[0].y, g[0].z, g[0].w, g[1].x, g[1].y, g[1].z, g[1].w,
+                          g[2].x, g[2].y, g[2].z, g[2].w, g[3].x, g[3].y, g[3].z, g[3].w};
 #pragma unroll
     for (int e = 0; e < NE; ++e)
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = __builtin_fmaf(gv[e], w[e][j], acc[j]);
-    *reinterpret_cast<uint4*>(dx + t * D + c0) =
+    *reinterpret_cast<uint4*>(dx + tt * D + c0) =
         make_uint4(pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3]),
                    pack_bf16x2(acc[4], acc[5]), pack_bf16x2(acc[6], acc[7]));
-    if (!more) break;
-    t = tn;
-    cur = nxt;
+  };
+  int2 pos[3];
+  uint4 ra[3], rb[3];
+  float4 gg[3][NE / 4];
+  // prologue: positions of tokens 0..2 (in units of step), rows and dlogits of
+  // tokens 0 and 1, positions of tokens 3 and 4
+  pos[0] = load_pos(t);
+  pos[1] = load_pos(ahead(t + step));
+  pos[2] = load_pos(ahead(t + 2 * step));
+  load_rows(pos[0], ra[0], rb[0]);
+  load_g(t, gg[0]);
+  load_rows(pos[1], ra[1], rb[1]);
+  load_g(ahead(t + step), gg[1]);
+  // the positions of tokens 0 and 1 are kept for their arithmetic (their slots
+  // take tokens 3 and 4 only after it)
+  int2 pc[3] = {pos[0], pos[1], pos[2]};
+  pos[0] = load_pos(ahead(t + 3 * step));
+  pos[1] = load_pos(ahead(t + 4 * step));
+  for (;;) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) {
+      // slot (k + 2) % 3 takes token + 2: its rows, dlogits, and the position
+      // of token + 5 into the position slot it frees
+      const int n2 = (k + 2) % 3;
+      load_rows(pos[n2], ra[n2], rb[n2]);
+      load_g(ahead(t + 2 * step), gg[n2]);
+      pc[n2] = pos[n2];
+      pos[n2] = load_pos(ahead(t + 5 * step));
+      compute(t, pc[k], ra[k], rb[k], gg[k]);
+      if (t + step >= n_tokens) return;
+      t += step;
+    }
   }
 }
 
