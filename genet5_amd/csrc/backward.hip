@@ -610,20 +610,24 @@ __global__ __launch_bounds__(256) void input_grad_persist_kernel(
   int2 pc[3] = {pos[0], pos[1], pos[2]};
   pos[0] = load_pos(ahead(t + 3 * step));
   pos[1] = load_pos(ahead(t + 4 * step));
-  for (;;) {
-#pragma unroll
-    for (int k = 0; k < 3; ++k) {
-      // slot (k + 2) % 3 takes token + 2: its rows, dlogits, and the position
-      // of token + 5 into the position slot it frees
-      const int n2 = (k + 2) % 3;
-      load_rows(pos[n2], ra[n2], rb[n2]);
-      load_g(ahead(t + 2 * step), gg[n2]);
-      pc[n2] = pos[n2];
-      pos[n2] = load_pos(ahead(t + 5 * step));
-      compute(t, pc[k], ra[k], rb[k], gg[k]);
-      if (t + step >= n_tokens) return;
-      t += step;
-    }
+  // one token in slot K (a compile-time index: the slots stay registers);
+  // false after the thread's last token
+  auto token = [&](auto kc) __attribute__((always_inline)) -> bool {
+    constexpr int K = decltype(kc)::value;
+    // slot (K + 2) % 3 takes token + 2: its rows, dlogits, and the position of
+    // token + 5 into the position slot it frees
+    constexpr int N2 = (K + 2) % 3;
+    load_rows(pos[N2], ra[N2], rb[N2]);
+    load_g(ahead(t + 2 * step), gg[N2]);
+    pc[N2] = pos[N2];
+    pos[N2] = load_pos(ahead(t + 5 * step));
+    compute(t, pc[K], ra[K], rb[K], gg[K]);
+    if (t + step >= n_tokens) return false;
+    t += step;
+    return true;
+  };
+  while (token(std::integral_constant<int, 0>{}) && token(std::integral_constant<int, 1>{}) &&
+         token(std::integral_constant<int, 2>{})) {
   }
 }
 
