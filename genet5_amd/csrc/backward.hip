@@ -48,9 +48,15 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
   constexpr int D = 64 * L;
   const int lane = threadIdx.x & 63;
   const int64_t a = int64_t(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // PAD: lane l <= E holds offsets[l]; issued beside the inv_pos load
+  // PAD: lane l <= E holds offsets[l]; issued beside the inv_pos load and the
+  // dY row (which does not depend on the position)
   const int ol = PAD ? offsets[lane <= n_experts ? lane : n_experts] : 0;
   const int32_t p = a < nk ? inv_pos[a] : -1;
+  const int64_t t = a < nk ? a / topk : 0;
+  const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
+  uint32_t gv[L / 2];
+#pragma unroll
+  for (int i = 0; i < L / 2; ++i) gv[i] = dyr[i];
   // PAD: padded row a = e * kmax + j is zeroed when j >= M_e, with e the
   // number of l in [1, E] with l * kmax <= a.  Decided here, before any store:
   // CDNA's vmcnt also counts stores, so a use of ol after them would wait for
@@ -65,7 +71,6 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
   }
   if (a < nk && p < 0 && lane == 0) dw[a] = 0.f;
   if (p >= 0) {
-    const int64_t t = a / topk;
     int64_t row = p;
     bool store = true;
     if constexpr (PAD) {
@@ -77,16 +82,12 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
       store = j < kmax;  // a kmax below the expert's count: keep the writes in bounds
     }
     const float w = topk_w[a];
-    const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
     const uint32_t* yr = reinterpret_cast<const uint32_t*>(y_perm + int64_t(p) * D + lane * L);
     uint32_t* outr = reinterpret_cast<uint32_t*>(dyp + row * D + lane * L);
     // every load of the row in flight before the first use
-    uint32_t gv[L / 2], yv[L / 2], ov[L / 2];
+    uint32_t yv[L / 2], ov[L / 2];
 #pragma unroll
-    for (int i = 0; i < L / 2; ++i) {
-      gv[i] = dyr[i];
-      yv[i] = yr[i];
-    }
+    for (int i = 0; i < L / 2; ++i) yv[i] = yr[i];
     float acc = 0.f;
 #pragma unroll
     for (int i = 0; i < L / 2; ++i) {
@@ -97,8 +98,7 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
     }
     // the reduction (which needs every load) ahead of the stores, so that no
     // wait for a load also waits for them
-#pragma unroll
-    for (int bit = 32; bit >= 1; bit >>= 1) acc = acc + __shfl_xor(acc, bit, 64);
+    acc = butterfly_sum64(acc);  // lane bits 5 .. 0, in registers (no LDS)
     if (store) {
 #pragma unroll
       for (int i = 0; i < L / 2; ++i) outr[i] = ov[i];

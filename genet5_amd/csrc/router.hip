@@ -171,31 +171,6 @@ struct NormArgs {
   void* normed_out;    // normed rows (the MoE input)
 };
 
-// Full xor butterfly in the contract's order (lane bits 5, 4, 3, 2, 1, 0): every
-// lane ends with the same sum, bit for bit.  Bits 5 and 4 swap a value with
-// itself (v_permlane32_swap / v_permlane16_swap: own + partner in one half,
-// partner + own in the other).  Bits 3..0 use DPP row rotates: row_ror:R hands
-// lane l the value of lane (l - R) mod 16, which differs from l ^ R only in row
-// bits above R (the borrow), over which the partial sums are already symmetric,
-// so it carries the xor partner's value.  No LDS (a __shfl_xor would be a
-// ds_bpermute per level).
-template <int R>
-__device__ __forceinline__ float row_ror(float v) {
-  return __uint_as_float(
-      __builtin_amdgcn_update_dpp(0u, __float_as_uint(v), 0x120 + R, 0xf, 0xf, false));
-}
-__device__ __forceinline__ float butterfly_sum64(float v) {
-  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
-  v = v + row_ror<8>(v);
-  v = v + row_ror<4>(v);
-  v = v + row_ror<2>(v);
-  v = v + row_ror<1>(v);
-  return v;
-}
-
 // Plain (residual add +) RMSNorm with the fused variant's arithmetic, so its
 // normed rows equal the ones g5moe_add_rmsnorm_router writes bit for bit: one
 // wave per row, lane c holding columns [c*L, c*L + L), kRowsPerWave rows per
