@@ -52,11 +52,15 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
   // dY row (which does not depend on the position)
   const int ol = PAD ? offsets[lane <= n_experts ? lane : n_experts] : 0;
   const int32_t p = a < nk ? inv_pos[a] : -1;
-  const int64_t t = a < nk ? a / topk : 0;
-  const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
+  // (only for an assignment: the padded grid also has waves past N k, and with
+  // N = 0 dY has no row to read)
+  const int64_t t = a / topk;
   uint32_t gv[L / 2];
+  if (a < nk) {
+    const uint32_t* dyr = reinterpret_cast<const uint32_t*>(dy + t * D + lane * L);
 #pragma unroll
-  for (int i = 0; i < L / 2; ++i) gv[i] = dyr[i];
+    for (int i = 0; i < L / 2; ++i) gv[i] = dyr[i];
+  }
   // PAD: padded row a = e * kmax + j is zeroed when j >= M_e, with e the
   // number of l in [1, E] with l * kmax <= a.  Decided here, before any store:
   // CDNA's vmcnt also counts stores, so a use of ol after them would wait for
