@@ -118,78 +118,109 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
 
 // Router weight gradient d_w_router = dlogits^T x (the nn.Linear weight
 // gradient of lib/blocks/_component.py's router projection, fp32).  Pass 1:
-// block g sums its chunk of tokens [g * chunk, (g + 1) * chunk) in token order,
-// thread i owning columns 4 i .. 4 i + 3 for every expert; partials[g][e][c].
-// The chunk's dlogits rows go through LDS in windows of kRwWin tokens (every
-// lane reads the same row: broadcast reads), and the x values of the next
-// kRwSub tokens are in flight while the current ones are used.  Pass 2 adds the
-// chunks in a fixed order (32 groups of consecutive chunks, then the groups), so
-// the result does not depend on scheduling.
+// block g reduces its chunk of tokens [g * chunk, (g + 1) * chunk) into
+// partials[g][e][c]; pass 2 adds the chunks in a fixed order (32 groups of
+// consecutive chunks, then the groups), so the result does not depend on
+// scheduling.
 constexpr int kRouterWgradMinChunk = 64;   // tokens per chunk at least ...
-constexpr int kRouterWgradMaxChunks = 512; // ... and at most this many chunks
-constexpr int kRwWin = 64;                 // tokens per LDS window of dlogits rows
-constexpr int kRwSub = 16;                 // tokens per register batch of x
-__global__ __launch_bounds__(256) void router_wgrad_partial_kernel(
+constexpr int kRouterWgradMaxChunks = 256; // ... and at most this many chunks (<= 512)
+
+// Pass 1 on the matrix cores (fp32 MFMA 16 x 16 x 4), for d a multiple of 64
+// and at most 16 experts: partials[g] = dlogits[chunk]^T x[chunk] with the
+// experts as the product's 16 rows, 4 tokens per MFMA step as its k, and 16
+// columns per MFMA.  Lane l of a wave is row / column l % 16 and step token
+// l / 16; it loads that token's dlogits entry (the A operand) and L = d / 64
+// consecutive x columns (the B operands of L MFMAs whose column n stands for
+// x column c0 + L n + j), so a wave covers d / 4 columns and the block all d.
+// Steps go in register batches of S, two batches used in turn (no register
+// copies, whose loads would be waited for); tokens past the chunk load its last
+// row with a zero dlogits entry.  fp32 products of bf16 x and fp32 dlogits,
+// summed by the matrix core in its own order within a step and in step order
+// across steps: deterministic, within the fp32 accumulation bound.
+template <int L>
+__global__ __launch_bounds__(256) void router_wgrad_mfma_kernel(
     const float* __restrict__ dlogits, const uint16_t* __restrict__ x,
-    float* __restrict__ partials, int64_t n_tokens, int n_experts, int d, int64_t chunk) {
-  __shared__ __attribute__((aligned(16))) float dls[kRwWin * kMaxExperts];
-  const int tid = threadIdx.x, nthr = blockDim.x;
-  const int c0 = tid * 4;
+    float* __restrict__ partials, int64_t n_tokens, int n_experts, int64_t chunk) {
+  constexpr int D = 64 * L;
+  constexpr int S = 6;              // 4-token steps per register batch
+  constexpr int W = L / 2;          // x words (bf16 pairs) per lane and token
+  typedef float f32x4 __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int m = lane & 15;
+  const int kq = lane >> 4;
+  const int c0 = wave * (D / 4) + m * L;
+  const int me = m < n_experts ? m : n_experts - 1;
   const int64_t t0 = int64_t(blockIdx.x) * chunk;
   const int64_t t1 = t0 + chunk < n_tokens ? t0 + chunk : n_tokens;
-  float acc[kMaxExperts][4];
+  f32x4 acc[L];
 #pragma unroll
-  for (int e = 0; e < kMaxExperts; ++e)
+  for (int j = 0; j < L; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+  struct Batch {
+    float a[S];
+    uint32_t xv[S][W];
+  };
+  // (called only with t1 > t0: every load is of a token of the chunk)
+  auto load = [&](Batch& b, int64_t tb) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[e][j] = 0.f;
-  // x values of tokens base + i (clamped to the chunk's last token: unconditional
-  // loads, never used past the end)
-  auto load_x = [&](uint2 (&xv)[kRwSub], int64_t base) __attribute__((always_inline)) {
+    for (int s = 0; s < S; ++s) {
+      const int64_t tk = tb + 4 * s + kq;
+      const bool ok = tk < t1 && m < n_experts;
+      const int64_t tc = tk < t1 ? tk : t1 - 1;
+      const float av = dlogits[tc * n_experts + me];
+      b.a[s] = ok ? av : 0.f;
+      const uint32_t* xr = reinterpret_cast<const uint32_t*>(x + tc * D + c0);
+      if constexpr (W % 4 == 0) {
 #pragma unroll
-    for (int i = 0; i < kRwSub; ++i) {
-      const int64_t t = base + i < t1 ? base + i : t1 - 1;
-      xv[i] = *reinterpret_cast<const uint2*>(x + t * d + c0);
+        for (int q = 0; q < W / 4; ++q) {
+          const uint4 v = reinterpret_cast<const uint4*>(xr)[q];
+          b.xv[s][4 * q] = v.x, b.xv[s][4 * q + 1] = v.y, b.xv[s][4 * q + 2] = v.z,
+          b.xv[s][4 * q + 3] = v.w;
+        }
+      } else if constexpr (W % 2 == 0) {
+#pragma unroll
+        for (int q = 0; q < W / 2; ++q) {
+          const uint2 v = reinterpret_cast<const uint2*>(xr)[q];
+          b.xv[s][2 * q] = v.x, b.xv[s][2 * q + 1] = v.y;
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < W; ++q) b.xv[s][q] = xr[q];
+      }
     }
   };
-  for (int64_t w0 = t0; w0 < t1; w0 += kRwWin) {
-    const int nw = int(t1 - w0 < kRwWin ? t1 - w0 : kRwWin);
-    __syncthreads();  // the previous window's rows are read
-    for (int i = tid; i < nw * kMaxExperts; i += nthr) {
-      const int r = i / kMaxExperts, e = i % kMaxExperts;
-      dls[i] = e < n_experts ? dlogits[(w0 + r) * n_experts + e] : 0.f;
-    }
-    __syncthreads();
-    uint2 xa[kRwSub], xb[kRwSub];
-    load_x(xa, w0);
-    for (int sb = 0; sb < nw; sb += kRwSub) {
-      load_x(xb, w0 + sb + kRwSub);
+  auto compute = [&](const Batch& b, int64_t tb) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < kRwSub; ++i) {
-        if (sb + i < nw) {
-          const float xf[4] = {bf_lo(xa[i].x), bf_hi(xa[i].x), bf_lo(xa[i].y), bf_hi(xa[i].y)};
-          const float4* dr = reinterpret_cast<const float4*>(dls + (sb + i) * kMaxExperts);
+    for (int s = 0; s < S; ++s) {
+      if (tb + 4 * s >= t1) break;  // block-uniform: no step of the chunk is left
 #pragma unroll
-          for (int q = 0; q < kMaxExperts / 4; ++q) {
-            const float4 w4 = dr[q];
-            const float wv[4] = {w4.x, w4.y, w4.z, w4.w};
-            // experts past n_experts have zero weights and are never stored
-#pragma unroll
-            for (int u = 0; u < 4; ++u)
-#pragma unroll
-              for (int j = 0; j < 4; ++j)
-                acc[4 * q + u][j] = __builtin_fmaf(wv[u], xf[j], acc[4 * q + u][j]);
-          }
-        }
+      for (int j = 0; j < L; ++j) {
+        const uint32_t wv = b.xv[s][j / 2];
+        const float xf = (j & 1) ? bf_hi(wv) : bf_lo(wv);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(b.a[s], xf, acc[j], 0, 0, 0);
       }
-#pragma unroll
-      for (int i = 0; i < kRwSub; ++i) xa[i] = xb[i];
+    }
+  };
+  if (t1 > t0) {
+    Batch b0, b1;
+    load(b0, t0);
+    for (int64_t tb = t0; tb < t1; tb += 8 * S) {
+      load(b1, tb + 4 * S);
+      compute(b0, tb);
+      load(b0, tb + 8 * S);
+      compute(b1, tb + 4 * S);
     }
   }
+  // lane holds rows 4 kq .. 4 kq + 3 (experts) of column m of each MFMA
 #pragma unroll
-  for (int e = 0; e < kMaxExperts; ++e)
-    if (e < n_experts)
-      *reinterpret_cast<float4*>(partials + (int64_t(blockIdx.x) * n_experts + e) * d + c0) =
-          make_float4(acc[e][0], acc[e][1], acc[e][2], acc[e][3]);
+  for (int i = 0; i < 4; ++i) {
+    const int e = 4 * kq + i;
+    if (e < n_experts) {
+      float* out = partials + (int64_t(blockIdx.x) * n_experts + e) * D + c0;
+#pragma unroll
+      for (int j = 0; j < L; ++j) out[j] = acc[j][i];
+    }
+  }
 }
 
 // Block: 8 float4 outputs x 32 chunk groups; group p sums chunks
@@ -933,12 +964,22 @@ int router_wgrad_chunks(int64_t n_tokens) {
 hipError_t launch_router_wgrad(const float* dlogits, const void* x, float* partials,
                                void* d_w_router, const g5moe_shape& s, hipStream_t st) {
   const int E = s.n_experts, d = s.d_model;
-  if (d % 4 != 0 || d / 4 > 256 || E < 1 || E > kMaxExperts) return hipErrorInvalidValue;
+  if (d % 64 != 0 || E < 1 || E > kMaxExperts) return hipErrorInvalidValue;
   const int G = router_wgrad_chunks(s.n_tokens);
   const int64_t chunk = (s.n_tokens + G - 1) / G;
-  hipLaunchKernelGGL(router_wgrad_partial_kernel, dim3(unsigned(G)), dim3(unsigned(d / 4)), 0,
-                     st, dlogits, static_cast<const uint16_t*>(x), partials, s.n_tokens, E, d,
-                     chunk);
+  auto mfma = [&](auto l_c) {
+    constexpr int LL = decltype(l_c)::value;
+    hipLaunchKernelGGL(router_wgrad_mfma_kernel<LL>, dim3(unsigned(G)), dim3(256), 0, st,
+                       dlogits, static_cast<const uint16_t*>(x), partials, s.n_tokens, E,
+                       chunk);
+  };
+  switch (d) {
+    case 128: mfma(std::integral_constant<int, 2>{}); break;
+    case 256: mfma(std::integral_constant<int, 4>{}); break;
+    case 512: mfma(std::integral_constant<int, 8>{}); break;
+    case 768: mfma(std::integral_constant<int, 12>{}); break;
+    default: return hipErrorInvalidValue;
+  }
   const int64_t q = int64_t(E) * d / 4;
   hipLaunchKernelGGL(router_wgrad_reduce_kernel, dim3(unsigned((q + 7) / 8)), dim3(256), 0, st,
                      partials, static_cast<uint16_t*>(d_w_router), G, q);
