@@ -277,8 +277,8 @@ def test_weight_grad_sorted_h_argument_checks(g5lib):
     assert fn(None, None, None, None, None, None, None, None, 384, ctypes.byref(s), None) == 0
 
 
-@pytest.mark.parametrize("n,chunks", [(0, 1), (1, 1), (64, 1), (65, 2), (36400, 512),
-                                      (10 ** 6, 512)])
+@pytest.mark.parametrize("n,chunks", [(0, 1), (1, 1), (64, 1), (65, 2), (36400, 256),
+                                      (10 ** 6, 256)])
 def test_router_weight_grad_scratch_size(g5lib, n, chunks):
     s = _lib.make_shape(n, 768, 3072, 16, 2, _lib.DTYPE_BF16)
     b = ctypes.c_size_t(0)
