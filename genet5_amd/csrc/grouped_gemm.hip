@@ -190,10 +190,17 @@ struct Units {
   int first, stride, count, base;
 };
 
+// Bytes of a wave's epilogue region: 8 KB, or 4 KB in the 128 x 128 tiles,
+// whose workgroups run two per CU (2 x 80 KB of LDS).
+template <int BM, int BN>
+constexpr int epi_bytes() {
+  return BM == 128 && BN == 128 ? 4096 : kEpiBytesPerWave;
+}
+
 // LDS bytes of the persistent kernel for a BM x BN tile (stages + epilogue).
 template <int BM, int BN, int BK, int S>
 constexpr int persist_smem_bytes() {
-  return S * (BM + BN) * BK * 2 + 4 * kEpiBytesPerWave;
+  return S * (BM + BN) * BK * 2 + 4 * epi_bytes<BM, BN>();
 }
 
 // One pass of the persistent tile loop over the units `un` (BN = BNF for full
@@ -234,7 +241,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   static_assert(NSLOT == 2 || (NSLOT == 3 && KS == 4), "fragment slots");
   static_assert(BK == 32 || BK == 64, "BK");
   static_assert(HALF ? 2 * BN == BNF : BN == BNF, "tile width");
-  static_assert(S >= 2 && S * STAGE + 4 * kEpiBytesPerWave <= 160 * 1024, "LDS");
+  constexpr int EPI = epi_bytes<BM, BNF>();  // the wave's epilogue region
+  static_assert(S >= 2 && S * STAGE + 4 * EPI <= 160 * 1024, "LDS");
   static_assert((S - 2) * PER < 64, "vmcnt range");
   constexpr bool SWIGLU = MODE == 1 || MODE == 3 || MODE == 5;
   static_assert(!SWIGLU || (NB % 2 == 0), "swiglu pairs n-blocks");
@@ -257,14 +265,14 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   // every tile's last step reads its A from the epilogue region: the next
   // tile's third A stage goes out after the epilogue), B buffers mod 2.
   constexpr bool A3 = G5_A3 && (MODE == 0 || MODE == 4) && NSLOT == 3 && S == 2 &&
-                      A_BYTES == 4 * kEpiBytesPerWave;
+                      A_BYTES == 4 * EPI;
   // Three B stages (the SwiGLU modes, whose weight tiles are the operand that
   // streams from beyond the L2): the same scheme with the roles swapped, B
   // buffer 2 being the epilogue region, B issued three k-steps ahead and A
   // two.  The next tile's gathered rows then travel through a VGPR instead of
   // that region.
   constexpr bool B3 = G5_B3 && SWIGLU && NSLOT == 3 && S == 2 &&
-                      B_BYTES == 4 * kEpiBytesPerWave;
+                      B_BYTES == 4 * EPI;
   auto decode_unit = [&](int i, TileCoord& tc) {
     const int h = un.first + i * un.stride;
     if constexpr (HALF) {
@@ -306,7 +314,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   // reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile: slot j's rows
   // (w * AI + j) * RPB + lrow.
   static_assert(!GATHER || AI * RPB == 64, "one 64-row perm block per wave");
-  char* epi = smem + S * STAGE + wave * kEpiBytesPerWave;
+  char* epi = smem + S * STAGE + wave * EPI;
   // rows_fill: byte offsets of the gathered rows of the tile whose stages
   // the refills load (the current tile, then the next from its first stage).
   uint32_t rows_fill[GATHER ? AI : 1];
@@ -674,7 +682,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
       constexpr int HRBY = OB * 32;  // h bytes per row
       constexpr int HCR = HRBY / 16;
       constexpr int HLPR = 256 / HRBY;
-      static_assert(RBY == 256 && kEpiBytesPerWave / RBY == 32, "one token block per pass");
+      static_assert(RBY == 256 && EPI / RBY == 32, "one token block per pass");
       const int col0 = cur.n0 + wn * WTN;
       const int hcol0 = col0 / 2;
       const int row = tok_l;
@@ -752,7 +760,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
       constexpr int OB = NB;
       constexpr int RBY = OB * 64;
       constexpr int CR = RBY / 16;
-      constexpr int ROWS = kEpiBytesPerWave / RBY;
+      constexpr int ROWS = EPI / RBY;
       constexpr int JP = ROWS / 32;
       constexpr int LPR = 256 / RBY;
       constexpr int NIT = ROWS * RBY / 1024;
@@ -849,7 +857,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int ROWS = EPI / RBY;
         constexpr int JP = ROWS / 32;  // token blocks per pass
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
@@ -896,7 +904,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = SWIGLU ? NB / 2 : NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int ROWS = EPI / RBY;
         constexpr int JP = ROWS / 32;  // token blocks per pass
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
@@ -953,7 +961,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int ROWS = EPI / RBY;
         constexpr int JP = ROWS / 32;  // token blocks per pass
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
@@ -1000,7 +1008,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = SWIGLU ? NB / 2 : NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = kEpiBytesPerWave / RBY;
+        constexpr int ROWS = EPI / RBY;
         constexpr int JP = ROWS / 32;  // token blocks per pass
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
@@ -1094,9 +1102,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
 // about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
 // the gate|up GEMM (K = 768), which therefore keeps whole tiles.
 template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
-          bool DROP = false>
-__global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
-  __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
+          bool DROP>
+__device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
   const int ntn = args.Nout / BN;
   const Offsets off = load_offsets(args.offsets, args.n_experts);
   int total = 0;
@@ -1161,6 +1168,26 @@ __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args
       }
     }
   }
+}
+
+// One workgroup per CU: up to 512 registers per lane (256 accumulators in AGPRs).
+template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
+          bool DROP = false>
+__global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
+  __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
+  persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP>(args, smem);
+}
+
+// Two workgroups per CU (two waves per SIMD, 256 registers per lane, at most 80
+// KB of LDS each): twice the operand bytes in flight per CU, for launches with
+// about one tile per CU, whose k-loops wait on load latency.
+template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
+          bool DROP = false>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+grouped_gemm_persist2_kernel(GemmArgs args) {
+  static_assert(persist_smem_bytes<BM, BN, BK, S>() <= 80 * 1024, "two workgroups per CU");
+  __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
+  persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP>(args, smem);
 }
 
 // Claim counters of the claimed-tail GEMM launches: kClaimSlots pairs {claim,
@@ -1266,6 +1293,26 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #ifndef G5_DN_GM
 #define G5_DN_GM 4
 #endif
+
+// Small-M down products on 128 x 128 tiles, two workgroups per CU (0: one
+// 128 x 256 workgroup per CU).
+#ifndef G5_SMALLM_TWO_PER_CU
+#define G5_SMALLM_TWO_PER_CU 1
+#endif
+
+// The two-per-CU kernel (grid up to twice the CU count).
+template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL, bool DROP = false>
+void launch_persist2(unsigned grid, const GemmArgs& a, hipStream_t st) {
+  const int nk = a.K / BK;
+  if (nk % 3 == 0 && nk >= 6)
+    hipLaunchKernelGGL(
+        (grouped_gemm_persist2_kernel<BM, BN, BK, S, 3, GM, MODE, HALF_TAIL, DROP>),
+        dim3(grid), dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL(
+        (grouped_gemm_persist2_kernel<BM, BN, BK, S, 2, GM, MODE, HALF_TAIL, DROP>),
+        dim3(grid), dim3(256), 0, st, a);
+}
 
 // Persistent launch: three fragment slots when the k-step count allows it.
 template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL, bool DROP = false>
@@ -1409,7 +1456,10 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
   a.ldc = s.d_model;
   if (a.K < G5_DN_STAGES * G5_DN_BK) return hipErrorInvalidValue;
   const unsigned ncu = unsigned(device_cu_count());
-  if (a.Nout % 256 == 0 && small_m(nk, a.Nout, ncu)) {
+  if (G5_SMALLM_TWO_PER_CU && a.Nout % 256 == 0 && small_m(nk, a.Nout, ncu)) {
+    const unsigned grid = std::min(grid_bound<128, 128>(nk, s.n_experts, a.Nout), 2 * ncu);
+    launch_persist2<128, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);
+  } else if (a.Nout % 256 == 0 && small_m(nk, a.Nout, ncu)) {
     const unsigned grid = std::min(grid_bound<128, 256>(nk, s.n_experts, a.Nout), ncu);
     launch_persist<128, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);
   } else if (a.Nout % 256 == 0) {
