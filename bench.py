@@ -451,6 +451,7 @@ def bench_train(args) -> dict:
     same kernels enqueued stage by stage (train_stage_breakdown)."""
     import torch
     from genet5_amd import synth
+    from genet5_amd import moe as moe_mod
     from genet5_amd.moe import MoEFeedForward
     dev = torch.device("cuda:0")
     inp = synth.make_config(args.config, seed=0)
@@ -473,7 +474,7 @@ def bench_train(args) -> dict:
         if update:
             # what an optimizer step does to the layer's caches (its own kernels are
             # not the layer's): the packed and transposed weights are rebuilt
-            m._packed_key = None
+            moe_mod.clear_weight_cache()
         m.zero_grad(set_to_none=True)
         xr.grad = None
         y = m(xr)

@@ -214,7 +214,8 @@ g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int3
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up (cast)"));
   const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                                   reinterpret_cast<uint16_t*>(w + L.h), nullptr, *shape, st),
+                                   reinterpret_cast<uint16_t*>(w + L.h), nullptr,
+                                   reinterpret_cast<int*>(w + L.claims), *shape, st),
                     "g5moe_expert_gate_up");
 }
 
@@ -246,7 +247,8 @@ g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train (cast)"));
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
                                    reinterpret_cast<uint16_t*>(w + L.h),
-                                   static_cast<uint16_t*>(gu), *shape, st, &drop),
+                                   static_cast<uint16_t*>(gu),
+                                   reinterpret_cast<int*>(w + L.claims), *shape, st, &drop),
                     "g5moe_expert_gate_up_train");
 }
 
@@ -276,8 +278,8 @@ g5moe_status g5moe_expert_gate_up_train_factors(const void* x, const int32_t* pe
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train_factors (cast)"));
   return hip_status(
       launch_gate_up_ab(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                        reinterpret_cast<uint16_t*>(w + L.h), static_cast<uint16_t*>(ab), *shape,
-                        st, drop),
+                        reinterpret_cast<uint16_t*>(w + L.h), static_cast<uint16_t*>(ab),
+                        reinterpret_cast<int*>(w + L.claims), *shape, st, drop),
       "g5moe_expert_gate_up_train_factors");
 }
 
@@ -288,9 +290,12 @@ g5moe_status g5moe_dh_swiglu_backward(const void* dy_pad, int32_t kmax, const in
   if (shape->d_ff % 256 != 0)
     return fail(G5MOE_ERR_UNSUPPORTED, "dh_swiglu_backward: d_ff %d must be a multiple of 256",
                 int(shape->d_ff));
-  if (kmax < 384 || kmax % 192 != 0)
+  if (kmax != 0 && (kmax < 384 || kmax % 192 != 0))
     return fail(G5MOE_ERR_INVALID_ARG,
-                "dh_swiglu_backward: kmax %d must be a multiple of 192 and >= 384", int(kmax));
+                "dh_swiglu_backward: kmax %d must be 0 (packed) or a multiple of 192 >= 384",
+                int(kmax));
+  if (packed_rows_bound(shape->n_tokens * shape->top_k, shape->n_experts) > INT32_MAX / 4)
+    return fail(G5MOE_ERR_UNSUPPORTED, "dh_swiglu_backward: too many rows");
   G5_NONNULL(dgu_pad);
   G5_NONNULL(offsets);
   if (shape->n_tokens > 0) {
@@ -441,9 +446,9 @@ g5moe_status g5moe_grouped_gemm(const void* a, const int32_t* offsets, const voi
 g5moe_status g5moe_grouped_gemm_padded(const void* a, int32_t kmax, const int32_t* offsets,
                                        const void* b, void* c, int64_t rows, int32_t k,
                                        int32_t n_out, int32_t n_experts, void* stream) {
-  if (kmax < 1 || int64_t(kmax) * kMaxExperts > int64_t(INT32_MAX) / 2)
+  if (kmax < 0 || int64_t(kmax) * kMaxExperts > int64_t(INT32_MAX) / 2)
     return fail(G5MOE_ERR_INVALID_ARG, "grouped_gemm_padded: kmax %d out of range", int(kmax));
-  if (rows < 0 || rows > int64_t(INT32_MAX) / 2)
+  if (rows < 0 || rows > int64_t(INT32_MAX) / 4)
     return fail(G5MOE_ERR_INVALID_ARG, "grouped_gemm_padded: rows %lld out of range",
                 (long long)rows);
   if (n_experts < 1 || n_experts > kMaxExperts)
@@ -459,7 +464,8 @@ g5moe_status g5moe_grouped_gemm_padded(const void* a, int32_t kmax, const int32_
   G5_NONNULL(c);
   return hip_status(launch_grouped_nt(static_cast<const uint16_t*>(a), offsets,
                                       static_cast<const uint16_t*>(b), static_cast<uint16_t*>(c),
-                                      rows, n_experts, k, n_out, kmax, as_stream(stream)),
+                                      rows, n_experts, k, n_out, kmax > 0 ? kmax : -1,
+                                      as_stream(stream)),
                     "g5moe_grouped_gemm_padded");
 }
 
@@ -491,7 +497,8 @@ g5moe_status g5moe_gate_grad_padded(const void* dy, const void* y_perm, const in
   if (shape->x_dtype != G5MOE_DTYPE_BF16)
     return fail(G5MOE_ERR_UNSUPPORTED, "the backward takes bf16 activations");
   if (kmax < 0) return fail(G5MOE_ERR_INVALID_ARG, "kmax %d < 0", int(kmax));
-  if (shape->n_tokens == 0 && kmax == 0) return G5MOE_OK;
+  if (packed_rows_bound(shape->n_tokens * shape->top_k, shape->n_experts) > INT32_MAX / 4)
+    return fail(G5MOE_ERR_UNSUPPORTED, "gate_grad_padded: too many rows");
   G5_NONNULL(offsets);
   G5_NONNULL(dy_pad);
   if (shape->n_tokens > 0) {
@@ -537,8 +544,11 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
   hipError_t err;
   const uint16_t* xb = gemm_input(x, static_cast<char*>(ws), *shape, st, &err);
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_raw (cast)"));
+  const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up_raw(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                                       static_cast<uint16_t*>(gu), *shape, st),
+                                       static_cast<uint16_t*>(gu),
+                                       reinterpret_cast<int*>(static_cast<char*>(ws) + L.claims),
+                                       *shape, st),
                     "g5moe_expert_gate_up_raw");
 }
 
@@ -548,14 +558,17 @@ g5moe_status g5moe_swiglu_backward(const void* dh, const void* gu, const int32_t
                                    const g5moe_shape* shape, void* stream) {
   G5_CHECK(check_shape(shape));
   if (kmax < 0) return fail(G5MOE_ERR_INVALID_ARG, "kmax %d < 0", int(kmax));
+  if (packed_rows_bound(shape->n_tokens * shape->top_k, shape->n_experts) > INT32_MAX / 4)
+    return fail(G5MOE_ERR_UNSUPPORTED, "swiglu_backward: too many rows");
   DropoutParams drop;
   G5_CHECK(dropout_params(dropout, &drop));
-  if (shape->n_tokens == 0 || kmax == 0) return G5MOE_OK;
-  G5_NONNULL(dh);
-  G5_NONNULL(gu);
   G5_NONNULL(offsets);
   G5_NONNULL(dgu_pad);
-  if (drop.on) G5_NONNULL(perm);
+  if (shape->n_tokens > 0) {  // no tokens: every padded row is a zero row
+    G5_NONNULL(dh);
+    G5_NONNULL(gu);
+    if (drop.on) G5_NONNULL(perm);
+  }
   return hip_status(launch_swiglu_bwd(static_cast<const uint16_t*>(dh),
                                       static_cast<const uint16_t*>(gu), perm, offsets,
                                       static_cast<uint16_t*>(dgu), static_cast<uint16_t*>(h_pad),
@@ -591,17 +604,19 @@ g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t*
     return fail(G5MOE_ERR_INVALID_ARG,
                 "pad_rows: cols %d must be a positive multiple of 8 and kmax %d >= 0", int(cols),
                 int(kmax));
-  if (kmax == 0) return G5MOE_OK;
   if (shape->n_tokens > 0) G5_NONNULL(src);  // no tokens: every row is a zero row
   G5_NONNULL(offsets);
   G5_NONNULL(out);
   if ((reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(out)) % 16 != 0)
     return fail(G5MOE_ERR_UNSUPPORTED, "pad_rows: src and out must be 16-byte aligned");
-  if (int64_t(shape->n_experts) * kmax * (cols / 8) >= (int64_t(1) << 40))
+  const int64_t nk = shape->n_tokens * shape->top_k;
+  const int64_t rows = kmax > 0 ? int64_t(shape->n_experts) * kmax
+                                : packed_rows_bound(nk, shape->n_experts);
+  if (rows > INT32_MAX / 4 || rows * (cols / 8) >= (int64_t(1) << 40))
     return fail(G5MOE_ERR_UNSUPPORTED, "pad_rows: output too large");
   return hip_status(launch_pad_rows(static_cast<const uint16_t*>(src), perm, offsets,
                                     static_cast<uint16_t*>(out), shape->n_experts, cols, kmax,
-                                    shape->top_k, as_stream(stream)),
+                                    shape->top_k, nk, as_stream(stream)),
                     "g5moe_pad_rows");
 }
 
@@ -621,9 +636,11 @@ g5moe_status weight_grad(const char* fn, const void* dy_pad, const void* h, bool
   if (shape->d_model % 256 != 0 || shape->d_ff % 256 != 0)
     return fail(G5MOE_ERR_UNSUPPORTED, "weight_grad: d_model %d and d_ff %d must be multiples "
                 "of 256", int(shape->d_model), int(shape->d_ff));
-  if (kmax < 384 || kmax % 192 != 0)
+  if (kmax != 0 && (kmax < 384 || kmax % 192 != 0))
     return fail(G5MOE_ERR_INVALID_ARG,
-                "weight_grad: kmax %d must be a multiple of 192 and >= 384", int(kmax));
+                "weight_grad: kmax %d must be 0 (packed) or a multiple of 192 >= 384", int(kmax));
+  if (packed_rows_bound(shape->n_tokens * shape->top_k, shape->n_experts) > INT32_MAX / 4)
+    return fail(G5MOE_ERR_UNSUPPORTED, "weight_grad: too many rows");
   if (d_w_down == nullptr && d_w_gate_up == nullptr) return G5MOE_OK;
   G5_NONNULL(offsets);
   uintptr_t align = 0;

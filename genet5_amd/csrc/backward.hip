@@ -36,9 +36,10 @@ __device__ __forceinline__ float bf_hi(uint32_t u) { return __uint_as_float(u & 
 // One wavefront per assignment a = t * k + s.  Lane c holds columns
 // [c * L, c * L + L); the dot product is an fma chain per lane added over lane
 // bits 5 .. 0, so dw is deterministic.  PAD: the scaled dY row of sorted
-// position p = offsets[e] + j goes to row e * kmax + j of the per-expert padded
-// layout [E, kmax, D] instead of row p, and wave a also zeroes padded row a
-// when a lies past its expert's count (the grid covers max(N k, E kmax) waves).
+// position p = offsets[e] + j goes to row start(e) + j of the per-expert padded
+// layout of kmax (start(e) = e * kmax, or the packed layout's start for kmax =
+// 0) instead of row p, and wave a also zeroes padded row a when a lies past its
+// expert's count (the grid covers max(N k, padded rows) waves).
 template <int L, bool PAD>
 __global__ __launch_bounds__(256) void gate_grad_kernel(
     const uint16_t* __restrict__ dy, const uint16_t* __restrict__ y_perm,
@@ -52,6 +53,8 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
   // dY row (which does not depend on the position)
   const int ol = PAD ? offsets[lane <= n_experts ? lane : n_experts] : 0;
   const int32_t p = a < nk ? inv_pos[a] : -1;
+  // PAD: lane l <= E holds the first padded row of expert l (lane E: the total)
+  const int sl = PAD ? pad_start_lane(ol, n_experts, kmax) : 0;
   // (only for an assignment: the padded grid also has waves past N k, and with
   // N = 0 dY has no row to read)
   const int64_t t = a / topk;
@@ -61,15 +64,15 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
 #pragma unroll
     for (int i = 0; i < L / 2; ++i) gv[i] = dyr[i];
   }
-  // PAD: padded row a = e * kmax + j is zeroed when j >= M_e, with e the
-  // number of l in [1, E] with l * kmax <= a.  Decided here, before any store:
-  // CDNA's vmcnt also counts stores, so a use of ol after them would wait for
-  // their completion.
+  // PAD: padded row a = start(e) + j is zeroed when j >= M_e, with e the
+  // number of l in [1, E] with start(l) <= a (starts increase: every expert has
+  // at least one padded row).  Decided here, before any store: CDNA's vmcnt also
+  // counts stores, so a use of ol after them would wait for their completion.
   bool zero_row = false;
   if constexpr (PAD) {
-    if (a < int64_t(n_experts) * kmax) {
-      const int e = __popcll(__ballot(lane >= 1 && lane <= n_experts && int64_t(lane) * kmax <= a));
-      const int64_t j = a - int64_t(e) * kmax;
+    if (a < int64_t(__shfl(sl, n_experts, 64))) {
+      const int e = __popcll(__ballot(lane >= 1 && lane <= n_experts && sl <= a));
+      const int64_t j = a - __shfl(sl, e, 64);
       zero_row = j >= __shfl(ol, e + 1, 64) - __shfl(ol, e, 64);
     }
   }
@@ -82,8 +85,10 @@ __global__ __launch_bounds__(256) void gate_grad_kernel(
       // l in [1, E] with offsets[l] <= p is p's expert
       const int e = __popcll(__ballot(lane >= 1 && lane <= n_experts && ol <= p));
       const int j = p - __shfl(ol, e, 64);
-      row = int64_t(e) * kmax + j;
-      store = j < kmax;  // a kmax below the expert's count: keep the writes in bounds
+      row = int64_t(__shfl(sl, e, 64)) + j;
+      // a kmax below the expert's count: keep the writes in bounds (the packed
+      // layout holds every row of every expert)
+      store = kmax == 0 || j < kmax;
     }
     const float w = topk_w[a];
     const uint32_t* yr = reinterpret_cast<const uint32_t*>(y_perm + int64_t(p) * D + lane * L);
@@ -295,8 +300,9 @@ __global__ __launch_bounds__(256) void router_grad_kernel(
 }
 
 // One thread per 8 consecutive h columns of one row of the expert-padded row
-// space: row e * kmax + j is sorted position offsets[e] + j for j < M_e and a
-// padding row (written as zeros in the padded outputs) otherwise.  gu rows
+// space of kmax (kmax = 0: the packed layout): row start(e) + j is sorted
+// position offsets[e] + j for j < M_e and a padding row (written as zeros in the
+// padded outputs) otherwise.  gu rows
 // interleave 32-column groups: entries [64q, 64q + 32) are g of columns
 // [32q, 32q + 32), the next 32 the matching u.  Outputs: h and dgu in the
 // padded row layout [E, kmax, .] the weight-gradient batched products and the
@@ -313,8 +319,12 @@ __global__ __launch_bounds__(256) void swiglu_bwd_kernel(
   const int cpr = F / 8;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t prow = i / cpr;
-  if (prow >= int64_t(n_experts) * kmax) return;
-  const int e = int(prow / kmax), jr = int(prow - int64_t(e) * kmax);
+  const int lane = threadIdx.x & 63;
+  const int sl = pad_start_lane(offsets[lane <= n_experts ? lane : n_experts], n_experts, kmax);
+  if (prow >= __builtin_amdgcn_readlane(sl, n_experts)) return;
+  int e = 0;
+  for (int l = 1; l < n_experts; ++l) e += __builtin_amdgcn_readlane(sl, l) <= prow ? 1 : 0;
+  const int jr = int(prow - __builtin_amdgcn_readlane(sl, e));
   const int f0 = int(i - prow * cpr) * 8;
   const int q = f0 >> 5, r = f0 & 31;
   const int64_t gpo = prow * 2 * F + 64 * q + r;
@@ -430,20 +440,28 @@ __global__ __launch_bounds__(256) void pad_transpose_kernel(
   }
 }
 
-// out[e][j][:] = the row of expert e's j-th sorted position, zero for j >= M_e:
-// the token-major per-expert padded operands of the weight-gradient products
-// (dY, and the gathered x rows).  The source row of sorted position p is p
+// out row start(e) + j = the row of expert e's j-th sorted position, zero for
+// j >= M_e: the token-major per-expert padded operands of the weight-gradient
+// products (dY, and the gathered x rows), in the padded layout of kmax (rows
+// e * kmax + j, or the packed layout for kmax = 0, whose padded rows past the
+// last expert are left alone).  The source row of sorted position p is p
 // itself (perm == nullptr) or the token perm[p] / topk.  One thread per 16 bytes.
 __global__ __launch_bounds__(256) void pad_rows_kernel(
     const uint16_t* __restrict__ src, const int32_t* __restrict__ perm,
     const int32_t* __restrict__ offsets, uint16_t* __restrict__ out, int C, int kmax,
-    int topk, int64_t total_chunks) {
+    int topk, int n_experts, int64_t total_chunks) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int ol = offsets[lane <= n_experts ? lane : n_experts];
+  const int sl = pad_start_lane(ol, n_experts, kmax);  // every lane, before the exit
   if (i >= total_chunks) return;
   const int cpr = C / 8;
   const int64_t prow = i / cpr;
   const int ch = int(i - prow * cpr);
-  const int e = int(prow / kmax), j = int(prow - int64_t(e) * kmax);
+  if (prow >= __builtin_amdgcn_readlane(sl, n_experts)) return;  // past the last expert
+  int e = 0;
+  for (int l = 1; l < n_experts; ++l) e += __builtin_amdgcn_readlane(sl, l) <= prow ? 1 : 0;
+  const int j = int(prow - __builtin_amdgcn_readlane(sl, e));
   uint4 v = make_uint4(0, 0, 0, 0);
   if (j < offsets[e + 1] - offsets[e]) {
     const int64_t pos = offsets[e] + j;
@@ -824,7 +842,9 @@ hipError_t launch_gate_grad(const uint16_t* dy, const uint16_t* y_perm, const in
                             hipStream_t st) {
   const int64_t nk = s.n_tokens * s.top_k;
   const bool pad = offsets != nullptr;
-  const int64_t waves = pad ? std::max<int64_t>(nk, int64_t(s.n_experts) * kmax) : nk;
+  const int64_t prows =
+      kmax > 0 ? int64_t(s.n_experts) * kmax : packed_rows_bound(nk, s.n_experts);
+  const int64_t waves = pad ? std::max<int64_t>(nk, prows) : nk;
   if (waves == 0) return hipSuccess;
   const unsigned grid = unsigned((waves + 3) / 4);
   switch (s.d_model / 64) {
@@ -864,9 +884,11 @@ hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32
                              const int32_t* offsets, uint16_t* dgu, uint16_t* h_pad,
                              uint16_t* dgu_pad, int kmax, const DropoutParams& drop,
                              const g5moe_shape& s, hipStream_t st) {
-  const int64_t work = int64_t(s.n_experts) * kmax * (s.d_ff / 8);
-  if (work == 0) return hipSuccess;
-  if (drop.on && perm == nullptr) return hipErrorInvalidValue;
+  const int64_t prows = kmax > 0 ? int64_t(s.n_experts) * kmax
+                                 : packed_rows_bound(s.n_tokens * s.top_k, s.n_experts);
+  const int64_t work = prows * (s.d_ff / 8);
+  if (work == 0 || kmax < 0) return kmax < 0 ? hipErrorInvalidValue : hipSuccess;
+  if (drop.on && perm == nullptr && s.n_tokens > 0) return hipErrorInvalidValue;
   const dim3 grid(unsigned((work + 255) / 256));
   if (drop.on)
     hipLaunchKernelGGL(swiglu_bwd_kernel<true>, grid, dim3(256), 0, st, dh, gu, perm, offsets,
@@ -878,13 +900,14 @@ hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32
 }
 
 hipError_t launch_pad_rows(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
-                           uint16_t* out, int n_experts, int C, int kmax, int topk,
+                           uint16_t* out, int n_experts, int C, int kmax, int topk, int64_t nk,
                            hipStream_t st) {
-  if (n_experts == 0 || C == 0 || kmax == 0) return hipSuccess;
-  if (C % 8 != 0) return hipErrorInvalidValue;
-  const int64_t chunks = int64_t(n_experts) * kmax * (C / 8);
+  if (n_experts == 0 || C == 0) return hipSuccess;
+  if (C % 8 != 0 || kmax < 0) return hipErrorInvalidValue;
+  const int64_t rows = kmax > 0 ? int64_t(n_experts) * kmax : packed_rows_bound(nk, n_experts);
+  const int64_t chunks = rows * (C / 8);
   hipLaunchKernelGGL(pad_rows_kernel, dim3(unsigned((chunks + 255) / 256)), dim3(256), 0, st,
-                     src, perm, offsets, out, C, kmax, topk, chunks);
+                     src, perm, offsets, out, C, kmax, topk, n_experts, chunks);
   return hipGetLastError();
 }
 

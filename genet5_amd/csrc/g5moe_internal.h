@@ -35,6 +35,7 @@ struct WorkspaceLayout {
   size_t rank;       // stable rank inside the block        [N*k]
   size_t h;          // SwiGLU activations, bf16            [N*k, F]
   size_t y_perm;     // expert outputs, bf16                [N*k, d]
+  size_t claims;     // the gate|up GEMM's tail-claim counters {claim, done} (256 B)
   size_t total;
   int64_t nblk;      // dispatch blocks
 };
@@ -60,6 +61,8 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   off += align256(size_t(nk + kHPadRows) * s.d_ff * 2);
   w.y_perm = off;
   off += align256(size_t(nk) * s.d_model * 2);
+  w.claims = off;
+  off += 256;
   w.total = off;
   return w;
 }
@@ -114,13 +117,17 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
 hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t* offsets,
                                    int32_t* perm, int32_t* inv_pos, const g5moe_shape& s,
                                    hipStream_t st);
+// The gate|up launchers take `claims`, the workspace's counter pair of the
+// claimed tail: they zero it with a fill kernel on `st` before a launch that
+// claims, and the launch's last workgroup leaves it at zero.
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
-                          hipStream_t st, const DropoutParams* drop = nullptr);
+                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, int* claims,
+                          const g5moe_shape& s, hipStream_t st,
+                          const DropoutParams* drop = nullptr);
 // Training gate|up for the fused SwiGLU backward: h (with dropout) into h, and the
 // derivative factors A = dh/dg, B = dh/du (dropout folded in) into ab [N*k, 2F].
 hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                             const uint16_t* wgu, uint16_t* h, uint16_t* ab,
+                             const uint16_t* wgu, uint16_t* h, uint16_t* ab, int* claims,
                              const g5moe_shape& s, hipStream_t st, const DropoutParams& drop);
 // dGU_pad (per-expert padded, wgrad_rows rows per expert) = (dY_pad Wd_e) * (A | B).
 hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* offsets,
@@ -129,8 +136,8 @@ hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* off
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                              const uint16_t* wgu, uint16_t* gu, const g5moe_shape& s,
-                              hipStream_t st);
+                              const uint16_t* wgu, uint16_t* gu, int* claims,
+                              const g5moe_shape& s, hipStream_t st);
 hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
                              uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
                              int a_rows_per_expert, hipStream_t st);
@@ -149,8 +156,9 @@ hipError_t launch_swiglu_bwd(const uint16_t* dh, const uint16_t* gu, const int32
 hipError_t launch_pad_transpose(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
                                 uint16_t* out, int n_experts, int C, int kmax, int topk,
                                 hipStream_t st);
+// kmax == 0: the packed layout, nk = the sorted positions (N k) its bound counts.
 hipError_t launch_pad_rows(const uint16_t* src, const int32_t* perm, const int32_t* offsets,
-                           uint16_t* out, int n_experts, int C, int kmax, int topk,
+                           uint16_t* out, int n_experts, int C, int kmax, int topk, int64_t nk,
                            hipStream_t st);
 // Problem 0: c0 = a0^T b0 per expert ([E * m0, n0]); b0_sorted: b0's rows of expert
 // e start at offsets[e] (sorted order, >= kWgradSlackRows finite rows after the last)
@@ -187,14 +195,44 @@ hipError_t launch_attn_fwd(const uint16_t* q, const uint16_t* k, const uint16_t*
                            hipStream_t st);
 
 // Rows of expert e the weight-gradient kernel reduces over: a multiple of 192
-// (three 64-row k-steps), at least 384, at most kmax.
+// (three 64-row k-steps), at least 384, and at most kmax when kmax > 0.
 __host__ __device__ __forceinline__ int wgrad_rows(int count, int kmax) {
-  const int r = 192 * ((count + 191) / 192);
-  return r < 384 ? (384 < kmax ? 384 : kmax) : (r < kmax ? r : kmax);
+  int r = 192 * ((count + 191) / 192);
+  if (r < 384) r = 384;
+  return kmax > 0 && r > kmax ? kmax : r;
+}
+
+// The per-expert padded row layout of the backward's operands (dY, the gathered
+// x rows, dGU), selected by kmax:
+//   kmax > 0   expert e's rows start at e * kmax, at most kmax of them;
+//   kmax == 0  "packed": expert e's wgrad_rows(M_e) rows start at the sum of
+//              wgrad_rows(M_e') over e' < e, laid end to end (at most
+//              N k + kPackedSlackPerExpert E rows in all, a bound the host knows
+//              without reading the expert counts).
+constexpr int kPackedSlackPerExpert = 384;
+__host__ __device__ __forceinline__ int64_t packed_rows_bound(int64_t nk, int n_experts) {
+  return nk + int64_t(kPackedSlackPerExpert) * n_experts;
 }
 
 // CUs of the current device (the persistent kernels' grid size).
 int device_cu_count();
+
+// First padded row of expert l = lane in the layout of kmax (lanes 0 .. E; lane
+// E holds the total), from ol = offsets[lane] in lanes 0 .. E.  Every lane of
+// the wave must call it (cross-lane shuffles).
+__device__ __forceinline__ int pad_start_lane(int ol, int n_experts, int kmax) {
+  const int lane = threadIdx.x & 63;
+  if (kmax > 0) return lane * kmax;
+  const int next = __shfl_down(ol, 1, 64);
+  int r = lane < n_experts ? wgrad_rows(next - ol, 0) : 0;
+#pragma unroll
+  for (int s = 1; s < 32; s <<= 1) {  // inclusive prefix over lanes 0 .. 31 (E <= 16)
+    const int v = __shfl_up(r, s, 64);
+    if (lane >= s) r += v;
+  }
+  const int ex = __shfl_up(r, 1, 64);
+  return lane == 0 ? 0 : ex;
+}
 
 // ---- device helpers -------------------------------------------------------
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t b) {

@@ -45,8 +45,6 @@
 // feature blocks 2j and 2j+1 hold gate and up of the same 32 h columns in the
 // same lanes; silu(g) * u is formed in registers and only h is stored (bf16).
 #include <algorithm>
-#include <atomic>
-#include <mutex>
 #include <type_traits>
 
 #include "gemm_common.h"
@@ -71,7 +69,8 @@ struct GemmArgs {
   int ldc2;
   int a_rows_per_expert;  // 0: A row of sorted position p is p; > 0: expert e's j-th
                           // row is A row e * a_rows_per_expert + j (per-expert padded
-                          // layout; at most a_rows_per_expert rows of each expert are used)
+                          // layout; at most a_rows_per_expert rows of each expert are
+                          // used); -1: the packed padded layout (pad_start)
   // MODE 3 / 5 with dropout (the kernel's DROP flag): the mask of g5moe_dropout
   uint32_t drop_seed_lo, drop_seed_hi, drop_thr;
   float drop_scale;
@@ -158,7 +157,18 @@ __device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& 
 #define G5_B3 1
 #endif
 
-template <int BM, int BN, int GM, bool WROWS = false>
+// First A row of expert e in the padded layouts (a_rows_per_expert != 0): e
+// times the per-expert row count, or, packed (-1), the sum of wgrad_rows(M_e')
+// over the experts before it.
+__device__ __forceinline__ int pad_start(const GemmArgs& args, const Offsets& off, int e) {
+  if (args.a_rows_per_expert > 0) return e * args.a_rows_per_expert;
+  int s = 0;
+  for (int i = 0; i < e; ++i) s += wgrad_rows(off(i + 1) - off(i), 0);
+  return s;
+}
+
+// PADA: A rows in a per-expert padded layout (a_rows_per_expert != 0).
+template <int BM, int BN, int GM, bool WROWS = false, bool PADA = false>
 __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, const Offsets& off, int u,
                                               TileCoord& tc) {
   const int ntn = args.Nout / BN;
@@ -179,7 +189,10 @@ __device__ __forceinline__ void decode_tile_u(const GemmArgs& args, const Offset
   tc.e = e;
   tc.p_begin = off(e) + mt * BM;
   tc.p_end = off(e) + expert_rows<WROWS>(args, off, e);
-  tc.a_row = args.a_rows_per_expert > 0 ? e * args.a_rows_per_expert + mt * BM : tc.p_begin;
+  if constexpr (PADA)
+    tc.a_row = pad_start(args, off, e) + mt * BM;
+  else
+    tc.a_row = tc.p_begin;
   tc.n0 = nt * BN;
 }
 
@@ -217,7 +230,7 @@ constexpr int persist_smem_bytes() {
 // unmasked; MODE 5's factors carry the mask), keyed on each row's assignment
 // perm[p].
 template <int BM, int BN, int BNF, int BK, int S, int NSLOT, int GM, int MODE, bool HALF,
-          bool DROP = false>
+          bool DROP = false, bool PADA = false>
 __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& off, char* smem,
                                           const Units un) {
   constexpr int WTM = BM / 2, WTN = BN / 2;
@@ -276,10 +289,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   auto decode_unit = [&](int i, TileCoord& tc) {
     const int h = un.first + i * un.stride;
     if constexpr (HALF) {
-      decode_tile_u<BM, BNF, GM, MODE == 4>(args, off, un.base + (h >> 1), tc);
+      decode_tile_u<BM, BNF, GM, MODE == 4, PADA || MODE == 4>(args, off, un.base + (h >> 1), tc);
       tc.n0 += (h & 1) * BN;
     } else {
-      decode_tile_u<BM, BNF, GM, MODE == 4>(args, off, h, tc);
+      decode_tile_u<BM, BNF, GM, MODE == 4, PADA || MODE == 4>(args, off, h, tc);
     }
   };
 
@@ -1102,7 +1115,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
 // about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
 // the gate|up GEMM (K = 768), which therefore keeps whole tiles.
 template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
-          bool DROP>
+          bool DROP, bool PADA>
 __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
   const int ntn = args.Nout / BN;
   const Offsets off = load_offsets(args.offsets, args.n_experts);
@@ -1121,13 +1134,13 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
   const int q = (hi - lo) / nslot, r = (hi - lo) % nslot;
   if constexpr (HALF_TAIL) {
     if (q > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false>(args, off, smem,
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, false, PADA>(args, off, smem,
                                                            Units{lo + slot, nslot, q, 0});
     if (slot < 2 * r) {
       // every wave's DMAs of the full pass have landed (each waited for its
       // own) before the half pass refills the stage buffers
       if (q > 0) __syncthreads();
-      tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, MODE, true>(
+      tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, MODE, true, false, PADA>(
           args, off, smem,
           Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
     }
@@ -1147,7 +1160,7 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
     Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
     if (claimed) st = Units{Qs * before + slot, nslot, Qs, 0};
     if (st.count > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP>(args, off, smem, st);
+      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP, PADA>(args, off, smem, st);
     if (claimed) {
       const int pool = total - Qs * ng;
       int* const mbox = reinterpret_cast<int*>(smem);
@@ -1158,7 +1171,7 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
         const int u = __builtin_amdgcn_readfirstlane(mbox[0]);
         __syncthreads();  // every wave has read the index before the stages refill
         if (u >= pool) break;
-        tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP>(
+        tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP, PADA>(
             args, off, smem, Units{Qs * ng + u, 1, 1, 0});
       }
       // the last workgroup out resets the counters for the slot's next launch
@@ -1172,10 +1185,10 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
 
 // One workgroup per CU: up to 512 registers per lane (256 accumulators in AGPRs).
 template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
-          bool DROP = false>
+          bool DROP = false, bool PADA = false>
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
-  persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP>(args, smem);
+  persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP, PADA>(args, smem);
 }
 
 // Two workgroups per CU (two waves per SIMD, 256 registers per lane, at most 80
@@ -1187,35 +1200,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2))) voi
 grouped_gemm_persist2_kernel(GemmArgs args) {
   static_assert(persist_smem_bytes<BM, BN, BK, S>() <= 80 * 1024, "two workgroups per CU");
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
-  persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP>(args, smem);
-}
-
-// Claim counters of the claimed-tail GEMM launches: kClaimSlots pairs {claim,
-// done}, zero at load; each launch takes the next slot (rotating), so launches
-// that overlap on different streams use different counters unless more than
-// kClaimSlots of them are in flight at once.
-constexpr int kClaimSlots = 64;
-__device__ __align__(256) int gemm_tail_claims[2 * kClaimSlots];
-
-// This launch's counter pair on the current device, or nullptr (static
-// schedule) if the symbol lookup fails.
-int* next_claim_slot() {
-  static std::mutex mu;
-  static int* addr[kMaxDevices] = {};
-  static std::atomic<unsigned> next{0};
-  int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return nullptr;
-  int* base;
-  {
-    std::lock_guard<std::mutex> lock(mu);
-    if (addr[dev] == nullptr) {
-      void* p = nullptr;
-      if (hipGetSymbolAddress(&p, HIP_SYMBOL(gemm_tail_claims)) != hipSuccess) return nullptr;
-      addr[dev] = static_cast<int*>(p);
-    }
-    base = addr[dev];
-  }
-  return base + 2 * (next.fetch_add(1) % kClaimSlots);
+  persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP, false>(args, smem);
 }
 
 }  // namespace
@@ -1241,6 +1226,19 @@ namespace {
 template <int BM, int BN>
 unsigned grid_bound(int64_t nk, int n_experts, int nout) {
   return unsigned(((nk + BM - 1) / BM + n_experts) * (nout / BN));
+}
+
+// The claimed tail's counters for a 256 x 256 gate|up launch of `tiles` tiles at
+// most on `grid` workgroups: the caller's pair, zeroed by a fill kernel on the
+// launch's stream (no memset node under graph capture), or nullptr when the
+// launch cannot claim (fewer than 8 tiles per workgroup) and keeps the static
+// schedule.  Launches that overlap on other streams use other workspaces, hence
+// other counters.
+int* claims_for(int* claims, unsigned tiles, unsigned grid, hipStream_t st, hipError_t* err) {
+  *err = hipSuccess;
+  if (claims == nullptr || tiles < 8u * grid) return nullptr;
+  *err = launch_zero16(claims, 1, st);
+  return claims;
 }
 
 // Packed gate|up from separate gate and up: row 64g + r <- gate[32g + r] (r < 32)
@@ -1315,24 +1313,26 @@ void launch_persist2(unsigned grid, const GemmArgs& a, hipStream_t st) {
 }
 
 // Persistent launch: three fragment slots when the k-step count allows it.
-template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL, bool DROP = false>
+// PADA: A rows in a per-expert padded layout (a.a_rows_per_expert != 0).
+template <int BM, int BN, int BK, int S, int GM, int MODE, bool HALF_TAIL, bool DROP = false,
+          bool PADA = false>
 void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
   const int nk = a.K / BK;
   if (nk % 3 == 0 && nk >= 6)
     hipLaunchKernelGGL(
-        (grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, MODE, HALF_TAIL, DROP>), dim3(grid),
-        dim3(256), 0, st, a);
+        (grouped_gemm_persist_kernel<BM, BN, BK, S, 3, GM, MODE, HALF_TAIL, DROP, PADA>),
+        dim3(grid), dim3(256), 0, st, a);
   else
     hipLaunchKernelGGL(
-        (grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, MODE, HALF_TAIL, DROP>), dim3(grid),
-        dim3(256), 0, st, a);
+        (grouped_gemm_persist_kernel<BM, BN, BK, S, 2, GM, MODE, HALF_TAIL, DROP, PADA>),
+        dim3(grid), dim3(256), 0, st, a);
 }
 
 }  // namespace
 
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
-                          hipStream_t st, const DropoutParams* drop) {
+                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, int* claims,
+                          const g5moe_shape& s, hipStream_t st, const DropoutParams* drop) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
   GemmArgs a{};
@@ -1351,7 +1351,9 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  a.claims = next_claim_slot();
+  hipError_t cerr;
+  a.claims = claims_for(claims, grid, pgrid, st, &cerr);
+  if (cerr != hipSuccess) return cerr;
   const bool dropout = drop != nullptr && drop->on;
   if (dropout) {
     if (gu == nullptr) return hipErrorInvalidValue;  // dropout is a training-forward mode
@@ -1370,7 +1372,7 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
 }
 
 hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                             const uint16_t* wgu, uint16_t* h, uint16_t* ab,
+                             const uint16_t* wgu, uint16_t* h, uint16_t* ab, int* claims,
                              const g5moe_shape& s, hipStream_t st, const DropoutParams& drop) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
@@ -1388,9 +1390,11 @@ hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int3
   a.ldc = s.d_ff;
   a.ldc2 = 2 * s.d_ff;
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
-  const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout),
-                                 unsigned(device_cu_count()));
-  a.claims = next_claim_slot();
+  const unsigned tiles = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+  const unsigned grid = std::min(tiles, unsigned(device_cu_count()));
+  hipError_t cerr;
+  a.claims = claims_for(claims, tiles, grid, st, &cerr);
+  if (cerr != hipSuccess) return cerr;
   if (drop.on) {
     a.drop_seed_lo = drop.seed_lo;
     a.drop_seed_hi = drop.seed_hi;
@@ -1407,12 +1411,15 @@ hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* off
                             const uint16_t* wd_t, const uint16_t* ab, uint16_t* dgu_pad,
                             const g5moe_shape& s, hipStream_t st) {
   const int E = s.n_experts, d = s.d_model, F = s.d_ff;
-  if (F % 256 != 0 || d % 64 != 0 || d < 128 || kmax < 384 || kmax % 192 != 0)
+  if (F % 256 != 0 || d % 64 != 0 || d < 128 || (kmax != 0 && (kmax < 384 || kmax % 192 != 0)))
     return hipErrorInvalidValue;
-  if (s.n_tokens * s.top_k == 0)  // every expert's rows are padding: zeros
-    return launch_zero16(dgu_pad, int64_t(E) * kmax * 2 * F * 2 / 16, st);
+  const int64_t nk = s.n_tokens * s.top_k;
+  if (nk == 0)  // every expert's rows are padding: zeros (packed: 384 rows per expert)
+    return launch_zero16(dgu_pad, int64_t(E) * (kmax > 0 ? kmax : 384) * 2 * F * 2 / 16, st);
+  // padded rows (kmax = 0: the packed layout's bound)
+  const int64_t prows = kmax > 0 ? int64_t(E) * kmax : packed_rows_bound(nk, E);
   GemmArgs a{};
-  a.a_rows_per_expert = kmax;
+  a.a_rows_per_expert = kmax > 0 ? kmax : -1;
   a.A = dy_pad;
   a.perm = nullptr;
   a.offsets = offsets;
@@ -1424,8 +1431,7 @@ hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* off
   a.K = d;
   a.Nout = F;
   a.ldc = 2 * F;
-  const unsigned grid = std::min(grid_bound<256, 256>(int64_t(E) * kmax, E, F),
-                                 unsigned(device_cu_count()));
+  const unsigned grid = std::min(grid_bound<256, 256>(prows, E, F), unsigned(device_cu_count()));
   launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 4, true>(grid, a, st);
   return hipGetLastError();
 }
@@ -1473,8 +1479,8 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
 }
 
 hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                              const uint16_t* wgu, uint16_t* gu, const g5moe_shape& s,
-                              hipStream_t st) {
+                              const uint16_t* wgu, uint16_t* gu, int* claims,
+                              const g5moe_shape& s, hipStream_t st) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
   GemmArgs a{};
@@ -1489,9 +1495,11 @@ hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int
   a.Nout = 2 * s.d_ff;
   a.ldc = 2 * s.d_ff;
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
-  const unsigned grid = std::min(grid_bound<256, 256>(nk, s.n_experts, a.Nout),
-                                 unsigned(device_cu_count()));
-  a.claims = next_claim_slot();
+  const unsigned tiles = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+  const unsigned grid = std::min(tiles, unsigned(device_cu_count()));
+  hipError_t cerr;
+  a.claims = claims_for(claims, tiles, grid, st, &cerr);
+  if (cerr != hipSuccess) return cerr;
   launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 2, false>(grid, a, st);
   return hipGetLastError();
 }
@@ -1500,7 +1508,7 @@ hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const ui
                              uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
                              int a_rows_per_expert, hipStream_t st) {
   if (rows == 0) return hipSuccess;
-  if (K % 64 != 0 || K < 128 || Nout % 128 != 0 || a_rows_per_expert < 0)
+  if (K % 64 != 0 || K < 128 || Nout % 128 != 0 || a_rows_per_expert < -1)
     return hipErrorInvalidValue;
   GemmArgs a{};
   a.a_rows_per_expert = a_rows_per_expert;
@@ -1515,6 +1523,22 @@ hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const ui
   a.Nout = Nout;
   a.ldc = Nout;
   const unsigned ncu = unsigned(device_cu_count());
+  if (a_rows_per_expert != 0) {  // A rows in a per-expert padded layout
+    if (Nout % 256 == 0 && small_m(rows, Nout, ncu)) {
+      const unsigned grid = std::min(grid_bound<128, 256>(rows, n_experts, Nout), ncu);
+      launch_persist<128, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false, false, true>(grid, a,
+                                                                                        st);
+    } else if (Nout % 256 == 0) {
+      const unsigned grid = std::min(grid_bound<256, 256>(rows, n_experts, Nout), ncu);
+      launch_persist<256, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, true, false, true>(grid, a,
+                                                                                       st);
+    } else {
+      const unsigned grid = std::min(grid_bound<256, 128>(rows, n_experts, Nout), ncu);
+      launch_persist<256, 128, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false, false, true>(grid, a,
+                                                                                        st);
+    }
+    return hipGetLastError();
+  }
   if (Nout % 256 == 0 && small_m(rows, Nout, ncu)) {
     const unsigned grid = std::min(grid_bound<128, 256>(rows, n_experts, Nout), ncu);
     launch_persist<128, 256, G5_DN_BK, G5_DN_STAGES, G5_DN_GM, 0, false>(grid, a, st);

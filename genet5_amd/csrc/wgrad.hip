@@ -6,9 +6,10 @@
 // per expert over the rows routed to it.
 //
 // For each problem p: C_p[e * M_p + i][j] = sum over t < K_e of
-// A_p[e][t][i] * B_p[e][t][j], with A_p [E, kmax, M_p] and B_p [E, kmax, N_p]
-// token-major in the per-expert padded layout (rows t >= M_e are zero) and
-// K_e = 64 * max(6, 3 * ceil(M_e / 192)) <= kmax: the zero rows add nothing.
+// A_p[e][t][i] * B_p[e][t][j], with A_p and B_p token-major in a per-expert
+// padded layout (rows t >= M_e are zero): expert e's rows at e * kmax + t, or
+// (kmax = 0) packed end to end, expert e's at the sum of K_e' over e' < e, where
+// K_e = 64 * max(6, 3 * ceil(M_e / 192)) (at most kmax): the zero rows add nothing.
 // B may instead be in sorted order (expert e's token t at row offsets[e] + t,
 // the forward's h): its rows t >= M_e are then other experts' finite rows, and
 // A's zero rows still cancel them (0 * finite = 0, so the sums are the padded
@@ -43,12 +44,12 @@ namespace {
 using namespace gemm;
 
 struct WgradProblem {
-  const uint16_t* A;  // [E, kmax, M] token-major, per-expert padded
-  const uint16_t* B;  // [E, kmax, N], or (b_sorted) [rows + kWgradSlackRows, N] in sorted order
+  const uint16_t* A;  // [padded rows, M] token-major, per-expert padded
+  const uint16_t* B;  // [padded rows, N], or (b_sorted) [rows + kWgradSlackRows, N] in sorted order
   uint16_t* C;        // [E * M, N]; with C_up, the gate rows [E * M / 2, N]
   uint16_t* C_up;     // nullptr, or the up rows [E * M / 2, N] of a packed gate|up C
   int M, N;           // multiples of 256
-  int b_sorted;       // B row of expert e's token t: offsets[e] + t instead of e * kmax + t
+  int b_sorted;       // B row of expert e's token t: offsets[e] + t instead of start(e) + t
 };
 
 struct WgradArgs {
@@ -56,7 +57,7 @@ struct WgradArgs {
   int n_problems;
   const int32_t* offsets;  // [E + 1]
   int n_experts;
-  int kmax;                // multiple of 192, >= 384
+  int kmax;                // multiple of 192, >= 384; or 0: the packed padded layout
 };
 
 constexpr int kTile = 256;                  // C rows and columns per tile
@@ -78,9 +79,18 @@ __device__ __forceinline__ int wgrad_ksteps(const Offsets& off, int e, int kmax)
   return wgrad_rows(off(e + 1) - off(e), kmax) / kBK;
 }
 
+// First padded row of expert e: e * kmax, or in the packed layout (kmax = 0)
+// the sum of wgrad_rows(M_e') over e' < e.
+__device__ __forceinline__ int64_t wgrad_pad_start(const Offsets& off, int e, int kmax) {
+  if (kmax > 0) return int64_t(e) * kmax;
+  int s = 0;
+  for (int i = 0; i < e; ++i) s += wgrad_rows(off(i + 1) - off(i), 0);
+  return s;
+}
+
 struct WTile {
   int p, e, m0, n0, nk;
-  const char* a;  // A row e * kmax + 16 * wave, column m0 (the wave's DMA rows at k = 0)
+  const char* a;  // A row start(e) + 16 * wave, column m0 (the wave's DMA rows at k = 0)
   const char* b;
   int lda2, ldb2; // row pitches in bytes
 };
@@ -111,7 +121,7 @@ __device__ __forceinline__ void wgrad_decode(const WgradArgs& args, const Offset
   t.nk = wgrad_ksteps(off, e, args.kmax);
   t.lda2 = pr.M * 2;
   t.ldb2 = pr.N * 2;
-  const int64_t row = int64_t(e) * args.kmax + 16 * wave;
+  const int64_t row = wgrad_pad_start(off, e, args.kmax) + 16 * wave;
   // a sorted B: the rows past the expert's count are the next experts' (or the
   // buffer's zero slack rows), multiplied by A's zero padding rows
   const int64_t brow = pr.b_sorted ? int64_t(off(e)) + 16 * wave : row;
@@ -409,7 +419,8 @@ hipError_t launch_wgrad(const uint16_t* a0, const uint16_t* b0, uint16_t* c0, in
                         bool b0_sorted, const uint16_t* a1, const uint16_t* b1, uint16_t* c1,
                         uint16_t* c1_up, int m1, int n1, const int32_t* offsets, int n_experts,
                         int kmax, hipStream_t st) {
-  if (n_experts < 1 || n_experts > kMaxExperts || kmax < 6 * kBK || kmax % (3 * kBK) != 0)
+  if (n_experts < 1 || n_experts > kMaxExperts ||
+      (kmax != 0 && (kmax < 6 * kBK || kmax % (3 * kBK) != 0)))
     return hipErrorInvalidValue;
   WgradArgs a{};
   a.offsets = offsets;

@@ -24,6 +24,7 @@ weight changes.
 from __future__ import annotations
 
 import math
+import weakref
 from collections import OrderedDict
 from typing import Optional, Tuple
 
@@ -33,9 +34,87 @@ import torch.nn as nn
 from . import ops
 
 
+class _ExpertWeightCache:
+    """The expert GEMMs' copies of one (w_gate, w_up, w_down) parameter set: the
+    bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F], and on request their
+    per-expert transposes [E, d, 2F] and [E, F, d] (the backward's operands).
+
+    An entry is keyed by the parameters' storage addresses and holds weak
+    references to the parameter objects; it is used while every reference still
+    names the very tensor passed in and each parameter's version counter (bumped by
+    every in-place update, such as an optimizer step) is unchanged, and rebuilt
+    otherwise.  So forwards and backwards between two optimizer steps (gradient
+    accumulation) share one copy, eager or compiled: torch.compile hands the
+    custom ops the parameter objects themselves.  An entry is dropped when one of
+    its parameters is freed.  `builds` counts the rebuilds."""
+
+    def __init__(self, max_entries: int = 64):
+        self._entries: "OrderedDict[tuple, tuple]" = OrderedDict()
+        self.max_entries = max_entries
+        self.builds = 0
+
+    @staticmethod
+    def _state(ws):
+        return tuple((w._version, w.dtype, tuple(w.shape), w.stride()) for w in ws)
+
+    def _drop(self, key):
+        def cb(_ref):
+            self._entries.pop(key, None)
+        return cb
+
+    def clear(self) -> None:
+        self._entries.clear()
+
+    def get(self, w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
+            transposed: bool = False):
+        ws = (w_gate, w_up, w_down)
+        key = tuple(w.data_ptr() for w in ws) + (w_gate.device,)
+        state = self._state(ws)
+        ent = self._entries.get(key)
+        if ent is not None:
+            refs, st, wgu, wd, tr = ent
+            if st == state and all(r() is w for r, w in zip(refs, ws)):
+                wd = w_down if wd is None else wd
+                if transposed and tr is None:
+                    with torch.no_grad():
+                        tr = (ops.transpose_experts(wgu), ops.transpose_experts(wd))
+                    self._entries[key] = (refs, st, wgu, ent[3], tr)
+                self._entries.move_to_end(key)
+                return (wgu, wd) + tr if transposed else (wgu, wd)
+        with torch.no_grad():
+            wg = w_gate.detach().to(torch.bfloat16).contiguous()
+            wu = w_up.detach().to(torch.bfloat16).contiguous()
+            wd = w_down.detach().to(torch.bfloat16).contiguous()
+            if transposed:
+                # the packed copy and its transpose in one pass over gate and up
+                wgu, wgu_t = ops.pack_gate_up_transposed(wg, wu)
+                tr = (wgu_t, ops.transpose_experts(wd))
+            else:
+                wgu, tr = ops.pack_gate_up(wg, wu), None
+        self.builds += 1
+        # a bf16 contiguous w_down is its own copy: not kept here, so the entry
+        # holds no strong reference to a parameter
+        own_wd = None if wd.data_ptr() == w_down.data_ptr() else wd
+        refs = tuple(weakref.ref(w, self._drop(key)) for w in ws)
+        self._entries[key] = (refs, state, wgu, own_wd, tr)
+        self._entries.move_to_end(key)
+        while len(self._entries) > self.max_entries:
+            self._entries.popitem(last=False)
+        return (wgu, wd) + tr if transposed else (wgu, wd)
+
+
+_WEIGHTS = _ExpertWeightCache()
+
+
+def clear_weight_cache() -> None:
+    """Drop every cached packed / transposed expert weight copy."""
+    _WEIGHTS.clear()
+
+
 @torch.library.custom_op("g5moe::moe_forward", mutates_args=())
 def _moe_forward_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
                     w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int) -> torch.Tensor:
+    """Inference forward on already packed bf16 expert weights."""
     return ops.moe_forward(x, w_router, w_gate_up, w_down, top_k, bias=bias)
 
 
@@ -44,15 +123,21 @@ def _(x, w_router, bias, w_gate_up, w_down, top_k):
     return torch.empty_like(x)
 
 
-@torch.library.custom_op("g5moe::pack_gate_up", mutates_args=())
-def _pack_gate_up_op(w_gate: torch.Tensor, w_up: torch.Tensor) -> torch.Tensor:
-    return ops.pack_gate_up(w_gate, w_up)
+@torch.library.custom_op("g5moe::moe_forward_params", mutates_args=())
+def _moe_forward_params_op(x: torch.Tensor, w_router: torch.Tensor,
+                           bias: Optional[torch.Tensor], w_gate: torch.Tensor,
+                           w_up: torch.Tensor, w_down: torch.Tensor,
+                           top_k: int) -> torch.Tensor:
+    """Inference forward on the expert parameters themselves ([E, F, d], [E, F, d],
+    [E, d, F], any float dtype): their packed bf16 copies come from the weight
+    cache, eager or compiled."""
+    wgu, wd = _WEIGHTS.get(w_gate, w_up, w_down)
+    return ops.moe_forward(x, w_router, wgu, wd, top_k, bias=bias)
 
 
-@_pack_gate_up_op.register_fake
-def _(w_gate, w_up):
-    E, F, d = w_gate.shape
-    return w_gate.new_empty((E, 2 * F, d))
+@_moe_forward_params_op.register_fake
+def _(x, w_router, bias, w_gate, w_up, w_down, top_k):
+    return torch.empty_like(x)
 
 
 def _no_backward(ctx, grad):
@@ -62,128 +147,117 @@ def _no_backward(ctx, grad):
 
 
 _moe_forward_op.register_autograd(_no_backward)
+_moe_forward_params_op.register_autograd(_no_backward)
 
 
-def _pack_backward(ctx, grad):
-    return ops.unpack_gate_up(grad.contiguous())
-
-
-_pack_gate_up_op.register_autograd(_pack_backward)
-
-
-@torch.library.custom_op("g5moe::transpose_experts", mutates_args=())
-def _transpose_experts_op(w: torch.Tensor) -> torch.Tensor:
-    return ops.transpose_experts(w)
-
-
-@_transpose_experts_op.register_fake
-def _(w):
-    E, R, C = w.shape
-    return w.new_empty((E, C, R))
-
-
-# Host copies of the expert offsets made by the training forward, waiting for
-# their autograd node: offsets' storage address -> (pinned int32 [E + 1], event
-# recorded after the non-blocking copy).  The backward needs the largest expert
-# count on the host (it sizes the padded operands); with the copy issued right
-# after the dispatch, reading it waits for that point of the forward only, not
-# for the device to drain.  Entries of forwards whose node never comes (no
-# gradient) are dropped oldest first.
-_HOST_OFFSETS: "OrderedDict[int, Tuple[torch.Tensor, torch.cuda.Event]]" = OrderedDict()
-_HOST_OFFSETS_MAX = 256
-
-
-def _fused_swiglu_backward(w_gate_up: torch.Tensor) -> bool:
+def _fused_swiglu_backward(d: int, F: int) -> bool:
     """Whether the training op keeps the SwiGLU derivative factors (the fused dh +
     SwiGLU backward, d and F multiples of 256) or the raw gate|up products."""
-    F2, d = w_gate_up.shape[1], w_gate_up.shape[2]
-    return d % 256 == 0 and (F2 // 2) % 256 == 0
+    return d % 256 == 0 and F % 256 == 0
 
 
 @torch.library.custom_op("g5moe::moe_forward_train", mutates_args=())
 def _moe_forward_train_op(x: torch.Tensor, w_router: torch.Tensor, bias: Optional[torch.Tensor],
                           w_gate: torch.Tensor, w_up: torch.Tensor, w_down: torch.Tensor,
-                          w_gate_up: torch.Tensor, w_gate_up_t: torch.Tensor,
-                          w_down_t: torch.Tensor, top_k: int, dropout_p: float, seed: int
+                          top_k: int, dropout_p: float
                           ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
                                      torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
-                                     torch.Tensor, torch.Tensor]:
-    """Training forward.  w_gate / w_up / w_down are the differentiable parameters
-    (bf16); the kernels read w_gate_up (their packed copy) and w_down, and the
-    backward the transposed copies w_gate_up_t [E, d, 2F] and w_down_t [E, F, d].
-    The last output is the forward's h [N*k + 384, F] (zero rows past N*k), which
-    the backward's down-weight gradient reads; the one before it the SwiGLU
-    derivative factors (or, for d or F not a multiple of 256, the raw gate|up
-    products), the backward's SwiGLU operand."""
-    E = w_router.shape[0]
-    host = torch.empty((E + 1,), dtype=torch.int32, pin_memory=True)
-    ready = torch.cuda.Event()
-    outs = ops.moe_forward_train(x, w_router, w_gate_up, w_down, top_k, bias=bias,
-                                 offsets_host=host, offsets_ready=ready,
+                                     torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Training forward on the expert parameters (their bf16 packed copy and its
+    transpose come from the weight cache).  Outputs: y, logits fp32 [N, E], topk_idx,
+    topk_w, offsets, perm, inv_pos, y_perm, the SwiGLU operand of the backward (the
+    derivative factors, or, for d or F not a multiple of 256, the raw gate|up
+    products; [N*k, 2F]), the forward's h [N*k + 384, F] (zero rows past N*k), which
+    the down-weight gradient reads, and the dropout seed (int64 [1] on the host).
+
+    With dropout_p > 0 the op draws the mask's 64-bit seed from torch's default CPU
+    generator (one draw per call, so torch.manual_seed makes it reproducible, and
+    activation checkpointing's recompute, which restores the generator, draws the
+    same one); the backward regenerates the mask from it.  Nothing is copied from
+    the device to the host."""
+    seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if dropout_p > 0 else 0
+    wgu, wd, _, _ = _WEIGHTS.get(w_gate, w_up, w_down, transposed=True)
+    outs = ops.moe_forward_train(x, w_router, wgu, wd, top_k, bias=bias,
                                  dropout=(dropout_p, seed) if dropout_p > 0 else None,
-                                 return_h=True, factors=_fused_swiglu_backward(w_gate_up))
-    _HOST_OFFSETS[outs[4].data_ptr()] = (host, ready)
-    while len(_HOST_OFFSETS) > _HOST_OFFSETS_MAX:
-        _HOST_OFFSETS.popitem(last=False)
-    return tuple(t.contiguous() for t in outs)
+                                 return_h=True,
+                                 factors=_fused_swiglu_backward(x.shape[1], w_gate.shape[1]))
+    return tuple(t.contiguous() for t in outs) + (torch.tensor([seed], dtype=torch.int64),)
 
 
 @_moe_forward_train_op.register_fake
-def _(x, w_router, bias, w_gate, w_up, w_down, w_gate_up, w_gate_up_t, w_down_t, top_k,
-      dropout_p, seed):
+def _(x, w_router, bias, w_gate, w_up, w_down, top_k, dropout_p):
     N, d = x.shape
-    E = w_router.shape[0]
+    E, F, _ = w_gate.shape
     i32 = dict(dtype=torch.int32, device=x.device)
     f32 = dict(dtype=torch.float32, device=x.device)
+    bf = dict(dtype=torch.bfloat16, device=x.device)
     return (torch.empty_like(x), torch.empty((N, E), **f32), torch.empty((N, top_k), **i32),
             torch.empty((N, top_k), **f32), torch.empty((E + 1,), **i32),
             torch.empty((N * top_k,), **i32), torch.empty((N * top_k,), **i32),
-            torch.empty((N * top_k, d), dtype=torch.bfloat16, device=x.device),
-            torch.empty((N * top_k, w_gate_up.shape[1]), dtype=torch.bfloat16, device=x.device),
-            torch.empty((N * top_k + ops.H_SLACK, w_gate_up.shape[1] // 2), dtype=torch.bfloat16,
-                        device=x.device))
+            torch.empty((N * top_k, d), **bf), torch.empty((N * top_k, 2 * F), **bf),
+            torch.empty((N * top_k + ops.H_SLACK, F), **bf),
+            torch.empty((1,), dtype=torch.int64, device="cpu"))
+
+
+@torch.library.custom_op("g5moe::moe_backward", mutates_args=())
+def _moe_backward_op(dy: torch.Tensor, dlogits: Optional[torch.Tensor], x: torch.Tensor,
+                     w_router: torch.Tensor, w_gate: torch.Tensor, w_up: torch.Tensor,
+                     w_down: torch.Tensor, idx: torch.Tensor, w: torch.Tensor,
+                     offsets: torch.Tensor, perm: torch.Tensor, inv_pos: torch.Tensor,
+                     y_perm: torch.Tensor, gu: torch.Tensor, h: torch.Tensor, top_k: int,
+                     dropout_p: float, seed: torch.Tensor
+                     ) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor,
+                                torch.Tensor]:
+    """The training op's backward as one op (AOT autograd records it as a single
+    node and never looks inside): (dx, d_w_router, d_w_gate, d_w_up, d_w_down), the
+    expert gradients in their parameters' dtypes.  dy: bf16 [N, d]; dlogits: the
+    fp32 gradient of the logits output (the load-balancing loss's) or None; seed:
+    the forward's dropout seed (host int64 [1])."""
+    wgu, wd, wgu_t, wd_t = _WEIGHTS.get(w_gate, w_up, w_down, transposed=True)
+    fused = _fused_swiglu_backward(x.shape[1], w_gate.shape[1])
+    dx, d_wr, d_wg, d_wu, d_wd = ops.moe_backward(
+        dy, x, w_router, wgu, wd, top_k, idx, w, offsets, perm, inv_pos, y_perm,
+        grad_logits=dlogits, w_down_t=wd_t, w_gate_up_t=wgu_t, h=h, split_gate_up=True,
+        **(dict(factors=gu) if fused else
+           dict(gu=gu, dropout=(dropout_p, int(seed[0])) if dropout_p > 0 else None)))
+    return (dx, d_wr, d_wg.to(w_gate.dtype), d_wu.to(w_up.dtype), d_wd.to(w_down.dtype))
+
+
+@_moe_backward_op.register_fake
+def _(dy, dlogits, x, w_router, w_gate, w_up, w_down, idx, w, offsets, perm, inv_pos, y_perm,
+      gu, h, top_k, dropout_p, seed):
+    return (torch.empty_like(x), torch.empty_like(w_router), torch.empty_like(w_gate),
+            torch.empty_like(w_up), torch.empty_like(w_down))
 
 
 def _train_setup(ctx, inputs, output):
-    (x, w_router, bias, w_gate, w_up, w_down, w_gate_up, w_gate_up_t, w_down_t, top_k,
-     dropout_p, seed) = inputs
-    _, _, idx, w, offsets, perm, inv_pos, y_perm, gu, h = output
+    (x, w_router, bias, w_gate, w_up, w_down, top_k, dropout_p) = inputs
+    _, _, idx, w, offsets, perm, inv_pos, y_perm, gu, h, seed = output
     ctx.top_k = top_k
-    ctx.dropout = (dropout_p, seed) if dropout_p > 0 else None
+    ctx.dropout_p = dropout_p
     # gradients of the outputs nobody differentiates (gu alone is 894 MB at 36,400
     # tokens) stay None instead of being filled with zeros
     ctx.set_materialize_grads(False)
-    try:
-        ctx.host_offsets = _HOST_OFFSETS.pop(offsets.data_ptr(), None)
-    except Exception:  # traced (fake) tensors have no storage: read on the device later
-        ctx.host_offsets = None
     # gu: the forward's SwiGLU derivative factors (or raw gate|up products), kept
     # so the backward does not recompute them (894 MB at 36,400 tokens: HBM for
     # time); h: the forward's SwiGLU outputs, the down-weight gradient's operand
     # (447 MB)
-    ctx.save_for_backward(x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w,
-                          offsets, perm, inv_pos, y_perm, gu, h)
-    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu, h)
+    ctx.save_for_backward(x, w_router, w_gate, w_up, w_down, idx, w, offsets, perm, inv_pos,
+                          y_perm, gu, h, seed)
+    ctx.mark_non_differentiable(idx, w, offsets, perm, inv_pos, y_perm, gu, h, seed)
 
 
 def _train_backward(ctx, dy, dlogits, *unused):
-    (x, w_router, w_gate_up, w_down, w_gate_up_t, w_down_t, idx, w, offsets, perm, inv_pos,
-     y_perm, gu, h) = ctx.saved_tensors
+    (x, w_router, w_gate, w_up, w_down, idx, w, offsets, perm, inv_pos, y_perm, gu, h,
+     seed) = ctx.saved_tensors
     if dy is None:
         dy = torch.zeros_like(x)
-    offsets_host = None
-    if ctx.host_offsets is not None:
-        offsets_host, ready = ctx.host_offsets
-        ready.synchronize()  # the copy issued right after the forward's dispatch
-    dx, d_wr, d_wg, d_wu, d_wd = ops.moe_backward(
-        dy.to(torch.bfloat16).contiguous(), x, w_router, w_gate_up, w_down, ctx.top_k, idx, w,
-        offsets, perm, inv_pos, y_perm,
-        grad_logits=None if dlogits is None else dlogits.float().contiguous(),
-        w_down_t=w_down_t, w_gate_up_t=w_gate_up_t, offsets_host=offsets_host, h=h,
-        split_gate_up=True,
-        **(dict(factors=gu) if _fused_swiglu_backward(w_gate_up) else
-           dict(gu=gu, dropout=ctx.dropout)))
-    return dx, d_wr, None, d_wg, d_wu, d_wd, None, None, None, None, None, None
+    dx, d_wr, d_wg, d_wu, d_wd = _moe_backward_op(
+        dy.to(torch.bfloat16).contiguous(),
+        None if dlogits is None else dlogits.float().contiguous(), x, w_router, w_gate, w_up,
+        w_down, idx, w, offsets, perm, inv_pos, y_perm, gu, h, ctx.top_k, ctx.dropout_p,
+        seed)
+    return dx, d_wr, None, d_wg, d_wu, d_wd, None, None
 
 
 _moe_forward_train_op.register_autograd(_train_backward, setup_context=_train_setup)
@@ -225,9 +299,6 @@ class MoEFeedForward(nn.Module):
         else:
             self.router_bias = None
         self.reset_parameters()
-        self._packed_key = None
-        self._packed = None
-        self._transposed = None
         # Switch-style load-balancing loss weight (0 = off); the loss of the last
         # differentiable forward is left in self.aux_loss.
         self.aux_loss_coef = 0.0
@@ -250,42 +321,10 @@ class MoEFeedForward(nn.Module):
     def _expert_weights(self, transposed: bool = False):
         """bf16 packed gate|up [E, 2F, d] and bf16 down [E, d, F] (with transposed:
         also their per-expert transposes [E, d, 2F] and [E, F, d], the backward's
-        operands), cached by the parameters' versions: rebuilt only when a weight
-        changes, so forwards and backwards between two optimizer steps (gradient
-        accumulation) share one copy.  Under torch.compile the cache (Python-side
-        state) is bypassed and the copies are made by custom ops on every call, from
-        detached parameters: the copies are kernel operands, and the gradients reach
-        the parameters through the training op's own inputs."""
-        if torch.compiler.is_compiling():
-            wgu = _pack_gate_up_op(self.w_gate.detach().to(torch.bfloat16),
-                                   self.w_up.detach().to(torch.bfloat16))
-            wd = self.w_down.detach().to(torch.bfloat16)
-            if not transposed:
-                return wgu, wd
-            return wgu, wd, _transpose_experts_op(wgu), _transpose_experts_op(wd)
-        key = (self.w_gate.data_ptr(), self.w_gate._version, self.w_up.data_ptr(),
-               self.w_up._version, self.w_down.data_ptr(), self.w_down._version,
-               self.w_gate.device, self.w_gate.dtype)
-        if self._packed_key != key:
-            with torch.no_grad():
-                wg = self.w_gate.detach().to(torch.bfloat16).contiguous()
-                wu = self.w_up.detach().to(torch.bfloat16).contiguous()
-                wd = self.w_down.detach().to(torch.bfloat16).contiguous()
-                if transposed:
-                    # the packed copy and its transpose in one pass over gate and up
-                    wgu, wgu_t = ops.pack_gate_up_transposed(wg, wu)
-                    self._packed = (wgu, wd)
-                    self._transposed = (wgu_t, ops.transpose_experts(wd))
-                else:
-                    self._packed = (ops.pack_gate_up(wg, wu), wd)
-                    self._transposed = None
-            self._packed_key = key
-        if not transposed:
-            return self._packed
-        if self._transposed is None:
-            with torch.no_grad():
-                self._transposed = tuple(ops.transpose_experts(w) for w in self._packed)
-        return self._packed + self._transposed
+        operands), from the weight cache: rebuilt only when a weight changes, so
+        forwards and backwards between two optimizer steps (gradient accumulation)
+        share one copy.  The custom ops consult the same cache themselves."""
+        return _WEIGHTS.get(self.w_gate, self.w_up, self.w_down, transposed)
 
     def _block_needs_grad(self, residual: torch.Tensor, norm_weight: torch.Tensor,
                           x_add: Optional[torch.Tensor]) -> bool:
@@ -312,8 +351,8 @@ class MoEFeedForward(nn.Module):
             w_router = w_router.to(x2.dtype)
         if self._needs_grad(x2) or (self.training and self.dropout > 0.0):
             return self._forward_train(x2, w_router.contiguous()).view(*lead, self.embed_dim)
-        wgu, wd = self._expert_weights()
-        y = _moe_forward_op(x2, w_router.contiguous(), self.router_bias, wgu, wd, self.top_k)
+        y = _moe_forward_params_op(x2, w_router.contiguous(), self.router_bias, self.w_gate,
+                                   self.w_up, self.w_down, self.top_k)
         return y.view(*lead, self.embed_dim)
 
     def _forward_train(self, x2: torch.Tensor, w_router: torch.Tensor) -> torch.Tensor:
@@ -331,12 +370,8 @@ class MoEFeedForward(nn.Module):
             raise TypeError("MoEFeedForward trains on bf16 activations (the model's autocast "
                             "dtype); got " + str(x2.dtype))
         p = self.dropout if self.training else 0.0
-        seed = int(torch.randint(0, 2 ** 62, (1,)).item()) if p > 0.0 else 0
-        wgu, wd, wgu_t, wd_t = self._expert_weights(transposed=True)
-        y, logits, idx, _, offsets, _, _, _, _, _ = _moe_forward_train_op(
-            x2, w_router, self.router_bias, self.w_gate.to(torch.bfloat16),
-            self.w_up.to(torch.bfloat16), self.w_down.to(torch.bfloat16), wgu, wgu_t, wd_t,
-            self.top_k, p, seed)
+        y, logits, idx, _, offsets, _, _, _, _, _, _ = _moe_forward_train_op(
+            x2, w_router, self.router_bias, self.w_gate, self.w_up, self.w_down, self.top_k, p)
         self.aux_loss = None
         if self.aux_loss_coef > 0:
             counts = (offsets[1:] - offsets[:-1]).float()

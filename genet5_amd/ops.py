@@ -324,6 +324,18 @@ def moe_forward(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torch.Tens
 
 ROW_PAD = 256  # padding rows of buffers read as the A operand of the grouped GEMM
 H_SLACK = 384  # rows after the workspace's h that the training gate|up zeroes
+PACKED_SLACK = 384  # the packed padded layout holds at most N*k + PACKED_SLACK * E rows
+
+
+def packed_rows(n_assignments: int, n_experts: int) -> int:
+    """Rows of the packed per-expert padded layout (kmax = 0) for N*k assignments:
+    expert e's max(384, 192 * ceil(M_e / 192)) rows laid end to end, at most this
+    many in all (a bound that needs no expert counts)."""
+    return n_assignments + PACKED_SLACK * n_experts
+
+
+def _padded_rows(kmax: int, n_assignments: int, n_experts: int) -> int:
+    return n_experts * kmax if kmax > 0 else packed_rows(n_assignments, n_experts)
 
 
 def _dropout_arg(dropout: Optional[Tuple[float, int]]):
@@ -418,11 +430,12 @@ def grouped_gemm(a_padded: torch.Tensor, rows: int, offsets: torch.Tensor,
 
 def grouped_gemm_padded(a_pad: torch.Tensor, kmax: int, rows: int, offsets: torch.Tensor,
                         b: torch.Tensor) -> torch.Tensor:
-    """c[offsets[e] + j] = a[e * kmax + j] . b_e^T for j < M_e: the grouped product over
-    a per-expert padded A ([E * kmax + ROW_PAD, K]; kmax >= every M_e)."""
+    """c[offsets[e] + j] = a[start(e) + j] . b_e^T for j < M_e: the grouped product over
+    a per-expert padded A: start(e) = e * kmax ([E * kmax + ROW_PAD, K]; kmax >= every
+    M_e), or, kmax = 0, the packed layout ([packed_rows(rows, E) + ROW_PAD, K])."""
     dev = _check_device(a_pad)
     E, n_out, K = b.shape
-    _require(a_pad, "a", (E * kmax + ROW_PAD, K), torch.bfloat16, dev)
+    _require(a_pad, "a", (_padded_rows(kmax, rows, E) + ROW_PAD, K), torch.bfloat16, dev)
     _require(b, "b", (E, n_out, K), torch.bfloat16, dev)
     _require(offsets, "offsets", (E + 1,), torch.int32, dev)
     c = torch.empty((rows, n_out), dtype=torch.bfloat16, device=dev)
@@ -451,23 +464,27 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     factors=True), with h): the dh product then computes dGU in its epilogue
     (g5moe_dh_swiglu_backward) and gu and dropout are not used.
 
-    offsets_host: a completed host copy of offsets (moe_forward_train's, after its
-    offsets_ready event); without it the offsets are read from the device here,
-    which waits for every kernel queued before the call.
+    offsets_host: for d or F not a multiple of 256 (the batched-product path, whose
+    operands are padded to a common kmax), a completed host copy of offsets
+    (moe_forward_train's, after its offsets_ready event); without it the offsets
+    are read from the device there, which waits for every kernel queued before
+    the call.  For d and F multiples of 256 (every GeneT5 shape) nothing is read
+    on the host: the padded operands use the packed layout, whose expert starts
+    the kernels compute from offsets and whose size N*k + 384 E the host knows.
     dropout: the forward's (p, seed); the SwiGLU backward regenerates its mask.
 
     HIP stages: gate gradient and dY (g5moe_gate_grad_padded: dY per expert
-    padded to kmax rows), router-logit gradient (g5moe_router_grad, plus
-    grad_logits), the gate|up recompute (g5moe_expert_gate_up_raw, unless gu
-    is given), dh = dY Wd_e (g5moe_grouped_gemm_padded on Wd^T), SwiGLU
-    backward (g5moe_swiglu_backward: h and dGU per expert padded), dX_perm =
-    dGU Wgu_e (g5moe_grouped_gemm_padded on the packed gate|up's transpose),
-    dx (g5moe_input_grad), the gathered X rows padded (g5moe_pad_rows) and the
-    weight gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e in one launch
-    (g5moe_weight_grad).  kmax is read from the offsets once on the host.
-    and dWr = dlogits^T x (g5moe_router_weight_grad).  For d or F not a multiple
-    of 256 the expert weight gradients are batched torch products over transposed
-    padded operands instead."""
+    padded), router-logit gradient (g5moe_router_grad, plus grad_logits), the
+    gate|up recompute (g5moe_expert_gate_up_raw, unless gu or factors are given),
+    dh = dY Wd_e with the SwiGLU backward (g5moe_dh_swiglu_backward with factors;
+    otherwise g5moe_grouped_gemm_padded on Wd^T and g5moe_swiglu_backward: dGU
+    per expert padded), dX_perm = dGU Wgu_e (g5moe_grouped_gemm_padded on the
+    packed gate|up's transpose), dx (g5moe_input_grad), the gathered X rows padded
+    (g5moe_pad_rows), the weight gradients dWd_e = dY_e^T h_e, dWgu_e = dGU_e^T X_e
+    in one launch (g5moe_weight_grad[_sorted_h]) and dWr = dlogits^T x
+    (g5moe_router_weight_grad).  For d or F not a multiple of 256 the expert
+    weight gradients are batched torch products over transposed padded operands
+    instead."""
     dev = _check_device(x2d)
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
@@ -479,19 +496,23 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     _require(y_perm, "y_perm", (N * k, d), torch.bfloat16, dev)
     shape = _lib.make_shape(N, d, F, E, k, _lib.DTYPE_BF16)
     S = _stream(dev)
-    # every expert's rows padded to kmax (>= max M_e) for the weight-gradient
-    # products; the host reads the offsets once here
-    offs = (offsets_host if offsets_host is not None else offsets).tolist()
-    if len(offs) != E + 1:
-        raise ValueError(f"offsets_host has {len(offs)} entries, expected {E + 1}")
-    m_max = max(b - a for a, b in zip(offs[:-1], offs[1:]))
     hip_wgrad = d % 256 == 0 and F % 256 == 0
-    kmax = wgrad_kmax(m_max) if hip_wgrad else max(64, -(-m_max // 64) * 64)
+    if hip_wgrad:
+        kmax = 0  # the packed padded layout: no host read of the offsets
+    else:
+        # the batched products need one row count for every expert: read the
+        # offsets once on the host
+        offs = (offsets_host if offsets_host is not None else offsets).tolist()
+        if len(offs) != E + 1:
+            raise ValueError(f"offsets_host has {len(offs)} entries, expected {E + 1}")
+        m_max = max(b - a for a, b in zip(offs[:-1], offs[1:]))
+        kmax = max(64, -(-m_max // 64) * 64)
+    prows = _padded_rows(kmax, N * k, E)
     dw = torch.empty((N, k), dtype=torch.float32, device=dev)
     if hip_wgrad:
         # dY scaled by the gates, straight into the padded layout the dh product
         # and the weight-gradient kernel both read
-        dy_buf = torch.empty((E * kmax + ROW_PAD, d), dtype=torch.bfloat16, device=dev)
+        dy_buf = torch.empty((prows + ROW_PAD, d), dtype=torch.bfloat16, device=dev)
         _lib.call("g5moe_gate_grad_padded", _ptr(dy), _ptr(y_perm), _ptr(inv_pos),
                   _ptr(topk_w), _ptr(offsets), _ptr(dw), _ptr(dy_buf), kmax,
                   ctypes.byref(shape), S)
@@ -510,8 +531,8 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     if w_down_t is None:
         w_down_t = transpose_experts(w_down)            # [E, F, d]
     # dGU per expert padded, with the grouped GEMM's ROW_PAD rows after the last
-    dgu_buf = torch.empty((E * kmax + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
-    dgu_pad = dgu_buf[:E * kmax].view(E, kmax, 2 * F)
+    dgu_buf = torch.empty((prows + ROW_PAD, 2 * F), dtype=torch.bfloat16, device=dev)
+    dgu_pad = dgu_buf[:prows] if kmax == 0 else dgu_buf[:prows].view(E, kmax, 2 * F)
     h_pad = None
     if factors is not None:
         # the dh product with the SwiGLU backward in its epilogue (the forward's
@@ -536,7 +557,8 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
         else:
             dh = grouped_gemm(dyp, N * k, offsets, w_down_t)
         if not sorted_h:
-            h_pad = torch.empty((E, kmax, F), dtype=torch.bfloat16, device=dev)
+            h_pad = torch.empty((prows, F) if kmax == 0 else (E, kmax, F), dtype=torch.bfloat16,
+                                device=dev)
         _lib.call("g5moe_swiglu_backward", _ptr(dh), _ptr(gu), _ptr(perm), _ptr(offsets), None,
                   _ptr(h_pad), _ptr(dgu_buf), kmax, _dropout_arg(dropout), ctypes.byref(shape),
                   S)
@@ -552,8 +574,8 @@ def moe_backward(dy: torch.Tensor, x2d: torch.Tensor, w_router: torch.Tensor,
     d_wr = router_weight_grad(dlogits, x2d, shape)
     if hip_wgrad:
         # weight gradients on the HIP kernel over token-major padded operands
-        dy_pad = dy_buf[:E * kmax].view(E, kmax, d)
-        x_pad = pad_rows(x2d, perm, offsets, E, kmax, k)
+        dy_pad = dy_buf[:prows]
+        x_pad = pad_rows(x2d, perm, offsets, E, kmax, k, n_assignments=N * k)
         if sorted_h:
             d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
             d_wg = torch.empty((E, F, d), dtype=torch.bfloat16, device=dev)
@@ -609,18 +631,30 @@ def wgrad_kmax(m_max: int) -> int:
 
 
 def pad_rows(src: torch.Tensor, perm: Optional[torch.Tensor], offsets: torch.Tensor,
-             n_experts: int, kmax: int, top_k: int = 1) -> torch.Tensor:
+             n_experts: int, kmax: int, top_k: int = 1,
+             n_assignments: Optional[int] = None) -> torch.Tensor:
     """out[e, j] = src row of expert e's j-th sorted position (src row p, or
-    src row perm[p] // top_k with perm), zero for j >= M_e: [E, kmax, cols]."""
+    src row perm[p] // top_k with perm), zero for j >= M_e: [E, kmax, cols]; or,
+    kmax = 0, the packed layout [packed_rows(n_assignments, E), cols] (expert e's
+    wgrad rows from its packed start; rows past the last expert are left
+    unwritten).  n_assignments: N*k (default: src's row count times top_k with
+    perm, its row count without)."""
     dev = _check_device(src)
     cols = src.shape[1]
     if src.dtype != torch.bfloat16 or not src.is_contiguous():
         raise TypeError("pad_rows takes a contiguous bf16 source")
     _require(offsets, "offsets", (n_experts + 1,), torch.int32, dev)
-    out = torch.empty((n_experts, kmax, cols), dtype=torch.bfloat16, device=dev)
-    # n_tokens: the source's row count (0 for an empty batch, when every output
+    if n_assignments is None:
+        n_assignments = src.shape[0] * (top_k if perm is not None else 1)
+    if kmax > 0:
+        out = torch.empty((n_experts, kmax, cols), dtype=torch.bfloat16, device=dev)
+    else:
+        out = torch.empty((packed_rows(n_assignments, n_experts), cols), dtype=torch.bfloat16,
+                          device=dev)
+    # n_tokens * top_k: the assignments (0 for an empty batch, when every output
     # row is a zero row); the kernel itself reads offsets and perm
-    shape = _lib.make_shape(src.shape[0], 256, 256, n_experts, top_k, _lib.DTYPE_BF16)
+    shape = _lib.make_shape(n_assignments // top_k, 256, 256, n_experts, top_k,
+                            _lib.DTYPE_BF16)
     _lib.call("g5moe_pad_rows", _ptr(src), _ptr(perm), _ptr(offsets), _ptr(out), cols, kmax,
               ctypes.byref(shape), _stream(dev))
     return out
@@ -630,19 +664,25 @@ def weight_grad(dy_pad: torch.Tensor, h_pad: torch.Tensor, dgu_pad: torch.Tensor
                 x_pad: torch.Tensor, offsets: torch.Tensor, kmax: int, top_k: int = 2):
     """(d_w_down [E, d, F], d_w_gate_up [E, 2F, d] packed) = per-expert
     dy_pad[e]^T h_pad[e] and dgu_pad[e]^T x_pad[e] over token-major padded
-    operands ([E, kmax, .], zero rows past each expert's count; kmax from
-    wgrad_kmax)."""
+    operands (zero rows past each expert's count): [E, kmax, .] with kmax from
+    wgrad_kmax, or, kmax = 0, the packed layout ([rows, .], rows from packed_rows)."""
     dev = _check_device(dy_pad)
-    E, _, d = dy_pad.shape
-    F = h_pad.shape[2]
-    _require(dy_pad, "dy_pad", (E, kmax, d), torch.bfloat16, dev)
-    _require(h_pad, "h_pad", (E, kmax, F), torch.bfloat16, dev)
-    _require(dgu_pad, "dgu_pad", (E, kmax, 2 * F), torch.bfloat16, dev)
-    _require(x_pad, "x_pad", (E, kmax, d), torch.bfloat16, dev)
+    E = offsets.shape[0] - 1
+    d = dy_pad.shape[-1]
+    F = h_pad.shape[-1]
+    lead = (E, kmax) if kmax > 0 else (dy_pad.shape[0],)
+    if kmax == 0 and (dy_pad.dim() != 2 or dy_pad.shape[0] < PACKED_SLACK * E):
+        raise ValueError("packed weight-gradient operands are 2-D with at least 384 E rows")
+    _require(dy_pad, "dy_pad", lead + (d,), torch.bfloat16, dev)
+    _require(h_pad, "h_pad", lead + (F,), torch.bfloat16, dev)
+    _require(dgu_pad, "dgu_pad", lead + (2 * F,), torch.bfloat16, dev)
+    _require(x_pad, "x_pad", lead + (d,), torch.bfloat16, dev)
     _require(offsets, "offsets", (E + 1,), torch.int32, dev)
     d_wd = torch.empty((E, d, F), dtype=torch.bfloat16, device=dev)
     d_wgu = torch.empty((E, 2 * F, d), dtype=torch.bfloat16, device=dev)
-    shape = _lib.make_shape(1, d, F, E, top_k, _lib.DTYPE_BF16)
+    # n_tokens: the packed layout's bound is N*k + 384 E rows
+    n_tok = 1 if kmax > 0 else max(0, lead[0] - PACKED_SLACK * E) // top_k
+    shape = _lib.make_shape(n_tok, d, F, E, top_k, _lib.DTYPE_BF16)
     _lib.call("g5moe_weight_grad", _ptr(dy_pad), _ptr(h_pad), _ptr(d_wd), _ptr(dgu_pad),
               _ptr(x_pad), _ptr(d_wgu), _ptr(offsets), kmax, ctypes.byref(shape), _stream(dev))
     return d_wd, d_wgu

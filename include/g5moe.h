@@ -21,11 +21,10 @@
  *     exception crosses the ABI.
  *   - Results are deterministic: the same inputs give bitwise-identical outputs.
  *   - Calls on different streams may overlap when each has its own workspace
- *     and outputs.  The gate|up GEMM launches share a library-owned ring of 64
- *     tail-claim counter pairs per GPU (each launch takes the next, and its
- *     last workgroup resets it): more than 64 of them in flight at once on one
- *     GPU would share counters.  g5moe_dispatch_noalloc's scratch is one array
- *     per GPU (see there).
+ *     and outputs (the gate|up GEMMs keep their tail-claim counters in the
+ *     workspace, zeroed on the call's stream before each launch, so a launch
+ *     captured in a HIP graph and replayed shares them with nothing else).
+ *     g5moe_dispatch_noalloc's scratch is one array per GPU (see there).
  *   - Tensors are row-major.  bf16 values are raw IEEE bfloat16 bit patterns
  *     (uint16); weights use nn.Linear orientation [out, in].
  */

@@ -5,6 +5,8 @@ this module, as the checker.
 
 diffusion_generate(model, prefix_ids, target_len, mask_token_id, pad_token_id,
                    num_steps, strategy)
+select_step(logits, masked, want, strategy)
+    One step's predictions, confidences and chosen positions (the driver's body).
     The reference's diffusion_generate (lib/inference/diffusion_engine.py:18-95)
     at temperature 0, one row at a time, in numpy float64:
       * the target starts fully masked after the prefix (:33-35);
@@ -70,6 +72,28 @@ def step_count(frac: float, target_len: int) -> int:
     return int(np.float32(frac * target_len))
 
 
+def select_step(logits: np.ndarray, masked: np.ndarray, want: int, strategy: str):
+    """One unmasking step on target logits [B, T, V] whose mask and pad columns are
+    already -inf (diffusion_engine.py:53-82): per row the argmax predictions, their
+    confidences, and the min(want, masked count) still-masked positions of largest
+    confidence (ties to the lower position).  Returns (preds [B, T] int64,
+    conf [B, T] float64, chosen [B, T] bool)."""
+    B, T, _ = logits.shape
+    preds = np.zeros((B, T), dtype=np.int64)
+    conf = np.zeros((B, T), dtype=np.float64)
+    chosen = np.zeros((B, T), dtype=bool)
+    for i in range(B):
+        preds[i] = logits[i].argmax(axis=-1)
+        conf[i] = confidence(logits[i], preds[i], strategy)
+        cand = np.flatnonzero(masked[i])
+        n = min(want, cand.size)
+        if n == 0:
+            continue
+        # the n largest confidences among the masked positions
+        chosen[i, cand[np.argsort(-conf[i, cand], kind="stable")[:n]]] = True
+    return preds, conf, chosen
+
+
 def diffusion_generate(model: Callable, prefix_ids: np.ndarray, target_len: int,
                        mask_token_id: int, pad_token_id: int, num_steps: int,
                        strategy: str = "confidence", stats: dict = None) -> np.ndarray:
@@ -84,18 +108,10 @@ def diffusion_generate(model: Callable, prefix_ids: np.ndarray, target_len: int,
         forwards += 1
         logits[:, :, mask_token_id] = -np.inf
         logits[:, :, pad_token_id] = -np.inf
-        want = step_count(frac, target_len)
-        for i in range(B):
-            preds = logits[i].argmax(axis=-1)
-            conf = confidence(logits[i], preds, strategy)
-            cand = np.flatnonzero(masked[i])
-            n = min(want, cand.size)
-            if n == 0:
-                continue
-            # the n largest confidences among the masked positions
-            chosen = cand[np.argsort(-conf[cand], kind="stable")[:n]]
-            ids[i, P + chosen] = preds[chosen]
-            masked[i, chosen] = False
+        preds, _, chosen = select_step(logits, masked, step_count(frac, target_len), strategy)
+        tgt = ids[:, P:]
+        tgt[chosen] = preds[chosen]
+        masked &= ~chosen
     if masked.any():
         logits = _logits_np(model, ids.copy())[:, P:]
         forwards += 1

@@ -53,7 +53,9 @@ def test_workspace_size_layout(g5lib):
     # h carries 384 rows after its last row: one 256-row GEMM tile of padding, and
     # the weight gradient's sorted-order slack (ops.H_SLACK)
     assert ops.H_SLACK == 384
-    assert n == a(0) + a(nblk * 16 * 4) + a(nk * 4) + a((nk + 384) * 3072 * 2) + a(nk * 768 * 2)
+    # the last 256 bytes: the gate|up GEMM's tail-claim counters
+    assert n == (a(0) + a(nblk * 16 * 4) + a(nk * 4) + a((nk + 384) * 3072 * 2) +
+                 a(nk * 768 * 2) + 256)
     n32 = _lib.workspace_size(shape(x_dtype=1))
     assert n32 == n + a(36400 * 768 * 2)
     assert ops._h_offset(s) == a(0) + a(nblk * 16 * 4) + a(nk * 4)
@@ -157,19 +159,28 @@ def test_fake_impl_traces_shape():
 def test_training_op_fake_impl_shapes():
     """The training op's fake implementation (torch.compile traces it) gives the
     real op's ten outputs: y, logits, routing, y_perm, the SwiGLU operand for the
-    backward [N*k, 2F] and the forward's h with its 384 slack rows."""
+    backward [N*k, 2F] and the forward's h with its 384 slack rows; the backward
+    op's fake gives one gradient per differentiable input, in its dtype."""
     from torch._subclasses.fake_tensor import FakeTensorMode
-    from genet5_amd.moe import _moe_forward_train_op
+    from genet5_amd.moe import _moe_backward_op, _moe_forward_train_op
     N, d, F, E, k = 10, 768, 3072, 16, 2
     with FakeTensorMode():
         b = dict(dtype=torch.bfloat16)
-        outs = _moe_forward_train_op(
-            torch.empty(N, d, **b), torch.empty(E, d, **b), None, torch.empty(E, F, d, **b),
-            torch.empty(E, F, d, **b), torch.empty(E, d, F, **b), torch.empty(E, 2 * F, d, **b),
-            torch.empty(E, d, 2 * F, **b), torch.empty(E, F, d, **b), k, 0.1, 123)
+        f = dict(dtype=torch.float32)
+        x = torch.empty(N, d, **b)
+        wr = torch.empty(E, d, **b)
+        wg, wu, wd = torch.empty(E, F, d, **f), torch.empty(E, F, d, **f), torch.empty(E, d, F, **f)
+        outs = _moe_forward_train_op(x, wr, None, wg, wu, wd, k, 0.1)
         shapes = [tuple(t.shape) for t in outs]
+        assert outs[10].device.type == "cpu" and outs[10].dtype == torch.int64
+        grads = _moe_backward_op(torch.empty(N, d, **b), None, x, wr, wg, wu, wd, *outs[2:10],
+                                 k, 0.1, outs[10])
+        gshapes = [(tuple(g.shape), g.dtype) for g in grads]
     assert shapes == [(N, d), (N, E), (N, k), (N, k), (E + 1,), (N * k,), (N * k,), (N * k, d),
-                      (N * k, 2 * F), (N * k + ops.H_SLACK, F)]
+                      (N * k, 2 * F), (N * k + ops.H_SLACK, F), (1,)]
+    assert gshapes == [((N, d), torch.bfloat16), ((E, d), torch.bfloat16),
+                       ((E, F, d), torch.float32), ((E, F, d), torch.float32),
+                       ((E, d, F), torch.float32)]
 
 
 @pytest.mark.parametrize("args,code,msg", [
@@ -220,13 +231,15 @@ def test_weight_grad_and_pad_rows_nothing_to_do(g5lib):
     # both outputs NULL: no work, no pointer touched
     assert g5lib.g5moe_weight_grad(None, None, None, None, None, None, None, 384,
                                    ctypes.byref(s), None) == 0
-    assert g5lib.g5moe_pad_rows(None, None, None, None, 768, 0, ctypes.byref(s), None) == 0
+    assert g5lib.g5moe_weight_grad(None, None, None, None, None, None, None, 0,
+                                   ctypes.byref(s), None) == 0
 
 
 @pytest.mark.parametrize("cols,kmax,code,msg", [
     (12, 64, 1, "multiple of 8"),
     (768, -1, 1, "kmax"),
     (768, 64, 1, "NULL"),
+    (768, 0, 1, "NULL"),  # kmax 0: the packed layout, which has rows to write
 ])
 def test_pad_rows_argument_checks(g5lib, cols, kmax, code, msg):
     s = _wg_shape()
@@ -247,9 +260,12 @@ def test_gate_grad_padded_argument_checks(g5lib, kw, code, msg):
     st = g5lib.g5moe_gate_grad_padded(p, p, p, p, a["offsets"], p, p, a["kmax"],
                                       ctypes.byref(s), None)
     assert st == code and msg in g5lib.g5moe_last_error().decode(), (st, g5lib.g5moe_last_error())
+    # no tokens: the padded rows still get their zeros (384 per expert in the packed
+    # layout), so offsets and dy_pad are needed, the token inputs are not
     s0 = _lib.make_shape(0, 768, 3072, 16, 2, _lib.DTYPE_BF16)
     assert g5lib.g5moe_gate_grad_padded(None, None, None, None, None, None, None, 0,
-                                        ctypes.byref(s0), None) == 0
+                                        ctypes.byref(s0), None) == 1
+    assert "NULL" in g5lib.g5moe_last_error().decode()
 
 
 def test_wgrad_kmax_rule():

@@ -28,7 +28,7 @@ def test_forward_graph_replays_equal_eager(cuda_device, n):
     torch.cuda.synchronize()
     s = torch.cuda.Stream(cuda_device)
     s.wait_stream(torch.cuda.current_stream(cuda_device))
-    with torch.cuda.stream(s):  # warm the capture stream (library caches, claim slots)
+    with torch.cuda.stream(s):  # warm the capture stream (library caches)
         ops.moe_forward(xin, wr, wgu, wd, k, buffers=buf)
     torch.cuda.current_stream(cuda_device).wait_stream(s)
     torch.cuda.synchronize()

@@ -374,18 +374,26 @@ def test_upcycled_checkpoint_layer_equals_dense(cuda_device):
 
 
 @pytest.mark.parametrize("dropout", [0.0, 0.1])
-def test_module_training_step_under_torch_compile(cuda_device, dropout):
+@pytest.mark.parametrize("d,F", [(128, 256), (256, 512)])
+def test_module_training_step_under_torch_compile(cuda_device, dropout, d, F):
     """GeneT5 compiles its encoder for training (torch.compile(model.encoder)): the
-    module's training op, its fake implementation and the autograd backward trace
-    under dynamo + AOT autograd (aot_eager backend), and the compiled step gives
-    the eager step's output and gradients bit for bit (same seed for the dropout
-    mask: torch.manual_seed before each)."""
-    print(f"compile training dropout={dropout}", flush=True)
+    module's training forward traces under dynamo with fullgraph=True (no graph
+    break), and AOT autograd traces its backward to one g5moe::moe_backward node
+    (the op's fake implementation; no data_ptr or host read inside the trace), with
+    no error swallowed while tracing the backward.  The compiled steps give the
+    eager step's output and gradients bit for bit (same seed for the dropout mask),
+    and the compiled micro-steps reuse the cached packed and transposed weights
+    (no rebuild after the first step).  d, F: the batched-product backward
+    (128, 256) and the fused HIP one (256, 512)."""
+    import warnings
+    from torch._dynamo.utils import counters
+    from genet5_amd import moe as moe_mod
+    print(f"compile training dropout={dropout} d={d} F={F}", flush=True)
     torch.manual_seed(0)
-    m = MoEFeedForward(128, 256, dropout, num_experts=4).to(cuda_device).to(torch.bfloat16)
+    m = MoEFeedForward(d, F, dropout, num_experts=4).to(cuda_device).to(torch.bfloat16)
     m.train()
-    x = torch.randn(96, 128, device=cuda_device).to(torch.bfloat16)
-    dy = torch.randn(96, 128, device=cuda_device).to(torch.bfloat16)
+    x = torch.randn(96, d, device=cuda_device).to(torch.bfloat16)
+    dy = torch.randn(96, d, device=cuda_device).to(torch.bfloat16)
 
     def step(fn):
         m.zero_grad(set_to_none=True)
@@ -397,10 +405,23 @@ def test_module_training_step_under_torch_compile(cuda_device, dropout):
                                      (m.router.weight, m.w_gate, m.w_up, m.w_down)]
 
     y0, dx0, g0 = step(m)
-    f = torch.compile(m, backend="aot_eager")
-    y1, dx1, g1 = step(f)
+    torch._dynamo.reset()
+    counters.clear()
+    f = torch.compile(m, backend="aot_eager", fullgraph=True)
+    with warnings.catch_warnings(record=True) as caught:
+        warnings.simplefilter("always")
+        y1, dx1, g1 = step(f)
+        builds = moe_mod._WEIGHTS.builds
+        for _ in range(2):   # gradient-accumulation micro-steps: the caches hold
+            y2, dx2, g2 = step(f)
     torch.cuda.synchronize()
-    assert torch.equal(y0, y1)
-    assert torch.equal(dx0, dx1)
-    for a, b in zip(g0, g1):
-        assert torch.equal(a, b)
+    errs = [str(w.message) for w in caught if "Error detected" in str(w.message)]
+    assert not errs, errs
+    assert counters["aot_autograd"]["not_ok"] == 0, dict(counters["aot_autograd"])
+    assert not counters["graph_break"], dict(counters["graph_break"])
+    assert moe_mod._WEIGHTS.builds == builds
+    for yy, dxx, gg in ((y1, dx1, g1), (y2, dx2, g2)):
+        assert torch.equal(y0, yy)
+        assert torch.equal(dx0, dxx)
+        for a, b in zip(g0, gg):
+            assert torch.equal(a, b)
