@@ -182,6 +182,8 @@ _SIGS = {
 
 _lock = threading.Lock()
 _lib = None
+# the major version of include/g5moe.h these bindings follow (g5moe_version() >> 16)
+ABI_MAJOR = 2
 
 
 def lib() -> ctypes.CDLL:
@@ -200,6 +202,10 @@ def lib() -> ctypes.CDLL:
                 fn = getattr(handle, name)
                 fn.argtypes = argtypes
                 fn.restype = restype
+            major = handle.g5moe_version() >> 16
+            if major != ABI_MAJOR:
+                raise ImportError(f"{LIB_PATH} has ABI major version {major}; these bindings "
+                                  f"are for {ABI_MAJOR} (rebuild with python -m genet5_amd.build)")
             _lib = handle
     return _lib
 

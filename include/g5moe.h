@@ -73,7 +73,11 @@ typedef struct g5moe_shape {
 /* Message of the last failing call on this thread ("" if none). */
 const char* g5moe_last_error(void);
 
-/* ABI version: (major << 16) | minor. */
+/* ABI version: (major << 16) | minor.  2.0: g5moe_expert_gate_up_train and
+ * g5moe_swiglu_backward take the g5moe_dropout descriptor (and the latter perm),
+ * the workspace ends with 256 bytes of GEMM tail-claim counters, and kmax = 0
+ * selects the packed padded layout (see "Padded row layouts") wherever the
+ * backward takes kmax. */
 int32_t g5moe_version(void);
 
 /* Bytes of workspace the stage entry points and g5moe_forward need for `shape`.
@@ -302,6 +306,20 @@ g5moe_status g5moe_combine_residual(const void* y_perm, const int32_t* inv_pos,
 g5moe_status g5moe_transpose_experts(const void* w, void* w_t, int32_t n_experts, int32_t rows,
                                      int32_t cols, void* stream);
 
+/* Padded row layouts.  The backward's per-expert operands (dY, dGU, the gathered
+ * x rows, h) give expert e a block of padded rows starting at start(e), whose
+ * first M_e rows are the expert's sorted positions in order and whose rest are
+ * zeros (R_e = max(384, 192 * ceil(M_e / 192)) rows are the weight gradient's
+ * reduction length).  The kmax argument selects the layout:
+ *   kmax > 0   start(e) = e * kmax, E * kmax rows; kmax must be >= every M_e
+ *              (and, where the weight-gradient row rule applies, a multiple of
+ *              192, >= 384): the caller needs the largest expert count.
+ *   kmax == 0  "packed": start(e) = R_0 + ... + R_{e-1}, computed by the kernels
+ *              from offsets, so the host needs no expert counts; at most
+ *              N*k + 384*E rows in all (size buffers for that), rows past the
+ *              last expert's are not written.
+ * Buffers read as a GEMM A operand need 256 more rows after those. */
+
 /* Grouped product over expert-contiguous rows: for sorted position p of expert
  * e (offsets[e] <= p < offsets[e+1]), c[p] = a[p] . b_e^T, fp32 accumulate,
  * bf16 out.  a : bf16 [rows + 256, k];  b : bf16 [E, n_out, k];
@@ -311,10 +329,11 @@ g5moe_status g5moe_grouped_gemm(const void* a, const int32_t* offsets, const voi
                                 int64_t rows, int32_t k, int32_t n_out, int32_t n_experts,
                                 void* stream);
 
-/* g5moe_grouped_gemm over the per-expert padded row layout: expert e's j-th
- * sorted position (offsets[e] + j, j < min(M_e, kmax)) reads A row
- * e*kmax + j and writes c row offsets[e] + j.  a : bf16 [E*kmax + 256, k]
- * (e.g. the SwiGLU backward's dgu_pad);  b, c, k, n_out as g5moe_grouped_gemm.
+/* g5moe_grouped_gemm over a per-expert padded row layout (kmax > 0, or 0 for the
+ * packed layout): expert e's j-th sorted position (offsets[e] + j, j < M_e, and
+ * j < kmax when kmax > 0) reads A row start(e) + j and writes c row
+ * offsets[e] + j.  a : bf16 [padded rows + 256, k] (e.g. the SwiGLU backward's
+ * dgu_pad);  b, c, k, n_out as g5moe_grouped_gemm.
  * The backward's dX product reads dGU this way, so the SwiGLU backward writes
  * dGU once. */
 g5moe_status g5moe_grouped_gemm_padded(const void* a, int32_t kmax, const int32_t* offsets,
@@ -331,14 +350,17 @@ g5moe_status g5moe_gate_grad(const void* dy, const void* y_perm, const int32_t* 
                              const float* topk_w, float* dw, void* dy_perm,
                              const g5moe_shape* shape, void* stream);
 
-/* g5moe_gate_grad with dy_perm written in the per-expert padded row layout:
- * sorted position offsets[e] + j goes to row e*kmax + j, and rows
- * e*kmax + j for j in [M_e, kmax) are zeroed.  dy_pad : bf16 [E*kmax + 256, d]
- * out (the last 256 rows are not written).  kmax >= every M_e (rows of an
+/* g5moe_gate_grad with dy_perm written in a per-expert padded row layout (kmax >
+ * 0, or 0 for the packed layout): sorted position offsets[e] + j goes to row
+ * start(e) + j, and the expert's padded rows start(e) + j for j in [M_e, kmax)
+ * (packed: [M_e, R_e)) are zeroed.  dy_pad : bf16 [padded rows + 256, d] out (the
+ * last 256 rows are not written).  With kmax > 0, kmax >= every M_e (rows of an
  * expert past kmax are not written).  dh = dY Wd^T then runs as
- * g5moe_grouped_gemm_padded over dy_pad, and dy_pad's first E*kmax rows are
+ * g5moe_grouped_gemm_padded over dy_pad, and dy_pad's padded rows are
  * g5moe_weight_grad's dy_pad operand, so no g5moe_pad_rows pass over dY is
- * needed.  One launch of max(N*k, E*kmax) wavefronts. */
+ * needed.  An empty batch (N = 0) still writes the zero rows (dy, y_perm,
+ * inv_pos, topk_w and dw may then be NULL).  One launch of max(N*k, padded rows)
+ * wavefronts. */
 g5moe_status g5moe_gate_grad_padded(const void* dy, const void* y_perm, const int32_t* inv_pos,
                                     const float* topk_w, const int32_t* offsets, float* dw,
                                     void* dy_pad, int32_t kmax, const g5moe_shape* shape,
@@ -346,18 +368,18 @@ g5moe_status g5moe_gate_grad_padded(const void* dy, const void* y_perm, const in
 
 /* The dh product and the SwiGLU backward in one launch (the derivative of
  * LigerSiLUMulFunction's silu(a) * b, lib/blocks/_component.py:31, :50): for
- * expert e's j-th row, dh = dy_pad[e*kmax + j] . Wd_e (fp32 accumulation, rounded
- * to bf16 as g5moe_grouped_gemm_padded stores it), and with A, B the factors of
- * row offsets[e] + j in ab (g5moe_expert_gate_up_train_factors):
- *   dgu_pad[e*kmax + j][gate f] = bf16(dh[f] * A[f]),
- *   dgu_pad[e*kmax + j][up f]   = bf16(dh[f] * B[f])   for j < M_e,
- *   zeros for M_e <= j < max(384, 192 * ceil(M_e / 192)) (the rows
- *   g5moe_weight_grad reads), rows past those not written.
- * dy_pad : bf16 [E*kmax + 256, d] (g5moe_gate_grad_padded's);  w_down_t : bf16
- * [E, F, d] (g5moe_transpose_experts of w_down);  dgu_pad : bf16 [E*kmax + 256, 2F]
- * (g5moe_grouped_gemm_padded's A operand for dX and g5moe_weight_grad's dgu_pad).
- * kmax a multiple of 192, >= 384 and >= every M_e; F a multiple of 256; buffers
- * 16-byte aligned. */
+ * expert e's j-th row, dh = dy_pad[start(e) + j] . Wd_e (fp32 accumulation,
+ * rounded to bf16 as g5moe_grouped_gemm_padded stores it), and with A, B the
+ * factors of row offsets[e] + j in ab (g5moe_expert_gate_up_train_factors):
+ *   dgu_pad[start(e) + j][gate f] = bf16(dh[f] * A[f]),
+ *   dgu_pad[start(e) + j][up f]   = bf16(dh[f] * B[f])   for j < M_e,
+ *   zeros for M_e <= j < R_e (the rows g5moe_weight_grad reads), rows past
+ *   those not written.
+ * dy_pad : bf16 [padded rows + 256, d] (g5moe_gate_grad_padded's);  w_down_t : bf16
+ * [E, F, d] (g5moe_transpose_experts of w_down);  dgu_pad : bf16 [padded rows +
+ * 256, 2F] (g5moe_grouped_gemm_padded's A operand for dX and g5moe_weight_grad's
+ * dgu_pad).  kmax 0 (packed) or a multiple of 192, >= 384 and >= every M_e; F a
+ * multiple of 256; buffers 16-byte aligned. */
 g5moe_status g5moe_dh_swiglu_backward(const void* dy_pad, int32_t kmax, const int32_t* offsets,
                                       const void* w_down_t, const void* ab, void* dgu_pad,
                                       const g5moe_shape* shape, void* stream);
@@ -381,11 +403,12 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
  * lib/blocks/_component.py:31, :50): with s = 1 / (1 + exp(-g)),
  *   dg = dh * u * s * (1 + g * (1 - s)),  du = dh * g * s,  h = g * s * u
  * (h recomputed for the down weight gradient).  dh : bf16 [N*k, F];
- * gu : bf16 [N*k, 2F] packed;  h_pad, dgu_pad : bf16 [E, kmax, F],
- * [E, kmax, 2F] out — rows placed per expert, row e*kmax + j = sorted position
- * offsets[e] + j, zero rows for j >= M_e (kmax >= every M_e): the weight
- * gradients' batched operands and g5moe_grouped_gemm_padded's A operand (give
- * dgu_pad 256 rows of padding after row E*kmax for that); h_pad may be NULL
+ * gu : bf16 [N*k, 2F] packed;  h_pad, dgu_pad : bf16 [padded rows, F],
+ * [padded rows, 2F] out — rows placed per expert in the layout of kmax (0:
+ * packed), row start(e) + j = sorted position offsets[e] + j, zero rows for
+ * j >= M_e (kmax >= every M_e when > 0; an empty batch writes only zero rows):
+ * the weight gradients' operands and g5moe_grouped_gemm_padded's A operand (give
+ * dgu_pad 256 rows of padding after the padded rows for that); h_pad may be NULL
  * (not written: g5moe_weight_grad_sorted_h reads the forward's h);  dgu : bf16
  * [N*k + 256, 2F] packed out in sorted order, or NULL (not written).
  * dropout (NULL = none; the forward's descriptor): dh is the gradient of h',
@@ -407,13 +430,14 @@ g5moe_status g5moe_pad_transpose(const void* src, const int32_t* perm, const int
                                  void* out, int32_t cols, int32_t kmax,
                                  const g5moe_shape* shape, void* stream);
 
-/* Per-expert padded rows (no transpose): out[e][j][c] = column c of the row of
- * expert e's j-th sorted position, 0 for j >= M_e; the row of sorted position
- * p is src row p (perm == NULL: dY) or src row perm[p] / k (the gathered x
- * row).  These are g5moe_weight_grad's token-major operands.
- *   src : bf16 [rows, cols];  out : bf16 [E, kmax, cols];  cols multiple of 8,
- *   kmax >= 0; src and out 16-byte aligned.  shape->n_tokens 0 (an empty
- *   batch, every offset 0) allows src NULL: out is all zeros. */
+/* Per-expert padded rows (no transpose): out row start(e) + j = the row of
+ * expert e's j-th sorted position, 0 for j >= M_e, in the layout of kmax (> 0:
+ * [E, kmax, cols]; 0: packed, [N*k + 384*E, cols] of which the rows past the last
+ * expert's are not written); the row of sorted position p is src row p (perm
+ * == NULL: dY) or src row perm[p] / k (the gathered x row).  These are
+ * g5moe_weight_grad's token-major operands.  cols multiple of 8; src and out
+ * 16-byte aligned.  shape->n_tokens 0 (an empty batch, every offset 0) allows
+ * src NULL: out is all zeros. */
 g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t* offsets,
                             void* out, int32_t cols, int32_t kmax, const g5moe_shape* shape,
                             void* stream);
@@ -424,9 +448,10 @@ g5moe_status g5moe_pad_rows(const void* src, const int32_t* perm, const int32_t*
  * expert's count; g5moe_pad_rows and g5moe_swiglu_backward write them):
  *   d_w_down[e]    = dy_pad[e]^T  h_pad[e]  : bf16 [E, d, F]
  *   d_w_gate_up[e] = dgu_pad[e]^T x_pad[e]  : bf16 [E, 2F, d] (packed gate|up)
- *   dy_pad, x_pad : bf16 [E, kmax, d];  h_pad : bf16 [E, kmax, F];
- *   dgu_pad : bf16 [E, kmax, 2F] (g5moe_swiglu_backward's dgu_pad rows).
- * kmax a multiple of 192, >= 384 and >= every expert's row count; d and F
+ *   dy_pad, x_pad : bf16 [padded rows, d];  h_pad : bf16 [padded rows, F];
+ *   dgu_pad : bf16 [padded rows, 2F] (g5moe_swiglu_backward's dgu_pad rows),
+ *   all in the layout of kmax: 0 (packed) or a multiple of 192, >= 384 and >=
+ *   every expert's row count (expert e then reduces over min(R_e, kmax) rows); d and F
  * multiples of 256; all buffers 16-byte aligned.  A product whose output is
  * NULL is skipped.  fp32 accumulation over the expert's rows in a fixed order,
  * one bf16 rounding. */
@@ -437,6 +462,7 @@ g5moe_status g5moe_weight_grad(const void* dy_pad, const void* h_pad, void* d_w_
 
 /* g5moe_weight_grad with h in sorted order and the gate|up gradient unpacked:
  *   d_w_down[e] = dy_pad[e]^T h[offsets[e] .. ]      : bf16 [E, d, F]
+ *   (dy_pad[e]: expert e's padded rows in the layout of kmax)
  *   d_w_gate[e], d_w_up[e] = the gate and up rows of dgu_pad[e]^T x_pad[e]
  *                                                     : bf16 [E, F, d] each
  * h : bf16 [N*k + 384, F], the forward's h (g5moe_expert_gate_up_train's, in the

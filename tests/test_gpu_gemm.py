@@ -60,3 +60,41 @@ def test_grouped_gemm_pipeline_variants(cuda_device, K, n_out, counts):
         ref = a[o0:o1].float() @ b[e].float().T
         torch.testing.assert_close(c[o0:o1].float(), ref, rtol=2e-2, atol=2e-2)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("d,counts", [
+    (768, [569, 570, 0, 568, 1, 1200, 571, 569, 569, 570, 0, 569, 1139, 568, 568, 569]),
+    (256, [569, 0, 4000, 1, 255, 256, 257, 1700]),
+    (768, [4550, 4550]),                                   # the EP-8 shard: 2 experts
+])
+def test_small_m_down_two_per_cu_equals_grouped_gemm(cuda_device, d, counts):
+    """The down product at small M (a DP-8 / EP-8 shard's rows) runs 128 x 128 tiles
+    with two workgroups per CU (g5moe_expert_down), while g5moe_grouped_gemm takes
+    one 128 x 256 workgroup per CU there: each output's MFMA chain runs over k in
+    the same order whatever the tile shape, so y_perm must equal the grouped GEMM
+    on the same h and w_down bit for bit, with empty experts and partial tiles."""
+    import ctypes
+    from genet5_amd import _lib
+    F, k = 3072, 2
+    E = len(counts)
+    rows = int(sum(counts))
+    assert rows % k == 0
+    print(f"small-M down d={d} E={E} rows={rows}", flush=True)
+    g = torch.Generator(device=cuda_device).manual_seed(rows + d)
+    off, t_off = _offsets(counts, cuda_device)
+    shape = _lib.make_shape(rows // k, d, F, E, k, _lib.DTYPE_BF16)
+    ws = ops.workspace(shape, cuda_device)
+    h = ws[ops._h_offset(shape):].view(torch.bfloat16)[:(rows + ops.ROW_PAD) * F].view(-1, F)
+    h.copy_(torch.randn(rows + ops.ROW_PAD, F, device=cuda_device, generator=g)
+            .to(torch.bfloat16))
+    wd = (torch.randn(E, d, F, device=cuda_device, generator=g) / F ** 0.5).to(torch.bfloat16)
+    y_perm = torch.empty(rows, d, dtype=torch.bfloat16, device=cuda_device)
+    _lib.call("g5moe_expert_down", ops._ptr(t_off), ops._ptr(wd), ops._ptr(y_perm),
+              ops._ptr(ws), ctypes.byref(shape), ops._stream(cuda_device))
+    ref = ops.grouped_gemm(h[:rows + ops.ROW_PAD].contiguous(), rows, t_off, wd)
+    torch.cuda.synchronize()
+    assert torch.equal(y_perm, ref)
+    e = int(np.argmax(counts))
+    o0, o1 = int(off[e]), int(off[e + 1])
+    torch.testing.assert_close(y_perm[o0:o1].float(), h[o0:o1].float() @ wd[e].float().T,
+                               rtol=2e-2, atol=2e-2)
