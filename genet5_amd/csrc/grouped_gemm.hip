@@ -156,6 +156,11 @@ __device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& 
 #ifndef G5_B3
 #define G5_B3 1
 #endif
+// The SwiGLU epilogue of the inference gate|up: 16 values per scheduling group,
+// stage by stage (0: 4 values per group, one after the other).
+#ifndef G5_SILU_STAGED
+#define G5_SILU_STAGED 1
+#endif
 
 // First A row of expert e in the padded layouts (a_rows_per_expert != 0): e
 // times the per-expert row count, or, packed (-1), the sum of wgrad_rows(M_e')
@@ -324,9 +329,10 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   // (which use that region), into a VGPR; the stage waits cover them, and
   // they become byte offsets of token rows of x when the tile's first stage
   // is issued.  Positions past the expert's end repeat its last row.  Wave w
-  // reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile: slot j's rows
-  // (w * AI + j) * RPB + lrow.
-  static_assert(!GATHER || AI * RPB == 64, "one 64-row perm block per wave");
+  // reads rows [w * BM / 4, (w + 1) * BM / 4) of a tile (64 rows, or 48 in the
+  // 192-row tiles, whose lanes 48 .. 63 load a clamped row nobody reads): slot
+  // j's rows (w * AI + j) * RPB + lrow.
+  static_assert(!GATHER || AI * RPB <= 64, "one perm block of at most 64 rows per wave");
   char* epi = smem + S * STAGE + wave * EPI;
   // rows_fill: byte offsets of the gathered rows of the tile whose stages
   // the refills load (the current tile, then the next from its first stage).
@@ -353,7 +359,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
   uint32_t perm_v = 0;
   auto dma_rows = [&](const TileCoord& tc) {
     if constexpr (GATHER) {
-      const int p = min(tc.p_begin + wave * 64 + lane, tc.p_end - 1);
+      const int p = min(tc.p_begin + wave * (AI * RPB) + lane, tc.p_end - 1);
       if constexpr (B3)
         perm_v = uint32_t(__builtin_nontemporal_load(args.perm + p));
       else
@@ -773,8 +779,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
       constexpr int OB = NB;
       constexpr int RBY = OB * 64;
       constexpr int CR = RBY / 16;
-      constexpr int ROWS = EPI / RBY;
-      constexpr int JP = ROWS / 32;
+      constexpr int JP = MB % (EPI / RBY / 32) == 0 ? EPI / RBY / 32 : 1;
+      constexpr int ROWS = 32 * JP;
       constexpr int LPR = 256 / RBY;
       constexpr int NIT = ROWS * RBY / 1024;
       static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
@@ -870,8 +876,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = EPI / RBY;
-        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int JP = MB % (EPI / RBY / 32) == 0 ? EPI / RBY / 32 : 1;  // token blocks per pass
+        constexpr int ROWS = 32 * JP;
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
         const int col0 = cur.n0 + wn * WTN;
@@ -917,8 +923,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = SWIGLU ? NB / 2 : NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = EPI / RBY;
-        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int JP = MB % (EPI / RBY / 32) == 0 ? EPI / RBY / 32 : 1;  // token blocks per pass
+        constexpr int ROWS = 32 * JP;
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
         const int col0 = SWIGLU ? (cur.n0 + wn * WTN) / 2 : cur.n0 + wn * WTN;
@@ -974,8 +980,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = EPI / RBY;
-        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int JP = MB % (EPI / RBY / 32) == 0 ? EPI / RBY / 32 : 1;  // token blocks per pass
+        constexpr int ROWS = 32 * JP;
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
         const int col0 = cur.n0 + wn * WTN;
@@ -1021,8 +1027,8 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
         constexpr int OB = SWIGLU ? NB / 2 : NB;
         constexpr int RBY = OB * 64;
         constexpr int CR = RBY / 16;
-        constexpr int ROWS = EPI / RBY;
-        constexpr int JP = ROWS / 32;  // token blocks per pass
+        constexpr int JP = MB % (EPI / RBY / 32) == 0 ? EPI / RBY / 32 : 1;  // token blocks per pass
+        constexpr int ROWS = 32 * JP;
         constexpr int LPR = 256 / RBY; // rows per 256-byte bank line
         static_assert(JP >= 1 && MB % JP == 0, "epilogue pass shape");
         const int col0 = SWIGLU ? (cur.n0 + wn * WTN) / 2 : cur.n0 + wn * WTN;
@@ -1035,6 +1041,39 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
             const int swz = (row / LPR) % CR;
 #pragma unroll
             for (int ob = 0; ob < OB; ++ob) {
+              if constexpr (SWIGLU && G5_SILU_STAGED) {
+                // The 16 h values of a gate/up block pair stage by stage: every
+                // exp, then every reciprocal, then the products, so the
+                // scheduler has 16 independent chains between two barriers and
+                // one value's quarter-rate exp and rcp overlap the others'
+                // plain VALU work (one chain at a time left every
+                // transcendental's latency exposed).  Same operations and
+                // order per value as silu_mul.
+                float g[16], u[16], r[16];
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                  g[i] = acc[2 * ob][j][i];
+                  u[i] = acc[2 * ob + 1][j][i];
+                }
+#pragma unroll
+                for (int i = 0; i < 16; ++i) r[i] = __expf(-g[i]);
+#pragma unroll
+                for (int i = 0; i < 16; ++i) r[i] = __builtin_amdgcn_rcpf(1.0f + r[i]);
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                  float h[4];
+#pragma unroll
+                  for (int uu = 0; uu < 4; ++uu)
+                    h[uu] = g[4 * q + uu] * r[4 * q + uu] * u[4 * q + uu];
+                  uint2 o;
+                  o.x = pack_bf16x2(h[0], h[1]);
+                  o.y = pack_bf16x2(h[2], h[3]);
+                  const int c = ob * 4 + q;
+                  *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
+                }
+                // keep only one block pair's accumulators in VGPRs at a time
+                __builtin_amdgcn_sched_barrier(0);
+              } else {
 #pragma unroll
               for (int q = 0; q < 4; ++q) {
                 float h[4];
@@ -1052,6 +1091,7 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
                 *reinterpret_cast<uint2*>(epi + row * RBY + ((c ^ swz) * 16) + half * 8) = o;
                 // keep only one group's accumulators in VGPRs at a time
                 __builtin_amdgcn_sched_barrier(0);
+              }
               }
             }
           }
@@ -1328,6 +1368,30 @@ void launch_persist(unsigned grid, const GemmArgs& a, hipStream_t st) {
         dim3(grid), dim3(256), 0, st, a);
 }
 
+// Token rows per m-tile of the gate|up GEMMs: 192 when, at the launch's mean
+// rows per expert, 192-row tiles pad to at least 10 % fewer rows than 256-row
+// ones (a shard's share of the tokens: 569 rows per expert fill three tiles
+// either way, 576 rows against 768, so a quarter less MFMA work), else 256 (the
+// 256-row tile moves 3/4 of the 192-row tile's operand bytes per flop).  Only
+// K with a k-step count that is a multiple of 3 (three fragment slots) has the
+// 192-row kernels.
+inline int gate_up_bm(int64_t nk, int n_experts, int K) {
+  const int nks = K / G5_GU_BK;
+  if (nks % 3 != 0 || nks < 6) return 256;
+  const int64_t m = (nk + n_experts - 1) / n_experts;
+  const int64_t r256 = (m + 255) / 256 * 256, r192 = (m + 191) / 192 * 192;
+  return r192 * 10 <= r256 * 9 ? 192 : 256;
+}
+
+// The 192-row gate|up launch (three fragment slots only).
+template <int MODE, bool DROP = false>
+void launch_gate_up192(unsigned grid, const GemmArgs& a, hipStream_t st) {
+  hipLaunchKernelGGL(
+      (grouped_gemm_persist_kernel<192, 256, G5_GU_BK, G5_GU_STAGES, 3, G5_GU_GM, MODE, false,
+                                   DROP>),
+      dim3(grid), dim3(256), 0, st, a);
+}
+
 }  // namespace
 
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
@@ -1348,8 +1412,11 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   a.Nout = 2 * s.d_ff;
   a.ldc = s.d_ff;
   a.ldc2 = 2 * s.d_ff;
-  const unsigned grid = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
+  // 192-row tiles for the inference gate|up at small mean expert counts
+  const bool bm192 = gu == nullptr && gate_up_bm(nk, s.n_experts, a.K) == 192;
+  const unsigned grid = bm192 ? grid_bound<192, 256>(nk, s.n_experts, a.Nout)
+                              : grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
   hipError_t cerr;
   a.claims = claims_for(claims, grid, pgrid, st, &cerr);
@@ -1366,6 +1433,8 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false, true>(pgrid, a, st);
   else if (gu != nullptr)  // h and the raw gate|up outputs (training forward)
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false>(pgrid, a, st);
+  else if (bm192)
+    launch_gate_up192<1>(pgrid, a, st);
   else
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);
   return hipGetLastError();
@@ -1390,7 +1459,9 @@ hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int3
   a.ldc = s.d_ff;
   a.ldc2 = 2 * s.d_ff;
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
-  const unsigned tiles = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
+  const bool bm192 = gate_up_bm(nk, s.n_experts, a.K) == 192;
+  const unsigned tiles = bm192 ? grid_bound<192, 256>(nk, s.n_experts, a.Nout)
+                               : grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned grid = std::min(tiles, unsigned(device_cu_count()));
   hipError_t cerr;
   a.claims = claims_for(claims, tiles, grid, st, &cerr);
@@ -1400,7 +1471,12 @@ hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int3
     a.drop_seed_hi = drop.seed_hi;
     a.drop_thr = drop.thr;
     a.drop_scale = drop.scale;
-    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 5, false, true>(grid, a, st);
+    if (bm192)
+      launch_gate_up192<5, true>(grid, a, st);
+    else
+      launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 5, false, true>(grid, a, st);
+  } else if (bm192) {
+    launch_gate_up192<5>(grid, a, st);
   } else {
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 5, false>(grid, a, st);
   }

@@ -263,3 +263,20 @@ def test_forward_empty(cuda_device):
     assert y.shape == (0, 128)
     assert host(r.counts).tolist() == [0, 0, 0, 0]
     assert host(r.offsets).tolist() == [0, 0, 0, 0, 0]
+
+
+@pytest.mark.parametrize("n_small,n_big", [(4550, 36400), (512, 9000), (2048, 6000)])
+def test_token_output_independent_of_batch(cuda_device, n_small, n_big):
+    """A token's layer output does not depend on the other tokens of its batch: the
+    first n_small tokens run alone and inside a batch of n_big give the same y bit
+    for bit.  The two launches tile differently (a shard-sized batch takes 192-row
+    gate|up tiles and the small-M down tiles, the large one 256 x 256 tiles, the
+    claimed tail and the n-half tail), and every output element's MFMA chain runs
+    over k in one fixed order whatever tile computes it."""
+    print(f"batch invariance n_small={n_small} n_big={n_big}", flush=True)
+    inp = synth.make_layer(n_big, seed=9, dtype="bf16")
+    x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
+    y_big = ops.moe_forward(x, wr, wgu, wd, 2).clone()
+    y_small = ops.moe_forward(x[:n_small].contiguous(), wr, wgu, wd, 2)
+    torch.cuda.synchronize()
+    assert torch.equal(y_small.view(torch.int16), y_big[:n_small].view(torch.int16))
