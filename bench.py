@@ -701,7 +701,7 @@ def main():
             "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
         },
         "roofline": {
-            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,1,false,false> (gate|up + SwiGLU)",
+            "kernel": "grouped_gemm_persist_kernel<256,256,64,2,3,4,1,false,false,false> (gate|up + SwiGLU)",
             "bound": "mfma",
             "achieved": gu_tflops,
             "peak": PEAK_BF16_TFLOPS,

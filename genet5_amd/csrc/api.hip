@@ -214,8 +214,7 @@ g5moe_status g5moe_expert_gate_up(const void* x, const int32_t* perm, const int3
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up (cast)"));
   const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                                   reinterpret_cast<uint16_t*>(w + L.h), nullptr,
-                                   reinterpret_cast<int*>(w + L.claims), *shape, st),
+                                   reinterpret_cast<uint16_t*>(w + L.h), nullptr, *shape, st),
                     "g5moe_expert_gate_up");
 }
 
@@ -247,8 +246,7 @@ g5moe_status g5moe_expert_gate_up_train(const void* x, const int32_t* perm,
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train (cast)"));
   return hip_status(launch_gate_up(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
                                    reinterpret_cast<uint16_t*>(w + L.h),
-                                   static_cast<uint16_t*>(gu),
-                                   reinterpret_cast<int*>(w + L.claims), *shape, st, &drop),
+                                   static_cast<uint16_t*>(gu), *shape, st, &drop),
                     "g5moe_expert_gate_up_train");
 }
 
@@ -278,8 +276,8 @@ g5moe_status g5moe_expert_gate_up_train_factors(const void* x, const int32_t* pe
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_train_factors (cast)"));
   return hip_status(
       launch_gate_up_ab(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                        reinterpret_cast<uint16_t*>(w + L.h), static_cast<uint16_t*>(ab),
-                        reinterpret_cast<int*>(w + L.claims), *shape, st, drop),
+                        reinterpret_cast<uint16_t*>(w + L.h), static_cast<uint16_t*>(ab), *shape,
+                        st, drop),
       "g5moe_expert_gate_up_train_factors");
 }
 
@@ -544,11 +542,8 @@ g5moe_status g5moe_expert_gate_up_raw(const void* x, const int32_t* perm, const 
   hipError_t err;
   const uint16_t* xb = gemm_input(x, static_cast<char*>(ws), *shape, st, &err);
   G5_CHECK(hip_status(err, "g5moe_expert_gate_up_raw (cast)"));
-  const WorkspaceLayout L = workspace_layout(*shape);
   return hip_status(launch_gate_up_raw(xb, perm, offsets, static_cast<const uint16_t*>(w_gate_up),
-                                       static_cast<uint16_t*>(gu),
-                                       reinterpret_cast<int*>(static_cast<char*>(ws) + L.claims),
-                                       *shape, st),
+                                       static_cast<uint16_t*>(gu), *shape, st),
                     "g5moe_expert_gate_up_raw");
 }
 

@@ -35,7 +35,6 @@ struct WorkspaceLayout {
   size_t rank;       // stable rank inside the block        [N*k]
   size_t h;          // SwiGLU activations, bf16            [N*k, F]
   size_t y_perm;     // expert outputs, bf16                [N*k, d]
-  size_t claims;     // the gate|up GEMM's tail-claim counters {claim, done} (256 B)
   size_t total;
   int64_t nblk;      // dispatch blocks
 };
@@ -61,8 +60,6 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   off += align256(size_t(nk + kHPadRows) * s.d_ff * 2);
   w.y_perm = off;
   off += align256(size_t(nk) * s.d_model * 2);
-  w.claims = off;
-  off += 256;
   w.total = off;
   return w;
 }
@@ -117,17 +114,13 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
 hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t* offsets,
                                    int32_t* perm, int32_t* inv_pos, const g5moe_shape& s,
                                    hipStream_t st);
-// The gate|up launchers take `claims`, the workspace's counter pair of the
-// claimed tail: they zero it with a fill kernel on `st` before a launch that
-// claims, and the launch's last workgroup leaves it at zero.
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, int* claims,
-                          const g5moe_shape& s, hipStream_t st,
-                          const DropoutParams* drop = nullptr);
+                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
+                          hipStream_t st, const DropoutParams* drop = nullptr);
 // Training gate|up for the fused SwiGLU backward: h (with dropout) into h, and the
 // derivative factors A = dh/dg, B = dh/du (dropout folded in) into ab [N*k, 2F].
 hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                             const uint16_t* wgu, uint16_t* h, uint16_t* ab, int* claims,
+                             const uint16_t* wgu, uint16_t* h, uint16_t* ab,
                              const g5moe_shape& s, hipStream_t st, const DropoutParams& drop);
 // dGU_pad (per-expert padded, wgrad_rows rows per expert) = (dY_pad Wd_e) * (A | B).
 hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* offsets,
@@ -136,8 +129,8 @@ hipError_t launch_dh_swiglu(const uint16_t* dy_pad, int kmax, const int32_t* off
 hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t* wd,
                        uint16_t* y_perm, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                              const uint16_t* wgu, uint16_t* gu, int* claims,
-                              const g5moe_shape& s, hipStream_t st);
+                              const uint16_t* wgu, uint16_t* gu, const g5moe_shape& s,
+                              hipStream_t st);
 hipError_t launch_grouped_nt(const uint16_t* A, const int32_t* offsets, const uint16_t* B,
                              uint16_t* C, int64_t rows, int n_experts, int K, int Nout,
                              int a_rows_per_expert, hipStream_t st);

@@ -76,8 +76,6 @@ struct GemmArgs {
   float drop_scale;
   const uint16_t* aux;    // MODE 4: the forward's SwiGLU derivative factors [N*k, 2 Nout]
                           // (packed gate|up order, sorted positions), read in the epilogue
-  int* claims;            // nullptr, or this launch's {claim, done} counters (zero at
-                          // launch; the last workgroup resets them): the claimed tail
 };
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
@@ -1185,41 +1183,14 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
           Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
     }
   } else {
-    // Static: the remainder tile of slots s < r is lo + s + q * nslot.  Claimed
-    // tail (with claim counters and at least 8 tiles per workgroup): every
-    // workgroup first runs Q = total / ng - 1 tiles of its XCD's contiguous range
-    // (slot-strided as above), and the remaining total - Q ng tiles (between ng
-    // and 2 ng of them) are claimed one at a time from a counter, so that XCDs
-    // that run faster take more of them.  A claim happens between tiles, outside
-    // the k-step stream: thread 0 takes the next index and passes it through LDS
-    // (every stage buffer is idle then).  With a few tiles per workgroup the
-    // claimed tiles' pipeline restarts cost more than the balance gains (3-7 %
-    // slower at 3-5 tiles per CU).
-    const bool claimed = args.claims != nullptr && total >= 8 * ng;
-    const int Qs = max(0, total / ng - 1);
-    Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
-    if (claimed) st = Units{Qs * before + slot, nslot, Qs, 0};
+    // Static: the remainder tile of slots s < r is lo + s + q * nslot.  (A
+    // claimed tail, the last tiles taken one at a time from an atomic counter so
+    // that faster XCDs take more, measured no faster at 36,400 tokens than this
+    // static split once its counters had to be zeroed per launch: gate|up
+    // 623.9 against 625.4 us, four alternating runs on one GPU.)
+    const Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
     if (st.count > 0)
       tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP, PADA>(args, off, smem, st);
-    if (claimed) {
-      const int pool = total - Qs * ng;
-      int* const mbox = reinterpret_cast<int*>(smem);
-      for (;;) {
-        __syncthreads();  // every wave is past the previous tile (its DMAs landed)
-        if (threadIdx.x == 0) mbox[0] = atomicAdd(args.claims, 1);
-        __syncthreads();
-        const int u = __builtin_amdgcn_readfirstlane(mbox[0]);
-        __syncthreads();  // every wave has read the index before the stages refill
-        if (u >= pool) break;
-        tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP, PADA>(
-            args, off, smem, Units{Qs * ng + u, 1, 1, 0});
-      }
-      // the last workgroup out resets the counters for the slot's next launch
-      if (threadIdx.x == 0 && atomicAdd(args.claims + 1, 1) == ng - 1) {
-        atomicExch(args.claims, 0);
-        atomicExch(args.claims + 1, 0);
-      }
-    }
   }
 }
 
@@ -1266,19 +1237,6 @@ namespace {
 template <int BM, int BN>
 unsigned grid_bound(int64_t nk, int n_experts, int nout) {
   return unsigned(((nk + BM - 1) / BM + n_experts) * (nout / BN));
-}
-
-// The claimed tail's counters for a 256 x 256 gate|up launch of `tiles` tiles at
-// most on `grid` workgroups: the caller's pair, zeroed by a fill kernel on the
-// launch's stream (no memset node under graph capture), or nullptr when the
-// launch cannot claim (fewer than 8 tiles per workgroup) and keeps the static
-// schedule.  Launches that overlap on other streams use other workspaces, hence
-// other counters.
-int* claims_for(int* claims, unsigned tiles, unsigned grid, hipStream_t st, hipError_t* err) {
-  *err = hipSuccess;
-  if (claims == nullptr || tiles < 8u * grid) return nullptr;
-  *err = launch_zero16(claims, 1, st);
-  return claims;
 }
 
 // Packed gate|up from separate gate and up: row 64g + r <- gate[32g + r] (r < 32)
@@ -1395,8 +1353,8 @@ void launch_gate_up192(unsigned grid, const GemmArgs& a, hipStream_t st) {
 }  // namespace
 
 hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, int* claims,
-                          const g5moe_shape& s, hipStream_t st, const DropoutParams* drop) {
+                          const uint16_t* wgu, uint16_t* h, uint16_t* gu, const g5moe_shape& s,
+                          hipStream_t st, const DropoutParams* drop) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
   GemmArgs a{};
@@ -1418,9 +1376,6 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
   const unsigned grid = bm192 ? grid_bound<192, 256>(nk, s.n_experts, a.Nout)
                               : grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
-  hipError_t cerr;
-  a.claims = claims_for(claims, grid, pgrid, st, &cerr);
-  if (cerr != hipSuccess) return cerr;
   const bool dropout = drop != nullptr && drop->on;
   if (dropout) {
     if (gu == nullptr) return hipErrorInvalidValue;  // dropout is a training-forward mode
@@ -1441,7 +1396,7 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
 }
 
 hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                             const uint16_t* wgu, uint16_t* h, uint16_t* ab, int* claims,
+                             const uint16_t* wgu, uint16_t* h, uint16_t* ab,
                              const g5moe_shape& s, hipStream_t st, const DropoutParams& drop) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
@@ -1463,9 +1418,6 @@ hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int3
   const unsigned tiles = bm192 ? grid_bound<192, 256>(nk, s.n_experts, a.Nout)
                                : grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned grid = std::min(tiles, unsigned(device_cu_count()));
-  hipError_t cerr;
-  a.claims = claims_for(claims, tiles, grid, st, &cerr);
-  if (cerr != hipSuccess) return cerr;
   if (drop.on) {
     a.drop_seed_lo = drop.seed_lo;
     a.drop_seed_hi = drop.seed_hi;
@@ -1555,8 +1507,8 @@ hipError_t launch_down(const uint16_t* h, const int32_t* offsets, const uint16_t
 }
 
 hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int32_t* offsets,
-                              const uint16_t* wgu, uint16_t* gu, int* claims,
-                              const g5moe_shape& s, hipStream_t st) {
+                              const uint16_t* wgu, uint16_t* gu, const g5moe_shape& s,
+                              hipStream_t st) {
   const int64_t nk = s.n_tokens * s.top_k;
   if (nk == 0) return hipSuccess;
   GemmArgs a{};
@@ -1573,9 +1525,6 @@ hipError_t launch_gate_up_raw(const uint16_t* xb, const int32_t* perm, const int
   if (a.K < G5_GU_STAGES * G5_GU_BK) return hipErrorInvalidValue;
   const unsigned tiles = grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned grid = std::min(tiles, unsigned(device_cu_count()));
-  hipError_t cerr;
-  a.claims = claims_for(claims, tiles, grid, st, &cerr);
-  if (cerr != hipSuccess) return cerr;
   launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 2, false>(grid, a, st);
   return hipGetLastError();
 }

@@ -21,9 +21,8 @@
  *     exception crosses the ABI.
  *   - Results are deterministic: the same inputs give bitwise-identical outputs.
  *   - Calls on different streams may overlap when each has its own workspace
- *     and outputs (the gate|up GEMMs keep their tail-claim counters in the
- *     workspace, zeroed on the call's stream before each launch, so a launch
- *     captured in a HIP graph and replayed shares them with nothing else).
+ *     and outputs: no entry point keeps state between launches, so a launch
+ *     captured in a HIP graph and replayed shares nothing with eager ones.
  *     g5moe_dispatch_noalloc's scratch is one array per GPU (see there).
  *   - Tensors are row-major.  bf16 values are raw IEEE bfloat16 bit patterns
  *     (uint16); weights use nn.Linear orientation [out, in].
@@ -75,9 +74,9 @@ const char* g5moe_last_error(void);
 
 /* ABI version: (major << 16) | minor.  2.0: g5moe_expert_gate_up_train and
  * g5moe_swiglu_backward take the g5moe_dropout descriptor (and the latter perm),
- * the workspace ends with 256 bytes of GEMM tail-claim counters, and kmax = 0
- * selects the packed padded layout (see "Padded row layouts") wherever the
- * backward takes kmax. */
+ * and kmax = 0 selects the packed padded layout (see "Padded row layouts")
+ * wherever the backward takes kmax (with no tokens, the padded outputs are still
+ * written as zeros). */
 int32_t g5moe_version(void);
 
 /* Bytes of workspace the stage entry points and g5moe_forward need for `shape`.

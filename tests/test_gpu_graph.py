@@ -1,5 +1,5 @@
 """The layer forward under HIP graph capture: g5moe_forward (router, dispatch, the
-grouped GEMMs with the gate|up launch's claimed tail, combine) allocates nothing,
+grouped GEMMs, combine) allocates nothing,
 synchronises nothing and records no memset nodes, so a serving loop can capture
 it once and replay it.  Each replay, with the program's own eager work and a
 synchronisation between replays, must give the eager result bit for bit; the

@@ -3,8 +3,7 @@ outputs (the ABI's contract for overlapping calls): both results must equal the
 same forwards run one after the other, bit for bit.  The two layers differ in
 shape (so one stream's launches are not a replay of the other's) and each stream
 runs several forwards back to back, so the gate|up launches of the two streams
-are in flight together, each claiming its tail through the counters in its own
-workspace.  The same holds for a forward captured in a HIP graph and replayed on
+are in flight together.  The same holds for a forward captured in a HIP graph and replayed on
 one stream while eager forwards with another workspace run on a second."""
 import pytest
 import torch
@@ -49,9 +48,9 @@ def test_two_streams_equal_serial(cuda_device):
 
 
 def test_graph_replay_beside_eager_stream(cuda_device):
-    """A captured forward (its claim counters in the capture's workspace, zeroed by a
-    fill kernel recorded in the graph) replayed on stream A while eager forwards with
-    their own workspace run on stream B: every output equals the serial result."""
+    """A captured forward (its workspace the capture's own) replayed on stream A while
+    eager forwards with their own workspace run on stream B: every output equals the
+    serial result."""
     print("graph replay beside an eager stream", flush=True)
     a = synth.make_layer(20000, d_model=768, d_ff=3072, n_experts=16, top_k=2, seed=7,
                          dtype="bf16")
