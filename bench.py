@@ -48,6 +48,12 @@ def parse():
                          "with all 16 experts (about 569 rows per expert), ep8 = the 2 experts "
                          "one GPU owns with their 4,550 rows each (4,550 tokens routed top-2 of "
                          "2); the layer's kernels at those shapes, no exchange")
+    ap.add_argument("--settle-ms", type=float, default=200.0,
+                    help="untimed calls of the step for this many milliseconds of wall time "
+                         "before the warm-up steps (0: none): after an idle spell the "
+                         "board's power controller lets the clock overshoot, then holds it "
+                         "low for about 20 ms before it settles, and the timed steps should "
+                         "see the steady state a continuously running layer sees")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the benchmark, run a 256 MiB elementwise copy (read 256 MiB, "
                          "write 256 MiB) whose FETCH_SIZE / WRITE_SIZE counters scale the "
@@ -190,8 +196,31 @@ def torch_eager_gpu_train(x, wr, w_gate, w_up, w_down, k, dy, dropout, steps=5,
                     f"{warmup} warm-up"}
 
 
-def timed(fn, steps: int, warmup: int) -> float:
+SETTLE_WHY = ("untimed calls of the step before the warm-up steps: after an idle spell the "
+              "board's power controller first lets the shader clock run high, then holds it "
+              "low for about 20 ms before it settles (gate|up 604 -> 874 -> 607 us per call "
+              "over the first 25 ms in profiles/moe_layer_cfg2_kernel_stats.md), so without "
+              "them a short timed region measures that transient instead of the steady state")
+
+
+def settle(fn, ms: float) -> dict:
+    """Call fn (untimed) for `ms` milliseconds of wall time, in groups of four calls
+    with a device synchronisation after each group; returns the settle record of the
+    JSON line."""
     import torch
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(4):
+            fn()
+        n += 4
+        torch.cuda.synchronize()
+    return {"ms": round((time.perf_counter() - t0) * 1e3, 1), "calls": n, "why": SETTLE_WHY}
+
+
+def timed(fn, steps: int, warmup: int, settle_ms: float = 0.0) -> float:
+    import torch
+    settle(fn, settle_ms)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -213,10 +242,10 @@ def bench_config4(args) -> dict:
     x = torch.from_numpy(cfg.x).view(torch.bfloat16).to(dev)
     N = x.shape[1]
     with torch.no_grad():
-        t = timed(lambda: stack(x), args.steps, args.warmup)
+        t = timed(lambda: stack(x), args.steps, args.warmup, args.settle_ms)
         # the same stack as the torch composition RMSNorm -> MoE -> residual add
         stack.set_fused(False)
-        t_unfused = timed(lambda: stack(x), args.steps, args.warmup)
+        t_unfused = timed(lambda: stack(x), args.steps, args.warmup, args.settle_ms)
         stack.set_fused(True)
     flops = 12 * 6 * 768 * 3072 * N * 2
     # the two fused memory-bound entry points on this batch (HIP events, 20 calls each)
@@ -259,7 +288,8 @@ def bench_config4(args) -> dict:
     return {
         "metric": "12-block RMSNorm->MoE->residual stack tokens/s, 45.5k packed tok, 16e top-2",
         "value": N / t, "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": t * 1e3, "higher_is_better": True,
+        "warmup": args.warmup, "settle": {"ms_per_loop": args.settle_ms, "why": SETTLE_WHY},
+        "ms_per_step": t * 1e3, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": "cfg4: 12 x (RMSNorm, MoE, residual), 45,500 tokens packed from "
                                "lengths U[1000, 9000], seeded N(0, 0.02) weights per layer",
@@ -422,6 +452,7 @@ def train_stage_breakdown(args) -> dict:
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]
+    settled = settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -481,6 +512,7 @@ def bench_train(args) -> dict:
         y.backward(dy)
 
     def run(steps, warmup, update):
+        settle(lambda: step(update), args.settle_ms)
         for _ in range(warmup):
             step(update)
         torch.cuda.synchronize()
@@ -503,7 +535,8 @@ def bench_train(args) -> dict:
     return {
         "metric": "MoE layer training step (forward + backward) tokens/s, 36.4k tok, 16e top-2",
         "value": N / (ms * 1e-3), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "settle": {"ms_per_loop": args.settle_ms, "why": SETTLE_WHY},
+        "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": synth.CONFIGS[args.config]["name"] + ", training step "
                                "(MoEFeedForward forward + autograd backward)",
@@ -514,9 +547,9 @@ def bench_train(args) -> dict:
         "step_expert_gemm_tflops": (9 * g) / (ms * 1e-3) / 1e12,
         "breakdown": bd,
         "torch_eager_gpu": eager,
-        "note": "every stage is this library's HIP kernels; the backward reads the expert "
-                "offsets from the forward's pinned host copy (no host synchronisation); "
-                "weight-gradient products in one g5moe_weight_grad launch over per-expert "
+        "note": "every stage is this library's HIP kernels; the backward's padded operands "
+                "use the packed per-expert layout sized from N k + 384 E rows, so nothing "
+                "is read back to the host (no host synchronisation); weight-gradient products in one g5moe_weight_grad launch over per-expert "
                 "operands padded to 192-row groups (their zero rows' products count in the "
                 "time, not in the FLOP)",
     }
@@ -595,6 +628,7 @@ def main():
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]
+    settled = settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -643,6 +677,7 @@ def main():
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             ops.moe_forward(x, wr, wgu, wd, k, bias=bias, buffers=buf)
+        settle(graph.replay, args.settle_ms)
         for _ in range(args.warmup):
             graph.replay()
         g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -677,6 +712,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": settled,
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
