@@ -154,6 +154,13 @@ __device__ __forceinline__ int expert_rows(const GemmArgs& args, const Offsets& 
 #ifndef G5_B3
 #define G5_B3 1
 #endif
+// MFMA issue order over a wave's 4 x 4 accumulator blocks within a 16-k substep:
+// 1 walks the rows as a snake (odd rows backwards), so consecutive MFMAs change
+// one operand; 0 walks them row-major.  The order within a substep does not
+// change any output bit (each accumulator still takes its k steps in order).
+#ifndef G5_SNAKE
+#define G5_SNAKE 1
+#endif
 // The SwiGLU epilogue of the inference gate|up: 16 values per scheduling group,
 // stage by stage (0: 4 values per group, one after the other).
 #ifndef G5_SILU_STAGED
@@ -598,7 +605,11 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
       }
 #pragma unroll
       for (int t = 0; t < MB * NB; ++t) {
+#if G5_SNAKE
+        const int i = t / MB, j = (i & 1) ? MB - 1 - t % MB : t % MB;
+#else
         const int i = t / MB, j = t % MB;
+#endif
         const int sl = slot(ks);
         if (FIRST && ks == 0)
           acc[i][j] =
