@@ -46,7 +46,9 @@ class _ExpertWeightCache:
     otherwise.  So forwards and backwards between two optimizer steps (gradient
     accumulation) share one copy, eager or compiled: torch.compile hands the
     custom ops the parameter objects themselves.  An entry is dropped when one of
-    its parameters is freed.  `builds` counts the rebuilds."""
+    its parameters is freed, and when the same parameter objects get a new entry
+    (their storage was replaced, e.g. `p.data = ...` by a checkpoint loader).
+    `builds` counts the rebuilds."""
 
     def __init__(self, max_entries: int = 64):
         self._entries: "OrderedDict[tuple, tuple]" = OrderedDict()
@@ -81,6 +83,10 @@ class _ExpertWeightCache:
                     self._entries[key] = (refs, st, wgu, ent[3], tr)
                 self._entries.move_to_end(key)
                 return (wgu, wd) + tr if transposed else (wgu, wd)
+        # the same parameter objects under an older storage address: that copy is stale
+        for k2 in [k2 for k2, e2 in self._entries.items()
+                   if k2 != key and all(r() is w for r, w in zip(e2[0], ws))]:
+            del self._entries[k2]
         with torch.no_grad():
             wg = w_gate.detach().to(torch.bfloat16).contiguous()
             wu = w_up.detach().to(torch.bfloat16).contiguous()
