@@ -35,7 +35,7 @@ FLAGS = [
     f"-I{INCLUDE_DIR}",
 ]
 SOURCES = ["api.hip", "router.hip", "dispatch.hip", "grouped_gemm.hip", "combine.hip",
-           "backward.hip", "attention.hip", "wgrad.hip"]
+           "backward.hip", "attention.hip", "wgrad.hip", "xcd_balance.hip"]
 
 
 def _compile(src: Path, obj: Path, verbose: bool) -> None:

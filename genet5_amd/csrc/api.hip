@@ -104,7 +104,7 @@ extern "C" {
 
 const char* g5moe_last_error(void) { return g_err; }
 
-int32_t g5moe_version(void) { return (2 << 16) | 0; }
+int32_t g5moe_version(void) { return (2 << 16) | 1; }
 
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes) {
   G5_CHECK(check_shape(shape));

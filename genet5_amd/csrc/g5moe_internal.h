@@ -210,6 +210,21 @@ __host__ __device__ __forceinline__ int64_t packed_rows_bound(int64_t nk, int n_
 // CUs of the current device (the persistent kernels' grid size).
 int device_cu_count();
 
+// Per-XCD tile shares of a persistent GEMM launch of 8 x 32 workgroups
+// (xcd_balance.hip).  w[8] == 0: equal ranges, no records.  Otherwise XCD x
+// takes tiles [total w[x] / w[8], total w[x + 1] / w[8]) of the launch's list,
+// and workgroup b writes (seq << 32) | its busy time (100 MHz ticks) to
+// probe[b] when it ends.
+struct XcdSplit {
+  int w[9];
+  unsigned long long* probe;
+  uint32_t seq;
+};
+// The split of the next launch of GEMM `site` (a launcher-chosen id for the mode
+// and tile shape) with this grid, K and Nout on the current device, from the
+// XCD rates the site's earlier launches recorded.
+XcdSplit xcd_split(int site, unsigned grid, int K, int nout, hipStream_t st);
+
 // First padded row of expert l = lane in the layout of kmax (lanes 0 .. E; lane
 // E holds the total), from ol = offsets[lane] in lanes 0 .. E.  Every lane of
 // the wave must call it (cross-lane shuffles).

@@ -76,6 +76,7 @@ struct GemmArgs {
   float drop_scale;
   const uint16_t* aux;    // MODE 4: the forward's SwiGLU derivative factors [N*k, 2 Nout]
                           // (packed gate|up order, sorted positions), read in the epilogue
+  XcdSplit xs;            // per-XCD tile shares (xs.w[8] == 0: equal)
 };
 
 // silu(g) * u with the hardware exp and reciprocal (about 1 ulp each, far
@@ -1178,8 +1179,14 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
   int before = 0;
   for (int y = 0; y < xcd; ++y) before += (ng - y + 7) >> 3;
   const int nslot = (ng - xcd + 7) >> 3;
-  const int lo = int(int64_t(total) * before / ng);
-  const int hi = int(int64_t(total) * (before + nslot) / ng);
+  // XCD x's contiguous range: equal per slot, or the launcher's measured shares
+  // (monotone cumulative weights with w[8] their sum, so the ranges partition
+  // [0, total) whatever the weights)
+  const bool wtd = args.xs.w[8] > 0;
+  const int lo = wtd ? int(int64_t(total) * args.xs.w[xcd] / args.xs.w[8])
+                     : int(int64_t(total) * before / ng);
+  const int hi = wtd ? int(int64_t(total) * args.xs.w[xcd + 1] / args.xs.w[8])
+                     : int(int64_t(total) * (before + nslot) / ng);
   const int q = (hi - lo) / nslot, r = (hi - lo) % nslot;
   if constexpr (HALF_TAIL) {
     if (q > 0)
@@ -1210,7 +1217,16 @@ template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_
           bool DROP = false, bool PADA = false>
 __global__ __launch_bounds__(256) void grouped_gemm_persist_kernel(GemmArgs args) {
   __shared__ __attribute__((aligned(1024))) char smem[persist_smem_bytes<BM, BN, BK, S>()];
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   persist_body<BM, BN, BK, S, NSLOT, GM, MODE, HALF_TAIL, DROP, PADA>(args, smem);
+  if (args.xs.probe != nullptr) {
+    // the workgroup's busy time, for the launcher's next per-XCD split
+    __syncthreads();
+    if (threadIdx.x == 0) {
+      const uint64_t t1 = __builtin_amdgcn_s_memrealtime();
+      args.xs.probe[blockIdx.x] = (uint64_t(args.xs.seq) << 32) | uint32_t(t1 - t0);
+    }
+  }
 }
 
 // Two workgroups per CU (two waves per SIMD, 256 registers per lane, at most 80
@@ -1388,6 +1404,7 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
                               : grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned pgrid = std::min<unsigned>(grid, unsigned(device_cu_count()));
   const bool dropout = drop != nullptr && drop->on;
+  a.xs = xcd_split(gu != nullptr ? (dropout ? 3 : 2) : (bm192 ? 1 : 0), pgrid, a.K, a.Nout, st);
   if (dropout) {
     if (gu == nullptr) return hipErrorInvalidValue;  // dropout is a training-forward mode
     a.drop_seed_lo = drop->seed_lo;
@@ -1429,6 +1446,7 @@ hipError_t launch_gate_up_ab(const uint16_t* xb, const int32_t* perm, const int3
   const unsigned tiles = bm192 ? grid_bound<192, 256>(nk, s.n_experts, a.Nout)
                                : grid_bound<256, 256>(nk, s.n_experts, a.Nout);
   const unsigned grid = std::min(tiles, unsigned(device_cu_count()));
+  a.xs = xcd_split(4 + (drop.on ? 2 : 0) + (bm192 ? 1 : 0), grid, a.K, a.Nout, st);
   if (drop.on) {
     a.drop_seed_lo = drop.seed_lo;
     a.drop_seed_hi = drop.seed_hi;

@@ -11,9 +11,15 @@
  * (genet5_amd/moe.py, class MoEFeedForward) binds these through ctypes.
  *
  * Conventions (all entry points):
- *   - Every buffer is device memory owned by the caller; the library allocates
- *     nothing.  `ws` is a caller-provided workspace of g5moe_workspace_size()
- *     bytes, 256-byte aligned.
+ *   - Every buffer is device memory owned by the caller.  `ws` is a
+ *     caller-provided workspace of g5moe_workspace_size() bytes, 256-byte
+ *     aligned.  The library's only own memory: the gate|up GEMM launches of 8 x
+ *     32 workgroups keep, per device and launch shape, a 2 KB pinned host buffer
+ *     into which each workgroup writes its busy time.  It is allocated by the
+ *     first such launch outside HIP graph capture and kept for the process (a
+ *     shape first launched under capture runs without it), and it is read by
+ *     the host to share the next launch's tiles among the XCDs by their
+ *     measured speed.  That share never changes an output bit.
  *   - Work is enqueued on `stream` (a hipStream_t passed as void*; NULL = the
  *     null stream) and runs asynchronously; no entry point synchronises the host.
  *   - Return value 0 (G5MOE_OK) on success; otherwise a status code and a
@@ -21,9 +27,12 @@
  *     exception crosses the ABI.
  *   - Results are deterministic: the same inputs give bitwise-identical outputs.
  *   - Calls on different streams may overlap when each has its own workspace
- *     and outputs: no entry point keeps state between launches, so a launch
- *     captured in a HIP graph and replayed shares nothing with eager ones.
- *     g5moe_dispatch_noalloc's scratch is one array per GPU (see there).
+ *     and outputs.  Between launches the library keeps only the per-XCD tile
+ *     shares above, which select where tiles run and never what they compute;
+ *     overlapping launches of one shape mix their busy-time records, which the
+ *     host then ignores.  A launch captured in a HIP graph keeps the shares of
+ *     its capture.  g5moe_dispatch_noalloc's scratch is one array per GPU (see
+ *     there).
  *   - Tensors are row-major.  bf16 values are raw IEEE bfloat16 bit patterns
  *     (uint16); weights use nn.Linear orientation [out, in].
  */
@@ -76,7 +85,9 @@ const char* g5moe_last_error(void);
  * g5moe_swiglu_backward take the g5moe_dropout descriptor (and the latter perm),
  * and kmax = 0 selects the packed padded layout (see "Padded row layouts")
  * wherever the backward takes kmax (with no tokens, the padded outputs are still
- * written as zeros). */
+ * written as zeros).  2.1: the gate|up launches share their tiles among the XCDs
+ * by measured speed (the pinned busy-time buffers of the Conventions); no
+ * signature changed. */
 int32_t g5moe_version(void);
 
 /* Bytes of workspace the stage entry points and g5moe_forward need for `shape`.

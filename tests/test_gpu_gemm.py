@@ -98,3 +98,32 @@ def test_small_m_down_two_per_cu_equals_grouped_gemm(cuda_device, d, counts):
     o0, o1 = int(off[e]), int(off[e + 1])
     torch.testing.assert_close(y_perm[o0:o1].float(), h[o0:o1].float() @ wd[e].float().T,
                                rtol=2e-2, atol=2e-2)
+
+
+def test_xcd_balanced_launches_equal_the_first(cuda_device):
+    """The gate|up launches of 8 x 32 workgroups split their tile list over the XCDs
+    by shares the launcher adapts to each XCD's measured speed (xcd_balance.hip), so
+    the tile -> workgroup mapping changes from call to call while the weights settle.
+    Every tile's arithmetic is the same whichever workgroup runs it: 40 forwards at
+    config 2, each synchronised so that its records reach the launcher, must equal
+    the first call's output bit for bit (the inference gate|up and, through the
+    training op, the factor-storing one)."""
+    from genet5_amd import synth
+    from test_gpu_parity import layer_tensors
+    print("xcd-balanced gate|up: 40 forwards against the first", flush=True)
+    x, wr, wgu, wd, b = layer_tensors(synth.make_config(2, seed=3), cuda_device)
+    buf = ops.ForwardBuffers(x.shape[0], x.shape[1], wd.shape[2], wd.shape[0], 2, x.dtype,
+                             cuda_device)
+    y0 = ops.moe_forward(x, wr, wgu, wd, 2, bias=b, buffers=buf).clone()
+    t0 = ops.moe_forward_train(x, wr, wgu, wd, 2, bias=b, return_h=True, factors=True)
+    t0 = [t.clone() for t in t0]
+    torch.cuda.synchronize()
+    for i in range(40):
+        y = ops.moe_forward(x, wr, wgu, wd, 2, bias=b, buffers=buf)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y0), f"forward {i}"
+        if i % 8 == 7:
+            t = ops.moe_forward_train(x, wr, wgu, wd, 2, bias=b, return_h=True, factors=True)
+            torch.cuda.synchronize()
+            for a, r in zip(t, t0):
+                assert torch.equal(a, r), f"training forward after {i}"
