@@ -119,9 +119,14 @@ XcdSplit xcd_split(int site, unsigned grid, int K, int nout, hipStream_t st) {
     s->K = K;
     s->nout = nout;
     for (int x = 0; x < 8; ++x) s->w[x] = kWeightSum / 8;
+    int can_map = 0;
     void* h = nullptr;
-    if (hipHostMalloc(&h, kWorkgroups * sizeof(unsigned long long),
-                      hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
+    if (hipDeviceGetAttribute(&can_map, hipDeviceAttributeCanMapHostMemory, dev) != hipSuccess ||
+        can_map == 0) {
+      (void)hipGetLastError();
+      s->disabled = true;  // the kernels could not address a host buffer: equal split
+    } else if (hipHostMalloc(&h, kWorkgroups * sizeof(unsigned long long),
+                             hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess) {
       (void)hipGetLastError();
       s->disabled = true;
     } else {
