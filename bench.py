@@ -2,8 +2,8 @@
 
     python bench.py [--steps K] [--warmup W] [--config 2|3] [--no-cpu-baseline]
 
-A step is one whole layer forward (router -> dispatch -> gate|up GEMM + SwiGLU
--> down GEMM -> combine) through the C ABI's stage entry points, on synthetic
+A step is one whole layer forward (router + dispatch in one g5moe_route call ->
+gate|up GEMM + SwiGLU -> down GEMM -> combine) through the C ABI's stage entry points, on synthetic
 inputs already resident in HBM (config 2: 36,400 tokens bf16, uniform routing).
 Prints ONE JSON line.  `value` is tokens/s of the whole layer; `roofline` is
 for the dominant kernel (the grouped gate|up GEMM), its average launch time
@@ -380,7 +380,7 @@ def bench_config5(args) -> dict:
 
 def train_stage_breakdown(args) -> dict:
     """The module's training step as its stages, for the per-stage times: the forward
-    (router with logits, dispatch, experts keeping the gate|up products, combine) and
+    (router with logits and the dispatch, experts keeping the gate|up products, combine) and
     every backward stage (gate/router gradients, the dh GEMM with the SwiGLU
     backward in its epilogue, dX GEMM, input gradient, weight-gradient operands, the
     expert weight gradients from the forward's h, the router weight gradient) through
@@ -597,46 +597,46 @@ def main():
     # One step = the whole layer through the C ABI's stage entry points (the
     # same kernels g5moe_forward enqueues), no host synchronisation inside the
     # loop.  HIP events on the stream the stages run on: the timed loop records
-    # them only around the two expert GEMMs (indices 2, 3, 4), so the roofline
+    # them only around the two expert GEMMs (indices 1, 2, 3), so the roofline
     # kernel's and the down product's averages come from the timed region
     # itself; each event between two kernels leaves the stream a gap, and the
     # six of a fully instrumented step cost about 1.5 % of it (0.967 against
     # 0.953 ms per step without events, three alternating rounds on one box).
-    # The router, dispatch and combine times come from a second loop of the
+    # The route (router + dispatch) and combine times come from a second loop of the
     # same steps with an event at every stage boundary, run right after.
     import ctypes
     from genet5_amd import _lib
     r = buf.routing
     y_perm = torch.empty((N * k, d), dtype=torch.bfloat16, device=dev)
     stream = torch.cuda.current_stream(dev)
-    names = ["router", "dispatch", "gate_up", "down", "combine"]
+    names = ["route", "gate_up", "down", "combine"]
     P = ops._ptr
     shape = buf.shape
     S = ops._stream(dev)
     ws = buf.ws
     every = frozenset(range(len(names) + 1))
-    timed_marks = frozenset((2, 3, 4))
+    timed_marks = frozenset((1, 2, 3))
 
     def step(ev=None, marks=every):
         def rec(i):
             if ev is not None and i in marks:
                 ev[i].record(stream)
         rec(0)
-        _lib.call("g5moe_router_topk", P(x), P(wr), P(bias), P(r.topk_idx), P(r.topk_w), None,
+        # router + dispatch: the router kernel also forms the dispatch's ranks,
+        # then one placement kernel
+        _lib.call("g5moe_route", P(x), P(wr), P(bias), P(r.topk_idx), P(r.topk_w), None,
+                  P(r.counts), P(r.offsets), P(r.perm), P(r.inv_pos), P(ws),
                   ctypes.byref(shape), S)
         rec(1)
-        _lib.call("g5moe_dispatch", P(r.topk_idx), P(r.counts), P(r.offsets), P(r.perm),
-                  P(r.inv_pos), P(ws), ctypes.byref(shape), S)
-        rec(2)
         _lib.call("g5moe_expert_gate_up", P(x), P(r.perm), P(r.offsets), P(wgu), P(ws),
                   ctypes.byref(shape), S)
-        rec(3)
+        rec(2)
         _lib.call("g5moe_expert_down", P(r.offsets), P(wd), P(y_perm), P(ws),
                   ctypes.byref(shape), S)
-        rec(4)
+        rec(3)
         _lib.call("g5moe_combine", P(y_perm), P(r.inv_pos), P(r.topk_w), P(buf.y),
                   ctypes.byref(shape), S)
-        rec(5)
+        rec(4)
 
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
               for _ in range(args.steps)]
@@ -752,7 +752,7 @@ def main():
         "stage_rates": {
             "gate_up_tflops": gu_tflops,
             "down_tflops": dn_tflops,
-            "router_gbs": router_bytes / (stage_ms["router"] * 1e-3) / 1e9,
+            "route_gbs": router_bytes / (stage_ms["route"] * 1e-3) / 1e9,
             "combine_gbs": combine_bytes / (stage_ms["combine"] * 1e-3) / 1e9,
         },
         "roofline": {

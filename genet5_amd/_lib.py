@@ -27,6 +27,7 @@ EXPORTED = (
     "g5moe_pack_gate_up_transposed",
     "g5moe_router_topk",
     "g5moe_dispatch",
+    "g5moe_route",
     "g5moe_dispatch_noalloc",
     "g5moe_expert_gate_up",
     "g5moe_expert_gate_up_train",
@@ -131,6 +132,7 @@ _SIGS = {
     "g5moe_pack_gate_up_transposed": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_router_topk": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_dispatch": ([_P, _P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_route": ([_P] * 11 + [_SHAPE_P, _P], ctypes.c_int),
     "g5moe_dispatch_noalloc": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up": ([_P, _P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_expert_gate_up_train": ([_P, _P, _P, _P, _P, _P, _DROP_P, _SHAPE_P, _P],

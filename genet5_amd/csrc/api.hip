@@ -104,7 +104,7 @@ extern "C" {
 
 const char* g5moe_last_error(void) { return g_err; }
 
-int32_t g5moe_version(void) { return (2 << 16) | 1; }
+int32_t g5moe_version(void) { return (2 << 16) | 2; }
 
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes) {
   G5_CHECK(check_shape(shape));
@@ -173,6 +173,28 @@ g5moe_status g5moe_dispatch(const int32_t* topk_idx, int32_t* counts, int32_t* o
   return hip_status(launch_dispatch(topk_idx, counts, offsets, perm, inv_pos,
                                     static_cast<char*>(ws), *shape, as_stream(stream)),
                     "g5moe_dispatch");
+}
+
+g5moe_status g5moe_route(const void* x, const void* w_router, const float* bias,
+                         int32_t* topk_idx, float* topk_w, float* logits, int32_t* counts,
+                         int32_t* offsets, int32_t* perm, int32_t* inv_pos, void* ws,
+                         const g5moe_shape* shape, void* stream) {
+  G5_CHECK(check_shape(shape));
+  G5_NONNULL(counts);
+  G5_NONNULL(offsets);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(x);
+    G5_NONNULL(w_router);
+    G5_NONNULL(topk_idx);
+    G5_NONNULL(topk_w);
+    G5_NONNULL(perm);
+    G5_NONNULL(inv_pos);
+    G5_NONNULL(ws);
+  }
+  return hip_status(launch_route(x, w_router, bias, topk_idx, topk_w, logits, counts, offsets,
+                                 perm, inv_pos, static_cast<char*>(ws), *shape,
+                                 as_stream(stream)),
+                    "g5moe_route");
 }
 
 g5moe_status g5moe_dispatch_noalloc(const int32_t* topk_idx, int32_t* counts, int32_t* offsets,
@@ -747,8 +769,8 @@ g5moe_status g5moe_forward(const void* x, const void* w_router, const float* bia
     G5_NONNULL(inv_pos);
     G5_NONNULL(ws);
   }
-  G5_CHECK(g5moe_router_topk(x, w_router, bias, topk_idx, topk_w, nullptr, shape, stream));
-  G5_CHECK(g5moe_dispatch(topk_idx, counts, offsets, perm, inv_pos, ws, shape, stream));
+  G5_CHECK(g5moe_route(x, w_router, bias, topk_idx, topk_w, nullptr, counts, offsets, perm,
+                       inv_pos, ws, shape, stream));
   if (shape->n_tokens == 0) return G5MOE_OK;
   const WorkspaceLayout L = workspace_layout(*shape);
   void* y_perm = static_cast<char*>(ws) + L.y_perm;

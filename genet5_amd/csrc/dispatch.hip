@@ -17,6 +17,14 @@
 //             offsets over experts, and writes position = offsets[e] + prefix +
 //             rank into perm and inv_pos; block 0 also writes counts[] and
 //             offsets[].  Integer sums are exact in any order.
+//
+// g5moe_route replaces the rank launch: the router kernel's workgroups rank
+// their own tokens' assignments (chunks of the token order, see
+// router_topk_kernel's RANK) and write per-chunk counts, and
+// dispatch_place_chunks_kernel places from those.  Same outputs, bit for bit;
+// at config 2 the two launches take 28.5 + 6.7 us against 27.0 + 4.6 + 4.8 us for
+// router, rank and place (kernel trace, one process), and the stream has one
+// launch fewer.
 #include <mutex>
 
 #include "g5moe_internal.h"
@@ -72,6 +80,10 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_place_kernel(
   __shared__ int32_t base[kMaxExperts];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t b = blockIdx.x;
+  // the thread's assignment, loaded first: its latency overlaps the count loads
+  const int64_t a = b * kDispatchBlock + tid;
+  const int ea = a < nk ? idx[a] : -1;
+  const int32_t ra = a < nk ? rank[a] : 0;
   // thread (g, ex) sums column ex over the blocks g, g + 16, ...
   const int ex = tid & 15, g = tid >> 4;
   int below = 0, total = 0;
@@ -129,14 +141,142 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_place_kernel(
     if (b == 0 && lane == n_experts - 1) offsets[n_experts] = inc;
   }
   __syncthreads();
-  const int64_t a = b * kDispatchBlock + tid;
   if (a >= nk) return;
-  const int e = idx[a];
+  if (ea < 0 || ea >= n_experts) {
+    inv_pos[a] = -1;
+    return;
+  }
+  const int32_t pos = base[ea] + ra;
+  perm[pos] = int32_t(a);
+  inv_pos[a] = pos;
+}
+
+// Placement from the router's fused rank pass (g5moe_route).  Chunk c holds the
+// assignments [c * chunk_a, (c + 1) * chunk_a) (chunk_a = 2 tpp k, one router
+// block's tokens), and chunk_counts[c][0 .. 16) its per-expert counts (0 past
+// n_experts).  Block b (1024 threads) places the assignments [1024 b, 1024 b +
+// 1024):
+//   * thread (g, quad) sums experts 4 quad .. 4 quad + 3 over the chunks g,
+//     g + 256, ... (one 16-byte load per chunk row; at N = 36,400 every thread's
+//     loads go out together): the counts of the chunks before the block's first
+//     chunk c_lo, and of all chunks; the 256 groups are then reduced (lane
+//     shuffles, then the 16 waves in LDS).  The rows of the block's own chunks
+//     c_lo .. c_hi (at most 1024 / chunk_a + 2) are also kept in LDS as they
+//     pass, and lanes e < 16 of wave 0 turn them into each chunk's exclusive
+//     prefix (no second round of loads);
+//   * position = offsets[e] + (e's count before c_lo) + (e's count in the chunks
+//     c_lo .. c - 1) + rank, c the assignment's chunk.
+// Integer sums are exact in any order; block 0 also writes counts[] and offsets[].
+constexpr int kPlaceThreads = 1024;
+constexpr int kPlaceWaves = kPlaceThreads / 64;
+constexpr int kPlaceGroups = kPlaceThreads / 4;
+constexpr int kMaxWindow = kPlaceThreads / kMinChunkTokens + 2;
+
+__global__ __launch_bounds__(kPlaceThreads) void dispatch_place_chunks_kernel(
+    const int32_t* __restrict__ idx, const int32_t* __restrict__ rank,
+    const int32_t* __restrict__ ccnt, int64_t nchunk, int64_t chunk_a, int64_t nk,
+    int n_experts, int32_t* __restrict__ perm, int32_t* __restrict__ inv_pos,
+    int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
+  static_assert(kMaxExperts == 16, "16 experts: 4 lanes of 4 per chunk row");
+  __shared__ int32_t part[kPlaceWaves][2][kMaxExperts];
+  __shared__ int4 wrow[kMaxWindow][kMaxExperts / 4];  // the block's chunk rows
+  __shared__ int32_t win[kMaxWindow][kMaxExperts];    // their exclusive prefixes
+  __shared__ int32_t base[kMaxExperts];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t b = blockIdx.x;
+  const int64_t a0 = b * kPlaceThreads;
+  const int64_t c_lo = a0 / chunk_a;
+  const int64_t c_hi = (min(a0 + int64_t(kPlaceThreads), nk) - 1) / chunk_a;
+  // the thread's assignment, loaded first: its latency overlaps the count loads
+  const int64_t a = a0 + tid;
+  const int e = a < nk ? idx[a] : -1;
+  const int32_t ra = a < nk ? rank[a] : 0;
+  const int quad = tid & 3, g = tid >> 2;
+  int below[4] = {0, 0, 0, 0}, total[4] = {0, 0, 0, 0};
+  constexpr int U = 4;  // chunk rows in flight per thread
+  for (int64_t c0 = g; c0 < nchunk; c0 += kPlaceGroups * U) {
+    int4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + kPlaceGroups * u;
+      v[u] = c < nchunk ? *reinterpret_cast<const int4*>(ccnt + c * kMaxExperts + 4 * quad)
+                        : make_int4(0, 0, 0, 0);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t c = c0 + kPlaceGroups * u;
+      if (c >= c_lo && c <= c_hi) wrow[c - c_lo][quad] = v[u];
+      const int m = c < c_lo ? 1 : 0;
+      total[0] += v[u].x;
+      total[1] += v[u].y;
+      total[2] += v[u].z;
+      total[3] += v[u].w;
+      below[0] += m * v[u].x;
+      below[1] += m * v[u].y;
+      below[2] += m * v[u].z;
+      below[3] += m * v[u].w;
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+#pragma unroll
+    for (int x = 4; x < 64; x <<= 1) {
+      below[i] += __shfl_xor(below[i], x, 64);
+      total[i] += __shfl_xor(total[i], x, 64);
+    }
+  }
+  if (lane < 4) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      part[wave][0][4 * lane + i] = below[i];
+      part[wave][1][4 * lane + i] = total[i];
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    if (lane < kMaxExperts) {
+      const int* rows = reinterpret_cast<const int*>(&wrow[0][0]);
+      int run = 0;
+      // the row reads do not depend on the running sum: unrolled, they pipeline
+#pragma unroll 8
+      for (int c = 0; c <= int(c_hi - c_lo); ++c) {
+        win[c][lane] = run;
+        run += rows[c * kMaxExperts + lane];
+      }
+    }
+    int pre = 0, tot = 0;
+    if (lane < kMaxExperts) {
+#pragma unroll
+      for (int w = 0; w < kPlaceWaves; ++w) {
+        pre += part[w][0][lane];
+        tot += part[w][1][lane];
+      }
+    }
+    int inc = tot;
+#pragma unroll
+    for (int dd = 1; dd < kMaxExperts; dd <<= 1) {
+      const int o = __shfl_up(inc, dd, 64);
+      if (lane >= dd) inc += o;
+    }
+    const int off = inc - tot;
+    if (lane < n_experts) {
+      base[lane] = off + pre;
+      if (b == 0) {
+        offsets[lane] = off;
+        counts[lane] = tot;
+      }
+    }
+    if (b == 0 && lane == n_experts - 1) offsets[n_experts] = inc;
+  }
+  __syncthreads();
+  if (a >= nk) return;
   if (e < 0 || e >= n_experts) {
     inv_pos[a] = -1;
     return;
   }
-  const int32_t pos = base[e] + rank[a];
+  // assignment indices fit in 32 bits (the shape check bounds N * k)
+  const int wi = int(uint32_t(a) / uint32_t(chunk_a) - uint32_t(c_lo));
+  const int32_t pos = base[e] + win[wi][e] + ra;
   perm[pos] = int32_t(a);
   inv_pos[a] = pos;
 }
@@ -177,6 +317,32 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
                            reinterpret_cast<int32_t*>(ws + L.rank),
                            reinterpret_cast<int32_t*>(ws + L.blk_counts),
                            s.n_tokens * s.top_k, s.n_experts, st);
+}
+
+hipError_t launch_route(const void* x, const void* wr, const float* bias, int32_t* idx,
+                        float* w, float* logits, int32_t* counts, int32_t* offsets,
+                        int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
+                        hipStream_t st) {
+  const int64_t nk = s.n_tokens * s.top_k;
+  if (nk == 0) {
+    hipLaunchKernelGGL(zero_counts_kernel, dim3(1), dim3(64), 0, st, counts, offsets,
+                       s.n_experts);
+    return hipGetLastError();
+  }
+  const WorkspaceLayout L = workspace_layout(s);
+  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
+  int32_t* cc = reinterpret_cast<int32_t*>(ws + L.chunk_counts);
+  const hipError_t e = launch_router_rank(x, wr, bias, idx, w, logits, RankArgs{rank, cc}, s, st);
+  if (e != hipSuccess) return e;
+  // the router's chunks: at least kMinChunkTokens tokens each, so at most the
+  // ceil(N / kMinChunkTokens) rows the workspace holds
+  const int64_t ct = router_chunk_tokens(s);
+  const int64_t nchunk = (s.n_tokens + ct - 1) / ct;
+  const int64_t nblk = (nk + kPlaceThreads - 1) / kPlaceThreads;
+  hipLaunchKernelGGL(dispatch_place_chunks_kernel, dim3(unsigned(nblk)), dim3(kPlaceThreads), 0,
+                     st, idx, rank, cc, nchunk, ct * s.top_k, nk, s.n_experts, perm, inv_pos,
+                     counts, offsets);
+  return hipGetLastError();
 }
 
 namespace {

@@ -28,13 +28,19 @@ constexpr size_t kNoAllocScratchBytes =
     kNoAllocRankBytes + size_t(kNoAllocMaxAssignments / kDispatchBlock) * kMaxExperts * 4;
 static_assert(kNoAllocRankBytes % 256 == 0, "block counts 256-byte aligned");
 
+// The fused router + rank pass (g5moe_route) ranks assignments inside chunks of
+// the token order, one chunk per router block and round: 2 * tpp tokens, tpp >= 2
+// tokens per wave pair, so at most ceil(N / kMinChunkTokens) chunks.
+constexpr int kMinChunkTokens = 4;
+
 // Byte offsets of the workspace regions (each 256-byte aligned).
 struct WorkspaceLayout {
   size_t xb;         // bf16 copy of x when x is f32        [N, d]
   size_t blk_counts; // per-dispatch-block expert counts    [nblk, E]
-  size_t rank;       // stable rank inside the block        [N*k]
+  size_t rank;       // stable rank inside the block/chunk  [N*k]
   size_t h;          // SwiGLU activations, bf16            [N*k, F]
   size_t y_perm;     // expert outputs, bf16                [N*k, d]
+  size_t chunk_counts;  // per-chunk expert counts (route)  [ceil(N / 4), 16]
   size_t total;
   int64_t nblk;      // dispatch blocks
 };
@@ -60,6 +66,8 @@ inline WorkspaceLayout workspace_layout(const g5moe_shape& s) {
   off += align256(size_t(nk + kHPadRows) * s.d_ff * 2);
   w.y_perm = off;
   off += align256(size_t(nk) * s.d_model * 2);
+  w.chunk_counts = off;
+  off += align256(size_t((s.n_tokens + kMinChunkTokens - 1) / kMinChunkTokens) * kMaxExperts * 4);
   w.total = off;
   return w;
 }
@@ -93,9 +101,22 @@ __host__ __device__ __forceinline__ uint32_t dropout_pair_bits(uint32_t key, uin
   return fmix32(key + c * 0x9e3779b9u);
 }
 
+// Outputs of the router's fused rank pass: rank [N*k] (stable rank inside the
+// assignment's chunk) and chunk_counts [nchunk, 16].
+struct RankArgs {
+  int32_t* rank;
+  int32_t* chunk_counts;
+};
+
 // ---- kernel launchers (each returns hipSuccess or the launch error) -------
 hipError_t launch_router(const void* x, const void* wr, const float* bias, int32_t* idx,
                          float* w, float* logits, const g5moe_shape& s, hipStream_t st);
+// The router with the dispatch's rank pass over chunks of
+// router_chunk_tokens(s) tokens (the same partition the launch uses).
+hipError_t launch_router_rank(const void* x, const void* wr, const float* bias, int32_t* idx,
+                              float* w, float* logits, const RankArgs& ra, const g5moe_shape& s,
+                              hipStream_t st);
+int64_t router_chunk_tokens(const g5moe_shape& s);
 hipError_t launch_norm_router(const void* x_add, const void* residual, const float* norm_w,
                               float eps, const void* wr, const float* bias, void* sum_out,
                               void* normed_out, int32_t* idx, float* w, float* logits,
@@ -109,6 +130,12 @@ hipError_t launch_combine_residual(const uint16_t* y_perm, const int32_t* inv_po
 hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets,
                            int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                            hipStream_t st);
+// Router, rank pass and placement (g5moe_route): launch_router_rank, then the
+// placement of every assignment from the chunk counts.
+hipError_t launch_route(const void* x, const void* wr, const float* bias, int32_t* idx,
+                        float* w, float* logits, int32_t* counts, int32_t* offsets,
+                        int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
+                        hipStream_t st);
 // g5moe_dispatch with its buffers in the library's per-device scratch array
 // (n_tokens * top_k <= kNoAllocMaxAssignments).
 hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t* offsets,

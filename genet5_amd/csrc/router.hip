@@ -351,13 +351,24 @@ constexpr int kMaxPairTokens = 64;
 // batch's rows loaded while the current one computes, and stages the logits in
 // LDS; after a block barrier one thread per token does the top-k scan.  The
 // weights are loaded into registers once per wave.
-template <typename XT, int L, int MODE, int TB = kTokBatch>
-__global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
+//
+// RANK: the dispatch's rank pass in the same launch.  A block's 2 * tpp tokens
+// of a round form chunk base / (2 tpp) + blockIdx.x of the token order; the
+// kernel writes each assignment's stable rank inside its chunk (RankArgs::rank)
+// and the chunk's per-expert counts (RankArgs::chunk_counts, 16 per chunk,
+// 0 past n_experts), which dispatch_place_chunks_kernel turns into positions.
+// WPE: the waves per SIMD the register allocation must allow (0: no bound).
+template <typename XT, int L, int MODE, int TB = kTokBatch, bool RANK = false, int WPE = 0>
+__global__ __launch_bounds__(kRouterThreads) __attribute__((amdgpu_waves_per_eu(WPE)))
+void router_topk_kernel(
     const XT* __restrict__ x, const XT* __restrict__ wr, const float* __restrict__ bias,
     int64_t n_tokens, int n_experts, int top_k, int32_t* __restrict__ topk_idx,
-    float* __restrict__ topk_w, float* __restrict__ logits_out, NormArgs na, int tpp) {
+    float* __restrict__ topk_w, float* __restrict__ logits_out, NormArgs na, int tpp,
+    RankArgs ra_out) {
   constexpr int D = 64 * L;
   __shared__ float lg[2 * kMaxPairTokens][kMaxExperts + 1];
+  // RANK: per range (first / second wave pair), the ballot mask of each expert
+  __shared__ uint64_t chunk_masks[2][kMaxExperts];
 
   const int lane = threadIdx.x & 63;
   // wave-uniform (scalar), so every row address is scalar arithmetic
@@ -526,7 +537,16 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
     {
       const int q = threadIdx.x >> 7, tl = threadIdx.x & 127;
       const int64_t t = base + (int64_t(blockIdx.x) * 2 + q) * tpp + tl;
-      if (tl < tpp && t < n_tokens) {
+      const bool active = tl < tpp && t < n_tokens;
+      uint32_t chosen = 0;
+      int sel[kMaxTopK];
+      float gate[kMaxTopK];
+#pragma unroll
+      for (int s = 0; s < kMaxTopK; ++s) {
+        sel[s] = -1;
+        gate[s] = 0.f;
+      }
+      if (active) {
         const float* row = &lg[q * kMaxPairTokens + tl][0];
         float l[kMaxExperts];
 #pragma unroll
@@ -534,8 +554,6 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
         if (logits_out != nullptr) {
           for (int e = 0; e < n_experts; ++e) logits_out[size_t(t) * n_experts + e] = l[e];
         }
-        uint32_t chosen = 0;
-        int sel[kMaxTopK];
         float sl[kMaxTopK];
 #pragma unroll
         for (int s = 0; s < kMaxTopK; ++s) {
@@ -566,11 +584,57 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
           }
         }
 #pragma unroll
+        for (int s = 0; s < kMaxTopK; ++s)
+          if (s < top_k) gate[s] = ex[s] / sum;
+      }
+      if constexpr (RANK) {
+        // The chunk's tokens sit in lanes 0 .. tpp-1 of wave 0 (first range) and
+        // of wave 2 (second range), in token order.  An assignment's rank is the
+        // number of earlier tokens of the chunk routed to its expert (a token's k
+        // experts are distinct): one ballot per expert (experts >= n_experts are
+        // never chosen: empty masks), kept in LDS, then per slot the mask of the
+        // lane's expert counted below the lane, plus the first range's count for
+        // tokens of the second range.
+        const int wv = threadIdx.x >> 6;
+        if (wv == 0 || wv == 2) {
+          // every lane stores the wave-uniform mask (the same 8 bytes): no
+          // per-expert lane predicate, whose 16 loop-invariant compare masks the
+          // compiler would keep in scalar registers across the round loop
+#pragma unroll
+          for (int e = 0; e < kMaxExperts; ++e)
+            chunk_masks[wv >> 1][e] = __ballot((chosen >> e) & 1u);
+        }
+      }
+      // the outputs after the ballots: their stores then do not hold up the
+      // rank pass (a store counts against the same wait counter as a load)
+      if (active) {
+#pragma unroll
         for (int s = 0; s < kMaxTopK; ++s) {
           if (s < top_k) {
             topk_idx[size_t(t) * top_k + s] = sel[s];
-            topk_w[size_t(t) * top_k + s] = ex[s] / sum;
+            topk_w[size_t(t) * top_k + s] = gate[s];
           }
+        }
+      }
+      if constexpr (RANK) {
+        __syncthreads();
+        const int64_t first = base + int64_t(blockIdx.x) * 2 * tpp;  // the chunk's first token
+        if (active) {
+#pragma unroll
+          for (int s = 0; s < kMaxTopK; ++s) {
+            if (s < top_k) {
+              const uint64_t m = chunk_masks[q][sel[s]];
+              int r = int(__builtin_amdgcn_mbcnt_hi(uint32_t(m >> 32),
+                                                    __builtin_amdgcn_mbcnt_lo(uint32_t(m), 0u)));
+              if (q) r += __popcll(chunk_masks[0][sel[s]]);
+              ra_out.rank[size_t(t) * top_k + s] = r;
+            }
+          }
+        }
+        if (threadIdx.x < kMaxExperts && first < n_tokens) {
+          const int e = threadIdx.x;
+          ra_out.chunk_counts[(first / (2 * tpp)) * kMaxExperts + e] =
+              __popcll(chunk_masks[0][e]) + __popcll(chunk_masks[1][e]);
         }
       }
     }
@@ -594,25 +658,42 @@ __global__ __launch_bounds__(kRouterThreads) void router_topk_kernel(
 #define G5_ROUTER_BPC0 3
 #endif
 
-template <typename XT, int MODE>
-hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* idx, float* w,
-                        float* logits, const NormArgs& na, const g5moe_shape& s,
-                        hipStream_t st) {
+// The router's persistent grid and tokens per wave pair (tpp) for n tokens: at
+// most the resident blocks per CU (each wave holds its 8 experts' weights and
+// two batches of rows in registers), at least one batch per pair.
+struct RouterGrid {
+  int64_t grid, tpp;
+};
+template <int MODE>
+RouterGrid router_grid(int64_t n) {
   constexpr int TB = MODE == 0 ? G5_ROUTER_TB0 : G5_ROUTER_TB12;
-  const int64_t n = s.n_tokens;
-  // at most the resident blocks per CU (each wave holds its 8 experts' weights
-  // and two batches of rows in registers), at least one batch per pair
   const int64_t max_grid = int64_t(MODE == 0 ? G5_ROUTER_BPC0 : 2) * int64_t(device_cu_count());
   const int64_t grid = std::max<int64_t>(
       1, std::min<int64_t>(max_grid, (n + 2 * TB - 1) / (2 * TB)));
   int64_t tpp = (n + 2 * grid - 1) / (2 * grid);
   tpp = std::min<int64_t>(kMaxPairTokens, (tpp + TB - 1) / TB * TB);
+  return {grid, tpp};
+}
+
+template <typename XT, int MODE, bool RANK>
+hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* idx, float* w,
+                        float* logits, const NormArgs& na, const RankArgs& ra,
+                        const g5moe_shape& s, hipStream_t st) {
+  constexpr int TB = MODE == 0 ? G5_ROUTER_TB0 : G5_ROUTER_TB12;
+  static_assert(2 * TB >= kMinChunkTokens, "a chunk holds at least kMinChunkTokens tokens");
+  // bf16 MODE 0 is launched with G5_ROUTER_BPC0 blocks per CU: keep its register
+  // allocation within that many waves per SIMD (the rank pass would otherwise
+  // take the d = 768 kernel from 164 to 170 VGPRs, one wave per SIMD fewer)
+  constexpr int WPE = MODE == 0 && sizeof(XT) == 2 ? G5_ROUTER_BPC0 : 0;
+  const int64_t n = s.n_tokens;
+  const RouterGrid rg = router_grid<MODE>(n);
+  const int64_t grid = rg.grid, tpp = rg.tpp;
   const int L = s.d_model / 64;
 #define G5_ROUTER_CASE(LL)                                                                  \
   case LL:                                                                                  \
-    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE, TB>), dim3(unsigned(grid)),         \
-                       dim3(kRouterThreads), 0, st, x, wr, bias, n, s.n_experts, s.top_k,    \
-                       idx, w, logits, na, int(tpp));                                        \
+    hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE, TB, RANK, WPE>),                    \
+                       dim3(unsigned(grid)), dim3(kRouterThreads), 0, st, x, wr, bias, n,    \
+                       s.n_experts, s.top_k, idx, w, logits, na, int(tpp), ra);              \
     break;
   switch (L) {
     G5_ROUTER_CASE(2)
@@ -626,16 +707,17 @@ hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* i
   return hipGetLastError();
 }
 
-template <int MODE>
+template <int MODE, bool RANK = false>
 hipError_t launch_mode(const void* x, const void* wr, const float* bias, int32_t* idx,
                        float* w, float* logits, const NormArgs& na, const g5moe_shape& s,
-                       hipStream_t st) {
+                       hipStream_t st, const RankArgs& ra = RankArgs{}) {
   if (s.x_dtype == G5MOE_DTYPE_BF16)
-    return launch_typed<uint16_t, MODE>(static_cast<const uint16_t*>(x),
-                                        static_cast<const uint16_t*>(wr), bias, idx, w,
-                                        logits, na, s, st);
-  return launch_typed<float, MODE>(static_cast<const float*>(x), static_cast<const float*>(wr),
-                                   bias, idx, w, logits, na, s, st);
+    return launch_typed<uint16_t, MODE, RANK>(static_cast<const uint16_t*>(x),
+                                              static_cast<const uint16_t*>(wr), bias, idx, w,
+                                              logits, na, ra, s, st);
+  return launch_typed<float, MODE, RANK>(static_cast<const float*>(x),
+                                         static_cast<const float*>(wr), bias, idx, w, logits,
+                                         na, ra, s, st);
 }
 
 }  // namespace
@@ -644,6 +726,17 @@ hipError_t launch_router(const void* x, const void* wr, const float* bias, int32
                          float* w, float* logits, const g5moe_shape& s, hipStream_t st) {
   if (s.n_tokens == 0) return hipSuccess;
   return launch_mode<0>(x, wr, bias, idx, w, logits, NormArgs{}, s, st);
+}
+
+int64_t router_chunk_tokens(const g5moe_shape& s) {
+  return 2 * router_grid<0>(s.n_tokens).tpp;
+}
+
+hipError_t launch_router_rank(const void* x, const void* wr, const float* bias, int32_t* idx,
+                              float* w, float* logits, const RankArgs& ra, const g5moe_shape& s,
+                              hipStream_t st) {
+  if (s.n_tokens == 0) return hipSuccess;
+  return launch_mode<0, true>(x, wr, bias, idx, w, logits, NormArgs{}, s, st, ra);
 }
 
 hipError_t launch_norm_router(const void* x_add, const void* residual, const float* norm_w,

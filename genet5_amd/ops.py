@@ -376,8 +376,26 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
     F = F2 // 2
-    idx, w, logits = router_topk(x2d, w_router, top_k, bias=bias, return_logits=True)
-    _, offsets, perm, inv_pos = dispatch(idx, E, d)
+    _require(x2d, "x", (N, d), x2d.dtype, dev)
+    _require(w_router, "w_router", (E, d), x2d.dtype, dev)
+    if bias is not None:
+        _require(bias, "bias", (E,), torch.float32, dev)
+    _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
+    shape = _lib.make_shape(N, d, F, E, top_k, _dtype_code(x2d.dtype))
+    ws = workspace(shape, dev)
+    S = _stream(dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    idx = torch.empty((N, top_k), **i32)
+    w = torch.empty((N, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((N, E), dtype=torch.float32, device=dev)
+    offsets = torch.empty((E + 1,), **i32)
+    perm = torch.empty((N * top_k,), **i32)
+    inv_pos = torch.empty((N * top_k,), **i32)
+    counts = torch.empty((E,), **i32)
+    # router + dispatch in two launches (the router kernel forms the ranks)
+    _lib.call("g5moe_route", _ptr(x2d), _ptr(w_router), _ptr(bias), _ptr(idx), _ptr(w),
+              _ptr(logits), _ptr(counts), _ptr(offsets), _ptr(perm), _ptr(inv_pos), _ptr(ws),
+              ctypes.byref(shape), S)
     if offsets_host is not None:
         if offsets_host.device.type != "cpu" or offsets_host.shape != (E + 1,) or \
                 offsets_host.dtype != torch.int32 or not offsets_host.is_pinned():
@@ -385,12 +403,8 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
         offsets_host.copy_(offsets, non_blocking=True)
         if offsets_ready is not None:
             offsets_ready.record(torch.cuda.current_stream(dev))
-    _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
-    shape = _lib.make_shape(N, d, F, E, top_k, _dtype_code(x2d.dtype))
-    ws = workspace(shape, dev)
     gu = torch.empty((N * top_k, F2), dtype=torch.bfloat16, device=dev)
     y_perm = torch.empty((N * top_k, d), dtype=torch.bfloat16, device=dev)
-    S = _stream(dev)
     _lib.call("g5moe_expert_gate_up_train_factors" if factors else "g5moe_expert_gate_up_train",
               _ptr(x2d), _ptr(perm), _ptr(offsets), _ptr(w_gate_up), _ptr(gu), _ptr(ws),
               _dropout_arg(dropout), ctypes.byref(shape), S)

@@ -87,14 +87,16 @@ const char* g5moe_last_error(void);
  * wherever the backward takes kmax (with no tokens, the padded outputs are still
  * written as zeros).  2.1: the gate|up launches share their tiles among the XCDs
  * by measured speed (the pinned busy-time buffers of the Conventions); no
- * signature changed. */
+ * signature changed.  2.2: g5moe_route (router and dispatch in two launches,
+ * used by g5moe_forward); the workspace gains its per-chunk count region. */
 int32_t g5moe_version(void);
 
 /* Bytes of workspace the stage entry points and g5moe_forward need for `shape`.
  * Layout (regions in this order, each starting 256-byte aligned): the bf16 copy
  * of x when x_dtype is F32 [N, d] (else empty); dispatch block counts
  * int32 [ceil(N*k / 256), E]; in-block ranks int32 [N*k]; h bf16 [N*k + 384, F]
- * (rows past N*k are padding); y_perm bf16 [N*k, d]. */
+ * (rows past N*k are padding); y_perm bf16 [N*k, d]; g5moe_route's per-chunk
+ * expert counts int32 [ceil(N / 4), 16]. */
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes);
 
 /* Repack the two expert input projections into the interleaved gate|up layout
@@ -146,6 +148,18 @@ g5moe_status g5moe_router_topk(const void* x, const void* w_router, const float*
 g5moe_status g5moe_dispatch(const int32_t* topk_idx, int32_t* counts, int32_t* offsets,
                             int32_t* perm, int32_t* inv_pos, void* ws,
                             const g5moe_shape* shape, void* stream);
+
+/* Router and dispatch together: the outputs of g5moe_router_topk followed by
+ * g5moe_dispatch, bit for bit, in two launches instead of three.  The router kernel also forms the dispatch's stable ranks, inside
+ * chunks of its own token partition (one router workgroup's tokens), and a
+ * placement kernel turns the chunk counts into positions.  Replaces the same
+ * reference step as g5moe_router_topk (README.md:12 "16 experts top-2"; the
+ * router orientation of lib/blocks/_component.py:42-44); new stage.
+ *   arguments as g5moe_router_topk and g5moe_dispatch; ws as g5moe_workspace_size. */
+g5moe_status g5moe_route(const void* x, const void* w_router, const float* bias,
+                         int32_t* topk_idx, float* topk_w, float* logits, int32_t* counts,
+                         int32_t* offsets, int32_t* perm, int32_t* inv_pos, void* ws,
+                         const g5moe_shape* shape, void* stream);
 
 /* g5moe_dispatch without a workspace, for callers that cannot allocate (code
  * under HIP graph capture, tight serving loops, harnesses that forbid
