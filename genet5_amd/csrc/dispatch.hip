@@ -22,7 +22,7 @@
 // their own tokens' assignments (chunks of the token order, see
 // router_topk_kernel's RANK) and write per-chunk counts, and
 // dispatch_place_chunks_kernel places from those.  Same outputs, bit for bit;
-// at config 2 the two launches take 28.5 + 6.7 us against 27.0 + 4.6 + 4.8 us for
+// at config 2 the two launches take 28.5 + 5.7 us against 27.0 + 4.7 + 4.9 us for
 // router, rank and place (kernel trace, one process), and the stream has one
 // launch fewer.
 #include <mutex>
@@ -154,27 +154,42 @@ __global__ __launch_bounds__(kDispatchBlock) void dispatch_place_kernel(
 // Placement from the router's fused rank pass (g5moe_route).  Chunk c holds the
 // assignments [c * chunk_a, (c + 1) * chunk_a) (chunk_a = 2 tpp k, one router
 // block's tokens), and chunk_counts[c][0 .. 16) its per-expert counts (0 past
-// n_experts).  Block b (1024 threads) places the assignments [1024 b, 1024 b +
-// 1024):
+// n_experts).  Block b (512 threads, 2 assignments each) places the assignments
+// [1024 b, 1024 b + 1024):
 //   * thread (g, quad) sums experts 4 quad .. 4 quad + 3 over the chunks g,
-//     g + 256, ... (one 16-byte load per chunk row; at N = 36,400 every thread's
+//     g + 128, ... (one 16-byte load per chunk row; at N = 36,400 every thread's
 //     loads go out together): the counts of the chunks before the block's first
-//     chunk c_lo, and of all chunks; the 256 groups are then reduced (lane
-//     shuffles, then the 16 waves in LDS).  The rows of the block's own chunks
+//     chunk c_lo, and of all chunks; the 128 groups are then reduced (lane
+//     shuffles, then the 8 waves in LDS).  The rows of the block's own chunks
 //     c_lo .. c_hi (at most 1024 / chunk_a + 2) are also kept in LDS as they
 //     pass, and lanes e < 16 of wave 0 turn them into each chunk's exclusive
 //     prefix (no second round of loads);
 //   * position = offsets[e] + (e's count before c_lo) + (e's count in the chunks
 //     c_lo .. c - 1) + rank, c the assignment's chunk.
 // Integer sums are exact in any order; block 0 also writes counts[] and offsets[].
-constexpr int kPlaceThreads = 1024;
+// Block shape: 512 threads placing 2 assignments each.  At config 2, two kernel
+// traces per shape in one session (64-bit index arithmetic then): 6.24-6.26 us
+// against 6.51-6.53 (256 threads x 1), 6.70-6.71 (1024 x 1) and 6.87-6.91 (256 x 4).
+#ifndef G5_PLACE_THREADS
+#define G5_PLACE_THREADS 512
+#endif
+#ifndef G5_PLACE_APT
+#define G5_PLACE_APT 2
+#endif
+#ifndef G5_PLACE_U
+#define G5_PLACE_U 8
+#endif
+constexpr int kPlaceThreads = G5_PLACE_THREADS;
+constexpr int kPlaceApt = G5_PLACE_APT;  // assignments per thread
+constexpr int kPlaceSpan = kPlaceThreads * kPlaceApt;
 constexpr int kPlaceWaves = kPlaceThreads / 64;
 constexpr int kPlaceGroups = kPlaceThreads / 4;
-constexpr int kMaxWindow = kPlaceThreads / kMinChunkTokens + 2;
+constexpr int kMaxWindow = kPlaceSpan / kMinChunkTokens + 2;
 
+// Index arithmetic in 32 bits: the shape check bounds N * k by 2^30.
 __global__ __launch_bounds__(kPlaceThreads) void dispatch_place_chunks_kernel(
     const int32_t* __restrict__ idx, const int32_t* __restrict__ rank,
-    const int32_t* __restrict__ ccnt, int64_t nchunk, int64_t chunk_a, int64_t nk,
+    const int32_t* __restrict__ ccnt, uint32_t nchunk, uint32_t chunk_a, uint32_t nk,
     int n_experts, int32_t* __restrict__ perm, int32_t* __restrict__ inv_pos,
     int32_t* __restrict__ counts, int32_t* __restrict__ offsets) {
   static_assert(kMaxExperts == 16, "16 experts: 4 lanes of 4 per chunk row");
@@ -183,28 +198,32 @@ __global__ __launch_bounds__(kPlaceThreads) void dispatch_place_chunks_kernel(
   __shared__ int32_t win[kMaxWindow][kMaxExperts];    // their exclusive prefixes
   __shared__ int32_t base[kMaxExperts];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t b = blockIdx.x;
-  const int64_t a0 = b * kPlaceThreads;
-  const int64_t c_lo = a0 / chunk_a;
-  const int64_t c_hi = (min(a0 + int64_t(kPlaceThreads), nk) - 1) / chunk_a;
-  // the thread's assignment, loaded first: its latency overlaps the count loads
-  const int64_t a = a0 + tid;
-  const int e = a < nk ? idx[a] : -1;
-  const int32_t ra = a < nk ? rank[a] : 0;
+  const uint32_t b = blockIdx.x;
+  const uint32_t a0 = b * kPlaceSpan;
+  const uint32_t c_lo = a0 / chunk_a;
+  const uint32_t c_hi = (min(a0 + uint32_t(kPlaceSpan), nk) - 1) / chunk_a;
+  // the thread's assignments, loaded first: their latency overlaps the count loads
+  int ea[kPlaceApt], ra[kPlaceApt];
+#pragma unroll
+  for (int j = 0; j < kPlaceApt; ++j) {
+    const uint32_t a = a0 + j * kPlaceThreads + tid;
+    ea[j] = a < nk ? idx[a] : -1;
+    ra[j] = a < nk ? rank[a] : 0;
+  }
   const int quad = tid & 3, g = tid >> 2;
   int below[4] = {0, 0, 0, 0}, total[4] = {0, 0, 0, 0};
-  constexpr int U = 4;  // chunk rows in flight per thread
-  for (int64_t c0 = g; c0 < nchunk; c0 += kPlaceGroups * U) {
+  constexpr int U = G5_PLACE_U;  // chunk rows in flight per thread
+  for (uint32_t c0 = g; c0 < nchunk; c0 += kPlaceGroups * U) {
     int4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + kPlaceGroups * u;
+      const uint32_t c = c0 + kPlaceGroups * u;
       v[u] = c < nchunk ? *reinterpret_cast<const int4*>(ccnt + c * kMaxExperts + 4 * quad)
                         : make_int4(0, 0, 0, 0);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int64_t c = c0 + kPlaceGroups * u;
+      const uint32_t c = c0 + kPlaceGroups * u;
       if (c >= c_lo && c <= c_hi) wrow[c - c_lo][quad] = v[u];
       const int m = c < c_lo ? 1 : 0;
       total[0] += v[u].x;
@@ -269,16 +288,21 @@ __global__ __launch_bounds__(kPlaceThreads) void dispatch_place_chunks_kernel(
     if (b == 0 && lane == n_experts - 1) offsets[n_experts] = inc;
   }
   __syncthreads();
-  if (a >= nk) return;
-  if (e < 0 || e >= n_experts) {
-    inv_pos[a] = -1;
-    return;
+#pragma unroll
+  for (int j = 0; j < kPlaceApt; ++j) {
+    const uint32_t a = a0 + j * kPlaceThreads + tid;
+    const int e = ea[j];
+    if (a < nk) {
+      if (e < 0 || e >= n_experts) {
+        inv_pos[a] = -1;
+      } else {
+        const int wi = int(a / chunk_a - c_lo);
+        const int32_t pos = base[e] + win[wi][e] + ra[j];
+        perm[pos] = int32_t(a);
+        inv_pos[a] = pos;
+      }
+    }
   }
-  // assignment indices fit in 32 bits (the shape check bounds N * k)
-  const int wi = int(uint32_t(a) / uint32_t(chunk_a) - uint32_t(c_lo));
-  const int32_t pos = base[e] + win[wi][e] + ra;
-  perm[pos] = int32_t(a);
-  inv_pos[a] = pos;
 }
 
 __global__ void zero_counts_kernel(int32_t* counts, int32_t* offsets, int n_experts) {
@@ -338,10 +362,10 @@ hipError_t launch_route(const void* x, const void* wr, const float* bias, int32_
   // ceil(N / kMinChunkTokens) rows the workspace holds
   const int64_t ct = router_chunk_tokens(s);
   const int64_t nchunk = (s.n_tokens + ct - 1) / ct;
-  const int64_t nblk = (nk + kPlaceThreads - 1) / kPlaceThreads;
+  const int64_t nblk = (nk + kPlaceSpan - 1) / kPlaceSpan;
   hipLaunchKernelGGL(dispatch_place_chunks_kernel, dim3(unsigned(nblk)), dim3(kPlaceThreads), 0,
-                     st, idx, rank, cc, nchunk, ct * s.top_k, nk, s.n_experts, perm, inv_pos,
-                     counts, offsets);
+                     st, idx, rank, cc, uint32_t(nchunk), uint32_t(ct * s.top_k), uint32_t(nk),
+                     s.n_experts, perm, inv_pos, counts, offsets);
   return hipGetLastError();
 }
 
