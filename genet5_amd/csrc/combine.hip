@@ -35,10 +35,11 @@ __global__ __launch_bounds__(256) void combine_kernel(const uint16_t* __restrict
                                                       void* y, int64_t n_tokens, int d,
                                                       int topk, const void* residual,
                                                       float alpha) {
-  const int cpr = d / 8;
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= n_tokens * cpr) return;
-  const int64_t t = i / cpr;
+  // 32-bit index arithmetic: the shape check bounds N * d * 2 below 2^32
+  const uint32_t cpr = uint32_t(d) / 8;
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= uint32_t(n_tokens) * cpr) return;
+  const uint32_t t = i / cpr;
   const int ch = int(i - t * cpr);
   float acc[8];
 #pragma unroll
