@@ -128,6 +128,40 @@ def dispatch(topk_idx: torch.Tensor, n_experts: int, d_model: int = 128):
     return counts, offsets, perm, inv_pos
 
 
+def route(x2d: torch.Tensor, w_router: torch.Tensor, top_k: int,
+          bias: Optional[torch.Tensor] = None, return_logits: bool = False,
+          ws: Optional[torch.Tensor] = None, d_ff: int = 128):
+    """router_topk then dispatch in two launches (g5moe_route: the router kernel
+    forms the dispatch's ranks) -> (topk_idx, topk_w, counts, offsets, perm, inv_pos[,
+    logits]), the same values as the two calls.  ws: a workspace for the shape
+    (N, d, d_ff, E, top_k), allocated here when None."""
+    dev = _check_device(x2d)
+    N, d = x2d.shape
+    E = w_router.shape[0]
+    _require(x2d, "x", (N, d), x2d.dtype, dev)
+    _require(w_router, "w_router", (E, d), x2d.dtype, dev)
+    if bias is not None:
+        _require(bias, "bias", (E,), torch.float32, dev)
+    shape = _lib.make_shape(N, d, d_ff, E, top_k, _dtype_code(x2d.dtype))
+    if ws is None:
+        ws = workspace(shape, dev)
+    elif ws.numel() < _lib.workspace_size(shape) or ws.device != dev:
+        raise ValueError("ws is smaller than the shape's workspace or on another device")
+    i32 = dict(dtype=torch.int32, device=dev)
+    idx = torch.empty((N, top_k), **i32)
+    w = torch.empty((N, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((N, E), dtype=torch.float32, device=dev) if return_logits else None
+    counts = torch.empty((E,), **i32)
+    offsets = torch.empty((E + 1,), **i32)
+    perm = torch.empty((N * top_k,), **i32)
+    inv_pos = torch.empty((N * top_k,), **i32)
+    _lib.call("g5moe_route", _ptr(x2d), _ptr(w_router), _ptr(bias), _ptr(idx), _ptr(w),
+              _ptr(logits), _ptr(counts), _ptr(offsets), _ptr(perm), _ptr(inv_pos), _ptr(ws),
+              ctypes.byref(shape), _stream(dev))
+    out = (idx, w, counts, offsets, perm, inv_pos)
+    return out + (logits,) if return_logits else out
+
+
 def expert_swiglu(x2d: torch.Tensor, perm: torch.Tensor, offsets: torch.Tensor,
                   w_gate_up: torch.Tensor, w_down: torch.Tensor, top_k: int,
                   return_h: bool = False):
@@ -376,26 +410,12 @@ def moe_forward_train(x2d: torch.Tensor, w_router: torch.Tensor, w_gate_up: torc
     N, d = x2d.shape
     E, F2, _ = w_gate_up.shape
     F = F2 // 2
-    _require(x2d, "x", (N, d), x2d.dtype, dev)
-    _require(w_router, "w_router", (E, d), x2d.dtype, dev)
-    if bias is not None:
-        _require(bias, "bias", (E,), torch.float32, dev)
     _require(w_down, "w_down", (E, d, F), torch.bfloat16, dev)
     shape = _lib.make_shape(N, d, F, E, top_k, _dtype_code(x2d.dtype))
     ws = workspace(shape, dev)
     S = _stream(dev)
-    i32 = dict(dtype=torch.int32, device=dev)
-    idx = torch.empty((N, top_k), **i32)
-    w = torch.empty((N, top_k), dtype=torch.float32, device=dev)
-    logits = torch.empty((N, E), dtype=torch.float32, device=dev)
-    offsets = torch.empty((E + 1,), **i32)
-    perm = torch.empty((N * top_k,), **i32)
-    inv_pos = torch.empty((N * top_k,), **i32)
-    counts = torch.empty((E,), **i32)
-    # router + dispatch in two launches (the router kernel forms the ranks)
-    _lib.call("g5moe_route", _ptr(x2d), _ptr(w_router), _ptr(bias), _ptr(idx), _ptr(w),
-              _ptr(logits), _ptr(counts), _ptr(offsets), _ptr(perm), _ptr(inv_pos), _ptr(ws),
-              ctypes.byref(shape), S)
+    idx, w, _, offsets, perm, inv_pos, logits = route(x2d, w_router, top_k, bias=bias,
+                                                      return_logits=True, ws=ws, d_ff=F)
     if offsets_host is not None:
         if offsets_host.device.type != "cpu" or offsets_host.shape != (E + 1,) or \
                 offsets_host.dtype != torch.int32 or not offsets_host.is_pinned():

@@ -113,3 +113,21 @@ def test_route_empty_batch(cuda_device):
               None, P(ws), ctypes.byref(s), ops._stream(dev))
     torch.cuda.synchronize()
     assert host(counts).tolist() == [0] * E and host(offsets).tolist() == [0] * (E + 1)
+
+
+def test_ops_route_equals_stage_calls(cuda_device):
+    """ops.route (the Python mirror, with logits, own or caller workspace) against
+    ops.router_topk + ops.dispatch."""
+    dev = cuda_device
+    print("ops.route N=4550 d=768 E=16 k=2", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(7)
+    x = torch.randn(4550, 768, generator=g).to(torch.bfloat16).to(dev)
+    wr = (torch.randn(16, 768, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    idx, w, logits = ops.router_topk(x, wr, 2, return_logits=True)
+    ref = (idx, w) + ops.dispatch(idx, 16, 768) + (logits,)
+    ws = ops.workspace(_lib.make_shape(4550, 768, 3072, 16, 2, _lib.DTYPE_BF16), dev)
+    for kw in (dict(), dict(ws=ws, d_ff=3072)):
+        got = ops.route(x, wr, 2, return_logits=True, **kw)
+        torch.cuda.synchronize()
+        for a, b in zip(got, ref):
+            assert torch.equal(a.view(torch.int32), b.view(torch.int32))
