@@ -16,6 +16,7 @@ module's autograd, and the training backward's freedom from host synchronisation
   backward that reads the offsets from the device.
 """
 import ctypes
+import warnings
 
 import numpy as np
 import pytest
@@ -181,7 +182,12 @@ def test_backward_has_no_host_sync(cuda_device):
         (y.float().square().sum() + m.aux_loss).backward()
         return y, [xr.grad] + [p.grad for p in (m.router.weight, m.w_gate, m.w_up, m.w_down)]
 
-    torch.cuda.set_sync_debug_mode("error")
+    # torch notes that the mode is a prototype which does not see every
+    # synchronising operation (the graph-capture test covers those); the notice
+    # itself is not a finding of this test
+    with warnings.catch_warnings():
+        warnings.filterwarnings("ignore", message="Synchronization debug mode is a prototype")
+        torch.cuda.set_sync_debug_mode("error")
     try:
         y, g_nosync = step()
     finally:
