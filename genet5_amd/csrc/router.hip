@@ -63,6 +63,7 @@
 #include <algorithm>
 
 #include "g5moe_internal.h"
+#include "gemm_common.h"
 
 namespace g5moe {
 namespace {
@@ -364,7 +365,7 @@ void router_topk_kernel(
     const XT* __restrict__ x, const XT* __restrict__ wr, const float* __restrict__ bias,
     int64_t n_tokens, int n_experts, int top_k, int32_t* __restrict__ topk_idx,
     float* __restrict__ topk_w, float* __restrict__ logits_out, NormArgs na, int tpp,
-    RankArgs ra_out) {
+    RankArgs ra_out, int wr_lds) {
   constexpr int D = 64 * L;
   __shared__ float lg[2 * kMaxPairTokens][kMaxExperts + 1];
   // RANK: per range (first / second wave pair), the ballot mask of each expert
@@ -378,11 +379,37 @@ void router_topk_kernel(
   const int e0 = half * kHalfExperts;
 
   // This lane's weight slice for its wave's 8 experts (0 for experts >= E).
+  // bf16 weights with a 16-byte aligned base (wr_lds) go through LDS: the
+  // workgroup copies w_router [E, d] once with 16-byte LDS DMA (24 KB at d = 768,
+  // E = 16; reads clamped to the array, so a partial last 1 KB block re-reads its
+  // tail), and each wave reads its slices from there.  Every wave loading its own
+  // 12 KB in 8-byte pieces (3,072 waves at config 2) held the first batch back:
+  // kernel trace, one box, two rounds: 26.3 against 27.6 us at config 2, 10.3
+  // against 11.4 us at 4,550 tokens.  Loading each round's first rows ahead of
+  // the staging as well measured -0.2 / +0.2 us there and is not done.
   float w[kHalfExperts][L];
+  constexpr bool kStaged = sizeof(XT) == 2;
+  __shared__ __attribute__((aligned(16))) uint16_t wl[kStaged ? kMaxExperts * D : 8];
+  if constexpr (kStaged) {
+    if (wr_lds) {
+      const uint32_t bytes = uint32_t(n_experts) * D * 2;
+      const uint32_t nblk = (bytes + 1023) / 1024;
+      const uint32_t lds0 = gemm::lds_addr(wl);
+      for (uint32_t k = uint32_t(wave); k < nblk; k += kRouterThreads / 64)
+        gemm::lds_dma16_s(wr, min(k * 1024u + uint32_t(lane) * 16u, bytes - 16u),
+                          lds0 + k * 1024u);
+      gemm::wait_vmcnt<0>();
+      __syncthreads();
+    }
+  }
 #pragma unroll
   for (int e = 0; e < kHalfExperts; ++e) {
     if (e0 + e < n_experts) {
-      RowLoader<XT, L>::load(wr + size_t(e0 + e) * D + lane * L, w[e]);
+      if (kStaged && wr_lds)
+        RowLoader<XT, L>::load(reinterpret_cast<const XT*>(wl) + size_t(e0 + e) * D + lane * L,
+                               w[e]);
+      else
+        RowLoader<XT, L>::load(wr + size_t(e0 + e) * D + lane * L, w[e]);
     } else {
 #pragma unroll
       for (int i = 0; i < L; ++i) w[e][i] = 0.f;
@@ -687,13 +714,15 @@ hipError_t launch_typed(const XT* x, const XT* wr, const float* bias, int32_t* i
   constexpr int WPE = MODE == 0 && sizeof(XT) == 2 ? G5_ROUTER_BPC0 : 0;
   const int64_t n = s.n_tokens;
   const RouterGrid rg = router_grid<MODE>(n);
+  // the LDS DMA moves 16-byte pieces of the weight array
+  const int wr_lds = sizeof(XT) == 2 && reinterpret_cast<uintptr_t>(wr) % 16 == 0;
   const int64_t grid = rg.grid, tpp = rg.tpp;
   const int L = s.d_model / 64;
 #define G5_ROUTER_CASE(LL)                                                                  \
   case LL:                                                                                  \
     hipLaunchKernelGGL((router_topk_kernel<XT, LL, MODE, TB, RANK, WPE>),                    \
                        dim3(unsigned(grid)), dim3(kRouterThreads), 0, st, x, wr, bias, n,    \
-                       s.n_experts, s.top_k, idx, w, logits, na, int(tpp), ra);              \
+                       s.n_experts, s.top_k, idx, w, logits, na, int(tpp), ra, wr_lds);      \
     break;
   switch (L) {
     G5_ROUTER_CASE(2)
