@@ -8,7 +8,8 @@ inputs already resident in HBM (config 2: 36,400 tokens bf16, uniform routing).
 Prints ONE JSON line.  `value` is tokens/s of the whole layer; `roofline` is
 for the dominant kernel (the grouped gate|up GEMM), its average launch time
 taken from HIP events recorded around it, on the stream it runs on, inside the
-timed loop (which records events only around the two expert GEMMs;
+timed loop (which records events only around the two expert GEMMs, created
+without a system-scope fence so that recording them costs the stream nothing;
 `stage_ms` holds every stage's time from a second loop of the same steps with
 an event at each stage boundary).  `cpu_baseline` times the CPU oracle (fp32,
 numpy/BLAS) on the same workload (all of its tokens unless --cpu-sample-tokens
@@ -203,6 +204,50 @@ SETTLE_WHY = ("untimed calls of the step before the warm-up steps: after an idle
               "low for about 20 ms before it settles (gate|up 604 -> 874 -> 607 us per call "
               "over the first 25 ms in profiles/moe_layer_cfg2_kernel_stats.md), so without "
               "them a short timed region measures that transient instead of the steady state")
+
+
+class TimingEvent:
+    """A HIP event used only for timing, created with hipEventDisableSystemFence.
+
+    torch.cuda.Event(enable_timing=True) is a default HIP event: recording it
+    performs a system-scope release (the L2 written back and invalidated), which
+    leaves a gap of several microseconds before the next kernel on the stream
+    and a cold L2 behind it.  An event created with hipEventDisableSystemFence
+    still timestamps its place in the stream, and hipEventElapsedTime still reads
+    it once the device has been synchronised.  The event comes from the HIP
+    runtime torch has loaded (RTLD_NOLOAD), so it shares torch's streams.
+    """
+
+    DISABLE_SYSTEM_FENCE = 0x20000000   # hipEventDisableSystemFence (hip_runtime_api.h)
+    _hip = None
+
+    def __init__(self):
+        import ctypes
+        if TimingEvent._hip is None:
+            TimingEvent._hip = ctypes.CDLL("libamdhip64.so.7",
+                                           mode=os.RTLD_NOLOAD | ctypes.RTLD_GLOBAL)
+        self._c = ctypes
+        self.h = ctypes.c_void_p()
+        rc = self._hip.hipEventCreateWithFlags(ctypes.byref(self.h),
+                                               ctypes.c_uint(self.DISABLE_SYSTEM_FENCE))
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+
+    def record(self, stream) -> None:
+        rc = self._hip.hipEventRecord(self.h, self._c.c_void_p(stream.cuda_stream))
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_time(self, end: "TimingEvent") -> float:
+        ms = self._c.c_float()
+        rc = self._hip.hipEventElapsedTime(self._c.byref(ms), self.h, end.h)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def __del__(self):
+        if self._hip is not None and self.h:
+            self._hip.hipEventDestroy(self.h)
 
 
 def settle(fn, ms: float) -> dict:
@@ -599,9 +644,10 @@ def main():
     # loop.  HIP events on the stream the stages run on: the timed loop records
     # them only around the two expert GEMMs (indices 1, 2, 3), so the roofline
     # kernel's and the down product's averages come from the timed region
-    # itself; each event between two kernels leaves the stream a gap, and the
-    # six of a fully instrumented step cost about 1.5 % of it (0.967 against
-    # 0.953 ms per step without events, three alternating rounds on one box).
+    # itself.  They are TimingEvents (no system-scope fence): with torch's
+    # default events the three records cost 0.7 % of the step (0.988 against
+    # 0.982 ms per step with TimingEvents and 0.981 with no events, three
+    # alternating rounds on one box).
     # The route (router + dispatch) and combine times come from a second loop of the
     # same steps with an event at every stage boundary, run right after.
     import ctypes
@@ -638,8 +684,7 @@ def main():
                   ctypes.byref(shape), S)
         rec(4)
 
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(len(names) + 1)]
-              for _ in range(args.steps)]
+    events = [[TimingEvent() for _ in range(len(names) + 1)] for _ in range(args.steps)]
     settled = settle(step, args.settle_ms)
     for _ in range(args.warmup):
         step()
@@ -749,6 +794,7 @@ def main():
         "expert_gemm_pct_bf16_peak": 100.0 * gemm_tflops / PEAK_BF16_TFLOPS,
         "stage_ms_timed": timed_ms,
         "stage_ms": stage_ms,
+        "timing_events": "HIP events created with hipEventDisableSystemFence, on the stages' stream",
         "stage_rates": {
             "gate_up_tflops": gu_tflops,
             "down_tflops": dn_tflops,
