@@ -1158,12 +1158,15 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
 // Persistent grouped GEMM: one workgroup per CU.  XCD x owns the contiguous
 // tile range [lo, hi) of the launch; each of its nslot workgroups runs q =
 // (hi - lo) / nslot tiles (slot s: lo + s, lo + s + nslot, ...).  The r tiles
-// left over run either whole, one each on slots 0 .. r - 1, or (HALF_TAIL, the
-// down GEMM) as 2r n-halves spread over the slots, so that no workgroup runs
+// left over run either whole, one each on slots 0 .. r - 1, or (HALF_TAIL: the
+// down GEMM, the 192-row inference gate|up) as 2r n-halves spread over the
+// slots, so that no workgroup runs
 // more than q tiles plus one half while r <= nslot / 2.  A tile's time is
 // dominated by its A rows and its MFMAs scale with its width, so a half takes
 // about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
-// the gate|up GEMM (K = 768), which therefore keeps whole tiles.
+// the gate|up GEMM (K = 768), whose 256-row launches therefore keep whole
+// tiles; its 192-row launches (small shards, a few tiles per CU, where the
+// remainder is a large share of the launch) take the halves.
 template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
           bool DROP, bool PADA>
 __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
@@ -1313,6 +1316,13 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #ifndef G5_GU_GM
 #define G5_GU_GM 4
 #endif
+// The 192-row inference gate|up splits its remainder tiles into n-halves (the
+// DP-8 shard's 1,152 tiles are 4.5 per CU: every slot then runs four tiles and a
+// half instead of half the slots running five): 103.3-105.0 against
+// 105.8-107.1 us, three alternating rounds on one box.
+#ifndef G5_GU192_HALF
+#define G5_GU192_HALF 1
+#endif
 #ifndef G5_DN_GM
 #define G5_DN_GM 4
 #endif
@@ -1372,8 +1382,8 @@ inline int gate_up_bm(int64_t nk, int n_experts, int K) {
 template <int MODE, bool DROP = false>
 void launch_gate_up192(unsigned grid, const GemmArgs& a, hipStream_t st) {
   hipLaunchKernelGGL(
-      (grouped_gemm_persist_kernel<192, 256, G5_GU_BK, G5_GU_STAGES, 3, G5_GU_GM, MODE, false,
-                                   DROP>),
+      (grouped_gemm_persist_kernel<192, 256, G5_GU_BK, G5_GU_STAGES, 3, G5_GU_GM, MODE,
+                                   MODE == 1 && G5_GU192_HALF, DROP>),
       dim3(grid), dim3(256), 0, st, a);
 }
 
