@@ -1158,15 +1158,14 @@ __device__ __forceinline__ void tile_loop(const GemmArgs& args, const Offsets& o
 // Persistent grouped GEMM: one workgroup per CU.  XCD x owns the contiguous
 // tile range [lo, hi) of the launch; each of its nslot workgroups runs q =
 // (hi - lo) / nslot tiles (slot s: lo + s, lo + s + nslot, ...).  The r tiles
-// left over run either whole, one each on slots 0 .. r - 1, or (HALF_TAIL: the
-// down GEMM, the 192-row inference gate|up) as 2r n-halves spread over the
-// slots, so that no workgroup runs
-// more than q tiles plus one half while r <= nslot / 2.  A tile's time is
-// dominated by its A rows and its MFMAs scale with its width, so a half takes
-// about 0.8 of a tile in the down GEMM (K = 3072) and nearly a whole tile in
-// the gate|up GEMM (K = 768), whose 256-row launches therefore keep whole
-// tiles; its 192-row launches (small shards, a few tiles per CU, where the
-// remainder is a large share of the launch) take the halves.
+// left over run either whole, one each on slots 0 .. r - 1, or (HALF_TAIL) as
+// 2r n-halves spread over the slots, so that no workgroup runs more than q
+// tiles plus one half; an XCD whose r exceeds nslot / 2 runs its remainder
+// whole.  A tile's time is dominated by its A rows and its MFMAs scale with its
+// width, so a half takes about 0.8 of a tile in the down GEMM (K = 3072) and
+// 0.86 in the gate|up GEMM (K = 768): the down GEMM always takes the halves,
+// the inference gate|up when it has a few tiles per CU (a shard's share, where
+// the remainder is a large part of the launch).
 template <int BM, int BN, int BK, int S, int NSLOT, int GM, int MODE, bool HALF_TAIL,
           bool DROP, bool PADA>
 __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
@@ -1192,27 +1191,32 @@ __device__ __forceinline__ void persist_body(const GemmArgs& args, char* smem) {
                      : int(int64_t(total) * (before + nslot) / ng);
   const int q = (hi - lo) / nslot, r = (hi - lo) % nslot;
   if constexpr (HALF_TAIL) {
-    if (q > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, false, PADA>(args, off, smem,
-                                                           Units{lo + slot, nslot, q, 0});
-    if (slot < 2 * r) {
-      // every wave's DMAs of the full pass have landed (each waited for its
-      // own) before the half pass refills the stage buffers
-      if (q > 0) __syncthreads();
-      tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, MODE, true, false, PADA>(
-          args, off, smem,
-          Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
+    // halves only while each slot gets at most one: with 2r > nslot some slots
+    // would run two halves, more than the whole remainder tile (uniform per
+    // workgroup: r and nslot depend on the XCD only)
+    if (2 * r <= nslot) {
+      if (q > 0)
+        tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, false, PADA>(
+            args, off, smem, Units{lo + slot, nslot, q, 0});
+      if (slot < 2 * r) {
+        // every wave's DMAs of the full pass have landed (each waited for its
+        // own) before the half pass refills the stage buffers
+        if (q > 0) __syncthreads();
+        tile_loop<BM, BN / 2, BN, BK, S, NSLOT, GM, MODE, true, false, PADA>(
+            args, off, smem,
+            Units{slot, nslot, (2 * r - slot + nslot - 1) / nslot, lo + q * nslot});
+      }
+      return;
     }
-  } else {
-    // Static: the remainder tile of slots s < r is lo + s + q * nslot.  (A
-    // claimed tail, the last tiles taken one at a time from an atomic counter so
-    // that faster XCDs take more, measured no faster at 36,400 tokens than this
-    // static split once its counters had to be zeroed per launch: gate|up
-    // 623.9 against 625.4 us, four alternating runs on one GPU.)
-    const Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
-    if (st.count > 0)
-      tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP, PADA>(args, off, smem, st);
   }
+  // Static: the remainder tile of slots s < r is lo + s + q * nslot.  (A
+  // claimed tail, the last tiles taken one at a time from an atomic counter so
+  // that faster XCDs take more, measured no faster at 36,400 tokens than this
+  // static split once its counters had to be zeroed per launch: gate|up
+  // 623.9 against 625.4 us, four alternating runs on one GPU.)
+  const Units st{lo + slot, nslot, q + (slot < r ? 1 : 0), 0};
+  if (st.count > 0)
+    tile_loop<BM, BN, BN, BK, S, NSLOT, GM, MODE, false, DROP, PADA>(args, off, smem, st);
 }
 
 // One workgroup per CU: up to 512 registers per lane (256 accumulators in AGPRs).
@@ -1323,6 +1327,12 @@ __global__ void cast_f32_bf16_kernel(const float* __restrict__ x, uint16_t* __re
 #ifndef G5_GU192_HALF
 #define G5_GU192_HALF 1
 #endif
+// ... and so do its 256-row launches with at most this many tiles per CU (the
+// tile count's upper bound; an EP-8 shard's two experts of 4,550 rows: 3.6):
+// EP-8 gate|up 85.9-86.2 against 87.9-88.1 us, three rounds on one box.
+#ifndef G5_GU_HALF_TILES_PER_CU
+#define G5_GU_HALF_TILES_PER_CU 8
+#endif
 #ifndef G5_DN_GM
 #define G5_DN_GM 4
 #endif
@@ -1428,6 +1438,8 @@ hipError_t launch_gate_up(const uint16_t* xb, const int32_t* perm, const int32_t
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 3, false>(pgrid, a, st);
   else if (bm192)
     launch_gate_up192<1>(pgrid, a, st);
+  else if (G5_GU192_HALF && grid <= unsigned(G5_GU_HALF_TILES_PER_CU * device_cu_count()))
+    launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, true>(pgrid, a, st);
   else
     launch_persist<256, 256, G5_GU_BK, G5_GU_STAGES, G5_GU_GM, 1, false>(pgrid, a, st);
   return hipGetLastError();
