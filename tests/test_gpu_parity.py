@@ -265,14 +265,16 @@ def test_forward_empty(cuda_device):
     assert host(r.offsets).tolist() == [0, 0, 0, 0, 0]
 
 
-@pytest.mark.parametrize("n_small,n_big", [(4550, 36400), (512, 9000), (2048, 6000)])
+@pytest.mark.parametrize("n_small,n_big",
+                         [(4550, 36400), (512, 9000), (2048, 6000), (2048, 36400)])
 def test_token_output_independent_of_batch(cuda_device, n_small, n_big):
     """A token's layer output does not depend on the other tokens of its batch: the
     first n_small tokens run alone and inside a batch of n_big give the same y bit
     for bit.  The two launches tile differently (a shard-sized batch takes 192-row
     gate|up tiles and the small-M down tiles, the large one 256 x 256 tiles and the
-    n-half tail), and every output element's MFMA chain runs
-    over k in one fixed order whatever tile computes it."""
+    n-half tail; 2,048 tokens take 256-row gate|up tiles with their remainder in
+    n-halves, 36,400 whole 256-row tiles), and every output element's MFMA chain
+    runs over k in one fixed order whatever tile computes it."""
     print(f"batch invariance n_small={n_small} n_big={n_big}", flush=True)
     inp = synth.make_layer(n_big, seed=9, dtype="bf16")
     x, wr, wgu, wd, _ = layer_tensors(inp, cuda_device)
