@@ -296,7 +296,7 @@ def bench_config4(args) -> dict:
         stack.set_fused(True)
     flops = 12 * 6 * 768 * 3072 * N * 2
     # the two fused memory-bound entry points on this batch (HIP events, 20 calls each)
-    from genet5_amd import ops
+    from genet5_amd import _lib, ops
     layer = stack.layers[0]
     x2 = x.reshape(-1, 768)
     nw = layer.norm.weight.float().contiguous()
@@ -320,6 +320,11 @@ def bench_config4(args) -> dict:
     t_norm = ev_time(lambda: ops.add_rmsnorm_router(x2, nw, 1e-6, wr, 2))
     t_addnorm = ev_time(lambda: ops.add_rmsnorm_router(x2, nw, 1e-6, wr, 2, x_add=xa))
     t_comb = ev_time(lambda: ops.combine_residual(y_perm, inv_pos, w, x2, 1.0))
+    ws4 = ops.workspace(_lib.make_shape(N, 768, 3072, 16, 2, _lib.DTYPE_BF16), dev)
+    t_route = ev_time(lambda: ops.add_rmsnorm_route(x2, nw, 1e-6, wr, 2, x_add=xa, ws=ws4,
+                                                    d_ff=3072))
+    t_unroute = ev_time(lambda: ops.dispatch(
+        ops.add_rmsnorm_router(x2, nw, 1e-6, wr, 2, x_add=xa)[2], 16, 768))
     nd2 = N * 768 * 2
     kernels = {
         "rmsnorm_router_us": t_norm * 1e6,
@@ -327,10 +332,13 @@ def bench_config4(args) -> dict:
         "add_rmsnorm_router_us": t_addnorm * 1e6,
         "add_rmsnorm_router_gbs": (4 * nd2 + N * 16) / t_addnorm / 1e9,
         "combine_residual_us": t_comb * 1e6,
+        "add_rmsnorm_route_us": t_route * 1e6,
+        "add_rmsnorm_router_then_dispatch_us": t_unroute * 1e6,
         "combine_residual_gbs": (2 * nd2 + N * 2 * 768 * 2 + N * 16) / t_comb / 1e9,
         "bytes": "rmsnorm_router: read rows, write normed, write idx/w (8 B/token each); "
                  "add_: + read x_add, write the sum; combine_residual: read y_perm (k rows), "
-                 "residual, write out, read inv_pos/w",
+                 "residual, write out, read inv_pos/w; add_rmsnorm_route: add_rmsnorm_router "
+                 "with the dispatch (two launches), against the two calls in three",
     }
     return {
         "metric": "12-block RMSNorm->MoE->residual stack tokens/s, 45.5k packed tok, 16e top-2",
@@ -342,7 +350,7 @@ def bench_config4(args) -> dict:
                                "lengths U[1000, 9000], seeded N(0, 0.02) weights per layer",
                    "n_tokens": N, "n_layers": 12, "n_sequences": len(cfg.cu_seqlens) - 1},
         "expert_gemm_tflops_incl_layer_overheads": flops / t / 1e12,
-        "blocks": "fused: g5moe_add_rmsnorm_router + dispatch + experts + g5moe_combine_residual",
+        "blocks": "fused: g5moe_add_rmsnorm_route + experts + g5moe_combine_residual",
         "unfused_ms_per_step": t_unfused * 1e3,
         "fused_kernels": kernels,
     }

@@ -37,6 +37,7 @@ EXPORTED = (
     "g5moe_expert_swiglu",
     "g5moe_combine",
     "g5moe_add_rmsnorm_router",
+    "g5moe_add_rmsnorm_route",
     "g5moe_combine_residual",
     "g5moe_rmsnorm",
     "g5moe_transpose_experts",
@@ -146,6 +147,8 @@ _SIGS = {
     "g5moe_combine": ([_P, _P, _P, _P, _SHAPE_P, _P], ctypes.c_int),
     "g5moe_add_rmsnorm_router": ([_P, _P, _P, ctypes.c_float, _P, _P, _P, _P, _P, _P, _P,
                                   _SHAPE_P, _P], ctypes.c_int),
+    "g5moe_add_rmsnorm_route": ([_P, _P, _P, ctypes.c_float] + [_P] * 12 + [_SHAPE_P, _P],
+                                ctypes.c_int),
     "g5moe_combine_residual": ([_P, _P, _P, _P, ctypes.c_float, _P, _SHAPE_P, _P],
                                ctypes.c_int),
     "g5moe_rmsnorm": ([_P, _P, _P, ctypes.c_float, _P, _P, ctypes.c_int64, ctypes.c_int32,

@@ -104,7 +104,7 @@ extern "C" {
 
 const char* g5moe_last_error(void) { return g_err; }
 
-int32_t g5moe_version(void) { return (2 << 16) | 2; }
+int32_t g5moe_version(void) { return (2 << 16) | 3; }
 
 g5moe_status g5moe_workspace_size(const g5moe_shape* shape, size_t* bytes) {
   G5_CHECK(check_shape(shape));
@@ -388,6 +388,37 @@ g5moe_status g5moe_add_rmsnorm_router(const void* x_add, const void* residual,
                                        sum_out, normed_out, topk_idx, topk_w, logits, *shape,
                                        as_stream(stream)),
                     "g5moe_add_rmsnorm_router");
+}
+
+g5moe_status g5moe_add_rmsnorm_route(const void* x_add, const void* residual,
+                                     const float* norm_weight, float eps, const void* w_router,
+                                     const float* bias, void* sum_out, void* normed_out,
+                                     int32_t* topk_idx, float* topk_w, float* logits,
+                                     int32_t* counts, int32_t* offsets, int32_t* perm,
+                                     int32_t* inv_pos, void* ws, const g5moe_shape* shape,
+                                     void* stream) {
+  G5_CHECK(check_shape(shape));
+  if (!(eps >= 0.0f)) return fail(G5MOE_ERR_INVALID_ARG, "eps must be >= 0 (got %g)", eps);
+  G5_NONNULL(counts);
+  G5_NONNULL(offsets);
+  if (shape->n_tokens > 0) {
+    G5_NONNULL(residual);
+    G5_NONNULL(norm_weight);
+    G5_NONNULL(w_router);
+    G5_NONNULL(normed_out);
+    G5_NONNULL(topk_idx);
+    G5_NONNULL(topk_w);
+    G5_NONNULL(perm);
+    G5_NONNULL(inv_pos);
+    G5_NONNULL(ws);
+  }
+  if (sum_out != nullptr && x_add == nullptr)
+    return fail(G5MOE_ERR_INVALID_ARG, "sum_out needs x_add (without it the sum is residual)");
+  return hip_status(launch_norm_route(x_add, residual, norm_weight, eps, w_router, bias, sum_out,
+                                      normed_out, topk_idx, topk_w, logits, counts, offsets,
+                                      perm, inv_pos, static_cast<char*>(ws), *shape,
+                                      as_stream(stream)),
+                    "g5moe_add_rmsnorm_route");
 }
 
 g5moe_status g5moe_rmsnorm(const void* x_add, const void* residual, const float* norm_weight,

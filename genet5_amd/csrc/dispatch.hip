@@ -343,12 +343,31 @@ hipError_t launch_dispatch(const int32_t* idx, int32_t* counts, int32_t* offsets
                            s.n_tokens * s.top_k, s.n_experts, st);
 }
 
+namespace {
+
+// The placement after a router launch with the rank pass (chunks of ct tokens,
+// ranks and chunk counts in the workspace).
+hipError_t launch_place_chunks(const int32_t* idx, const int32_t* rank, const int32_t* cc,
+                               int64_t ct, int32_t* counts, int32_t* offsets, int32_t* perm,
+                               int32_t* inv_pos, const g5moe_shape& s, hipStream_t st) {
+  const int64_t nk = s.n_tokens * s.top_k;
+  // the router's chunks: at least kMinChunkTokens tokens each, so at most the
+  // ceil(N / kMinChunkTokens) rows the workspace holds
+  const int64_t nchunk = (s.n_tokens + ct - 1) / ct;
+  const int64_t nblk = (nk + kPlaceSpan - 1) / kPlaceSpan;
+  hipLaunchKernelGGL(dispatch_place_chunks_kernel, dim3(unsigned(nblk)), dim3(kPlaceThreads), 0,
+                     st, idx, rank, cc, uint32_t(nchunk), uint32_t(ct * s.top_k), uint32_t(nk),
+                     s.n_experts, perm, inv_pos, counts, offsets);
+  return hipGetLastError();
+}
+
+}  // namespace
+
 hipError_t launch_route(const void* x, const void* wr, const float* bias, int32_t* idx,
                         float* w, float* logits, int32_t* counts, int32_t* offsets,
                         int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                         hipStream_t st) {
-  const int64_t nk = s.n_tokens * s.top_k;
-  if (nk == 0) {
+  if (s.n_tokens * s.top_k == 0) {
     hipLaunchKernelGGL(zero_counts_kernel, dim3(1), dim3(64), 0, st, counts, offsets,
                        s.n_experts);
     return hipGetLastError();
@@ -358,15 +377,29 @@ hipError_t launch_route(const void* x, const void* wr, const float* bias, int32_
   int32_t* cc = reinterpret_cast<int32_t*>(ws + L.chunk_counts);
   const hipError_t e = launch_router_rank(x, wr, bias, idx, w, logits, RankArgs{rank, cc}, s, st);
   if (e != hipSuccess) return e;
-  // the router's chunks: at least kMinChunkTokens tokens each, so at most the
-  // ceil(N / kMinChunkTokens) rows the workspace holds
-  const int64_t ct = router_chunk_tokens(s);
-  const int64_t nchunk = (s.n_tokens + ct - 1) / ct;
-  const int64_t nblk = (nk + kPlaceSpan - 1) / kPlaceSpan;
-  hipLaunchKernelGGL(dispatch_place_chunks_kernel, dim3(unsigned(nblk)), dim3(kPlaceThreads), 0,
-                     st, idx, rank, cc, uint32_t(nchunk), uint32_t(ct * s.top_k), uint32_t(nk),
-                     s.n_experts, perm, inv_pos, counts, offsets);
-  return hipGetLastError();
+  return launch_place_chunks(idx, rank, cc, router_chunk_tokens(s, false), counts, offsets, perm,
+                             inv_pos, s, st);
+}
+
+hipError_t launch_norm_route(const void* x_add, const void* residual, const float* norm_w,
+                             float eps, const void* wr, const float* bias, void* sum_out,
+                             void* normed_out, int32_t* idx, float* w, float* logits,
+                             int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv_pos,
+                             char* ws, const g5moe_shape& s, hipStream_t st) {
+  if (s.n_tokens * s.top_k == 0) {
+    hipLaunchKernelGGL(zero_counts_kernel, dim3(1), dim3(64), 0, st, counts, offsets,
+                       s.n_experts);
+    return hipGetLastError();
+  }
+  const WorkspaceLayout L = workspace_layout(s);
+  int32_t* rank = reinterpret_cast<int32_t*>(ws + L.rank);
+  int32_t* cc = reinterpret_cast<int32_t*>(ws + L.chunk_counts);
+  const hipError_t e = launch_norm_router_rank(x_add, residual, norm_w, eps, wr, bias, sum_out,
+                                               normed_out, idx, w, logits, RankArgs{rank, cc},
+                                               s, st);
+  if (e != hipSuccess) return e;
+  return launch_place_chunks(idx, rank, cc, router_chunk_tokens(s, true), counts, offsets, perm,
+                             inv_pos, s, st);
 }
 
 namespace {

@@ -112,15 +112,22 @@ struct RankArgs {
 hipError_t launch_router(const void* x, const void* wr, const float* bias, int32_t* idx,
                          float* w, float* logits, const g5moe_shape& s, hipStream_t st);
 // The router with the dispatch's rank pass over chunks of
-// router_chunk_tokens(s) tokens (the same partition the launch uses).
+// router_chunk_tokens(s, false) tokens (the same partition the launch uses).
 hipError_t launch_router_rank(const void* x, const void* wr, const float* bias, int32_t* idx,
                               float* w, float* logits, const RankArgs& ra, const g5moe_shape& s,
                               hipStream_t st);
-int64_t router_chunk_tokens(const g5moe_shape& s);
+// Tokens per rank-pass chunk: of the plain router (norm = false) or of the
+// add + RMSNorm + router (norm = true), whose grids differ.
+int64_t router_chunk_tokens(const g5moe_shape& s, bool norm);
 hipError_t launch_norm_router(const void* x_add, const void* residual, const float* norm_w,
                               float eps, const void* wr, const float* bias, void* sum_out,
                               void* normed_out, int32_t* idx, float* w, float* logits,
                               const g5moe_shape& s, hipStream_t st);
+// launch_norm_router with the rank pass over chunks of router_chunk_tokens(s, true).
+hipError_t launch_norm_router_rank(const void* x_add, const void* residual, const float* norm_w,
+                                   float eps, const void* wr, const float* bias, void* sum_out,
+                                   void* normed_out, int32_t* idx, float* w, float* logits,
+                                   const RankArgs& ra, const g5moe_shape& s, hipStream_t st);
 hipError_t launch_rmsnorm(const void* x_add, const void* residual, const float* norm_w, float eps,
                           void* sum_out, void* normed_out, int64_t n, int d, int dtype,
                           hipStream_t st);
@@ -136,6 +143,13 @@ hipError_t launch_route(const void* x, const void* wr, const float* bias, int32_
                         float* w, float* logits, int32_t* counts, int32_t* offsets,
                         int32_t* perm, int32_t* inv_pos, char* ws, const g5moe_shape& s,
                         hipStream_t st);
+// The same with the residual add + RMSNorm in front (g5moe_add_rmsnorm_route):
+// launch_norm_router_rank, then the placement.
+hipError_t launch_norm_route(const void* x_add, const void* residual, const float* norm_w,
+                             float eps, const void* wr, const float* bias, void* sum_out,
+                             void* normed_out, int32_t* idx, float* w, float* logits,
+                             int32_t* counts, int32_t* offsets, int32_t* perm, int32_t* inv_pos,
+                             char* ws, const g5moe_shape& s, hipStream_t st);
 // g5moe_dispatch with its buffers in the library's per-device scratch array
 // (n_tokens * top_k <= kNoAllocMaxAssignments).
 hipError_t launch_dispatch_noalloc(const int32_t* idx, int32_t* counts, int32_t* offsets,

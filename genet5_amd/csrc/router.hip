@@ -757,8 +757,8 @@ hipError_t launch_router(const void* x, const void* wr, const float* bias, int32
   return launch_mode<0>(x, wr, bias, idx, w, logits, NormArgs{}, s, st);
 }
 
-int64_t router_chunk_tokens(const g5moe_shape& s) {
-  return 2 * router_grid<0>(s.n_tokens).tpp;
+int64_t router_chunk_tokens(const g5moe_shape& s, bool norm) {
+  return 2 * (norm ? router_grid<1>(s.n_tokens).tpp : router_grid<0>(s.n_tokens).tpp);
 }
 
 hipError_t launch_router_rank(const void* x, const void* wr, const float* bias, int32_t* idx,
@@ -777,6 +777,17 @@ hipError_t launch_norm_router(const void* x_add, const void* residual, const flo
   if (x_add != nullptr)
     return launch_mode<2>(residual, wr, bias, idx, w, logits, na, s, st);
   return launch_mode<1>(residual, wr, bias, idx, w, logits, na, s, st);
+}
+
+hipError_t launch_norm_router_rank(const void* x_add, const void* residual, const float* norm_w,
+                                   float eps, const void* wr, const float* bias, void* sum_out,
+                                   void* normed_out, int32_t* idx, float* w, float* logits,
+                                   const RankArgs& ra, const g5moe_shape& s, hipStream_t st) {
+  if (s.n_tokens == 0) return hipSuccess;
+  const NormArgs na{x_add, norm_w, eps, sum_out, normed_out};
+  if (x_add != nullptr)
+    return launch_mode<2, true>(residual, wr, bias, idx, w, logits, na, s, st, ra);
+  return launch_mode<1, true>(residual, wr, bias, idx, w, logits, na, s, st, ra);
 }
 
 

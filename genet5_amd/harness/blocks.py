@@ -53,8 +53,9 @@ class RMSNorm(nn.Module):
 class MoEBlock(nn.Module):
     """h <- h + alpha * MoE(RMSNorm(h)).
 
-    fused (default): MoEFeedForward.residual_block — the RMSNorm and the router in
-    one pass (g5moe_add_rmsnorm_router) and the residual add inside the combine
+    fused (default): MoEFeedForward.residual_block — the RMSNorm, the router and
+    the dispatch's ranks in one pass (g5moe_add_rmsnorm_route) and the residual add
+    inside the combine
     (g5moe_combine_residual).  fused = False: the reference-shaped composition of
     this module's torch RMSNorm, the MoE module and a torch residual add."""
 

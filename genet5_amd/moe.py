@@ -396,10 +396,11 @@ class MoEFeedForward(nn.Module):
 
         i.e. `fused_add_rmsnorm(x_add, residual, norm2.weight, eps)` then
         `hidden + ff(normed) * alpha` (lib/blocks/encoder.py:80-89,
-        lib/blocks/_component.py:17-20), as g5moe_add_rmsnorm_router ->
-        g5moe_dispatch -> g5moe_expert_swiglu -> g5moe_combine_residual: the
-        normalised rows feed the router in the same pass, and the layer output is
-        added into the residual inside the combine.  The RMSNorm follows the C
+        lib/blocks/_component.py:17-20), as g5moe_add_rmsnorm_route (add + norm +
+        router with the dispatch's ranks, then the placement) ->
+        g5moe_expert_swiglu -> g5moe_combine_residual: the normalised rows feed the
+        router in the same pass, and the layer output is added into the residual
+        inside the combine.  The RMSNorm follows the C
         ABI's reduction order (fp32, correctly rounded sqrt and division).
 
         The fused kernels build no autograd graph and apply no dropout.  When a
@@ -423,10 +424,9 @@ class MoEFeedForward(nn.Module):
         xa2 = None if x_add is None else x_add.reshape(-1, d).to(r2.dtype).contiguous()
         w_router = self.router.weight.to(r2.dtype).contiguous()
         nw = norm_weight.detach().to(torch.float32).contiguous()
-        normed, ssum, idx, w = ops.add_rmsnorm_router(r2, nw, eps, w_router, self.top_k,
-                                                      x_add=xa2, bias=self.router_bias)
+        normed, ssum, idx, w, _, offsets, perm, inv_pos = ops.add_rmsnorm_route(
+            r2, nw, eps, w_router, self.top_k, x_add=xa2, bias=self.router_bias)
         base = ssum if xa2 is not None else r2
-        _, offsets, perm, inv_pos = ops.dispatch(idx, self.num_experts, d)
         wgu, wd = self._expert_weights()
         y_perm = ops.expert_swiglu(normed, perm, offsets, wgu, wd, self.top_k)
         out = ops.combine_residual(y_perm, inv_pos, w, base, alpha)

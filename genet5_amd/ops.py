@@ -248,6 +248,50 @@ def add_rmsnorm_router(residual: torch.Tensor, norm_weight: torch.Tensor, eps: f
     return out + (logits,) if return_logits else out
 
 
+def add_rmsnorm_route(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                      w_router: torch.Tensor, top_k: int,
+                      x_add: Optional[torch.Tensor] = None,
+                      bias: Optional[torch.Tensor] = None, return_logits: bool = False,
+                      ws: Optional[torch.Tensor] = None, d_ff: int = 128):
+    """add_rmsnorm_router then dispatch in two launches (g5moe_add_rmsnorm_route: the
+    norm-and-router kernel forms the dispatch's ranks) -> (normed, sum_or_None,
+    topk_idx, topk_w, counts, offsets, perm, inv_pos[, logits]), the same values as
+    the two calls.  ws: a workspace for the shape (N, d, d_ff, E, top_k), allocated
+    here when None."""
+    dev = _check_device(residual)
+    N, d = residual.shape
+    E = w_router.shape[0]
+    dt = residual.dtype
+    _require(residual, "residual", (N, d), dt, dev)
+    if x_add is not None:
+        _require(x_add, "x_add", (N, d), dt, dev)
+    _require(norm_weight, "norm_weight", (d,), torch.float32, dev)
+    _require(w_router, "w_router", (E, d), dt, dev)
+    if bias is not None:
+        _require(bias, "bias", (E,), torch.float32, dev)
+    shape = _lib.make_shape(N, d, d_ff, E, top_k, _dtype_code(dt))
+    if ws is None:
+        ws = workspace(shape, dev)
+    elif ws.numel() < _lib.workspace_size(shape) or ws.device != dev:
+        raise ValueError("ws is smaller than the shape's workspace or on another device")
+    i32 = dict(dtype=torch.int32, device=dev)
+    normed = torch.empty((N, d), dtype=dt, device=dev)
+    ssum = torch.empty((N, d), dtype=dt, device=dev) if x_add is not None else None
+    idx = torch.empty((N, top_k), **i32)
+    w = torch.empty((N, top_k), dtype=torch.float32, device=dev)
+    logits = torch.empty((N, E), dtype=torch.float32, device=dev) if return_logits else None
+    counts = torch.empty((E,), **i32)
+    offsets = torch.empty((E + 1,), **i32)
+    perm = torch.empty((N * top_k,), **i32)
+    inv_pos = torch.empty((N * top_k,), **i32)
+    _lib.call("g5moe_add_rmsnorm_route", _ptr(x_add), _ptr(residual), _ptr(norm_weight),
+              ctypes.c_float(eps), _ptr(w_router), _ptr(bias), _ptr(ssum), _ptr(normed),
+              _ptr(idx), _ptr(w), _ptr(logits), _ptr(counts), _ptr(offsets), _ptr(perm),
+              _ptr(inv_pos), _ptr(ws), ctypes.byref(shape), _stream(dev))
+    out = (normed, ssum, idx, w, counts, offsets, perm, inv_pos)
+    return out + (logits,) if return_logits else out
+
+
 def rmsnorm(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
             x_add: Optional[torch.Tensor] = None, return_sum: bool = False):
     """(Residual add +) RMSNorm of [N, d] rows (g5moe_rmsnorm), the same arithmetic as

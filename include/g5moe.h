@@ -88,7 +88,9 @@ const char* g5moe_last_error(void);
  * written as zeros).  2.1: the gate|up launches share their tiles among the XCDs
  * by measured speed (the pinned busy-time buffers of the Conventions); no
  * signature changed.  2.2: g5moe_route (router and dispatch in two launches,
- * used by g5moe_forward); the workspace gains its per-chunk count region. */
+ * used by g5moe_forward); the workspace gains its per-chunk count region.
+ * 2.3: g5moe_add_rmsnorm_route (the same for the residual add + RMSNorm +
+ * router). */
 int32_t g5moe_version(void);
 
 /* Bytes of workspace the stage entry points and g5moe_forward need for `shape`.
@@ -284,6 +286,25 @@ g5moe_status g5moe_add_rmsnorm_router(const void* x_add, const void* residual,
                                       const void* w_router, const float* bias, void* sum_out,
                                       void* normed_out, int32_t* topk_idx, float* topk_w,
                                       float* logits, const g5moe_shape* shape, void* stream);
+
+/* Residual add + RMSNorm + router and dispatch together: the outputs of
+ * g5moe_add_rmsnorm_router followed by g5moe_dispatch on its topk_idx, bit for
+ * bit, in two launches instead of three (the norm-and-router kernel also forms
+ * the dispatch's stable ranks inside chunks of its own token partition, and a
+ * placement kernel turns the chunk counts into positions, as in g5moe_route).
+ * Replaces the same reference step as g5moe_add_rmsnorm_router
+ * (lib/blocks/_component.py:17-20 at lib/blocks/encoder.py:80-83) followed by the
+ * dispatch of the MoE that consumes normed_out; new stage.
+ *   arguments as g5moe_add_rmsnorm_router and g5moe_dispatch;
+ *   ws as g5moe_workspace_size.  With n_tokens = 0 only counts and offsets are
+ *   written (zeros). */
+g5moe_status g5moe_add_rmsnorm_route(const void* x_add, const void* residual,
+                                     const float* norm_weight, float eps, const void* w_router,
+                                     const float* bias, void* sum_out, void* normed_out,
+                                     int32_t* topk_idx, float* topk_w, float* logits,
+                                     int32_t* counts, int32_t* offsets, int32_t* perm,
+                                     int32_t* inv_pos, void* ws, const g5moe_shape* shape,
+                                     void* stream);
 
 /* Residual add + RMSNorm alone, with g5moe_add_rmsnorm_router's arithmetic (its
  * normed rows bit for bit): the encoder block's attention pre-norm
