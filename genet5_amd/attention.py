@@ -28,7 +28,7 @@ from typing import List, Optional, Tuple
 import torch
 import torch.nn as nn
 
-from . import _lib
+from . import _lib, ops
 from .ops import _check_device, _ptr, _stream
 
 HEAD_DIM = 64
@@ -96,7 +96,9 @@ def attn_varlen_fwd(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         if alibi_slopes.device != dev or alibi_slopes.dtype != torch.float32 \
                 or tuple(alibi_slopes.shape) != (H,) or not alibi_slopes.is_contiguous():
             raise ValueError(f"alibi_slopes must be a contiguous float32 [{H}] tensor on {dev}")
-    out = torch.empty((T, H, HEAD_DIM), dtype=torch.bfloat16, device=dev)
+    # ops.ROW_PAD rows of slack after the output, so that the output projection's
+    # grouped GEMM (ops.linear) reads it in place
+    out = torch.empty((T + ops.ROW_PAD, H, HEAD_DIM), dtype=torch.bfloat16, device=dev)[:T]
     lse = torch.empty((H, T), dtype=torch.float32, device=dev) if return_lse else None
     shape = _lib.AttnShape(
         cu_seqlens.numel() - 1, int(max_seqlen), T, H, Hkv, HEAD_DIM, 0,

@@ -37,7 +37,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from .. import attention
+from .. import attention, ops
 from ..attention import alibi_slopes  # noqa: F401  (re-exported for the harness)
 from ..moe import MoEFeedForward
 from .blocks import RMSNorm
@@ -100,6 +100,20 @@ class ALiBiSelfAttention(nn.Module):
                                              scale=1.0 / math.sqrt(self.head_dim))
         return self.o(out.transpose(1, 2).reshape(B, L, D))
 
+    def project(self, x2d: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+        """x2d @ weight^T (no bias): the grouped GEMM as a one-expert product
+        (ops.linear) for bf16 rows on the GPU when no gradient is needed, F.linear
+        (hipBLASLt) otherwise.  At this encoder's shapes the grouped GEMM is the
+        faster of the two (36,400 rows, K = 768: N = 2,304 in 127 against 140 us,
+        N = 768 in 47 against 55 us)."""
+        needs_grad = torch.is_grad_enabled() and (x2d.requires_grad or weight.requires_grad)
+        K, N = x2d.shape[1], weight.shape[0]
+        if (not needs_grad and x2d.is_cuda and x2d.dtype == torch.bfloat16
+                and weight.dtype == torch.bfloat16 and K % 64 == 0 and K >= 128
+                and N % 128 == 0 and weight.is_contiguous()):
+            return ops.linear(x2d, weight)
+        return F.linear(x2d, weight)
+
     def qkv_weight(self) -> torch.Tensor:
         """[3D, D] concatenation of the q, k and v weights, rebuilt when any changes."""
         key = tuple((p.data_ptr(), p._version, p.dtype) for p in
@@ -113,7 +127,7 @@ class ALiBiSelfAttention(nn.Module):
         B, L, D = h.shape
         H, hd = self.num_heads, self.head_dim
         # one projection for q, k and v; the kernel reads them as strided views
-        qkv = F.linear(h, self.qkv_weight()).view(B * L, 3, H, hd)
+        qkv = self.project(h.reshape(B * L, D), self.qkv_weight()).view(B * L, 3, H, hd)
         q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
         if cu_seqlens is None:
             key = (B, L, h.device)
@@ -129,7 +143,7 @@ class ALiBiSelfAttention(nn.Module):
         out = attention.flash_attn_varlen_func(q, k, v, cu, cu, max_len, max_len,
                                                softmax_scale=1.0 / math.sqrt(hd),
                                                alibi_slopes=self.slopes_on(h.device))
-        return self.o(out.view(B, L, D))
+        return self.project(out.view(B * L, D), self.o.weight).view(B, L, D)
 
     def forward(self, h: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None) -> torch.Tensor:
         if self.backend == "hip":
@@ -203,7 +217,14 @@ class GeneT5MoE(nn.Module):
         h = self.embed(input_ids)
         for layer in self.layers:
             h = layer(h, cu_seqlens)
-        return {"logits": self.lm_head(self.final_norm(h))}
+        hn = self.final_norm(h)
+        if self.layers and self.layers[0].self_attn.backend == "hip":
+            # the tied LM head through the same projection as the attention's
+            lead = hn.shape[:-1]
+            w = self.lm_head.weight
+            return {"logits": self.layers[0].self_attn.project(hn.reshape(-1, hn.shape[-1]),
+                                                               w).view(*lead, w.shape[0])}
+        return {"logits": self.lm_head(hn)}
 
 
 def linear_unmask_schedule(num_steps: int, eps: float = 1e-3) -> List[float]:

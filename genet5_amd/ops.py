@@ -296,7 +296,8 @@ def rmsnorm(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
             x_add: Optional[torch.Tensor] = None, return_sum: bool = False):
     """(Residual add +) RMSNorm of [N, d] rows (g5moe_rmsnorm), the same arithmetic as
     add_rmsnorm_router's normed rows.  Returns normed, or (normed, x_add + residual)
-    with return_sum (x_add given)."""
+    with return_sum (x_add given).  normed is allocated with empty_row_padded (it is
+    the next projection's input)."""
     dev = _check_device(residual)
     N, d = residual.shape
     dt = residual.dtype
@@ -306,7 +307,7 @@ def rmsnorm(residual: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     elif return_sum:
         raise ValueError("return_sum needs x_add")
     _require(norm_weight, "norm_weight", (d,), torch.float32, dev)
-    normed = torch.empty((N, d), dtype=dt, device=dev)
+    normed = empty_row_padded(N, d, dt, dev)
     ssum = torch.empty((N, d), dtype=dt, device=dev) if return_sum else None
     _lib.call("g5moe_rmsnorm", _ptr(x_add), _ptr(residual), _ptr(norm_weight), ctypes.c_float(eps),
               _ptr(ssum), _ptr(normed), N, d, _dtype_code(dt), _stream(dev))
@@ -504,6 +505,54 @@ def grouped_gemm(a_padded: torch.Tensor, rows: int, offsets: torch.Tensor,
     _lib.call("g5moe_grouped_gemm", _ptr(a_padded), _ptr(offsets), _ptr(b), _ptr(c), rows, K,
               n_out, E, _stream(dev))
     return c
+
+
+def empty_row_padded(rows: int, cols: int, dtype: torch.dtype,
+                     device: torch.device) -> torch.Tensor:
+    """An uninitialised [rows, cols] tensor whose storage holds ROW_PAD more rows after
+    its last, so that linear() can read it as its A operand without a copy."""
+    return torch.empty((rows + ROW_PAD, cols), dtype=dtype, device=device)[:rows]
+
+
+def _has_row_pad(x: torch.Tensor) -> bool:
+    """x is a contiguous 2-D tensor whose storage extends ROW_PAD rows past its end."""
+    if x.dim() != 2 or not x.is_contiguous():
+        return False
+    need = (x.storage_offset() + (x.shape[0] + ROW_PAD) * x.shape[1]) * x.element_size()
+    return x.untyped_storage().nbytes() >= need
+
+
+_ROW_OFFSETS: dict = {}
+
+
+def linear(x2d: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """x2d [M, K] @ weight[N, K]^T -> bf16 [M, N], as F.linear without bias, on the
+    grouped GEMM with one expert (fp32 accumulate in a fixed k order, one rounding).
+    K a multiple of 64 (>= 128), N a multiple of 128, bf16 operands.  The GEMM reads
+    ROW_PAD rows past A's last one: a tensor from empty_row_padded (or any contiguous
+    one whose storage extends that far) is read in place, any other is copied into
+    such a buffer first.  No autograd."""
+    dev = _check_device(x2d)
+    M, K = x2d.shape
+    N = weight.shape[0]
+    _require(weight, "weight", (N, K), torch.bfloat16, dev)
+    if x2d.dtype != torch.bfloat16:
+        raise TypeError(f"x has dtype {x2d.dtype}; linear takes bfloat16")
+    if not _has_row_pad(x2d):
+        xp = empty_row_padded(M, K, torch.bfloat16, dev)
+        xp.copy_(x2d)
+        x2d = xp
+    key = (dev, M)
+    off = _ROW_OFFSETS.get(key)
+    if off is None:
+        off = torch.tensor([0, M], dtype=torch.int32, device=dev)
+        if len(_ROW_OFFSETS) > 64:
+            _ROW_OFFSETS.clear()
+        _ROW_OFFSETS[key] = off
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+    _lib.call("g5moe_grouped_gemm", _ptr(x2d), _ptr(off), _ptr(weight), _ptr(y), M, K, N, 1,
+              _stream(dev))
+    return y
 
 
 def grouped_gemm_padded(a_pad: torch.Tensor, kmax: int, rows: int, offsets: torch.Tensor,

@@ -6,7 +6,8 @@ fused blocks) on 8 sequences of 4,550 tokens (2,275 prefix + 2,275 [MASK]), and 
 One forward of the unmasking run's first input with hooks; for each of the 12
 layers, on the inputs that forward actually produced:
   * attention: the hooked attention output is the HIP kernel's core output
-    through the o projection (recomputed bit for bit), and that core output is
+    through the o projection (the module's own projection, ops.linear: recomputed
+    bit for bit), and that core output is
     within the attention bar of the float64 oracle (oracle.attention_varlen) on
     sampled query rows of every sequence (block and diagonal boundaries, both
     ends, random rows);
@@ -20,7 +21,6 @@ untouched, no [MASK] left."""
 import numpy as np
 import pytest
 import torch
-import torch.nn.functional as F
 
 import oracle
 from genet5_amd import attention, ops
@@ -87,12 +87,14 @@ def test_config5_full_size_per_layer(cuda_device):
         sa = layer.self_attn
         with torch.no_grad():
             # attention core on this layer's actual normed input
-            qkv = F.linear(attn_in[li], sa.qkv_weight()).view(B * L, 3, H, HD)
+            qkv = sa.project(attn_in[li].reshape(B * L, D), sa.qkv_weight()).view(B * L, 3, H,
+                                                                                   HD)
             q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
             core = attention.flash_attn_varlen_func(q, k, v, cu, cu, L, L,
                                                     softmax_scale=1.0 / 8.0,
                                                     alibi_slopes=sa.slopes_on(cuda_device))
-            assert torch.equal(sa.o(core.view(B, L, D)), attn_out[li])
+            assert torch.equal(sa.project(core.view(B * L, D), sa.o.weight).view(B, L, D),
+                               attn_out[li])
         sl = np.asarray(sa.slopes, np.float64)
         ref_a = oracle.attention_varlen(q.float().cpu().numpy(), k.float().cpu().numpy(),
                                         v.float().cpu().numpy(), cu_np, 1.0 / 8.0, sl, rows=rows)

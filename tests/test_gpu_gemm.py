@@ -127,3 +127,27 @@ def test_xcd_balanced_launches_equal_the_first(cuda_device):
             torch.cuda.synchronize()
             for a, r in zip(t, t0):
                 assert torch.equal(a, r), f"training forward after {i}"
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 768, 128), (700, 768, 768), (36400, 768, 2304),
+                                   (5000, 256, 4096), (0, 768, 768)])
+def test_linear_one_expert_product(cuda_device, M, K, N):
+    """ops.linear (the grouped GEMM as a one-expert product, the config-5 encoder's
+    projections): within bf16 rounding of a float32 product; bit-identical whether A
+    is read in place (padded storage) or copied into a padded buffer first."""
+    print(f"linear M={M} K={K} N={N}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M + K + N)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(cuda_device)
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).to(cuda_device)
+    xp = ops.empty_row_padded(M, K, torch.bfloat16, cuda_device)
+    xp.copy_(x)
+    assert ops._has_row_pad(xp) and (M == 0 or not ops._has_row_pad(x))
+    y1 = ops.linear(x, w)
+    y2 = ops.linear(xp, w)
+    torch.cuda.synchronize()
+    assert y1.shape == (M, N) and torch.equal(y1.view(torch.int16), y2.view(torch.int16))
+    if M:
+        ref = x.float() @ w.float().t()
+        err = (y1.float() - ref).abs()
+        # one bf16 rounding of an fp32 sum: |err| <= 2^-8 |ref| (plus fp32 order noise)
+        assert (err <= ref.abs() * 2.0 ** -8 + 1e-3).all()
