@@ -266,11 +266,45 @@ class FlashAttention(nn.Module):
             self._slopes_dev[device] = t
         return t
 
+    def qkv_weight(self) -> torch.Tensor:
+        """[H*hd + 2*Hkv*hd, D] concatenation of the q, k and v weights, rebuilt when
+        any of them changes."""
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in
+                    (self.q.weight, self.k.weight, self.v.weight))
+        if getattr(self, "_qkv_key", None) != key:
+            self._qkv = torch.cat([self.q.weight, self.k.weight, self.v.weight]).detach()
+            self._qkv_key = key
+        return self._qkv
+
+    def _fused_projections(self, hidden_states: torch.Tensor) -> bool:
+        """In inference (no gradient) with bf16 on the GPU, q, k and v come from one
+        product and o from another on the grouped GEMM (ops.linear), faster than
+        three nn.Linear calls at GeneT5's shapes; the module's parameters, outputs'
+        shapes and meaning are unchanged (values differ from nn.Linear's only by the
+        bf16 rounding of a different fp32 summation order)."""
+        D = hidden_states.shape[-1]
+        nq = self.num_heads * self.head_dim + 2 * self.kv_dim
+        needs_grad = torch.is_grad_enabled() and (
+            hidden_states.requires_grad or any(p.requires_grad for p in self.parameters()))
+        return (not needs_grad and hidden_states.is_cuda
+                and hidden_states.dtype == torch.bfloat16
+                and all(p.dtype == torch.bfloat16 for p in self.parameters())
+                and D % 64 == 0 and D >= 128 and nq % 128 == 0 and D % 128 == 0
+                and self.num_heads * self.head_dim >= 128)
+
     def forward(self, hidden_states, cu_seqlens=None, max_seqlen=None):
         B, L, _ = hidden_states.shape
-        q = self.q(hidden_states).view(B * L, self.num_heads, self.head_dim)
-        k = self.k(hidden_states).view(B * L, self.num_kv_heads, self.head_dim)
-        v = self.v(hidden_states).view(B * L, self.num_kv_heads, self.head_dim)
+        fused = self._fused_projections(hidden_states)
+        if fused:
+            hq = self.num_heads * self.head_dim
+            qkv = ops.linear(hidden_states.reshape(B * L, -1), self.qkv_weight())
+            q = qkv[:, :hq].view(B * L, self.num_heads, self.head_dim)
+            k = qkv[:, hq:hq + self.kv_dim].view(B * L, self.num_kv_heads, self.head_dim)
+            v = qkv[:, hq + self.kv_dim:].view(B * L, self.num_kv_heads, self.head_dim)
+        else:
+            q = self.q(hidden_states).view(B * L, self.num_heads, self.head_dim)
+            k = self.k(hidden_states).view(B * L, self.num_kv_heads, self.head_dim)
+            v = self.v(hidden_states).view(B * L, self.num_kv_heads, self.head_dim)
         drop_p = self.dropout.p if self.training else 0.0
         if cu_seqlens is None:
             cu_seqlens = _uniform_cu_seqlens(B, L, hidden_states.device)
@@ -279,5 +313,9 @@ class FlashAttention(nn.Module):
                                      dropout_p=drop_p, softmax_scale=self.softmax_scale,
                                      causal=False,
                                      alibi_slopes=self.alibi_slopes(hidden_states.device))
-        out = self.o(out.reshape(B, L, self.num_heads * self.head_dim))
+        if fused:
+            out = ops.linear(out.reshape(B * L, self.num_heads * self.head_dim),
+                             self.o.weight).view(B, L, -1)
+        else:
+            out = self.o(out.reshape(B, L, self.num_heads * self.head_dim))
         return self.dropout(out), None

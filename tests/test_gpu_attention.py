@@ -14,7 +14,7 @@ import pytest
 import torch
 
 import oracle
-from genet5_amd import attention
+from genet5_amd import attention, ops
 from genet5_amd.attention import alibi_slopes
 
 pytestmark = pytest.mark.gpu
@@ -167,10 +167,12 @@ def test_flash_attn_func_and_module(cuda_device):
     with torch.no_grad():
         out, none = m(h, cu_seqlens=cu, max_seqlen=L)
         out_b, _ = m(h.view(3, L, 768))
-        # reference composition: projections in torch, fp32 attention per sequence
-        qq = m.q(h).view(3 * L, 12, 64)
-        kk = m.k(h).view(3 * L, 12, 64)
-        vv = m.v(h).view(3 * L, 12, 64)
+        # reference composition: the module's own inference projections (one fused
+        # q|k|v product on ops.linear), fp32 attention per sequence
+        qkv = ops.linear(h.reshape(3 * L, 768), m.qkv_weight())
+        qq = qkv[:, :768].view(3 * L, 12, 64)
+        kk = qkv[:, 768:1536].view(3 * L, 12, 64)
+        vv = qkv[:, 1536:].view(3 * L, 12, 64)
     assert none is None and out.shape == h.shape
     assert torch.equal(out.view(3, L, 768), out_b)
     ref = oracle.attention_varlen(qq.float().cpu().numpy(), kk.float().cpu().numpy(),
@@ -180,8 +182,19 @@ def test_flash_attn_func_and_module(cuda_device):
     mx, mean = errs(attn, ref)
     assert mx <= MAX_TOL and mean <= MEAN_TOL, (mx, mean)
     with torch.no_grad():
-        ref_out = m.o(attn.reshape(1, 3 * L, 768))
+        ref_out = ops.linear(attn.reshape(3 * L, 768), m.o.weight).view(1, 3 * L, 768)
     assert torch.equal(out, ref_out)
+    # with a gradient the projections are the nn.Linear modules (hipBLASLt): the
+    # same values up to the bf16 rounding of another fp32 summation order
+    with torch.enable_grad():
+        hg = h.clone().requires_grad_(True)
+        try:
+            out_g, _ = m(hg, cu_seqlens=cu, max_seqlen=L)
+        except NotImplementedError:
+            out_g = None  # an inference-only kernel may refuse the autograd path
+    if out_g is not None:
+        d = (out_g.detach().float() - out.float()).abs()
+        assert d.max().item() <= 5e-2 * out.float().abs().max().item()
 
 
 def test_harness_attention_backends_agree(cuda_device):
