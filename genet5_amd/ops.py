@@ -545,7 +545,11 @@ def linear(x2d: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     key = (dev, M)
     off = _ROW_OFFSETS.get(key)
     if off is None:
-        off = torch.tensor([0, M], dtype=torch.int32, device=dev)
+        # [0, M] written by fill kernels (no host-to-device copy, so a first call
+        # under graph capture works too)
+        off = torch.empty((2,), dtype=torch.int32, device=dev)
+        off[:1].fill_(0)
+        off[1:].fill_(M)
         if len(_ROW_OFFSETS) > 64:
             _ROW_OFFSETS.clear()
         _ROW_OFFSETS[key] = off
