@@ -546,13 +546,16 @@ def linear(x2d: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
     off = _ROW_OFFSETS.get(key)
     if off is None:
         # [0, M] written by fill kernels (no host-to-device copy, so a first call
-        # under graph capture works too)
+        # under graph capture works too).  Under capture the fills are only
+        # recorded (the graph writes the values before its GEMM reads them), so
+        # that tensor is the graph's own and is not cached for eager calls.
         off = torch.empty((2,), dtype=torch.int32, device=dev)
         off[:1].fill_(0)
         off[1:].fill_(M)
-        if len(_ROW_OFFSETS) > 64:
-            _ROW_OFFSETS.clear()
-        _ROW_OFFSETS[key] = off
+        if not torch.cuda.is_current_stream_capturing():
+            if len(_ROW_OFFSETS) > 64:
+                _ROW_OFFSETS.clear()
+            _ROW_OFFSETS[key] = off
     y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
     _lib.call("g5moe_grouped_gemm", _ptr(x2d), _ptr(off), _ptr(weight), _ptr(y), M, K, N, 1,
               _stream(dev))
