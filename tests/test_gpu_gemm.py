@@ -151,3 +151,30 @@ def test_linear_one_expert_product(cuda_device, M, K, N):
         err = (y1.float() - ref).abs()
         # one bf16 rounding of an fp32 sum: |err| <= 2^-8 |ref| (plus fp32 order noise)
         assert (err <= ref.abs() * 2.0 ** -8 + 1e-3).all()
+
+
+def test_linear_first_call_under_graph_capture(cuda_device):
+    """ops.linear's first call for a row count made under HIP graph capture (its
+    [0, M] offsets then exist only in the graph): every replay, with eager calls of
+    the same shape between them, equals the eager product bit for bit."""
+    print("linear under graph capture", flush=True)
+    M, K, N = 1237, 768, 768
+    g = torch.Generator(device="cpu").manual_seed(3)
+    xp = ops.empty_row_padded(M, K, torch.bfloat16, cuda_device)
+    xp.copy_(torch.randn(M, K, generator=g).to(torch.bfloat16))
+    w = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16).to(cuda_device)
+    assert (cuda_device, M) not in ops._ROW_OFFSETS
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream(cuda_device)
+    side.wait_stream(torch.cuda.current_stream(cuda_device))
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            y = ops.linear(xp, w)
+    torch.cuda.current_stream(cuda_device).wait_stream(side)
+    assert (cuda_device, M) not in ops._ROW_OFFSETS
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = ops.linear(xp, w)
+        torch.cuda.synchronize()
+        assert torch.equal(y.view(torch.int16), eager.view(torch.int16))
