@@ -264,3 +264,26 @@ def test_key_bounds_equal_dense(cuda_device, scale):
                                   v.float().cpu().numpy(), cu, 0.125, alibi_slopes(H), rows=rows)
     mx, mean = errs(out_s, ref, rows)
     assert mx <= MAX_TOL and mean <= MEAN_TOL, (mx, mean)
+
+
+@pytest.mark.parametrize("kv_heads", [12, 4])
+def test_flash_attention_module_fused_projections(cuda_device, kv_heads):
+    """The drop-in FlashAttention module in inference (one fused q|k|v product and
+    the o product on ops.linear), with and without GQA, against the same module
+    with its nn.Linear projections (forced): equal up to the bf16 rounding of the
+    projections' different fp32 summation orders."""
+    print(f"FlashAttention fused projections kv_heads={kv_heads}", flush=True)
+    torch.manual_seed(23)
+    cfg = attention.FlashAttentionConfig(embed_dim=768, num_heads=12, num_kv_heads=kv_heads)
+    m = attention.FlashAttention(cfg).to(cuda_device).to(torch.bfloat16).eval()
+    h = torch.randn(2, 1000, 768, device=cuda_device).to(torch.bfloat16)
+    with torch.no_grad():
+        assert m._fused_projections(h)
+        fused, _ = m(h)
+        m._fused_projections = lambda x: False
+        plain, _ = m(h)
+    torch.cuda.synchronize()
+    d = (fused.float() - plain.float()).abs()
+    ref = plain.float().abs()
+    assert d.max().item() <= 2e-2 * ref.max().item()
+    assert d.mean().item() <= 4e-3 * ref.mean().item()
